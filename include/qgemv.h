@@ -1,0 +1,117 @@
+/*
+ * qgemv.h -- C ABI of the MI355X (gfx950) quantized mat-vec library
+ * (rust-inference_amd/libqgemv.so).
+ *
+ * It replaces the wgpu backend of yudono/rust-inference on the path
+ * QuantizedMatrix::mat_vec_mul (src/quant.rs:178-206) ->
+ * GpuContext::mat_vec_mul (src/gpu_backend.rs:429-450).  Plain pointers and
+ * sizes only.  Matrix types are the GGML ids of src/gguf.rs:43-59:
+ * F32=0 F16=1 Q4_0=2 Q5_0=6 Q8_0=8 Q4_K=12 Q5_K=13 Q6_K=14 (Q4_1, Q5_1,
+ * Q8_1, Q2_K, Q3_K are rejected, as src/model.rs:176-179 skips them).
+ *
+ * Layout: a matrix is the raw GGUF byte stream; element (r, c) is flat index
+ * r*cols + c and block b starts at byte b*block_bytes (src/quant.rs:82-86,
+ * 195-203).  Rows may straddle blocks (cols % block_elems != 0).
+ *
+ * Every function returns a qg_status (0 = QG_OK) and never aborts; a caller
+ * maps a nonzero status to its CPU path, as the reference falls back to
+ * fallback_cpu (src/gpu_backend.rs:438-447).  Contexts are not thread safe:
+ * one per host thread, as the reference's GpuContext is !Sync
+ * (src/gpu_backend.rs:17).  `stream` arguments are hipStream_t values passed
+ * as void* (NULL = the context's own stream).
+ */
+#ifndef QGEMV_H
+#define QGEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum qg_status {
+    QG_OK = 0,
+    QG_ERR_INVALID_ARG = 1,      /* NULL pointer, bad device, misaligned buffer */
+    QG_ERR_UNSUPPORTED_TYPE = 2, /* type id outside the supported set */
+    QG_ERR_SHORT_DATA = 3,       /* fewer bytes than ceil(rows*cols/bs)*bb */
+    QG_ERR_NO_DEVICE = 4,        /* no HIP device */
+    QG_ERR_HIP = 5,              /* a HIP runtime call failed */
+    QG_ERR_OUT_OF_MEMORY = 6,
+    QG_ERR_SHAPE = 7             /* length / shape mismatch (quant.rs:179-180 asserts) */
+} qg_status;
+
+typedef struct qg_ctx qg_ctx;   /* one device + stream + staging buffers */
+typedef struct qg_mat qg_mat;   /* one matrix resident in HBM */
+
+/* Replaces GpuContext::try_init (src/gpu_backend.rs:317-348): opens HIP
+ * device `device`, creates a stream.  QG_ERR_NO_DEVICE where the reference
+ * returns None. */
+int qg_init(int device, qg_ctx **out);
+/* Releases the context (the reference drops GpuContext). Frees its matrices. */
+int qg_destroy(qg_ctx *ctx);
+
+/* Human-readable text for a status / the context's last error. */
+const char *qg_status_string(int status);
+const char *qg_last_error(const qg_ctx *ctx);
+
+/* Replaces QuantizedMatrix::new (src/quant.rs:53-55) at the load_mat! site
+ * (src/model.rs:197-203, lm_head 221-226): copies the raw GGUF bytes to HBM
+ * once; they stay resident and are never expanded.  nbytes must cover
+ * ceil(rows*cols/block_elems) blocks (extra bytes are ignored). */
+int qg_upload(qg_ctx *ctx, const void *raw, size_t nbytes, uint32_t ggml_type,
+              size_t rows, size_t cols, qg_mat **out);
+/* Wraps bytes already in HBM (device pointer, at least 16-byte aligned,
+ * followed by >= 512 readable bytes) without copying; the caller keeps them
+ * alive for the handle's lifetime. */
+int qg_wrap_device(qg_ctx *ctx, const void *d_raw, size_t nbytes, uint32_t ggml_type,
+                   size_t rows, size_t cols, qg_mat **out);
+int qg_mat_free(qg_ctx *ctx, qg_mat *mat);
+int qg_mat_info(const qg_mat *mat, uint32_t *ggml_type, size_t *rows, size_t *cols,
+                size_t *nbytes);
+/* Kernel choice fixed at upload: 1 = fast team kernel, 0 = generic. */
+int qg_mat_kernel_kind(const qg_mat *mat);
+
+/* Device-resident mat-vec: y[r] = sum_c W[r,c] * x[c] (src/quant.rs:178-206).
+ * d_x: cols floats, d_y: rows floats, both device pointers (d_x 16-byte
+ * aligned for the fast kernel; otherwise the generic kernel runs).
+ * Asynchronous on `stream`. */
+int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, void *stream);
+
+/* Host-buffer drop-in for QuantizedMatrix::mat_vec_mul(x, out, Some(gpu))
+ * (src/quant.rs:178-186): synchronous; stages x/y through pinned buffers
+ * allocated once per context.  x: cols floats, y: rows floats. */
+int qg_matvec_host(qg_ctx *ctx, const qg_mat *mat, const float *x, float *y);
+
+/* Exact drop-in for GpuContext::mat_vec_mul(weight_data, dtype, x, out, rows,
+ * cols) (src/gpu_backend.rs:429-437): device copies are keyed by
+ * (weight_data, nbytes, dtype, rows, cols), uploaded on first sight and
+ * reused afterwards (weights are immutable after Model::load). */
+int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint32_t dtype,
+                       const float *x, float *out, size_t rows, size_t cols);
+
+/* quant::dequantize (src/quant.rs:356-372) on device: rows*cols f32 values,
+ * bit-exact with the CPU path.  The reference's Vec for Q4_K/Q5_K is padded
+ * to whole blocks; only the first rows*cols values are written here. */
+int qg_dequant_dev(qg_ctx *ctx, const qg_mat *mat, float *d_out, void *stream);
+int qg_dequant_host(qg_ctx *ctx, const qg_mat *mat, float *out);
+
+/* QuantizedMatrix::dequantize_row (src/quant.rs:152-174) on device, with the
+ * reference's placement for rows that straddle blocks: only the positions the
+ * reference writes are written (the caller zero-fills, as transformer.rs:74's
+ * fresh vec! does). */
+int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_out,
+                          void *stream);
+
+/* Waits for all work on the context's stream. */
+int qg_synchronize(qg_ctx *ctx);
+/* The context's stream (a hipStream_t). */
+void *qg_stream(qg_ctx *ctx);
+/* Number of compute units of the context's device. */
+int qg_device_cu_count(const qg_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QGEMV_H */

@@ -1,0 +1,244 @@
+"""rust-inference_amd -- MI355X (gfx950) quantized mat-vec for yudono/rust-inference.
+
+Python plumbing over the C ABI of ``include/qgemv.h`` (``libqgemv.so``, built
+in-tree by ``__graft_entry__.build()``).  The product is the HIP library; this
+module only binds it with ctypes for tests and ``bench.py``, and mirrors the
+reference's host API names so that tests read like calls of the reference:
+
+* ``GpuContext.try_init()``            -- src/gpu_backend.rs:317-348
+* ``GpuContext.mat_vec_mul(...)``      -- src/gpu_backend.rs:429-450
+* ``QuantizedMatrix(data, dtype, rows, cols)`` and ``.mat_vec_mul(x, out, gpu)``
+                                        -- src/quant.rs:44-55, 178-206
+
+There is no CPU fallback in this package: if the library is missing or no
+HIP device is present the calls raise.
+
+The directory name contains a hyphen, so load it with importlib under the
+module name ``rust_inference_amd`` (``__graft_entry__.load_package()`` does).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import re
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libqgemv.so"
+HEADER_PATH = HERE.parent / "include" / "qgemv.h"
+
+# GGML type ids, src/gguf.rs:43-59
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = (
+    0, 1, 2, 3, 6, 7, 8, 9, 10, 11, 12, 13, 14)
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0",
+              Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+TYPE_IDS = {v: k for k, v in TYPE_NAMES.items()}
+SUPPORTED = tuple(TYPE_NAMES)
+# (block elements, block bytes), src/quant.rs:57-79
+BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_0: (32, 18), Q5_0: (32, 22),
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+QG_OK = 0
+STATUS = {0: "QG_OK", 1: "QG_ERR_INVALID_ARG", 2: "QG_ERR_UNSUPPORTED_TYPE",
+          3: "QG_ERR_SHORT_DATA", 4: "QG_ERR_NO_DEVICE", 5: "QG_ERR_HIP",
+          6: "QG_ERR_OUT_OF_MEMORY", 7: "QG_ERR_SHAPE"}
+
+
+def nbytes_for(dtype: int, rows: int, cols: int) -> int:
+    """ceil(rows*cols/bs)*bb -- the byte count src/model.rs:167-175 reads."""
+    bs, bb = BLOCK[dtype]
+    return -(-(rows * cols) // bs) * bb
+
+
+class QgemvError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what}: {STATUS.get(status, status)}")
+        self.status = status
+
+
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+_U32 = ctypes.c_uint32
+_FP = ctypes.POINTER(ctypes.c_float)
+
+_SIGS = {
+    "qg_init": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_P)]),
+    "qg_destroy": (ctypes.c_int, [_P]),
+    "qg_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "qg_last_error": (ctypes.c_char_p, [_P]),
+    "qg_upload": (ctypes.c_int, [_P, _P, _SZ, _U32, _SZ, _SZ, ctypes.POINTER(_P)]),
+    "qg_wrap_device": (ctypes.c_int, [_P, _P, _SZ, _U32, _SZ, _SZ, ctypes.POINTER(_P)]),
+    "qg_mat_free": (ctypes.c_int, [_P, _P]),
+    "qg_mat_info": (ctypes.c_int, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_SZ),
+                                   ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "qg_mat_kernel_kind": (ctypes.c_int, [_P]),
+    "qg_matvec_dev": (ctypes.c_int, [_P, _P, _P, _P, _P]),
+    "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
+    "qg_gpu_mat_vec_mul": (ctypes.c_int, [_P, _P, _SZ, _U32, _P, _P, _SZ, _SZ]),
+    "qg_dequant_dev": (ctypes.c_int, [_P, _P, _P, _P]),
+    "qg_dequant_host": (ctypes.c_int, [_P, _P, _P]),
+    "qg_dequantize_row_dev": (ctypes.c_int, [_P, _P, _SZ, _P, _P]),
+    "qg_synchronize": (ctypes.c_int, [_P]),
+    "qg_stream": (_P, [_P]),
+    "qg_device_cu_count": (ctypes.c_int, [_P]),
+}
+
+_lib = None
+
+
+def header_symbols(path: pathlib.Path = HEADER_PATH) -> list[str]:
+    """Every function the C ABI header declares."""
+    text = path.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qg_[a-z0-9_]+)\s*\(", text)))
+
+
+def load_library(path: pathlib.Path | str = LIB_PATH):
+    """Load libqgemv.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None and path == LIB_PATH:
+        return _lib
+    p = pathlib.Path(path)
+    # torch ships its own libamdhip64.so with the same SONAME as /opt/rocm's.
+    # Importing torch first makes this library bind to that already-loaded
+    # runtime, so a process that also uses torch tensors has one HIP runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    if not p.exists():
+        raise ImportError(f"{p} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path == LIB_PATH:
+        _lib = lib
+    return lib
+
+
+def _ptr(a):
+    """Address of a numpy array's data or a torch tensor's storage."""
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):
+        return ctypes.c_void_p(a.data_ptr())
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class GpuContext:
+    """One HIP device and stream (mirror of the reference's GpuContext)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = _P()
+        rc = self.lib.qg_init(device, ctypes.byref(h))
+        if rc != QG_OK:
+            raise QgemvError(rc, f"qg_init(device={device})")
+        self.h = h
+        self._mats = []
+
+    @classmethod
+    def try_init(cls, device: int = 0):
+        """None when no device can be opened (src/gpu_backend.rs:317-348)."""
+        try:
+            return cls(device)
+        except (QgemvError, OSError, ImportError):
+            return None
+
+    def check(self, rc: int, what: str):
+        if rc != QG_OK:
+            err = self.lib.qg_last_error(self.h)
+            raise QgemvError(rc, f"{what} ({err.decode() if err else ''})")
+
+    def close(self):
+        if self.h:
+            self.lib.qg_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return self.lib.qg_stream(self.h) or 0
+
+    @property
+    def cu_count(self) -> int:
+        return self.lib.qg_device_cu_count(self.h)
+
+    def synchronize(self):
+        self.check(self.lib.qg_synchronize(self.h), "qg_synchronize")
+
+    def upload(self, raw, dtype: int, rows: int, cols: int) -> "DeviceMatrix":
+        m = _P()
+        rc = self.lib.qg_upload(self.h, _ptr(raw), raw.nbytes, dtype, rows, cols, ctypes.byref(m))
+        self.check(rc, "qg_upload")
+        return DeviceMatrix(self, m, dtype, rows, cols)
+
+    def mat_vec_mul(self, weight_data, dtype: int, x, out, rows: int, cols: int):
+        """src/gpu_backend.rs:429-437 signature; host numpy arrays in and out."""
+        rc = self.lib.qg_gpu_mat_vec_mul(self.h, _ptr(weight_data), weight_data.nbytes, dtype,
+                                         _ptr(x), _ptr(out), rows, cols)
+        self.check(rc, "qg_gpu_mat_vec_mul")
+
+
+class DeviceMatrix:
+    """A matrix resident in HBM (qg_mat)."""
+
+    def __init__(self, ctx: GpuContext, h, dtype: int, rows: int, cols: int):
+        self.ctx, self.h, self.dtype, self.rows, self.cols = ctx, h, dtype, rows, cols
+
+    def free(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.qg_mat_free(self.ctx.h, self.h), "qg_mat_free")
+            self.h = None
+
+    @property
+    def kernel_kind(self) -> int:
+        return self.ctx.lib.qg_mat_kernel_kind(self.h)
+
+    def matvec_dev(self, d_x, d_y, stream=None):
+        """d_x, d_y: torch device tensors (float32)."""
+        rc = self.ctx.lib.qg_matvec_dev(self.ctx.h, self.h, _ptr(d_x), _ptr(d_y),
+                                        ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_matvec_dev")
+
+    def matvec_host(self, x, y):
+        self.ctx.check(self.ctx.lib.qg_matvec_host(self.ctx.h, self.h, _ptr(x), _ptr(y)),
+                       "qg_matvec_host")
+
+    def dequant_host(self, out):
+        self.ctx.check(self.ctx.lib.qg_dequant_host(self.ctx.h, self.h, _ptr(out)),
+                       "qg_dequant_host")
+
+    def dequant_dev(self, d_out, stream=None):
+        rc = self.ctx.lib.qg_dequant_dev(self.ctx.h, self.h, _ptr(d_out),
+                                         ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_dequant_dev")
+
+    def dequantize_row_dev(self, row: int, d_out, stream=None):
+        rc = self.ctx.lib.qg_dequantize_row_dev(self.ctx.h, self.h, row, _ptr(d_out),
+                                                ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_dequantize_row_dev")
+
+
+class QuantizedMatrix:
+    """Mirror of src/quant.rs:44-55: raw GGUF bytes plus dtype/rows/cols."""
+
+    def __init__(self, data, dtype: int, rows: int, cols: int):
+        self.data, self.dtype, self.rows, self.cols = data, dtype, rows, cols
+
+    def mat_vec_mul(self, x, out, gpu: GpuContext):
+        """src/quant.rs:178-186 with Some(gpu); this package has no CPU branch."""
+        if len(x) != self.cols or len(out) != self.rows:     # quant.rs:179-180
+            raise QgemvError(7, "mat_vec_mul length mismatch")
+        gpu.mat_vec_mul(self.data, self.dtype, x, out, self.rows, self.cols)
+
+
+def env_flag(name: str) -> bool:
+    return os.environ.get(name, "") not in ("", "0")

@@ -1,0 +1,69 @@
+// qg_common.h -- shared definitions for the gfx950 quantized GEMV library.
+//
+// Layout facts restated from yudono/rust-inference:
+//   GGML type ids                 src/gguf.rs:43-59
+//   (block elements, block bytes) src/quant.rs:57-79
+//   element (r, c) = flat index r*cols + c; block b starts at byte b*bb
+//                                 src/quant.rs:82-86, 195-203
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qg {
+
+enum : uint32_t {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8,
+    T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14
+};
+
+constexpr uint32_t block_elems(uint32_t t)
+{
+    return t == T_F32 || t == T_F16 ? 1u
+         : t == T_Q4_0 || t == T_Q5_0 || t == T_Q8_0 ? 32u
+         : t == T_Q4_K || t == T_Q5_K || t == T_Q6_K ? 256u : 0u;
+}
+
+constexpr uint32_t block_bytes(uint32_t t)
+{
+    return t == T_F32 ? 4u : t == T_F16 ? 2u : t == T_Q8_0 ? 34u : t == T_Q4_0 ? 18u
+         : t == T_Q5_0 ? 22u : t == T_Q4_K ? 144u : t == T_Q5_K ? 176u
+         : t == T_Q6_K ? 210u : 0u;
+}
+
+constexpr bool type_supported(uint32_t t) { return block_bytes(t) != 0; }
+
+// Bytes of zero padding after every uploaded matrix: the GEMV kernels read
+// whole aligned windows and two-block items, which may run up to this far past
+// the last block of the matrix.
+constexpr size_t kTailPad = 512;
+
+// How a matrix is mat-vec'd; fixed at upload time.
+struct Plan {
+    int kind;              // 0 = generic per-element kernel, 1 = team kernel
+    uint32_t g;            // rows per row group (team kernel)
+    uint32_t n_groups;     // ceil(rows / g)
+    uint32_t ni;           // items (64- or 32-element units) per row group
+    uint32_t tsub;         // team lanes if <= 64, else 0 (one team = one workgroup)
+    uint32_t ts;           // team lanes
+    uint64_t group_bytes;  // bytes per row group
+    uint32_t n_teams;      // teams in the grid
+    uint32_t grid, block;  // launch shape
+};
+
+}  // namespace qg
+
+// Launchers implemented in qgemv_kernels.hip (C++ linkage, library-internal).
+struct ihipStream_t;
+namespace qg {
+int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p);
+int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
+                size_t cols, const float *x, float *y, ihipStream_t *stream);
+int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
+                        const float *x, float *y, ihipStream_t *stream);
+int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,
+                   ihipStream_t *stream);
+int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
+                          size_t row, float *out, ihipStream_t *stream);
+int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
+}  // namespace qg

@@ -1,0 +1,400 @@
+// qgemv_api.cpp -- the C ABI of include/qgemv.h on HIP.
+//
+// Replaces yudono/rust-inference's GpuContext (src/gpu_backend.rs:14-18,
+// 315-567).  Where the reference creates five wgpu buffers and re-uploads the
+// whole weight matrix on every call (gpu_backend.rs:468-514) and then blocks
+// on a staging readback (525-540), this keeps each matrix resident in HBM
+// from upload on, and stages host vectors through pinned buffers allocated
+// once per context.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <new>
+#include <set>
+#include <string>
+#include <tuple>
+
+#include "qg_common.h"
+#include "qgemv.h"
+
+struct qg_mat {
+    qg_ctx *ctx;
+    uint8_t *d;        // device bytes (nbytes data + kTailPad zeros)
+    size_t nbytes;     // bytes the kernels may treat as data
+    uint32_t type;
+    size_t rows, cols;
+    bool owned;
+    qg::Plan plan;
+};
+
+struct qg_ctx {
+    int device = 0;
+    int n_cu = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    float *h_x = nullptr, *h_y = nullptr;   // pinned staging
+    size_t h_x_cap = 0, h_y_cap = 0;
+    float *d_x = nullptr, *d_y = nullptr;   // device staging
+    size_t d_x_cap = 0, d_y_cap = 0;
+    std::set<qg_mat *> mats;
+    std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
+};
+
+namespace {
+
+int fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess)
+{
+    if (ctx) {
+        char buf[256];
+        if (e != hipSuccess)
+            snprintf(buf, sizeof buf, "%s: %s", what, hipGetErrorString(e));
+        else
+            snprintf(buf, sizeof buf, "%s", what);
+        ctx->err = buf;
+    }
+    return status;
+}
+
+#define QG_HIP(ctx, call)                                                   \
+    do {                                                                    \
+        hipError_t e_ = (call);                                             \
+        if (e_ != hipSuccess) return fail((ctx), QG_ERR_HIP, #call, e_);    \
+    } while (0)
+
+bool mul_overflows(size_t a, size_t b, size_t *out)
+{
+    if (a != 0 && b > SIZE_MAX / a) return true;
+    *out = a * b;
+    return false;
+}
+
+// Bytes a rows x cols matrix of `type` occupies: ceil(rows*cols/bs)*bb.
+int required_bytes(uint32_t type, size_t rows, size_t cols, size_t *need)
+{
+    if (!qg::type_supported(type)) return QG_ERR_UNSUPPORTED_TYPE;
+    size_t n;
+    if (mul_overflows(rows, cols, &n)) return QG_ERR_SHAPE;
+    const size_t bs = qg::block_elems(type), bb = qg::block_bytes(type);
+    size_t nb = n / bs + (n % bs != 0);
+    if (mul_overflows(nb, bb, need)) return QG_ERR_SHAPE;
+    return QG_OK;
+}
+
+hipStream_t pick(qg_ctx *ctx, void *stream)
+{
+    return stream ? (hipStream_t)stream : ctx->stream;
+}
+
+int grow_pinned(qg_ctx *ctx, float **p, size_t *cap, size_t n)
+{
+    if (*cap >= n) return QG_OK;
+    if (*p) (void)hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    hipError_t e = hipHostMalloc((void **)p, (n ? n : 1) * sizeof(float), hipHostMallocDefault);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipHostMalloc", e);
+    *cap = n;
+    return QG_OK;
+}
+
+int grow_device(qg_ctx *ctx, float **p, size_t *cap, size_t n)
+{
+    if (*cap >= n) return QG_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    hipError_t e = hipMalloc((void **)p, (n ? n : 1) * sizeof(float));
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc staging", e);
+    *cap = n;
+    return QG_OK;
+}
+
+int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, size_t cols,
+            bool owned, qg_mat **out)
+{
+    qg_mat *m = new (std::nothrow) qg_mat;
+    if (!m) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "host allocation");
+    m->ctx = ctx;
+    m->d = d;
+    m->nbytes = nbytes;
+    m->type = type;
+    m->rows = rows;
+    m->cols = cols;
+    m->owned = owned;
+    if (qg::make_plan(type, rows, cols, ctx->n_cu, &m->plan) != 0) {
+        delete m;
+        return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
+    }
+    ctx->mats.insert(m);
+    *out = m;
+    return QG_OK;
+}
+
+void drop_mat(qg_ctx *ctx, qg_mat *m)
+{
+    if (m->owned && m->d) (void)hipFree(m->d);
+    ctx->mats.erase(m);
+    for (auto it = ctx->keyed.begin(); it != ctx->keyed.end();) {
+        if (it->second == m)
+            it = ctx->keyed.erase(it);
+        else
+            ++it;
+    }
+    delete m;
+}
+
+int check_mat(qg_ctx *ctx, const qg_mat *mat)
+{
+    if (!ctx) return QG_ERR_INVALID_ARG;
+    if (!mat || mat->ctx != ctx) return fail(ctx, QG_ERR_INVALID_ARG, "matrix not of this context");
+    return QG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *qg_status_string(int s)
+{
+    switch (s) {
+    case QG_OK: return "ok";
+    case QG_ERR_INVALID_ARG: return "invalid argument";
+    case QG_ERR_UNSUPPORTED_TYPE: return "unsupported GGML type";
+    case QG_ERR_SHORT_DATA: return "raw data shorter than the matrix needs";
+    case QG_ERR_NO_DEVICE: return "no HIP device";
+    case QG_ERR_HIP: return "HIP runtime error";
+    case QG_ERR_OUT_OF_MEMORY: return "out of memory";
+    case QG_ERR_SHAPE: return "shape mismatch";
+    default: return "unknown status";
+    }
+}
+
+const char *qg_last_error(const qg_ctx *ctx) { return ctx ? ctx->err.c_str() : ""; }
+
+int qg_init(int device, qg_ctx **out)
+{
+    if (!out) return QG_ERR_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return QG_ERR_NO_DEVICE;
+    if (device < 0 || device >= n) return QG_ERR_INVALID_ARG;
+    if (hipSetDevice(device) != hipSuccess) return QG_ERR_HIP;
+    qg_ctx *ctx = new (std::nothrow) qg_ctx;
+    if (!ctx) return QG_ERR_OUT_OF_MEMORY;
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        delete ctx;
+        return QG_ERR_HIP;
+    }
+    ctx->n_cu = prop.multiProcessorCount;
+    // default-priority stream (hipStreamCreateWithFlags keeps the default priority)
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return QG_ERR_HIP;
+    }
+    *out = ctx;
+    return QG_OK;
+}
+
+int qg_destroy(qg_ctx *ctx)
+{
+    if (!ctx) return QG_ERR_INVALID_ARG;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    while (!ctx->mats.empty()) drop_mat(ctx, *ctx->mats.begin());
+    if (ctx->h_x) (void)hipHostFree(ctx->h_x);
+    if (ctx->h_y) (void)hipHostFree(ctx->h_y);
+    if (ctx->d_x) (void)hipFree(ctx->d_x);
+    if (ctx->d_y) (void)hipFree(ctx->d_y);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return QG_OK;
+}
+
+int qg_upload(qg_ctx *ctx, const void *raw, size_t nbytes, uint32_t type, size_t rows,
+              size_t cols, qg_mat **out)
+{
+    if (!ctx || !out) return QG_ERR_INVALID_ARG;
+    *out = nullptr;
+    size_t need = 0;
+    int rc = required_bytes(type, rows, cols, &need);
+    if (rc != QG_OK) return fail(ctx, rc, rc == QG_ERR_SHAPE ? "rows*cols overflows" : "unsupported type");
+    if (nbytes < need) return fail(ctx, QG_ERR_SHORT_DATA, "raw data shorter than the matrix needs");
+    if (need > 0 && !raw) return fail(ctx, QG_ERR_INVALID_ARG, "raw == NULL");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    uint8_t *d = nullptr;
+    hipError_t e = hipMalloc((void **)&d, need + qg::kTailPad);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc matrix", e);
+    e = hipMemcpy(d, raw, need, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(d + need, 0, qg::kTailPad);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return fail(ctx, QG_ERR_HIP, "upload", e);
+    }
+    rc = new_mat(ctx, d, need, type, rows, cols, true, out);
+    if (rc != QG_OK) (void)hipFree(d);
+    return rc;
+}
+
+int qg_wrap_device(qg_ctx *ctx, const void *d_raw, size_t nbytes, uint32_t type, size_t rows,
+                   size_t cols, qg_mat **out)
+{
+    if (!ctx || !out) return QG_ERR_INVALID_ARG;
+    *out = nullptr;
+    size_t need = 0;
+    int rc = required_bytes(type, rows, cols, &need);
+    if (rc != QG_OK) return fail(ctx, rc, "unsupported type or shape");
+    if (nbytes < need) return fail(ctx, QG_ERR_SHORT_DATA, "raw data shorter than the matrix needs");
+    if (!d_raw || ((uintptr_t)d_raw & 15u)) return fail(ctx, QG_ERR_INVALID_ARG, "device pointer NULL or not 16-byte aligned");
+    return new_mat(ctx, (uint8_t *)d_raw, need, type, rows, cols, false, out);
+}
+
+int qg_mat_free(qg_ctx *ctx, qg_mat *mat)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    drop_mat(ctx, mat);
+    return QG_OK;
+}
+
+int qg_mat_info(const qg_mat *mat, uint32_t *type, size_t *rows, size_t *cols, size_t *nbytes)
+{
+    if (!mat) return QG_ERR_INVALID_ARG;
+    if (type) *type = mat->type;
+    if (rows) *rows = mat->rows;
+    if (cols) *cols = mat->cols;
+    if (nbytes) *nbytes = mat->nbytes;
+    return QG_OK;
+}
+
+int qg_mat_kernel_kind(const qg_mat *mat) { return mat ? mat->plan.kind : -1; }
+
+int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, void *stream)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    if (mat->rows == 0) return QG_OK;
+    if (!d_y || (mat->cols > 0 && !d_x)) return fail(ctx, QG_ERR_INVALID_ARG, "x or y is NULL");
+    if (((uintptr_t)d_x & 3u) || ((uintptr_t)d_y & 3u)) return fail(ctx, QG_ERR_INVALID_ARG, "x/y not 4-byte aligned");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    hipStream_t st = pick(ctx, stream);
+    int lr;
+    if (mat->cols == 0)                                   // out.fill(0.0), quant.rs:189
+        lr = qg::launch_fill(d_y, mat->rows, 0.0f, (ihipStream_t *)st);
+    else if (mat->plan.kind == 1 && ((uintptr_t)d_x & 15u) == 0)
+        lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, mat->cols, d_x,
+                             d_y, (ihipStream_t *)st);
+    else
+        lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, mat->cols, d_x, d_y,
+                                     (ihipStream_t *)st);
+    if (lr != 0) return fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError());
+    return QG_OK;
+}
+
+int qg_matvec_host(qg_ctx *ctx, const qg_mat *mat, const float *x, float *y)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    if (mat->rows == 0) return QG_OK;
+    if (!y || (mat->cols > 0 && !x)) return fail(ctx, QG_ERR_INVALID_ARG, "x or y is NULL");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if ((rc = grow_pinned(ctx, &ctx->h_x, &ctx->h_x_cap, mat->cols)) ||
+        (rc = grow_pinned(ctx, &ctx->h_y, &ctx->h_y_cap, mat->rows)) ||
+        (rc = grow_device(ctx, &ctx->d_x, &ctx->d_x_cap, mat->cols)) ||
+        (rc = grow_device(ctx, &ctx->d_y, &ctx->d_y_cap, mat->rows)))
+        return rc;
+    if (mat->cols) memcpy(ctx->h_x, x, mat->cols * sizeof(float));
+    if (mat->cols)
+        QG_HIP(ctx, hipMemcpyAsync(ctx->d_x, ctx->h_x, mat->cols * sizeof(float),
+                                   hipMemcpyHostToDevice, ctx->stream));
+    rc = qg_matvec_dev(ctx, mat, ctx->d_x, ctx->d_y, ctx->stream);
+    if (rc) return rc;
+    QG_HIP(ctx, hipMemcpyAsync(ctx->h_y, ctx->d_y, mat->rows * sizeof(float), hipMemcpyDeviceToHost,
+                               ctx->stream));
+    QG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    memcpy(y, ctx->h_y, mat->rows * sizeof(float));
+    return QG_OK;
+}
+
+int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint32_t dtype,
+                       const float *x, float *out, size_t rows, size_t cols)
+{
+    if (!ctx) return QG_ERR_INVALID_ARG;
+    auto key = std::make_tuple((uintptr_t)weight_data, nbytes, dtype, rows, cols);
+    qg_mat *m = nullptr;
+    auto it = ctx->keyed.find(key);
+    if (it != ctx->keyed.end()) {
+        m = it->second;
+    } else {
+        int rc = qg_upload(ctx, weight_data, nbytes, dtype, rows, cols, &m);
+        if (rc) return rc;
+        ctx->keyed[key] = m;
+    }
+    return qg_matvec_host(ctx, m, x, out);
+}
+
+int qg_dequant_dev(qg_ctx *ctx, const qg_mat *mat, float *d_out, void *stream)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    size_t n = mat->rows * mat->cols;
+    if (n == 0) return QG_OK;
+    if (!d_out) return fail(ctx, QG_ERR_INVALID_ARG, "out is NULL");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if (qg::launch_dequant(mat->type, mat->d, n, d_out, (ihipStream_t *)pick(ctx, stream)))
+        return fail(ctx, QG_ERR_HIP, "dequant launch", hipGetLastError());
+    return QG_OK;
+}
+
+int qg_dequant_host(qg_ctx *ctx, const qg_mat *mat, float *out)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    size_t n = mat->rows * mat->cols;
+    if (n == 0) return QG_OK;
+    if (!out) return fail(ctx, QG_ERR_INVALID_ARG, "out is NULL");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    float *d = nullptr;
+    hipError_t e = hipMalloc((void **)&d, n * sizeof(float));
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc dequant", e);
+    rc = qg_dequant_dev(ctx, mat, d, ctx->stream);
+    if (rc == QG_OK) {
+        e = hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) rc = fail(ctx, QG_ERR_HIP, "dequant readback", e);
+    }
+    (void)hipFree(d);
+    return rc;
+}
+
+int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_out, void *stream)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    if (row >= mat->rows) return fail(ctx, QG_ERR_SHAPE, "row out of range");   // quant.rs:153
+    if (!d_out) return fail(ctx, QG_ERR_INVALID_ARG, "out is NULL");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if (qg::launch_dequantize_row(mat->type, mat->d, mat->rows, mat->cols, row, d_out,
+                                  (ihipStream_t *)pick(ctx, stream)))
+        return fail(ctx, QG_ERR_HIP, "dequantize_row launch", hipGetLastError());
+    return QG_OK;
+}
+
+int qg_synchronize(qg_ctx *ctx)
+{
+    if (!ctx) return QG_ERR_INVALID_ARG;
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    QG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return QG_OK;
+}
+
+void *qg_stream(qg_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int qg_device_cu_count(const qg_ctx *ctx) { return ctx ? ctx->n_cu : 0; }
+
+}  // extern "C"
