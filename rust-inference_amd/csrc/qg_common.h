@@ -49,6 +49,12 @@ struct Plan {
     uint64_t group_bytes;  // bytes per row group
     uint32_t n_teams;      // teams in the grid
     uint32_t grid, block;  // launch shape
+    uint32_t R;            // row groups per batch
+    uint32_t n_batches;    // ceil(n_groups / R)
+    uint32_t per_team;     // batches each team runs
+    uint32_t wpt;          // waves per team when a team spans several waves
+    uint32_t lds;          // dynamic LDS bytes (x staged per workgroup)
+    const void *fn;        // kernel chosen for this matrix
 };
 
 }  // namespace qg
@@ -58,7 +64,9 @@ struct ihipStream_t;
 namespace qg {
 int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p);
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
-                size_t cols, const float *x, float *y, ihipStream_t *stream);
+                size_t cols, const float *x, float *y, uint8_t *img, ihipStream_t *stream);
+// bytes of the fixed-point x image the quant-type kernels need for `cols`
+size_t x_image_bytes(size_t cols);
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                         const float *x, float *y, ihipStream_t *stream);
 int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,

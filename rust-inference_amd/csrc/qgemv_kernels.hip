@@ -10,10 +10,13 @@
 //   deq_row_k<T>      one row with the reference's straddle placement
 //                     (quant.rs:152-174)
 //   gemv_generic<T>   one wave per row, per-element decode; any shape
-//   gemv_team<T,..>   the fast path: a "team" of lanes owns one row group,
-//                     each lane one 64-weight item (32 for F32) whose x slice
-//                     stays in VGPRs for every row group the team visits
+//   gemv_team<T,..>   the fast path: x staged once per workgroup in LDS; a
+//                     "team" of lanes owns whole row groups, each lane one
+//                     64-weight item (32 for F32) whose x slice stays in VGPRs
+//                     for every row group the team visits
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "qg_common.h"
 
@@ -71,6 +74,19 @@ __device__ __forceinline__ void k4sm(uint32_t j, uint32_t s0, uint32_t s1, uint3
         sc = ((s2 >> sh) & 15u) | (((s0 >> (sh + 6u)) & 3u) << 4);
         m = ((s2 >> (sh + 4u)) & 15u) | (((s1 >> (sh + 6u)) & 3u) << 4);
     }
+}
+
+// The scales and mins of sub-blocks j = 2p and 2p+1 (quant.rs:606-615) as
+// bytes 0 and 1 of SC and MN, branch-free for a per-lane pair index p.
+__device__ __forceinline__ void k4pair(uint32_t p, uint32_t s0, uint32_t s1, uint32_t s2,
+                                       uint32_t &SC, uint32_t &MN)
+{
+    const bool hs = p >= 2u;                     // j >= 4: 4+2 bit splice
+    const uint32_t sh = (p & 1u) * 16u;          // 8 * (j mod 4)
+    const uint32_t A = hs ? s2 : s0, C = hs ? (s2 >> 4) : s1;
+    const uint32_t mA = hs ? 0x0F0Fu : 0x3F3Fu, mB = hs ? 0x3030u : 0u;
+    SC = ((A >> sh) & mA) | ((s0 >> (sh + 2u)) & mB);
+    MN = ((C >> sh) & mA) | ((s1 >> (sh + 2u)) & mB);
 }
 
 // ------------------------------------------- bit-exact element decoders
@@ -217,14 +233,141 @@ __global__ void __launch_bounds__(256) gemv_generic(const uint8_t *__restrict__ 
     if (lane == 0) y[row] = acc;
 }
 
+// ------------------------------------------------------ x in fixed point
+//
+// Quant types multiply integer codes by x with integer dot products.  While a
+// workgroup stages x into LDS it rewrites every 32-element segment of x, with
+// m = max |x| over the segment and k = 8388000 / m, as the 24-bit integers
+// Y = rint(x * k) (|Y| < 2^23), split into bytes d0, d1 (unsigned) and d2
+// (signed): Y = d0 + 256*d1 + 65536*d2.  For weight codes q in 0..127
+//     sum q*Y = udot4(q, d0) + 256 * udot4(q, d1) + 65536 * sdot4(q, d2)
+// exactly, and sum q*x = (sum q*Y) / k, within about 2^-23 of m per element.
+// Every segment also keeps {1/k, sum x[0..16), sum x[16..32), sum (Y & 0xFFFF)}.
+// F16 and F32 weights keep x in f32.
+//
+// LDS layout (planes): segment g at byte 96g + 16(g/2) holds 32 bytes of d0,
+// 32 of d1, 32 of d2 (16 bytes of padding per segment pair keep the per-lane
+// reads below conflict-free); the segment records follow at `meta`.  Q4_0
+// stores each segment's planes in even-then-odd element order, matching its
+// interleaved nibbles.  f32 layout: float4 i of x at xl4[i + i/16].
+
+constexpr float kFix = 8388000.0f;
+
+__device__ __forceinline__ uint32_t plane_off(uint32_t g) { return 96u * g + 16u * (g >> 1); }
+__host__ __device__ constexpr uint32_t planes_bytes(uint32_t cols)
+{
+    return (cols / 64) * 208u + ((cols / 32) & 1u) * 96u;
+}
+
+// DPP move (gfx9 encodings): quad_perm 0x00-0xFF, row_mirror 0x140,
+// row_half_mirror 0x141, row_bcast15 0x142, row_bcast31 0x143.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 ROW_MASK, 0xF, false));
+}
+template <int CTRL> __device__ __forceinline__ int dppi(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// Sum over aligned groups of N lanes (N = 8, 16, 32, 64); the group's last
+// lane ends up holding the group sum.
+template <int N> __device__ __forceinline__ float group_sum(float v)
+{
+    v += dpp<0xB1>(v);                       // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);                       // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);                      // row_half_mirror
+    if (N >= 16) v += dpp<0x140>(v);         // row_mirror
+    if (N >= 32) v += dpp<0x142, 0xA>(v);    // row_bcast15 -> rows 1, 3
+    if (N >= 64) v += dpp<0x143, 0xC>(v);    // row_bcast31 -> rows 2, 3
+    return v;
+}
+
+// Stage float4 i of x (already loaded into v) as fixed-point planes; each
+// aligned group of 8 lanes holds one 32-element segment and must be active
+// together.
+template <bool EVEN_ODD>
+__device__ __forceinline__ void stage_planes1(float4 v, uint32_t i, uint8_t *lds, uint32_t meta)
+{
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float bad = (__builtin_isfinite(v.x) && __builtin_isfinite(v.y) && __builtin_isfinite(v.z) &&
+                 __builtin_isfinite(v.w)) ? 0.f : 1.f;
+    m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m));
+    bad = fmaxf(bad, dpp<0xB1>(bad)); bad = fmaxf(bad, dpp<0x4E>(bad)); bad = fmaxf(bad, dpp<0x141>(bad));
+    // k capped at 2^64 for tiny segments; non-finite x makes the segment NaN
+    const float k = (bad == 0.f && m > 0.f) ? fminf(kFix / m, 1.8446744e19f) : 0.f;
+    const float ik = bad != 0.f ? __builtin_nanf("") : (k > 0.f ? 1.0f / k : 0.f);
+    int Y[4];
+    int sd = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        Y[e] = bad != 0.f ? 0 : __float2int_rn(vv[e] * k);
+        sd += Y[e] & 0xFFFF;
+    }
+    float sx = (v.x + v.y) + (v.z + v.w);
+    sx += dpp<0xB1>(sx); sx += dpp<0x4E>(sx);                         // 16-element half sums
+    sd += dppi<0xB1>(sd); sd += dppi<0x4E>(sd); sd += dppi<0x141>(sd);  // whole segment
+    const uint32_t g = i >> 3, j = i & 7u;
+    uint8_t *seg = lds + plane_off(g);
+    if (!EVEN_ODD) {
+        // bytes p of Y0..Y3 -> one dword per plane
+        const uint32_t P01 = __builtin_amdgcn_perm((uint32_t)Y[1], (uint32_t)Y[0], 0x05010400u);
+        const uint32_t P23 = __builtin_amdgcn_perm((uint32_t)Y[3], (uint32_t)Y[2], 0x05010400u);
+        const uint32_t Q01 = __builtin_amdgcn_perm((uint32_t)Y[1], (uint32_t)Y[0], 0x0C0C0602u);
+        const uint32_t Q23 = __builtin_amdgcn_perm((uint32_t)Y[3], (uint32_t)Y[2], 0x0C0C0602u);
+        *(uint32_t *)(seg + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x05040100u);
+        *(uint32_t *)(seg + 32 + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x07060302u);
+        *(uint32_t *)(seg + 64 + 4 * j) = __builtin_amdgcn_perm(Q23, Q01, 0x05040100u);
+    } else {
+        // elements 4j, 4j+2 -> even positions 2j, 2j+1; 4j+1, 4j+3 -> odd positions 16+2j, 17+2j
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const uint32_t ev = ((uint32_t)(Y[0] >> (8 * p)) & 0xFFu) | (((uint32_t)(Y[2] >> (8 * p)) & 0xFFu) << 8);
+            const uint32_t od = ((uint32_t)(Y[1] >> (8 * p)) & 0xFFu) | (((uint32_t)(Y[3] >> (8 * p)) & 0xFFu) << 8);
+            *(uint16_t *)(seg + 32 * p + 2 * j) = (uint16_t)ev;
+            *(uint16_t *)(seg + 32 * p + 16 + 2 * j) = (uint16_t)od;
+        }
+    }
+    float *rec = (float *)(lds + meta + 16u * g);
+    if (j == 0) { rec[0] = ik; rec[1] = sx; rec[3] = __builtin_bit_cast(float, sd); }
+    if (j == 4) rec[2] = sx;
+}
+
+// sum q*Y from the three plane dot products (see above)
+__device__ __forceinline__ float fix3(uint32_t d0, uint32_t d1, int d2)
+{
+    return __builtin_fmaf((float)(d2 * 256 + (int)d1), 256.0f, (float)d0);
+}
+
+// A lane's x for its item: S slots of SEG elements (planes or f32).
+template <int S, int SEG> struct XP {
+    uint32_t p[S][3][SEG / 4];
+    float ik[S], sx[S];
+    int sd[S];
+};
+template <int S, int SEG> struct XF {
+    float v[S * SEG];
+    float sx[S];
+};
+
+__device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c)
+{
+    return __builtin_amdgcn_udot4(a, b, c, false);
+}
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
 // ------------------------------------------------------ team GEMV items
 //
-// An item is the unit one lane decodes per row group: 64 consecutive-in-block
-// weights (32 for F32), split into S segments of SEG weights that each lie in
-// one row.  Every quant type is reduced to unsigned codes u (one byte each,
-// converted with v_cvt_f32_ubyte) so that a segment contributes
-//     scale * (sum u*x) - offset_or_min * (sum x)
-// with sum x precomputed once per lane (x never changes during a launch).
+// An item is the unit one lane decodes per row group: 64 weights (32 for
+// F32) in S slots of SEG weights that each lie in one row.  load() fetches
+// the raw bytes of one item; compute() returns each slot's contribution to
+// its row's dot product.
 
 template <uint32_t T> struct Item;
 
@@ -232,63 +375,54 @@ template <uint32_t T> struct Item;
 // and 2p+1 (high nibbles) of qs[32p .. 32p+32].
 template <> struct Item<T_Q4_K> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 12, UNIT = 256;
+    static constexpr bool PLANES = true, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s)
     {
         return (it >> 2) * 256u + (it & 3u) * 64u + s * 32u;
     }
     __device__ static uint32_t item_byte(uint32_t it) { return (it >> 2) * 144u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t it, uint32_t (&r)[NRAW])
     {
-        const uint8_t *b = gb + (it >> 2) * 144u;
-        const uint4 h = *(const uint4 *)b;
-        const uint4 *q = (const uint4 *)(b + 16u + (it & 3u) * 32u);
+        const uint4 h = *(const uint4 *)ip;
+        const uint4 *q = (const uint4 *)(ip + 16u + (it & 3u) * 32u);
         const uint4 q0 = q[0], q1 = q[1];
         r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
         r[4] = q0.x; r[5] = q0.y; r[6] = q0.z; r[7] = q0.w;
         r[8] = q1.x; r[9] = q1.y; r[10] = q1.z; r[11] = q1.w;
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&sx)[S], uint32_t it, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                   float (&out)[S])
     {
         const float d = h2f(r[0]), dmin = h2f(r[0] >> 16);
-        const uint32_t j = (it & 3u) * 2u;
-        uint32_t sc0, m0, sc1, m1;
-        k4sm(j, r[1], r[2], r[3], sc0, m0);
-        k4sm(j + 1u, r[1], r[2], r[3], sc1, m1);
-        float a = 0.f, b = 0.f, a2 = 0.f, b2 = 0.f;
+        uint32_t SC, MN;
+        k4pair(it & 3u, r[1], r[2], r[3], SC, MN);
+        uint32_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+        int a2 = 0, b2 = 0;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const uint32_t lo = andm(r[4 + t], 0x0F0F0F0Fu), hi = andm(r[4 + t], 0xF0F0F0F0u);
-            a = __builtin_fmaf(ub(lo, 0), xs[4 * t + 0], a);
-            b = __builtin_fmaf(ub(hi, 0), xs[32 + 4 * t + 0], b);
-            a2 = __builtin_fmaf(ub(lo, 1), xs[4 * t + 1], a2);
-            b2 = __builtin_fmaf(ub(hi, 1), xs[32 + 4 * t + 1], b2);
-            a = __builtin_fmaf(ub(lo, 2), xs[4 * t + 2], a);
-            b = __builtin_fmaf(ub(hi, 2), xs[32 + 4 * t + 2], b);
-            a2 = __builtin_fmaf(ub(lo, 3), xs[4 * t + 3], a2);
-            b2 = __builtin_fmaf(ub(hi, 3), xs[32 + 4 * t + 3], b2);
+            const uint32_t lo = andm(r[4 + t], 0x0F0F0F0Fu), hi = andm(r[4 + t] >> 4, 0x0F0F0F0Fu);
+            a0 = udot4(lo, x.p[0][0][t], a0); a1 = udot4(lo, x.p[0][1][t], a1); a2 = sdot4(lo, x.p[0][2][t], a2);
+            b0 = udot4(hi, x.p[1][0][t], b0); b1 = udot4(hi, x.p[1][1][t], b1); b2 = sdot4(hi, x.p[1][2][t], b2);
         }
-        a += a2;
-        b += b2;
-        out[0] = __builtin_fmaf(d * (float)sc0, a, -(dmin * (float)m0) * sx[0]);
-        out[1] = __builtin_fmaf(d * (float)sc1 * 0.0625f, b, -(dmin * (float)m1) * sx[1]);
+        out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
+        out[1] = __builtin_fmaf(d * ub(SC, 1), fix3(b0, b1, b2) * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
     }
 };
 
 // Q5_K (quant.rs:231-262): as Q4_K plus the fifth bit, bit j of qh[l].
 template <> struct Item<T_Q5_K> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 20, UNIT = 256;
+    static constexpr bool PLANES = true, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s)
     {
         return (it >> 2) * 256u + (it & 3u) * 64u + s * 32u;
     }
     __device__ static uint32_t item_byte(uint32_t it) { return (it >> 2) * 176u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t it, uint32_t (&r)[NRAW])
     {
-        const uint8_t *b = gb + (it >> 2) * 176u;
-        const uint4 h = *(const uint4 *)b;
-        const uint4 *qh = (const uint4 *)(b + 16u);
-        const uint4 *q = (const uint4 *)(b + 48u + (it & 3u) * 32u);
+        const uint4 h = *(const uint4 *)ip;
+        const uint4 *qh = (const uint4 *)(ip + 16u);
+        const uint4 *q = (const uint4 *)(ip + 48u + (it & 3u) * 32u);
         const uint4 h0 = qh[0], h1 = qh[1], q0 = q[0], q1 = q[1];
         r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
         r[4] = h0.x; r[5] = h0.y; r[6] = h0.z; r[7] = h0.w;
@@ -296,50 +430,43 @@ template <> struct Item<T_Q5_K> {
         r[12] = q0.x; r[13] = q0.y; r[14] = q0.z; r[15] = q0.w;
         r[16] = q1.x; r[17] = q1.y; r[18] = q1.z; r[19] = q1.w;
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&sx)[S], uint32_t it, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                   float (&out)[S])
     {
         const float d = h2f(r[0]), dmin = h2f(r[0] >> 16);
         const uint32_t j = (it & 3u) * 2u;
-        uint32_t sc0, m0, sc1, m1;
-        k4sm(j, r[1], r[2], r[3], sc0, m0);
-        k4sm(j + 1u, r[1], r[2], r[3], sc1, m1);
-        float a = 0.f, b = 0.f, a2 = 0.f, b2 = 0.f;
+        uint32_t SC, MN;
+        k4pair(it & 3u, r[1], r[2], r[3], SC, MN);
+        uint32_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+        int a2 = 0, b2 = 0;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const uint32_t w = r[12 + t], hb = r[4 + t];
             const uint32_t qa = andm(w, 0x0F0F0F0Fu) | (((hb >> j) & 0x01010101u) << 4);
             const uint32_t qb = andm(w >> 4, 0x0F0F0F0Fu) | (((hb >> (j + 1u)) & 0x01010101u) << 4);
-            a = __builtin_fmaf(ub(qa, 0), xs[4 * t + 0], a);
-            b = __builtin_fmaf(ub(qb, 0), xs[32 + 4 * t + 0], b);
-            a2 = __builtin_fmaf(ub(qa, 1), xs[4 * t + 1], a2);
-            b2 = __builtin_fmaf(ub(qb, 1), xs[32 + 4 * t + 1], b2);
-            a = __builtin_fmaf(ub(qa, 2), xs[4 * t + 2], a);
-            b = __builtin_fmaf(ub(qb, 2), xs[32 + 4 * t + 2], b);
-            a2 = __builtin_fmaf(ub(qa, 3), xs[4 * t + 3], a2);
-            b2 = __builtin_fmaf(ub(qb, 3), xs[32 + 4 * t + 3], b2);
+            a0 = udot4(qa, x.p[0][0][t], a0); a1 = udot4(qa, x.p[0][1][t], a1); a2 = sdot4(qa, x.p[0][2][t], a2);
+            b0 = udot4(qb, x.p[1][0][t], b0); b1 = udot4(qb, x.p[1][1][t], b1); b2 = sdot4(qb, x.p[1][2][t], b2);
         }
-        a += a2;
-        b += b2;
-        out[0] = __builtin_fmaf(d * (float)sc0, a, -(dmin * (float)m0) * sx[0]);
-        out[1] = __builtin_fmaf(d * (float)sc1, b, -(dmin * (float)m1) * sx[1]);
+        out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
+        out[1] = __builtin_fmaf(d * ub(SC, 1), fix3(b0, b1, b2) * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
     }
 };
 
-// Q6_K (quant.rs:265-292): item = (block, half n, i = l/16): 4 segments of 16,
+// Q6_K (quant.rs:265-292): item = (block, half n, i = l/16): 4 slots of 16,
 // elements 128n + 32k + 16i + (0..15), k = 0..3.  Blocks are 210 bytes, so
 // fields sit at 2-byte alignment: load aligned dword windows and realign
 // with v_alignbyte.
 template <> struct Item<T_Q6_K> {
     static constexpr uint32_t IE = 64, S = 4, SEG = 16, NRAW = 15, UNIT = 256;
+    static constexpr bool PLANES = true, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s)
     {
         return (it >> 2) * 256u + ((it >> 1) & 1u) * 128u + s * 32u + (it & 1u) * 16u;
     }
     __device__ static uint32_t item_byte(uint32_t it) { return (it >> 2) * 210u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t it, uint32_t (&r)[NRAW])
     {
-        const uint8_t *b = gb + (it >> 2) * 210u;
+        const uint8_t *b = ip;
         const uint32_t n = (it >> 1) & 1u, i = it & 1u;
         const uint32_t mis = (uint32_t)((uintptr_t)b & 3u);
         const uint32_t *base = (const uint32_t *)(b - mis);
@@ -366,12 +493,13 @@ template <> struct Item<T_Q6_K> {
         r[13] = __builtin_amdgcn_alignbyte(S2, S1, sh);
         r[14] = D >> (8u * sh);
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&sx)[S], uint32_t it, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                   float (&out)[S])
     {
         const float d = h2f(r[14]);
         const uint32_t i8 = (it & 1u) * 8u;
-        float dot[4] = {0.f, 0.f, 0.f, 0.f};
+        uint32_t u0[4] = {0, 0, 0, 0}, u1[4] = {0, 0, 0, 0};
+        int s2[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const uint32_t A = r[t], B = r[4 + t], H = r[8 + t];
@@ -380,30 +508,33 @@ template <> struct Item<T_Q6_K> {
                                    andm(A >> 4, 0x0F0F0F0Fu) | (H & 0x30303030u),
                                    andm(B >> 4, 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u)};
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++)
-                    dot[k] = __builtin_fmaf(ub(q[k], bb), xs[16 * k + 4 * t + bb], dot[k]);
+            for (int k = 0; k < 4; k++) {
+                u0[k] = udot4(q[k], x.p[k][0][t], u0[k]);
+                u1[k] = udot4(q[k], x.p[k][1][t], u1[k]);
+                s2[k] = sdot4(q[k], x.p[k][2][t], s2[k]);
+            }
         }
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             // sc[8n + i + 2k]: byte (i + 2(k&1)) of dword r[12 + k/2]
             const int sc = __builtin_amdgcn_sbfe((int)r[12 + (k >> 1)], (int)(i8 + 16u * (k & 1)), 8);
-            out[k] = (d * (float)sc) * __builtin_fmaf(-32.0f, sx[k], dot[k]);
+            out[k] = (d * (float)sc) * __builtin_fmaf(-32.0f, x.sx[k], fix3(u0[k], u1[k], s2[k]) * x.ik[k]);
         }
     }
 };
 
 // Q8_0 (quant.rs:106-113): item = two blocks (68 bytes, 4-byte aligned).
 // Block 0's codes sit at byte 2 (realigned), block 1's at byte 36 (aligned).
-// Signed codes become unsigned with ^0x80: q = u - 128.
+// Signed codes: the unsigned planes take u = q ^ 0x80 = q + 128 and subtract
+// 128 * sum(d0 + 256 d1) afterwards; the signed plane takes q itself.
 template <> struct Item<T_Q8_0> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 17, UNIT = 64;
+    static constexpr bool PLANES = true, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s) { return it * 64u + s * 32u; }
     __device__ static uint32_t item_byte(uint32_t it) { return it * 68u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t, uint32_t (&r)[NRAW])
     {
-        const uint32_t *p = (const uint32_t *)(gb + it * 68u);
+        const uint32_t *p = (const uint32_t *)ip;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const U4a u = *(const U4a *)(p + 4 * v);
@@ -411,63 +542,59 @@ template <> struct Item<T_Q8_0> {
         }
         r[16] = p[16];
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&sx)[S], uint32_t, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t,
+                                   float (&out)[S])
     {
-        const float d0 = h2f(r[0]), d1 = h2f(r[8] >> 16);
-        float a = 0.f, b = 0.f, a2 = 0.f, b2 = 0.f;
+        const float dd[2] = {h2f(r[0]), h2f(r[8] >> 16)};
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const uint32_t u0 = xorm(__builtin_amdgcn_alignbyte(r[t + 1], r[t], 2u), 0x80808080u);
-            const uint32_t u1 = xorm(r[9 + t], 0x80808080u);
-            a = __builtin_fmaf(ub(u0, 0), xs[4 * t + 0], a);
-            b = __builtin_fmaf(ub(u1, 0), xs[32 + 4 * t + 0], b);
-            a2 = __builtin_fmaf(ub(u0, 1), xs[4 * t + 1], a2);
-            b2 = __builtin_fmaf(ub(u1, 1), xs[32 + 4 * t + 1], b2);
-            a = __builtin_fmaf(ub(u0, 2), xs[4 * t + 2], a);
-            b = __builtin_fmaf(ub(u1, 2), xs[32 + 4 * t + 2], b);
-            a2 = __builtin_fmaf(ub(u0, 3), xs[4 * t + 3], a2);
-            b2 = __builtin_fmaf(ub(u1, 3), xs[32 + 4 * t + 3], b2);
+        for (int s = 0; s < 2; s++) {
+            uint32_t a0 = 0, a1 = 0;
+            int a2 = 0;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t q = s == 0 ? __builtin_amdgcn_alignbyte(r[t + 1], r[t], 2u) : r[9 + t];
+                const uint32_t u = xorm(q, 0x80808080u);
+                a0 = udot4(u, x.p[s][0][t], a0); a1 = udot4(u, x.p[s][1][t], a1); a2 = sdot4(q, x.p[s][2][t], a2);
+            }
+            const int lo = (int)(a0 + 256u * a1) - 128 * x.sd[s];
+            out[s] = dd[s] * (__builtin_fmaf((float)a2, 65536.0f, (float)lo) * x.ik[s]);
         }
-        a += a2;
-        b += b2;
-        out[0] = d0 * __builtin_fmaf(-128.0f, sx[0], a);
-        out[1] = d1 * __builtin_fmaf(-128.0f, sx[1], b);
     }
 };
 
 // Q4_0 (quant.rs:114-121): two blocks (36 bytes).  Interleaved nibble order:
-// byte j holds element 2j (low nibble) and 2j+1 (high nibble).
+// byte j holds element 2j (low nibble) and 2j+1 (high nibble); x planes are
+// staged even-then-odd to match.
 template <> struct Item<T_Q4_0> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 9, UNIT = 64;
+    static constexpr bool PLANES = true, EVEN_ODD = true;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s) { return it * 64u + s * 32u; }
     __device__ static uint32_t item_byte(uint32_t it) { return it * 36u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t, uint32_t (&r)[NRAW])
     {
-        const uint32_t *p = (const uint32_t *)(gb + it * 36u);
+        const uint32_t *p = (const uint32_t *)ip;
         const U4a u0 = *(const U4a *)p, u1 = *(const U4a *)(p + 4);
         r[0] = u0.a; r[1] = u0.b; r[2] = u0.c; r[3] = u0.d;
         r[4] = u1.a; r[5] = u1.b; r[6] = u1.c; r[7] = u1.d;
         r[8] = p[8];
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&sx)[S], uint32_t, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t,
+                                   float (&out)[S])
     {
         const float dd[2] = {h2f(r[0]), h2f(r[4] >> 16)};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            float e = 0.f, o = 0.f;
+            uint32_t a0 = 0, a1 = 0;
+            int a2 = 0;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const uint32_t q = s == 0 ? __builtin_amdgcn_alignbyte(r[t + 1], r[t], 2u) : r[5 + t];
-                const uint32_t lo = andm(q, 0x0F0F0F0Fu), hi = andm(q, 0xF0F0F0F0u);
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    e = __builtin_fmaf(ub(lo, bb), xs[32 * s + 8 * t + 2 * bb], e);
-                    o = __builtin_fmaf(ub(hi, bb), xs[32 * s + 8 * t + 2 * bb + 1], o);
-                }
+                const uint32_t lo = andm(q, 0x0F0F0F0Fu), hi = andm(q >> 4, 0x0F0F0F0Fu);
+                a0 = udot4(lo, x.p[s][0][t], a0); a1 = udot4(lo, x.p[s][1][t], a1); a2 = sdot4(lo, x.p[s][2][t], a2);
+                a0 = udot4(hi, x.p[s][0][4 + t], a0); a1 = udot4(hi, x.p[s][1][4 + t], a1);
+                a2 = sdot4(hi, x.p[s][2][4 + t], a2);
             }
-            out[s] = dd[s] * (__builtin_fmaf(o, 0.0625f, e) - 8.0f * sx[s]);
+            out[s] = dd[s] * __builtin_fmaf(-8.0f, x.sx[s], fix3(a0, a1, a2) * x.ik[s]);
         }
     }
 };
@@ -480,211 +607,321 @@ __device__ __forceinline__ uint32_t spread4(uint32_t v)  // bit k of v -> bit 8k
 }
 template <> struct Item<T_Q5_0> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 11, UNIT = 64;
+    static constexpr bool PLANES = true, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s) { return it * 64u + s * 32u; }
     __device__ static uint32_t item_byte(uint32_t it) { return it * 44u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t, uint32_t (&r)[NRAW])
     {
-        const uint32_t *p = (const uint32_t *)(gb + it * 44u);
+        const uint32_t *p = (const uint32_t *)ip;
         const U4a u0 = *(const U4a *)p, u1 = *(const U4a *)(p + 4);
         r[0] = u0.a; r[1] = u0.b; r[2] = u0.c; r[3] = u0.d;
         r[4] = u1.a; r[5] = u1.b; r[6] = u1.c; r[7] = u1.d;
         r[8] = p[8]; r[9] = p[9]; r[10] = p[10];
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&sx)[S], uint32_t, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t,
+                                   float (&out)[S])
     {
         const float dd[2] = {h2f(r[0]), h2f(r[5] >> 16)};
         const uint32_t qh[2] = {__builtin_amdgcn_alignbyte(r[1], r[0], 2u), r[6]};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            float a = 0.f, b = 0.f;
+            uint32_t a0 = 0, a1 = 0;
+            int a2 = 0;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const uint32_t q = s == 0 ? __builtin_amdgcn_alignbyte(r[t + 2], r[t + 1], 2u) : r[7 + t];
                 const uint32_t lo = andm(q, 0x0F0F0F0Fu) | spread4(qh[s] >> (4 * t));
                 const uint32_t hi = andm(q >> 4, 0x0F0F0F0Fu) | spread4(qh[s] >> (16 + 4 * t));
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    a = __builtin_fmaf(ub(lo, bb), xs[32 * s + 4 * t + bb], a);
-                    b = __builtin_fmaf(ub(hi, bb), xs[32 * s + 16 + 4 * t + bb], b);
-                }
+                a0 = udot4(lo, x.p[s][0][t], a0); a1 = udot4(lo, x.p[s][1][t], a1); a2 = sdot4(lo, x.p[s][2][t], a2);
+                a0 = udot4(hi, x.p[s][0][4 + t], a0); a1 = udot4(hi, x.p[s][1][4 + t], a1);
+                a2 = sdot4(hi, x.p[s][2][4 + t], a2);
             }
-            out[s] = dd[s] * __builtin_fmaf(-16.0f, sx[s], a + b);
+            out[s] = dd[s] * __builtin_fmaf(-16.0f, x.sx[s], fix3(a0, a1, a2) * x.ik[s]);
         }
     }
 };
 
-// F16: 64 halves (128 bytes, 16-byte aligned).
+// F16: 64 halves (128 bytes, 16-byte aligned); x stays f32.
 template <> struct Item<T_F16> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 32, UNIT = 64;
+    static constexpr bool PLANES = false, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s) { return it * 64u + s * 32u; }
     __device__ static uint32_t item_byte(uint32_t it) { return it * 128u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t, uint32_t (&r)[NRAW])
     {
-        const uint4 *p = (const uint4 *)(gb + it * 128u);
+        const uint4 *p = (const uint4 *)ip;
 #pragma unroll
         for (int v = 0; v < 8; v++) {
             const uint4 u = p[v];
             r[4 * v] = u.x; r[4 * v + 1] = u.y; r[4 * v + 2] = u.z; r[4 * v + 3] = u.w;
         }
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&)[S], uint32_t, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XF<S, SEG> &x, uint32_t,
+                                   float (&out)[S])
     {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             float a = 0.f, b = 0.f;
 #pragma unroll
             for (int t = 0; t < 16; t++) {
-                a = __builtin_fmaf(h2f(r[16 * s + t]), xs[32 * s + 2 * t], a);
-                b = __builtin_fmaf(h2f(r[16 * s + t] >> 16), xs[32 * s + 2 * t + 1], b);
+                a = __builtin_fmaf(h2f(r[16 * s + t]), x.v[32 * s + 2 * t], a);
+                b = __builtin_fmaf(h2f(r[16 * s + t] >> 16), x.v[32 * s + 2 * t + 1], b);
             }
             out[s] = a + b;
         }
     }
 };
 
-// F32: 32 floats (128 bytes).
+// F32: 32 floats (128 bytes); x stays f32.
 template <> struct Item<T_F32> {
     static constexpr uint32_t IE = 32, S = 1, SEG = 32, NRAW = 32, UNIT = 32;
+    static constexpr bool PLANES = false, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t) { return it * 32u; }
     __device__ static uint32_t item_byte(uint32_t it) { return it * 128u; }
-    __device__ static void load(const uint8_t *gb, uint32_t it, uint32_t (&r)[NRAW])
+    __device__ static void load(const uint8_t *ip, uint32_t, uint32_t (&r)[NRAW])
     {
-        const uint4 *p = (const uint4 *)(gb + it * 128u);
+        const uint4 *p = (const uint4 *)ip;
 #pragma unroll
         for (int v = 0; v < 8; v++) {
             const uint4 u = p[v];
             r[4 * v] = u.x; r[4 * v + 1] = u.y; r[4 * v + 2] = u.z; r[4 * v + 3] = u.w;
         }
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const float (&xs)[S * SEG],
-                                   const float (&)[S], uint32_t, float (&out)[S])
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XF<S, SEG> &x, uint32_t,
+                                   float (&out)[S])
     {
         float a = 0.f, b = 0.f;
 #pragma unroll
         for (int t = 0; t < 16; t++) {
-            a = __builtin_fmaf(__uint_as_float(r[2 * t]), xs[2 * t], a);
-            b = __builtin_fmaf(__uint_as_float(r[2 * t + 1]), xs[2 * t + 1], b);
+            a = __builtin_fmaf(__uint_as_float(r[2 * t]), x.v[2 * t], a);
+            b = __builtin_fmaf(__uint_as_float(r[2 * t + 1]), x.v[2 * t + 1], b);
         }
         out[0] = a + b;
     }
 };
 
-template <uint32_t T> constexpr int rows_per_batch()
+// Rows (row groups) per batch of the pipelined loop.
+template <uint32_t T> constexpr int rows_pipe()
 {
-    return T == T_Q4_K ? 4 : T == T_Q4_0 ? 4 : T == T_Q5_0 ? 4 : T == T_F16 || T == T_F32 ? 1 : 2;
+    return T == T_Q4_K || T == T_Q4_0 || T == T_Q5_0 ? 2 : 1;
+}
+// Largest single-batch R whose loads fit the register budget.
+template <uint32_t T> constexpr int rows_single_max() { return Item<T>::NRAW < 12 ? 6 : Item<T>::NRAW <= 20 ? 4 : 2; }
+
+// ------------------------------------------------------- x preparation
+//
+// The quant-type team kernels read x as the fixed-point image described
+// above (planes + segment records).  It is built once per mat-vec by xprep_k
+// (or by the kernel that produces x) and each workgroup copies it into LDS.
+
+__host__ __device__ constexpr uint32_t image_bytes(bool planes, uint32_t cols)
+{
+    return planes ? planes_bytes(cols) + (cols / 32) * 16u : (cols / 4 + cols / 64 + 1) * 16u;
+}
+
+template <bool EVEN_ODD>
+__global__ void __launch_bounds__(256) xprep_k(const float *__restrict__ x, uint32_t cols,
+                                               uint8_t *__restrict__ img)
+{
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    // cols % 32 == 0: the 8 lanes of a segment are in range together
+    if (i < cols / 4) stage_planes1<EVEN_ODD>(((const float4 *)x)[i], i, img, planes_bytes(cols));
 }
 
 // ------------------------------------------------------- team GEMV kernel
+//
+// A workgroup copies the x image into LDS once and runs several teams.  A
+// team owns whole row groups: its lanes each decode one item of every row
+// group, and a team spans 1..8 waves (wpt) when a row has more than 64 items.
+// Row groups are dealt to teams band-wise: team t takes t, t + NT, t + 2NT, ...
+// (NT = teams in the grid), so that at any moment the whole grid streams one
+// contiguous band of the matrix.  Every team runs the same number of batches,
+// so the cross-wave reduction may use workgroup barriers.
+
+constexpr int kMaxWG = 768;        // 12 waves: 3 per SIMD
+constexpr int kStage = 8;          // 16-byte pieces of x each thread loads before the weights
 
 struct TeamArgs {
     const uint8_t *w;
-    const float *x;
+    const void *x;                 // x image (quant types) or x itself (F16/F32)
     float *y;
-    uint64_t nbytes, group_bytes;
-    uint32_t rows, cols, g, n_groups, ni, n_teams, n_batches;
+    uint32_t nbytes, group_bytes, rows, cols, g, n_groups, ni;
+    uint32_t n_teams;              // NT
+    uint32_t per_team;             // batches every team runs
+    uint32_t wpt;                  // waves per team (TSUB == 0)
 };
 
-// TSUB > 0: teams of TSUB lanes inside 256-thread workgroups (several teams per
-// wave when TSUB < 64).  TSUB == 0: one team per workgroup of blockDim.x lanes
-// (up to 8 waves), reduced across waves through LDS.
-template <uint32_t T, int TSUB>
-__global__ void __launch_bounds__(TSUB ? 256 : 512) gemv_team(TeamArgs a)
+// Workgroup barrier that waits for this wave's LDS traffic only: global loads
+// issued before it stay in flight.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Loads of batch i of team t: R row groups t + (i*R + r)*NT, every load
+// unconditional (row groups past the end read the matrix's first bytes and
+// are masked out later) so that all of them are in flight together.  Byte
+// offsets fit in 32 bits (the planner sends larger matrices elsewhere).
+template <uint32_t T, int R>
+__device__ __forceinline__ void issue(const TeamArgs &a, uint32_t t, uint32_t i, uint32_t it,
+                                      uint32_t ib, bool active, uint32_t (&raw)[R][Item<T>::NRAW])
+{
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t grp = t + (i * R + r) * a.n_teams;
+        const uint32_t off = grp * a.group_bytes + ib;
+        const bool ok = active && grp < a.n_groups && off < a.nbytes;
+        Item<T>::load(a.w + (ok ? off : 0u), it, raw[r]);
+    }
+}
+
+template <uint32_t T, int TSUB, int R, bool PIPE, bool G1>
+__global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
 {
     using I = Item<T>;
-    constexpr int S = I::S, SEG = I::SEG, R = rows_per_batch<T>();
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lt = TSUB ? (tid & (uint32_t)(TSUB - 1)) : tid;
-    const uint32_t team = TSUB ? blockIdx.x * (256u / TSUB) + tid / TSUB : blockIdx.x;
-    const bool active = lt < a.ni;
+    constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
+    constexpr int RED = G1 ? R : R * 8;
+    extern __shared__ float4 xl4[];              // x image, one copy per workgroup
+    __shared__ float red[kMaxWG / 64][RED];
+    uint8_t *lds = (uint8_t *)xl4;
 
-    float xs[S * SEG], sx[S];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t TL = TSUB ? (uint32_t)TSUB : 64u * a.wpt;   // lanes per team
+    const uint32_t lt = tid % TL, tw = tid / TL, tpw = blockDim.x / TL;
+    const bool active = lt < a.ni;
+    const uint32_t it = active ? lt : 0u;
+    const uint32_t ib = I::item_byte(it);
+    const uint32_t team = blockIdx.x * tpw + tw;
+
+    // 1. x loads first, then this team's weight loads (two batches when
+    //    pipelined): vmcnt counts in order, so the LDS writes below wait for
+    //    x only and the weights stay in flight
+    const uint32_t n16 = I::PLANES ? image_bytes(true, a.cols) / 16u : a.cols / 4u;
+    const uint4 *src = (const uint4 *)a.x;
+    uint4 xv[kStage];
+#pragma unroll
+    for (int k = 0; k < kStage; k++) {
+        const uint32_t j = tid + k * blockDim.x;
+        xv[k] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
+    }
+    uint32_t rawA[R][NR];
+    uint32_t rawB[PIPE ? R : 1][PIPE ? NR : 1];
+    issue<T, R>(a, team, 0, it, ib, active, rawA);
+    if constexpr (PIPE) {
+        if (a.per_team > 1) issue<T, R>(a, team, 1, it, ib, active, rawB);
+    }
+    uint4 *l4 = (uint4 *)xl4;
+    // f32 layout: float4 j of x at j + j/16 (16 bytes of padding per 64 floats)
+#pragma unroll
+    for (int k = 0; k < kStage; k++) {
+        const uint32_t j = tid + k * blockDim.x;
+        if (j < n16) l4[I::PLANES ? j : j + (j >> 4)] = xv[k];
+    }
+    for (uint32_t j = tid + kStage * blockDim.x; j < n16; j += blockDim.x)
+        l4[I::PLANES ? j : j + (j >> 4)] = src[j];
+    lds_barrier();
+
+    // 2. this lane's slice of x, held in VGPRs for every row group it visits
+    const uint32_t meta = planes_bytes(a.cols);
+    using XT = typename std::conditional<I::PLANES, XP<S, SEG>, XF<S, SEG>>::type;
+    XT xs;
     uint32_t srow[S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
-        sx[s] = 0.f;
-        srow[s] = 0xFFFFFFFFu;
+        const uint32_t e = I::seg_elem(it, s);
+        srow[s] = e / a.cols;
+        const uint32_t c = e - srow[s] * a.cols;
+        if constexpr (I::PLANES) {
+            const uint32_t g = c / 32u, h = (c / 16u) & 1u;
+            const uint8_t *sp = lds + plane_off(g) + (SEG == 16 ? 16u * h : 0u);
 #pragma unroll
-        for (int e = 0; e < SEG; e++) xs[s * SEG + e] = 0.f;
-    }
-    if (active) {
+            for (int p = 0; p < 3; p++)
 #pragma unroll
-        for (int s = 0; s < S; s++) {
-            const uint32_t e = I::seg_elem(lt, s);
-            srow[s] = e / a.cols;
-            const float4 *xp = (const float4 *)(a.x + (e - srow[s] * a.cols));
+                for (int v = 0; v < SEG / 16; v++) {
+                    const uint4 q = active ? *(const uint4 *)(sp + 32 * p + 16 * v) : make_uint4(0, 0, 0, 0);
+                    xs.p[s][p][4 * v] = q.x; xs.p[s][p][4 * v + 1] = q.y;
+                    xs.p[s][p][4 * v + 2] = q.z; xs.p[s][p][4 * v + 3] = q.w;
+                }
+            const float4 m = active ? *(const float4 *)(lds + meta + 16u * g) : make_float4(0.f, 0.f, 0.f, 0.f);
+            xs.ik[s] = m.x;
+            xs.sx[s] = SEG == 32 ? m.y + m.z : (h ? m.z : m.y);
+            xs.sd[s] = __builtin_bit_cast(int, m.w);
+        } else {
+            const uint32_t j = c / 4;                   // segments never straddle a pad
+            const float4 *xp = xl4 + j + (j >> 4);
 #pragma unroll
             for (int v = 0; v < SEG / 4; v++) {
-                const float4 f = xp[v];
-                xs[s * SEG + 4 * v] = f.x; xs[s * SEG + 4 * v + 1] = f.y;
-                xs[s * SEG + 4 * v + 2] = f.z; xs[s * SEG + 4 * v + 3] = f.w;
+                const float4 f = active ? xp[v] : make_float4(0.f, 0.f, 0.f, 0.f);
+                xs.v[s * SEG + 4 * v] = f.x; xs.v[s * SEG + 4 * v + 1] = f.y;
+                xs.v[s * SEG + 4 * v + 2] = f.z; xs.v[s * SEG + 4 * v + 3] = f.w;
             }
-            float t = 0.f;
-#pragma unroll
-            for (int e2 = 0; e2 < SEG; e2++) t += xs[s * SEG + e2];
-            sx[s] = t;
         }
     }
-    const uint64_t ib = I::item_byte(lt);
-    __shared__ float red[TSUB ? 1 : 8][R * 8];
 
-    for (uint32_t bt = team; bt < a.n_batches; bt += a.n_teams) {
-        uint32_t raw[R][I::NRAW];
-        bool ok[R];
+    auto process = [&](const uint32_t (&raw)[R][NR], uint32_t i) {
+        float v[RED];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t grp = bt * R + r;
-            const uint64_t gbase = (uint64_t)grp * a.group_bytes;
-            ok[r] = active && grp < a.n_groups && gbase + ib < a.nbytes;
-            if (ok[r]) I::load(a.w + gbase, lt, raw[r]);
-        }
-        float acc[R][S];
+            const uint32_t grp = team + (i * R + r) * a.n_teams;
+            const bool ok = active && grp < a.n_groups && grp * a.group_bytes + ib < a.nbytes;
+            float acc[S];
+            I::compute(raw[r], xs, it, acc);
+            if (G1) {
+                float t = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (ok[r]) {
-                I::compute(raw[r], xs, sx, lt, acc[r]);
+                for (int s = 0; s < S; s++) t += acc[s];
+                v[r] = ok ? t : 0.f;
             } else {
 #pragma unroll
-                for (int s = 0; s < S; s++) acc[r][s] = 0.f;
+                for (int gi = 0; gi < 8; gi++) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int s = 0; s < S; s++) t += srow[s] == (uint32_t)gi ? acc[s] : 0.f;
+                    v[r * 8 + gi] = ok ? t : 0.f;
+                }
             }
         }
-        if (TSUB) {
+        const uint32_t g = G1 ? 1u : a.g;
+        if constexpr (TSUB != 0) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint32_t grp = bt * R + r;
-                if (grp >= a.n_groups) break;                   // team-uniform
-                for (uint32_t gi = 0; gi < a.g; gi++) {
-                    float v = 0.f;
-#pragma unroll
-                    for (int s = 0; s < S; s++) v += srow[s] == gi ? acc[r][s] : 0.f;
-#pragma unroll
-                    for (int o = TSUB / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, TSUB);
-                    const uint32_t row = grp * a.g + gi;
-                    if (lt == 0 && row < a.rows) a.y[row] = v;
-                }
+            for (int k = 0; k < RED; k++) {
+                const uint32_t r = G1 ? k : k / 8, gi = G1 ? 0 : k % 8;
+                if (!G1 && gi >= g) continue;
+                const float sum = group_sum<TSUB>(v[k]);
+                const uint32_t grp = team + (i * R + r) * a.n_teams, row = grp * g + gi;
+                if (lt == (uint32_t)TSUB - 1u && grp < a.n_groups && row < a.rows) a.y[row] = sum;
             }
         } else {
             const uint32_t wave = tid >> 6, lane = tid & 63u;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                for (uint32_t gi = 0; gi < a.g; gi++) {
-                    float v = 0.f;
-#pragma unroll
-                    for (int s = 0; s < S; s++) v += srow[s] == gi ? acc[r][s] : 0.f;
-                    v = wave_sum(v);
-                    if (lane == 0) red[wave][r * a.g + gi] = v;
-                }
+            for (int k = 0; k < RED; k++) {
+                const float sum = group_sum<64>(v[k]);
+                if (lane == 63u) red[wave][k] = sum;
             }
-            __syncthreads();
-            if (tid < R * a.g) {
-                const uint32_t r = tid / a.g, gi = tid - r * a.g, grp = bt * R + r;
-                float s = 0.f;
-                for (uint32_t wv = 0; wv < (blockDim.x >> 6); wv++) s += red[wv][tid];
-                const uint32_t row = grp * a.g + gi;
-                if (grp < a.n_groups && row < a.rows) a.y[row] = s;
+            lds_barrier();
+            if (lt < (uint32_t)RED) {                   // lane k of each team finishes row k
+                const uint32_t k = lt;
+                const uint32_t r = G1 ? k : k / 8, gi = G1 ? 0 : k % 8;
+                const uint32_t grp = team + (i * R + r) * a.n_teams, row = grp * g + gi;
+                float sum = 0.f;
+                for (uint32_t wv = 0; wv < a.wpt; wv++) sum += red[tw * a.wpt + wv][k];
+                if (gi < g && grp < a.n_groups && row < a.rows) a.y[row] = sum;
             }
-            __syncthreads();
+            lds_barrier();
+        }
+    };
+
+    // 3. the team's batches (the same count in every team); pipelined: batch
+    //    i+2 is issued as soon as batch i's registers are free
+    if constexpr (!PIPE) {
+        process(rawA, 0);
+    } else {
+        for (uint32_t i = 0; i < a.per_team; i += 2) {
+            process(rawA, i);
+            if (i + 2 < a.per_team) issue<T, R>(a, team, i + 2, it, ib, active, rawA);
+            if (i + 1 >= a.per_team) break;
+            process(rawB, i + 1);
+            if (i + 3 < a.per_team) issue<T, R>(a, team, i + 3, it, ib, active, rawB);
         }
     }
 }
@@ -697,36 +934,124 @@ static uint32_t gcd_u(uint64_t a, uint64_t b)
     return (uint32_t)a;
 }
 
+template <uint32_t T, int R, bool PIPE, bool G1> static const void *fn_tsub(uint32_t tsub)
+{
+    switch (tsub) {
+    case 16: return (const void *)gemv_team<T, 16, R, PIPE, G1>;
+    case 32: return (const void *)gemv_team<T, 32, R, PIPE, G1>;
+    case 64: return (const void *)gemv_team<T, 64, R, PIPE, G1>;
+    case 0: return (const void *)gemv_team<T, 0, R, PIPE, G1>;
+    default: return nullptr;
+    }
+}
+
+// single-batch kernel with R rows per team (g == 1 only)
+template <uint32_t T> static const void *single_fn(uint32_t tsub, int R)
+{
+    constexpr int RM = rows_single_max<T>();
+    switch (R) {
+    case 1: return fn_tsub<T, 1, false, true>(tsub);
+    case 2: return fn_tsub<T, 2, false, true>(tsub);
+    case 4: if constexpr (RM >= 4) return fn_tsub<T, 4, false, true>(tsub); else return nullptr;
+    case 6: if constexpr (RM >= 6) return fn_tsub<T, 6, false, true>(tsub); else return nullptr;
+    default: return nullptr;
+    }
+}
+
+template <uint32_t T> static const void *pipe_fn(uint32_t tsub, bool g1)
+{
+    return g1 ? fn_tsub<T, rows_pipe<T>(), true, true>(tsub)
+              : fn_tsub<T, rows_pipe<T>(), true, false>(tsub);
+}
+
+static int max_lds_bytes()
+{
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 65536;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+        return 65536;
+    return v;
+}
+
 template <uint32_t T> static void plan_team(size_t rows, size_t cols, int n_cu, Plan *p)
 {
     using I = Item<T>;
-    constexpr uint32_t R = rows_per_batch<T>();
     p->kind = 0;
     if (cols % 32 != 0 || rows == 0 || cols == 0) return;
-    const uint64_t unit = I::UNIT;                       // elements per aligned row-group unit
+    const uint64_t unit = I::UNIT;                        // elements per aligned row-group unit
     const uint64_t g = unit / gcd_u(cols, unit);
     const uint64_t gel = g * cols;
     const uint64_t ni = gel / I::IE;
     if (ni > 512 || g > 8) return;
-    uint32_t ts;
-    if (ni <= 64) { ts = 4; while (ts < ni) ts <<= 1; }
-    else ts = (uint32_t)((ni + 63) / 64 * 64);
+    const uint64_t gbytes = gel / block_elems(T) * block_bytes(T);
+    const uint64_t n_groups = (rows + g - 1) / g;
+    // 32-bit byte offsets inside the kernel (with the tail pad)
+    if ((n_groups + 8) * gbytes + kTailPad >= 0xFFFFFFFFull) return;
+    const uint64_t lds = image_bytes(I::PLANES, (uint32_t)cols);
+    if (lds + 2048 > (uint64_t)max_lds_bytes()) return;
+    uint32_t tsub = 0, wpt = 1, tl;
+    if (ni <= 64) { tsub = 16; while (tsub < ni) tsub <<= 1; tl = tsub; }
+    else { wpt = (uint32_t)((ni + 63) / 64); tl = 64 * wpt; }
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
-    p->ts = ts;
-    p->tsub = ts <= 64 ? ts : 0;
-    p->n_groups = (uint32_t)((rows + g - 1) / g);
-    p->group_bytes = gel / block_elems(T) * block_bytes(T);
-    const uint64_t n_batches = (p->n_groups + R - 1) / R;
-    // aim for ~16 waves per CU resident, then balance batches per team
-    const uint64_t waves_target = (uint64_t)(n_cu > 0 ? n_cu : 256) * 16;
-    const uint64_t teams_target = ts <= 64 ? waves_target * (64 / ts) : waves_target / (ts / 64);
-    const uint64_t per_team = (n_batches + teams_target - 1) / (teams_target ? teams_target : 1);
-    uint64_t n_teams = (n_batches + per_team - 1) / per_team;
-    const uint32_t tpb = p->tsub ? 256u / ts : 1u;
-    p->block = p->tsub ? 256u : ts;
-    p->grid = (uint32_t)((n_teams + tpb - 1) / tpb);
-    p->n_teams = p->grid * tpb;
+    p->ts = tl;
+    p->tsub = tsub;
+    p->wpt = wpt;
+    p->n_groups = (uint32_t)n_groups;
+    p->group_bytes = gbytes;
+    p->lds = (uint32_t)lds;
+    const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
+    // resident teams of a kernel: the best of 768-, 512- and 256-thread
+    // workgroups (teams per workgroup share one staged copy of x)
+    auto resident = [&](const void *fn, uint32_t &block, uint32_t &tpw) {
+        uint64_t best = 0;
+        for (uint32_t bs : {768u, 512u, 256u}) {
+            const uint32_t t = bs / tl;
+            if (t == 0) continue;
+            int res = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&res, fn, (int)(t * tl), lds) != hipSuccess)
+                res = 0;
+            const uint64_t teams = ncu * (uint64_t)res * t;
+            if (teams > best) { best = teams; block = t * tl; tpw = t; }
+        }
+        return best;
+    };
+    // one batch per team when the smallest R in {1, 2, 4, 6} lets every batch
+    // have a resident team: all loads are issued at once
+    if (g == 1) {
+        for (int R : {1, 2, 4, 6}) {
+            const void *fn = single_fn<T>(tsub, R);
+            if (!fn) break;
+            uint32_t block = 0, tpw = 0;
+            const uint64_t teams = resident(fn, block, tpw);
+            const uint64_t nbat = (n_groups + R - 1) / R;
+            if (teams == 0 || nbat > teams) continue;
+            p->fn = fn;
+            p->R = (uint32_t)R;
+            p->n_batches = (uint32_t)nbat;
+            p->per_team = 1;
+            p->block = block;
+            p->grid = (uint32_t)((nbat + tpw - 1) / tpw);
+            p->n_teams = p->grid * tpw;
+            p->kind = 1;
+            return;
+        }
+    }
+    // otherwise resident teams loop over batches, two batches in flight
+    const void *fn = pipe_fn<T>(tsub, g == 1);
+    uint32_t block = 0, tpw = 0;
+    const uint64_t teams = resident(fn, block, tpw);
+    if (teams == 0) return;                               // no launchable shape: generic kernel
+    const uint64_t R = rows_pipe<T>();
+    const uint64_t nbat = (n_groups + R - 1) / R;
+    const uint64_t per = (nbat + teams - 1) / teams;
+    p->fn = fn;
+    p->R = (uint32_t)R;
+    p->n_batches = (uint32_t)nbat;
+    p->per_team = (uint32_t)per;
+    p->block = block;
+    p->grid = (uint32_t)((nbat + tpw * per - 1) / (tpw * per));
+    p->n_teams = p->grid * tpw;
     p->kind = 1;
 }
 
@@ -750,45 +1075,37 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p)
 
 // ------------------------------------------------------------ launchers
 
-template <uint32_t T>
-static int launch_team_t(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
-                         const float *x, float *y, hipStream_t st)
+static int launch_team(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                       const void *x, float *y, hipStream_t st)
 {
     TeamArgs a;
-    a.w = w; a.x = x; a.y = y; a.nbytes = nbytes; a.group_bytes = p.group_bytes;
+    a.w = w; a.x = x; a.y = y; a.nbytes = (uint32_t)nbytes; a.group_bytes = (uint32_t)p.group_bytes;
     a.rows = (uint32_t)rows; a.cols = (uint32_t)cols; a.g = p.g; a.n_groups = p.n_groups;
-    a.ni = p.ni; a.n_teams = p.n_teams;
-    a.n_batches = (p.n_groups + rows_per_batch<T>() - 1) / rows_per_batch<T>();
-    dim3 grid(p.grid), block(p.block);
-    switch (p.tsub) {
-    case 4: hipLaunchKernelGGL((gemv_team<T, 4>), grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL((gemv_team<T, 8>), grid, block, 0, st, a); break;
-    case 16: hipLaunchKernelGGL((gemv_team<T, 16>), grid, block, 0, st, a); break;
-    case 32: hipLaunchKernelGGL((gemv_team<T, 32>), grid, block, 0, st, a); break;
-    case 64: hipLaunchKernelGGL((gemv_team<T, 64>), grid, block, 0, st, a); break;
-    case 0: hipLaunchKernelGGL((gemv_team<T, 0>), grid, block, 0, st, a); break;
-    default: return -1;
-    }
-    return hipGetLastError() == hipSuccess ? 0 : -2;
+    a.ni = p.ni; a.n_teams = p.n_teams; a.per_team = p.per_team; a.wpt = p.wpt;
+    void *args[] = {&a};
+    if (hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) != hipSuccess) return -2;
+    return 0;
 }
 
+// Quant types read x through the fixed-point image: xprep_k builds it in
+// `img` (image_bytes(true, cols) bytes, 16-byte aligned) first.
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
-                size_t cols, const float *x, float *y, ihipStream_t *stream)
+                size_t cols, const float *x, float *y, uint8_t *img, ihipStream_t *stream)
 {
     hipStream_t st = (hipStream_t)stream;
-    if (p.kind != 1) return launch_gemv_generic(type, w, rows, cols, x, y, stream);
-    switch (type) {
-    case T_F32: return launch_team_t<T_F32>(p, w, nbytes, rows, cols, x, y, st);
-    case T_F16: return launch_team_t<T_F16>(p, w, nbytes, rows, cols, x, y, st);
-    case T_Q4_0: return launch_team_t<T_Q4_0>(p, w, nbytes, rows, cols, x, y, st);
-    case T_Q5_0: return launch_team_t<T_Q5_0>(p, w, nbytes, rows, cols, x, y, st);
-    case T_Q8_0: return launch_team_t<T_Q8_0>(p, w, nbytes, rows, cols, x, y, st);
-    case T_Q4_K: return launch_team_t<T_Q4_K>(p, w, nbytes, rows, cols, x, y, st);
-    case T_Q5_K: return launch_team_t<T_Q5_K>(p, w, nbytes, rows, cols, x, y, st);
-    case T_Q6_K: return launch_team_t<T_Q6_K>(p, w, nbytes, rows, cols, x, y, st);
-    default: return -1;
-    }
+    if (p.kind != 1 || !p.fn) return launch_gemv_generic(type, w, rows, cols, x, y, stream);
+    if (type == T_F16 || type == T_F32) return launch_team(p, w, nbytes, rows, cols, x, y, st);
+    if (!img) return -1;
+    const uint32_t n4 = (uint32_t)(cols / 4);
+    if (type == T_Q4_0)
+        hipLaunchKernelGGL(xprep_k<true>, dim3((n4 + 255) / 256), dim3(256), 0, st, x, (uint32_t)cols, img);
+    else
+        hipLaunchKernelGGL(xprep_k<false>, dim3((n4 + 255) / 256), dim3(256), 0, st, x, (uint32_t)cols, img);
+    if (hipGetLastError() != hipSuccess) return -2;
+    return launch_team(p, w, nbytes, rows, cols, img, y, st);
 }
+
+size_t x_image_bytes(size_t cols) { return image_bytes(true, (uint32_t)cols); }
 
 template <uint32_t T>
 static int launch_generic_t(const uint8_t *w, size_t rows, size_t cols, const float *x, float *y,
