@@ -40,11 +40,11 @@ constexpr size_t kTailPad = 512;
 
 // How a matrix is mat-vec'd; fixed at upload time.
 struct Plan {
-    int kind;              // 0 = generic per-element kernel, 1 = team kernel
-    uint32_t g;            // rows per row group (team kernel)
+    int kind;              // 0 = generic per-element kernel, 1 = stream kernel
+    uint32_t g;            // rows per row group
     uint32_t n_groups;     // ceil(rows / g)
     uint32_t ni;           // items (64- or 32-element units) per row group
-    uint32_t tsub;         // team lanes if <= 64, else 0 (one team = one workgroup)
+    uint32_t tsub;         // team lanes if <= 64, else 0 (a team spans wpt waves)
     uint32_t ts;           // team lanes
     uint64_t group_bytes;  // bytes per row group
     uint32_t n_teams;      // teams in the grid
@@ -53,7 +53,9 @@ struct Plan {
     uint32_t n_batches;    // ceil(n_groups / R)
     uint32_t per_team;     // batches each team runs
     uint32_t wpt;          // waves per team when a team spans several waves
-    uint32_t lds;          // dynamic LDS bytes (x staged per workgroup)
+    uint32_t chunk;        // batches per partial-sum flush (several-wave teams)
+    uint32_t red_off;      // LDS offset of the partial-sum slots
+    uint32_t lds;          // dynamic LDS bytes
     const void *fn;        // kernel chosen for this matrix
 };
 
@@ -64,9 +66,7 @@ struct ihipStream_t;
 namespace qg {
 int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p);
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
-                size_t cols, const float *x, float *y, uint8_t *img, ihipStream_t *stream);
-// bytes of the fixed-point x image the quant-type kernels need for `cols`
-size_t x_image_bytes(size_t cols);
+                size_t cols, const float *x, float *y, ihipStream_t *stream);
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                         const float *x, float *y, ihipStream_t *stream);
 int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,

@@ -38,8 +38,6 @@ struct qg_ctx {
     size_t h_x_cap = 0, h_y_cap = 0;
     float *d_x = nullptr, *d_y = nullptr;   // device staging
     size_t d_x_cap = 0, d_y_cap = 0;
-    uint8_t *img = nullptr;                 // fixed-point x image (quant types), sized at upload
-    size_t img_cap = 0;
     std::set<qg_mat *> mats;
     std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
 };
@@ -129,23 +127,6 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
         delete m;
         return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
     }
-    // the x image is allocated here, never inside a mat-vec (which may be
-    // captured in a graph)
-    const size_t need = qg::x_image_bytes(cols);
-    if (m->plan.kind == 1 && need > ctx->img_cap) {
-        uint8_t *buf = nullptr;
-        hipError_t e = hipMalloc((void **)&buf, need);
-        if (e != hipSuccess) {
-            delete m;
-            return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc x image", e);
-        }
-        if (ctx->img) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(ctx->img);
-        }
-        ctx->img = buf;
-        ctx->img_cap = need;
-    }
     ctx->mats.insert(m);
     *out = m;
     return QG_OK;
@@ -228,7 +209,6 @@ int qg_destroy(qg_ctx *ctx)
     if (ctx->h_y) (void)hipHostFree(ctx->h_y);
     if (ctx->d_x) (void)hipFree(ctx->d_x);
     if (ctx->d_y) (void)hipFree(ctx->d_y);
-    if (ctx->img) (void)hipFree(ctx->img);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QG_OK;
@@ -308,7 +288,7 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
         lr = qg::launch_fill(d_y, mat->rows, 0.0f, (ihipStream_t *)st);
     else if (mat->plan.kind == 1 && ((uintptr_t)d_x & 15u) == 0)
         lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, mat->cols, d_x,
-                             d_y, ctx->img, (ihipStream_t *)st);
+                             d_y, (ihipStream_t *)st);
     else
         lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, mat->cols, d_x, d_y,
                                      (ihipStream_t *)st);

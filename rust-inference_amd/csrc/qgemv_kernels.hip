@@ -10,10 +10,11 @@
 //   deq_row_k<T>      one row with the reference's straddle placement
 //                     (quant.rs:152-174)
 //   gemv_generic<T>   one wave per row, per-element decode; any shape
-//   gemv_team<T,..>   the fast path: x staged once per workgroup in LDS; a
-//                     "team" of lanes owns whole row groups, each lane one
-//                     64-weight item (32 for F32) whose x slice stays in VGPRs
-//                     for every row group the team visits
+//   gemv_stream<T,..> the fast path: a persistent workgroup stages x once in
+//                     LDS (as fixed-point planes for quant types); a "team"
+//                     of lanes owns whole row groups, each lane one 64-weight
+//                     item (32 for F32) whose x slice stays in VGPRs while the
+//                     team streams its row groups
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -24,19 +25,13 @@ namespace qg {
 
 // ---------------------------------------------------------------- helpers
 
-// Opaque AND/XOR: hides the mask from the instruction combiner, which would
+// Opaque AND: hides the mask from the instruction combiner, which would
 // otherwise turn "(w & 0x0F0F0F0F) >> 8k & 0xFF" into one v_bfe per byte
 // instead of one v_and per four bytes feeding v_cvt_f32_ubyte{0..3}.
 __device__ __forceinline__ uint32_t andm(uint32_t a, uint32_t m)
 {
     uint32_t r;
     asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(m), "v"(a));
-    return r;
-}
-__device__ __forceinline__ uint32_t xorm(uint32_t a, uint32_t m)
-{
-    uint32_t r;
-    asm("v_xor_b32 %0, %1, %2" : "=v"(r) : "v"(m), "v"(a));
     return r;
 }
 
@@ -235,23 +230,31 @@ __global__ void __launch_bounds__(256) gemv_generic(const uint8_t *__restrict__ 
 
 // ------------------------------------------------------ x in fixed point
 //
-// Quant types multiply integer codes by x with integer dot products.  While a
-// workgroup stages x into LDS it rewrites every 32-element segment of x, with
-// m = max |x| over the segment and k = 8388000 / m, as the 24-bit integers
-// Y = rint(x * k) (|Y| < 2^23), split into bytes d0, d1 (unsigned) and d2
-// (signed): Y = d0 + 256*d1 + 65536*d2.  For weight codes q in 0..127
-//     sum q*Y = udot4(q, d0) + 256 * udot4(q, d1) + 65536 * sdot4(q, d2)
-// exactly, and sum q*x = (sum q*Y) / k, within about 2^-23 of m per element.
-// Every segment also keeps {1/k, sum x[0..16), sum x[16..32), sum (Y & 0xFFFF)}.
-// F16 and F32 weights keep x in f32.
+// Quant types multiply integer codes by x with integer dot products.  Every
+// 32-element segment of x, with m = max |x| over the segment and
+// k = kFix / m, becomes the integers Y = rint(x * k), |Y| < 2^22, written in
+// balanced base 256: Y = e0 + 256 e1 + 65536 e2 with every digit a signed
+// byte in [-128, 127].  For any byte-sized weight code q (signed or not)
+//     sum q*Y = sdot4(q, e0) + 256 * sdot4(q, e1) + 65536 * sdot4(q, e2)
+// exactly, and sum q*x = (sum q*Y) / k, within about 2^-22 of m per element.
+// Signed digits let a high nibble be used in place, unshifted, as the signed
+// byte 16*h - 128 (one AND-XOR): sum h*Y = (sum (16h - 128)*Y + 128 sum Y) / 16.
+// Every segment also keeps the record {1/k, sum x[0..16), sum x[16..32), sY},
+// sY = sum of Y over the elements that high nibbles meet (all 32, or the odd
+// half for Q4_0's even-then-odd order).  A segment whose sum is not finite
+// (any inf or NaN in it) gets 1/k = NaN, so every dot product that uses it
+// is NaN.  F16 and F32 weights keep x in f32.
 //
-// LDS layout (planes): segment g at byte 96g + 16(g/2) holds 32 bytes of d0,
-// 32 of d1, 32 of d2 (16 bytes of padding per segment pair keep the per-lane
+// LDS layout (planes): segment g at byte 96g + 16(g/2) holds 32 bytes of e0,
+// 32 of e1, 32 of e2 (16 bytes of padding per segment pair keep the per-lane
 // reads below conflict-free); the segment records follow at `meta`.  Q4_0
 // stores each segment's planes in even-then-odd element order, matching its
 // interleaved nibbles.  f32 layout: float4 i of x at xl4[i + i/16].
 
-constexpr float kFix = 8388000.0f;
+constexpr float kFix = 4194000.0f;
+// fma(x, k, kMagic) holds rint(x * k) in its low mantissa bits for |x k| < 2^22
+constexpr float kMagic = 12582912.0f;            // 1.5 * 2^23
+constexpr int kMagicBits = 0x4B400000;
 
 __device__ __forceinline__ uint32_t plane_off(uint32_t g) { return 96u * g + 16u * (g >> 1); }
 __host__ __device__ constexpr uint32_t planes_bytes(uint32_t cols)
@@ -266,10 +269,6 @@ __device__ __forceinline__ float dpp(float v)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
                                                                  ROW_MASK, 0xF, false));
-}
-template <int CTRL> __device__ __forceinline__ int dppi(int v)
-{
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 
 // Sum over aligned groups of N lanes (N = 8, 16, 32, 64); the group's last
@@ -291,76 +290,72 @@ template <int N> __device__ __forceinline__ float group_sum(float v)
 template <bool EVEN_ODD>
 __device__ __forceinline__ void stage_planes1(float4 v, uint32_t i, uint8_t *lds, uint32_t meta)
 {
-    const float vv[4] = {v.x, v.y, v.z, v.w};
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    float bad = (__builtin_isfinite(v.x) && __builtin_isfinite(v.y) && __builtin_isfinite(v.z) &&
-                 __builtin_isfinite(v.w)) ? 0.f : 1.f;
     m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m));
-    bad = fmaxf(bad, dpp<0xB1>(bad)); bad = fmaxf(bad, dpp<0x4E>(bad)); bad = fmaxf(bad, dpp<0x141>(bad));
-    // k capped at 2^64 for tiny segments; non-finite x makes the segment NaN
-    const float k = (bad == 0.f && m > 0.f) ? fminf(kFix / m, 1.8446744e19f) : 0.f;
-    const float ik = bad != 0.f ? __builtin_nanf("") : (k > 0.f ? 1.0f / k : 0.f);
-    int Y[4];
-    int sd = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        Y[e] = bad != 0.f ? 0 : __float2int_rn(vv[e] * k);
-        sd += Y[e] & 0xFFFF;
-    }
-    float sx = (v.x + v.y) + (v.z + v.w);
-    sx += dpp<0xB1>(sx); sx += dpp<0x4E>(sx);                         // 16-element half sums
-    sd += dppi<0xB1>(sd); sd += dppi<0x4E>(sd); sd += dppi<0x141>(sd);  // whole segment
+    float s = (v.x + v.y) + (v.z + v.w);
+    s += dpp<0xB1>(s); s += dpp<0x4E>(s);            // 16-element half sums
+    const float h = dpp<0x141>(s);                   // the other half's sum
+    const bool bad = !__builtin_isfinite(s + h);
+    // k capped at 2^64 for tiny segments
+    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.8446744e19f) : 0.f;
+    const float ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
+    // Yb = Y + 0x8080: byte 2 is e2; bytes 0 and 1 are e0 and e1 with the top bit flipped
+    const int off = 0x8080 - kMagicBits;
+    const uint32_t Y0 = (uint32_t)(__float_as_int(__builtin_fmaf(v.x, k, kMagic)) + off);
+    const uint32_t Y1 = (uint32_t)(__float_as_int(__builtin_fmaf(v.y, k, kMagic)) + off);
+    const uint32_t Y2 = (uint32_t)(__float_as_int(__builtin_fmaf(v.z, k, kMagic)) + off);
+    const uint32_t Y3 = (uint32_t)(__float_as_int(__builtin_fmaf(v.w, k, kMagic)) + off);
+    const int sy_part = EVEN_ODD ? (int)(Y1 + Y3) - 2 * 0x8080 : (int)((Y0 + Y1) + (Y2 + Y3)) - 4 * 0x8080;
+    float sy = (float)sy_part;
+    sy += dpp<0xB1>(sy); sy += dpp<0x4E>(sy); sy += dpp<0x141>(sy);
     const uint32_t g = i >> 3, j = i & 7u;
     uint8_t *seg = lds + plane_off(g);
     if (!EVEN_ODD) {
-        // bytes p of Y0..Y3 -> one dword per plane
-        const uint32_t P01 = __builtin_amdgcn_perm((uint32_t)Y[1], (uint32_t)Y[0], 0x05010400u);
-        const uint32_t P23 = __builtin_amdgcn_perm((uint32_t)Y[3], (uint32_t)Y[2], 0x05010400u);
-        const uint32_t Q01 = __builtin_amdgcn_perm((uint32_t)Y[1], (uint32_t)Y[0], 0x0C0C0602u);
-        const uint32_t Q23 = __builtin_amdgcn_perm((uint32_t)Y[3], (uint32_t)Y[2], 0x0C0C0602u);
-        *(uint32_t *)(seg + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x05040100u);
-        *(uint32_t *)(seg + 32 + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x07060302u);
+        const uint32_t P01 = __builtin_amdgcn_perm(Y1, Y0, 0x05010400u);   // Y0.b0 Y1.b0 Y0.b1 Y1.b1
+        const uint32_t P23 = __builtin_amdgcn_perm(Y3, Y2, 0x05010400u);
+        const uint32_t Q01 = __builtin_amdgcn_perm(Y1, Y0, 0x0C0C0602u);   // Y0.b2 Y1.b2
+        const uint32_t Q23 = __builtin_amdgcn_perm(Y3, Y2, 0x0C0C0602u);
+        *(uint32_t *)(seg + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x05040100u) ^ 0x80808080u;
+        *(uint32_t *)(seg + 32 + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x07060302u) ^ 0x80808080u;
         *(uint32_t *)(seg + 64 + 4 * j) = __builtin_amdgcn_perm(Q23, Q01, 0x05040100u);
     } else {
         // elements 4j, 4j+2 -> even positions 2j, 2j+1; 4j+1, 4j+3 -> odd positions 16+2j, 17+2j
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const uint32_t ev = ((uint32_t)(Y[0] >> (8 * p)) & 0xFFu) | (((uint32_t)(Y[2] >> (8 * p)) & 0xFFu) << 8);
-            const uint32_t od = ((uint32_t)(Y[1] >> (8 * p)) & 0xFFu) | (((uint32_t)(Y[3] >> (8 * p)) & 0xFFu) << 8);
-            *(uint16_t *)(seg + 32 * p + 2 * j) = (uint16_t)ev;
-            *(uint16_t *)(seg + 32 * p + 16 + 2 * j) = (uint16_t)od;
-        }
+        const uint32_t E = __builtin_amdgcn_perm(Y2, Y0, 0x05010400u);     // Y0.b0 Y2.b0 Y0.b1 Y2.b1
+        const uint32_t O = __builtin_amdgcn_perm(Y3, Y1, 0x05010400u);
+        const uint32_t E2 = __builtin_amdgcn_perm(Y2, Y0, 0x0C0C0602u);    // Y0.b2 Y2.b2
+        const uint32_t O2 = __builtin_amdgcn_perm(Y3, Y1, 0x0C0C0602u);
+        *(uint16_t *)(seg + 2 * j) = (uint16_t)(E ^ 0x8080u);
+        *(uint16_t *)(seg + 32 + 2 * j) = (uint16_t)((E >> 16) ^ 0x8080u);
+        *(uint16_t *)(seg + 64 + 2 * j) = (uint16_t)E2;
+        *(uint16_t *)(seg + 16 + 2 * j) = (uint16_t)(O ^ 0x8080u);
+        *(uint16_t *)(seg + 48 + 2 * j) = (uint16_t)((O >> 16) ^ 0x8080u);
+        *(uint16_t *)(seg + 80 + 2 * j) = (uint16_t)O2;
     }
-    float *rec = (float *)(lds + meta + 16u * g);
-    if (j == 0) { rec[0] = ik; rec[1] = sx; rec[3] = __builtin_bit_cast(float, sd); }
-    if (j == 4) rec[2] = sx;
+    if (j == 0) *(float4 *)(lds + meta + 16u * g) = make_float4(ik, s, h, sy);
 }
 
 // sum q*Y from the three plane dot products (see above)
-__device__ __forceinline__ float fix3(uint32_t d0, uint32_t d1, int d2)
+__device__ __forceinline__ float fix3(int d0, int d1, int d2)
 {
-    return __builtin_fmaf((float)(d2 * 256 + (int)d1), 256.0f, (float)d0);
+    return __builtin_fmaf((float)(d2 * 256 + d1), 256.0f, (float)d0);
 }
 
 // A lane's x for its item: S slots of SEG elements (planes or f32).
 template <int S, int SEG> struct XP {
     uint32_t p[S][3][SEG / 4];
-    float ik[S], sx[S];
-    int sd[S];
+    float ik[S], sx[S], sy[S];
 };
 template <int S, int SEG> struct XF {
     float v[S * SEG];
     float sx[S];
 };
 
-__device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c)
-{
-    return __builtin_amdgcn_udot4(a, b, c, false);
-}
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
 {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
+// high nibbles as the signed bytes 16*h - 128
+__device__ __forceinline__ uint32_t hi_s(uint32_t w) { return (w & 0xF0F0F0F0u) ^ 0x80808080u; }
 
 // ------------------------------------------------------ team GEMV items
 //
@@ -396,16 +391,16 @@ template <> struct Item<T_Q4_K> {
         const float d = h2f(r[0]), dmin = h2f(r[0] >> 16);
         uint32_t SC, MN;
         k4pair(it & 3u, r[1], r[2], r[3], SC, MN);
-        uint32_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
-        int a2 = 0, b2 = 0;
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const uint32_t lo = andm(r[4 + t], 0x0F0F0F0Fu), hi = andm(r[4 + t] >> 4, 0x0F0F0F0Fu);
-            a0 = udot4(lo, x.p[0][0][t], a0); a1 = udot4(lo, x.p[0][1][t], a1); a2 = sdot4(lo, x.p[0][2][t], a2);
-            b0 = udot4(hi, x.p[1][0][t], b0); b1 = udot4(hi, x.p[1][1][t], b1); b2 = sdot4(hi, x.p[1][2][t], b2);
+            const uint32_t lo = andm(r[4 + t], 0x0F0F0F0Fu), hi = hi_s(r[4 + t]);
+            a0 = sdot4(lo, x.p[0][0][t], a0); a1 = sdot4(lo, x.p[0][1][t], a1); a2 = sdot4(lo, x.p[0][2][t], a2);
+            b0 = sdot4(hi, x.p[1][0][t], b0); b1 = sdot4(hi, x.p[1][1][t], b1); b2 = sdot4(hi, x.p[1][2][t], b2);
         }
+        const float hb = __builtin_fmaf(128.0f, x.sy[1], fix3(b0, b1, b2));
         out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
-        out[1] = __builtin_fmaf(d * ub(SC, 1), fix3(b0, b1, b2) * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
+        out[1] = __builtin_fmaf((d * 0.0625f) * ub(SC, 1), hb * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
     }
 };
 
@@ -437,15 +432,14 @@ template <> struct Item<T_Q5_K> {
         const uint32_t j = (it & 3u) * 2u;
         uint32_t SC, MN;
         k4pair(it & 3u, r[1], r[2], r[3], SC, MN);
-        uint32_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
-        int a2 = 0, b2 = 0;
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const uint32_t w = r[12 + t], hb = r[4 + t];
             const uint32_t qa = andm(w, 0x0F0F0F0Fu) | (((hb >> j) & 0x01010101u) << 4);
             const uint32_t qb = andm(w >> 4, 0x0F0F0F0Fu) | (((hb >> (j + 1u)) & 0x01010101u) << 4);
-            a0 = udot4(qa, x.p[0][0][t], a0); a1 = udot4(qa, x.p[0][1][t], a1); a2 = sdot4(qa, x.p[0][2][t], a2);
-            b0 = udot4(qb, x.p[1][0][t], b0); b1 = udot4(qb, x.p[1][1][t], b1); b2 = sdot4(qb, x.p[1][2][t], b2);
+            a0 = sdot4(qa, x.p[0][0][t], a0); a1 = sdot4(qa, x.p[0][1][t], a1); a2 = sdot4(qa, x.p[0][2][t], a2);
+            b0 = sdot4(qb, x.p[1][0][t], b0); b1 = sdot4(qb, x.p[1][1][t], b1); b2 = sdot4(qb, x.p[1][2][t], b2);
         }
         out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
         out[1] = __builtin_fmaf(d * ub(SC, 1), fix3(b0, b1, b2) * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
@@ -498,8 +492,7 @@ template <> struct Item<T_Q6_K> {
     {
         const float d = h2f(r[14]);
         const uint32_t i8 = (it & 1u) * 8u;
-        uint32_t u0[4] = {0, 0, 0, 0}, u1[4] = {0, 0, 0, 0};
-        int s2[4] = {0, 0, 0, 0};
+        int u0[4] = {0, 0, 0, 0}, u1[4] = {0, 0, 0, 0}, s2[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const uint32_t A = r[t], B = r[4 + t], H = r[8 + t];
@@ -509,8 +502,8 @@ template <> struct Item<T_Q6_K> {
                                    andm(B >> 4, 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u)};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                u0[k] = udot4(q[k], x.p[k][0][t], u0[k]);
-                u1[k] = udot4(q[k], x.p[k][1][t], u1[k]);
+                u0[k] = sdot4(q[k], x.p[k][0][t], u0[k]);
+                u1[k] = sdot4(q[k], x.p[k][1][t], u1[k]);
                 s2[k] = sdot4(q[k], x.p[k][2][t], s2[k]);
             }
         }
@@ -524,9 +517,8 @@ template <> struct Item<T_Q6_K> {
 };
 
 // Q8_0 (quant.rs:106-113): item = two blocks (68 bytes, 4-byte aligned).
-// Block 0's codes sit at byte 2 (realigned), block 1's at byte 36 (aligned).
-// Signed codes: the unsigned planes take u = q ^ 0x80 = q + 128 and subtract
-// 128 * sum(d0 + 256 d1) afterwards; the signed plane takes q itself.
+// Block 0's codes sit at byte 2 (realigned), block 1's at byte 36 (aligned);
+// the signed codes meet the signed digits directly.
 template <> struct Item<T_Q8_0> {
     static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 17, UNIT = 64;
     static constexpr bool PLANES = true, EVEN_ODD = false;
@@ -548,16 +540,13 @@ template <> struct Item<T_Q8_0> {
         const float dd[2] = {h2f(r[0]), h2f(r[8] >> 16)};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            uint32_t a0 = 0, a1 = 0;
-            int a2 = 0;
+            int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const uint32_t q = s == 0 ? __builtin_amdgcn_alignbyte(r[t + 1], r[t], 2u) : r[9 + t];
-                const uint32_t u = xorm(q, 0x80808080u);
-                a0 = udot4(u, x.p[s][0][t], a0); a1 = udot4(u, x.p[s][1][t], a1); a2 = sdot4(q, x.p[s][2][t], a2);
+                a0 = sdot4(q, x.p[s][0][t], a0); a1 = sdot4(q, x.p[s][1][t], a1); a2 = sdot4(q, x.p[s][2][t], a2);
             }
-            const int lo = (int)(a0 + 256u * a1) - 128 * x.sd[s];
-            out[s] = dd[s] * (__builtin_fmaf((float)a2, 65536.0f, (float)lo) * x.ik[s]);
+            out[s] = dd[s] * (fix3(a0, a1, a2) * x.ik[s]);
         }
     }
 };
@@ -584,17 +573,18 @@ template <> struct Item<T_Q4_0> {
         const float dd[2] = {h2f(r[0]), h2f(r[4] >> 16)};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            uint32_t a0 = 0, a1 = 0;
-            int a2 = 0;
+            int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const uint32_t q = s == 0 ? __builtin_amdgcn_alignbyte(r[t + 1], r[t], 2u) : r[5 + t];
-                const uint32_t lo = andm(q, 0x0F0F0F0Fu), hi = andm(q >> 4, 0x0F0F0F0Fu);
-                a0 = udot4(lo, x.p[s][0][t], a0); a1 = udot4(lo, x.p[s][1][t], a1); a2 = sdot4(lo, x.p[s][2][t], a2);
-                a0 = udot4(hi, x.p[s][0][4 + t], a0); a1 = udot4(hi, x.p[s][1][4 + t], a1);
-                a2 = sdot4(hi, x.p[s][2][4 + t], a2);
+                const uint32_t lo = andm(q, 0x0F0F0F0Fu), hi = hi_s(q);
+                a0 = sdot4(lo, x.p[s][0][t], a0); a1 = sdot4(lo, x.p[s][1][t], a1); a2 = sdot4(lo, x.p[s][2][t], a2);
+                b0 = sdot4(hi, x.p[s][0][4 + t], b0); b1 = sdot4(hi, x.p[s][1][4 + t], b1);
+                b2 = sdot4(hi, x.p[s][2][4 + t], b2);
             }
-            out[s] = dd[s] * __builtin_fmaf(-8.0f, x.sx[s], fix3(a0, a1, a2) * x.ik[s]);
+            const float qy = __builtin_fmaf(__builtin_fmaf(128.0f, x.sy[s], fix3(b0, b1, b2)), 0.0625f,
+                                            fix3(a0, a1, a2));
+            out[s] = dd[s] * __builtin_fmaf(-8.0f, x.sx[s], qy * x.ik[s]);
         }
     }
 };
@@ -625,15 +615,14 @@ template <> struct Item<T_Q5_0> {
         const uint32_t qh[2] = {__builtin_amdgcn_alignbyte(r[1], r[0], 2u), r[6]};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            uint32_t a0 = 0, a1 = 0;
-            int a2 = 0;
+            int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const uint32_t q = s == 0 ? __builtin_amdgcn_alignbyte(r[t + 2], r[t + 1], 2u) : r[7 + t];
                 const uint32_t lo = andm(q, 0x0F0F0F0Fu) | spread4(qh[s] >> (4 * t));
                 const uint32_t hi = andm(q >> 4, 0x0F0F0F0Fu) | spread4(qh[s] >> (16 + 4 * t));
-                a0 = udot4(lo, x.p[s][0][t], a0); a1 = udot4(lo, x.p[s][1][t], a1); a2 = sdot4(lo, x.p[s][2][t], a2);
-                a0 = udot4(hi, x.p[s][0][4 + t], a0); a1 = udot4(hi, x.p[s][1][4 + t], a1);
+                a0 = sdot4(lo, x.p[s][0][t], a0); a1 = sdot4(lo, x.p[s][1][t], a1); a2 = sdot4(lo, x.p[s][2][t], a2);
+                a0 = sdot4(hi, x.p[s][0][4 + t], a0); a1 = sdot4(hi, x.p[s][1][4 + t], a1);
                 a2 = sdot4(hi, x.p[s][2][4 + t], a2);
             }
             out[s] = dd[s] * __builtin_fmaf(-16.0f, x.sx[s], fix3(a0, a1, a2) * x.ik[s]);
@@ -700,55 +689,37 @@ template <> struct Item<T_F32> {
     }
 };
 
-// Rows (row groups) per batch of the pipelined loop.
-template <uint32_t T> constexpr int rows_pipe()
-{
-    return T == T_Q4_K || T == T_Q4_0 || T == T_Q5_0 ? 2 : 1;
-}
-// Largest single-batch R whose loads fit the register budget.
-template <uint32_t T> constexpr int rows_single_max() { return Item<T>::NRAW < 12 ? 6 : Item<T>::NRAW <= 20 ? 4 : 2; }
-
-// ------------------------------------------------------- x preparation
+// ------------------------------------------------------- row streaming
 //
-// The quant-type team kernels read x as the fixed-point image described
-// above (planes + segment records).  It is built once per mat-vec by xprep_k
-// (or by the kernel that produces x) and each workgroup copies it into LDS.
+// Row groups: g = UNIT / gcd(cols, UNIT) consecutive rows hold whole units
+// (superblocks for K-quants, item pairs of blocks otherwise), so every row
+// group starts at a whole item and rows of a group share items only where a
+// row boundary falls inside one (each slot of an item lies in one row).  A
+// team of lanes owns whole row groups: lane i decodes item i of each of them,
+// and a team spans 1..8 waves (wpt) when a row group has more than 64 items.
+// Row groups are dealt to teams band-wise: team t takes t, t + NT, t + 2NT,
+// ... (NT = teams in the grid), so at any moment the whole grid streams one
+// contiguous band of the matrix.
 
+// x as the kernel stages it in LDS: planes + records (quant types) or padded f32
 __host__ __device__ constexpr uint32_t image_bytes(bool planes, uint32_t cols)
 {
     return planes ? planes_bytes(cols) + (cols / 32) * 16u : (cols / 4 + cols / 64 + 1) * 16u;
 }
 
-template <bool EVEN_ODD>
-__global__ void __launch_bounds__(256) xprep_k(const float *__restrict__ x, uint32_t cols,
-                                               uint8_t *__restrict__ img)
-{
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    // cols % 32 == 0: the 8 lanes of a segment are in range together
-    if (i < cols / 4) stage_planes1<EVEN_ODD>(((const float4 *)x)[i], i, img, planes_bytes(cols));
-}
-
-// ------------------------------------------------------- team GEMV kernel
-//
-// A workgroup copies the x image into LDS once and runs several teams.  A
-// team owns whole row groups: its lanes each decode one item of every row
-// group, and a team spans 1..8 waves (wpt) when a row has more than 64 items.
-// Row groups are dealt to teams band-wise: team t takes t, t + NT, t + 2NT, ...
-// (NT = teams in the grid), so that at any moment the whole grid streams one
-// contiguous band of the matrix.  Every team runs the same number of batches,
-// so the cross-wave reduction may use workgroup barriers.
-
 constexpr int kMaxWG = 768;        // 12 waves: 3 per SIMD
 constexpr int kStage = 8;          // 16-byte pieces of x each thread loads before the weights
 
-struct TeamArgs {
+struct StreamArgs {
     const uint8_t *w;
-    const void *x;                 // x image (quant types) or x itself (F16/F32)
+    const float *x;
     float *y;
     uint32_t nbytes, group_bytes, rows, cols, g, n_groups, ni;
     uint32_t n_teams;              // NT
     uint32_t per_team;             // batches every team runs
     uint32_t wpt;                  // waves per team (TSUB == 0)
+    uint32_t chunk;                // batches per partial-sum flush (TSUB == 0)
+    uint32_t red_off;              // LDS byte offset of the partial-sum slots
 };
 
 // Workgroup barrier that waits for this wave's LDS traffic only: global loads
@@ -763,7 +734,7 @@ __device__ __forceinline__ void lds_barrier()
 // are masked out later) so that all of them are in flight together.  Byte
 // offsets fit in 32 bits (the planner sends larger matrices elsewhere).
 template <uint32_t T, int R>
-__device__ __forceinline__ void issue(const TeamArgs &a, uint32_t t, uint32_t i, uint32_t it,
+__device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t i, uint32_t it,
                                       uint32_t ib, bool active, uint32_t (&raw)[R][Item<T>::NRAW])
 {
 #pragma unroll
@@ -775,54 +746,73 @@ __device__ __forceinline__ void issue(const TeamArgs &a, uint32_t t, uint32_t i,
     }
 }
 
-template <uint32_t T, int TSUB, int R, bool PIPE, bool G1>
-__global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
+// CONV: a.x is x itself (f32) and the workgroup converts it to the
+// fixed-point planes while the weight loads are in flight; otherwise a.x is
+// the prepared image (quant types) or x (F16/F32).  XS: 16-byte pieces of x
+// each thread loads before the weights.
+// ------------------------------------------------------ stream GEMV kernel
+//
+// Persistent form of the team kernel.  A workgroup (TPW teams) stages x once,
+// holds each lane's x slice in VGPRs and then streams its teams' batches of R
+// row groups with D batches of loads in flight: batch i + D is issued as soon
+// as batch i has been consumed, so compute runs while the matrix streams and
+// no wave ever holds more than D batches of loads (more would stall the
+// issue of every load behind a full memory queue).  Before the first batch
+// only D batches are issued, so x is staged early.
+//
+// Teams of one wave or less (TSUB > 0) reduce with DPP and write y directly.
+// Teams of several waves (TSUB == 0) park each wave's per-row partial sums in
+// LDS slots and add them up every `chunk` batches (two workgroup barriers per
+// chunk instead of per batch).
+
+template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB>
+__global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 {
     using I = Item<T>;
     constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
     constexpr int RED = G1 ? R : R * 8;
-    extern __shared__ float4 xl4[];              // x image, one copy per workgroup
-    __shared__ float red[kMaxWG / 64][RED];
+    constexpr bool CV = CONV && I::PLANES;
+    extern __shared__ float4 xl4[];
     uint8_t *lds = (uint8_t *)xl4;
 
     const uint32_t tid = threadIdx.x;
-    const uint32_t TL = TSUB ? (uint32_t)TSUB : 64u * a.wpt;   // lanes per team
+    const uint32_t TL = TSUB ? (uint32_t)TSUB : 64u * a.wpt;
     const uint32_t lt = tid % TL, tw = tid / TL, tpw = blockDim.x / TL;
     const bool active = lt < a.ni;
     const uint32_t it = active ? lt : 0u;
     const uint32_t ib = I::item_byte(it);
     const uint32_t team = blockIdx.x * tpw + tw;
+    const uint32_t g = G1 ? 1u : a.g;
 
-    // 1. x loads first, then this team's weight loads (two batches when
-    //    pipelined): vmcnt counts in order, so the LDS writes below wait for
-    //    x only and the weights stay in flight
-    const uint32_t n16 = I::PLANES ? image_bytes(true, a.cols) / 16u : a.cols / 4u;
+    // 1. x loads, then the first D batches of weight loads
+    const uint32_t n16 = I::PLANES && !CV ? image_bytes(true, a.cols) / 16u : a.cols / 4u;
     const uint4 *src = (const uint4 *)a.x;
-    uint4 xv[kStage];
+    const uint32_t meta = planes_bytes(a.cols);
+    uint4 xv[XS];
 #pragma unroll
-    for (int k = 0; k < kStage; k++) {
+    for (int k = 0; k < XS; k++) {
         const uint32_t j = tid + k * blockDim.x;
         xv[k] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
     }
-    uint32_t rawA[R][NR];
-    uint32_t rawB[PIPE ? R : 1][PIPE ? NR : 1];
-    issue<T, R>(a, team, 0, it, ib, active, rawA);
-    if constexpr (PIPE) {
-        if (a.per_team > 1) issue<T, R>(a, team, 1, it, ib, active, rawB);
-    }
-    uint4 *l4 = (uint4 *)xl4;
-    // f32 layout: float4 j of x at j + j/16 (16 bytes of padding per 64 floats)
+    uint32_t raw[D][R][NR];
 #pragma unroll
-    for (int k = 0; k < kStage; k++) {
+    for (int d = 0; d < D; d++)
+        if ((uint32_t)d < a.per_team) issue<T, R>(a, team, d, it, ib, active, raw[d]);
+
+    // 2. stage x, then this lane's slice into VGPRs
+    uint4 *l4 = (uint4 *)xl4;
+    auto put = [&](uint4 v, uint32_t j) {
+        if constexpr (CV) stage_planes1<I::EVEN_ODD>(__builtin_bit_cast(float4, v), j, lds, meta);
+        else l4[I::PLANES ? j : j + (j >> 4)] = v;
+    };
+#pragma unroll
+    for (int k = 0; k < XS; k++) {
         const uint32_t j = tid + k * blockDim.x;
-        if (j < n16) l4[I::PLANES ? j : j + (j >> 4)] = xv[k];
+        if (j < n16) put(xv[k], j);
     }
-    for (uint32_t j = tid + kStage * blockDim.x; j < n16; j += blockDim.x)
-        l4[I::PLANES ? j : j + (j >> 4)] = src[j];
+    for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(src[j], j);
     lds_barrier();
 
-    // 2. this lane's slice of x, held in VGPRs for every row group it visits
-    const uint32_t meta = planes_bytes(a.cols);
     using XT = typename std::conditional<I::PLANES, XP<S, SEG>, XF<S, SEG>>::type;
     XT xs;
     uint32_t srow[S];
@@ -832,8 +822,8 @@ __global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
         srow[s] = e / a.cols;
         const uint32_t c = e - srow[s] * a.cols;
         if constexpr (I::PLANES) {
-            const uint32_t g = c / 32u, h = (c / 16u) & 1u;
-            const uint8_t *sp = lds + plane_off(g) + (SEG == 16 ? 16u * h : 0u);
+            const uint32_t gs = c / 32u, h = (c / 16u) & 1u;
+            const uint8_t *sp = lds + plane_off(gs) + (SEG == 16 ? 16u * h : 0u);
 #pragma unroll
             for (int p = 0; p < 3; p++)
 #pragma unroll
@@ -842,12 +832,12 @@ __global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
                     xs.p[s][p][4 * v] = q.x; xs.p[s][p][4 * v + 1] = q.y;
                     xs.p[s][p][4 * v + 2] = q.z; xs.p[s][p][4 * v + 3] = q.w;
                 }
-            const float4 m = active ? *(const float4 *)(lds + meta + 16u * g) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 m = active ? *(const float4 *)(lds + meta + 16u * gs) : make_float4(0.f, 0.f, 0.f, 0.f);
             xs.ik[s] = m.x;
             xs.sx[s] = SEG == 32 ? m.y + m.z : (h ? m.z : m.y);
-            xs.sd[s] = __builtin_bit_cast(int, m.w);
+            xs.sy[s] = m.w;
         } else {
-            const uint32_t j = c / 4;                   // segments never straddle a pad
+            const uint32_t j = c / 4;
             const float4 *xp = xl4 + j + (j >> 4);
 #pragma unroll
             for (int v = 0; v < SEG / 4; v++) {
@@ -858,14 +848,30 @@ __global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
         }
     }
 
-    auto process = [&](const uint32_t (&raw)[R][NR], uint32_t i) {
+    // 3. stream the batches
+    float *red = (float *)(lds + a.red_off);
+    const uint32_t wave = tid >> 6, lane = tid & 63u;
+    auto flush = [&](uint32_t i0, uint32_t nb) {
+        lds_barrier();
+        for (uint32_t o = lt; o < nb * RED; o += TL) {
+            const uint32_t b = o / RED, k = o % RED;
+            const uint32_t r = G1 ? k : k / 8, gi = G1 ? 0 : k % 8;
+            const uint32_t grp = team + ((i0 + b) * R + r) * a.n_teams, row = grp * g + gi;
+            float sum = 0.f;
+            for (uint32_t wv = 0; wv < a.wpt; wv++)
+                sum += red[((tw * a.wpt + wv) * a.chunk + b) * RED + k];
+            if (gi < g && grp < a.n_groups && row < a.rows) a.y[row] = sum;
+        }
+        lds_barrier();
+    };
+    auto process = [&](const uint32_t (&rw)[R][NR], uint32_t i) {
         float v[RED];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t grp = team + (i * R + r) * a.n_teams;
             const bool ok = active && grp < a.n_groups && grp * a.group_bytes + ib < a.nbytes;
             float acc[S];
-            I::compute(raw[r], xs, it, acc);
+            I::compute(rw[r], xs, it, acc);
             if (G1) {
                 float t = 0.f;
 #pragma unroll
@@ -881,7 +887,6 @@ __global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
                 }
             }
         }
-        const uint32_t g = G1 ? 1u : a.g;
         if constexpr (TSUB != 0) {
 #pragma unroll
             for (int k = 0; k < RED; k++) {
@@ -892,36 +897,22 @@ __global__ void __launch_bounds__(kMaxWG) gemv_team(TeamArgs a)
                 if (lt == (uint32_t)TSUB - 1u && grp < a.n_groups && row < a.rows) a.y[row] = sum;
             }
         } else {
-            const uint32_t wave = tid >> 6, lane = tid & 63u;
+            const uint32_t slot = i % a.chunk;
 #pragma unroll
             for (int k = 0; k < RED; k++) {
                 const float sum = group_sum<64>(v[k]);
-                if (lane == 63u) red[wave][k] = sum;
+                if (lane == 63u) red[(wave * a.chunk + slot) * RED + k] = sum;
             }
-            lds_barrier();
-            if (lt < (uint32_t)RED) {                   // lane k of each team finishes row k
-                const uint32_t k = lt;
-                const uint32_t r = G1 ? k : k / 8, gi = G1 ? 0 : k % 8;
-                const uint32_t grp = team + (i * R + r) * a.n_teams, row = grp * g + gi;
-                float sum = 0.f;
-                for (uint32_t wv = 0; wv < a.wpt; wv++) sum += red[tw * a.wpt + wv][k];
-                if (gi < g && grp < a.n_groups && row < a.rows) a.y[row] = sum;
-            }
-            lds_barrier();
+            if (slot + 1 == a.chunk || i + 1 == a.per_team) flush(i - slot, slot + 1);
         }
     };
-
-    // 3. the team's batches (the same count in every team); pipelined: batch
-    //    i+2 is issued as soon as batch i's registers are free
-    if constexpr (!PIPE) {
-        process(rawA, 0);
-    } else {
-        for (uint32_t i = 0; i < a.per_team; i += 2) {
-            process(rawA, i);
-            if (i + 2 < a.per_team) issue<T, R>(a, team, i + 2, it, ib, active, rawA);
-            if (i + 1 >= a.per_team) break;
-            process(rawB, i + 1);
-            if (i + 3 < a.per_team) issue<T, R>(a, team, i + 3, it, ib, active, rawB);
+    for (uint32_t i = 0; i < a.per_team; i += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            if (i + d < a.per_team) {
+                process(raw[d], i + d);
+                if (i + d + D < a.per_team) issue<T, R>(a, team, i + d + D, it, ib, active, raw[d]);
+            }
         }
     }
 }
@@ -934,34 +925,16 @@ static uint32_t gcd_u(uint64_t a, uint64_t b)
     return (uint32_t)a;
 }
 
-template <uint32_t T, int R, bool PIPE, bool G1> static const void *fn_tsub(uint32_t tsub)
+template <uint32_t T, bool G1> static const void *stream_fn_g(uint32_t tsub)
 {
+    constexpr int R = 1, D = 2;
     switch (tsub) {
-    case 16: return (const void *)gemv_team<T, 16, R, PIPE, G1>;
-    case 32: return (const void *)gemv_team<T, 32, R, PIPE, G1>;
-    case 64: return (const void *)gemv_team<T, 64, R, PIPE, G1>;
-    case 0: return (const void *)gemv_team<T, 0, R, PIPE, G1>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, kMaxWG>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, kMaxWG>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, kMaxWG>;
+    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, kMaxWG>;
     default: return nullptr;
     }
-}
-
-// single-batch kernel with R rows per team (g == 1 only)
-template <uint32_t T> static const void *single_fn(uint32_t tsub, int R)
-{
-    constexpr int RM = rows_single_max<T>();
-    switch (R) {
-    case 1: return fn_tsub<T, 1, false, true>(tsub);
-    case 2: return fn_tsub<T, 2, false, true>(tsub);
-    case 4: if constexpr (RM >= 4) return fn_tsub<T, 4, false, true>(tsub); else return nullptr;
-    case 6: if constexpr (RM >= 6) return fn_tsub<T, 6, false, true>(tsub); else return nullptr;
-    default: return nullptr;
-    }
-}
-
-template <uint32_t T> static const void *pipe_fn(uint32_t tsub, bool g1)
-{
-    return g1 ? fn_tsub<T, rows_pipe<T>(), true, true>(tsub)
-              : fn_tsub<T, rows_pipe<T>(), true, false>(tsub);
 }
 
 static int max_lds_bytes()
@@ -973,25 +946,57 @@ static int max_lds_bytes()
     return v;
 }
 
-template <uint32_t T> static void plan_team(size_t rows, size_t cols, int n_cu, Plan *p)
+// Stream kernel plan (kind 1); leaves kind 0 (generic kernel) where it does
+// not apply: cols % 32 != 0, row groups longer than 768 items, more than 8
+// rows per group, byte offsets past 32 bits, or x larger than LDS.
+template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu, Plan *p)
 {
     using I = Item<T>;
     p->kind = 0;
     if (cols % 32 != 0 || rows == 0 || cols == 0) return;
-    const uint64_t unit = I::UNIT;                        // elements per aligned row-group unit
+    const uint64_t unit = I::UNIT;
     const uint64_t g = unit / gcd_u(cols, unit);
     const uint64_t gel = g * cols;
     const uint64_t ni = gel / I::IE;
-    if (ni > 512 || g > 8) return;
+    if (ni > (uint64_t)kMaxWG || g > 8) return;
     const uint64_t gbytes = gel / block_elems(T) * block_bytes(T);
     const uint64_t n_groups = (rows + g - 1) / g;
-    // 32-bit byte offsets inside the kernel (with the tail pad)
     if ((n_groups + 8) * gbytes + kTailPad >= 0xFFFFFFFFull) return;
-    const uint64_t lds = image_bytes(I::PLANES, (uint32_t)cols);
-    if (lds + 2048 > (uint64_t)max_lds_bytes()) return;
     uint32_t tsub = 0, wpt = 1, tl;
     if (ni <= 64) { tsub = 16; while (tsub < ni) tsub <<= 1; tl = tsub; }
     else { wpt = (uint32_t)((ni + 63) / 64); tl = 64 * wpt; }
+    const void *fn = g == 1 ? stream_fn_g<T, true>(tsub) : stream_fn_g<T, false>(tsub);
+    if (!fn) return;
+    const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
+    const uint32_t img = (image_bytes(I::PLANES, (uint32_t)cols) + 15u) & ~15u;
+    const uint32_t red = g == 1 ? 1u : 8u;                 // partial sums per batch per wave
+    const uint64_t nbat = n_groups;                        // R = 1 row group per batch
+    // Full workgroups (768 threads) on every CU when there is enough work;
+    // otherwise smaller workgroups, one team batch each, spread over the CUs.
+    const uint32_t tpw_max = tl >= (uint32_t)kMaxWG ? 1u : (uint32_t)kMaxWG / tl;
+    const uint32_t tpw_min = tl >= 64u ? 1u : 64u / tl;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, (int)(tpw_max * tl), img + 4096) != hipSuccess)
+        occ = 0;
+    if (occ <= 0) return;
+    uint32_t tpw, per;
+    if (nbat > ncu * (uint64_t)occ * tpw_max) {
+        tpw = tpw_max;
+        per = (uint32_t)((nbat + ncu * occ * tpw - 1) / (ncu * occ * tpw));
+    } else {
+        const uint64_t t = (nbat + ncu - 1) / ncu;         // teams per CU
+        tpw = (uint32_t)(t < tpw_min ? tpw_min : t > tpw_max ? tpw_max : t);
+        per = 1;
+    }
+    const uint32_t grid = (uint32_t)((nbat + (uint64_t)tpw * per - 1) / ((uint64_t)tpw * per));
+    // partial-sum slots for a chunk of batches (several-wave teams)
+    const uint32_t nw = tpw * tl / 64u;
+    const uint32_t room = (uint32_t)max_lds_bytes() > img ? (uint32_t)max_lds_bytes() - img : 0u;
+    uint32_t chunk = per < 64u ? per : 64u;
+    while (chunk > 1 && nw * chunk * red * 4u > room) chunk >>= 1;
+    const uint32_t lds = img + (tsub == 0 ? nw * chunk * red * 4u : 0u);
+    if (lds > (uint32_t)max_lds_bytes()) return;
+    p->fn = fn;
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
     p->ts = tl;
@@ -999,59 +1004,15 @@ template <uint32_t T> static void plan_team(size_t rows, size_t cols, int n_cu, 
     p->wpt = wpt;
     p->n_groups = (uint32_t)n_groups;
     p->group_bytes = gbytes;
-    p->lds = (uint32_t)lds;
-    const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
-    // resident teams of a kernel: the best of 768-, 512- and 256-thread
-    // workgroups (teams per workgroup share one staged copy of x)
-    auto resident = [&](const void *fn, uint32_t &block, uint32_t &tpw) {
-        uint64_t best = 0;
-        for (uint32_t bs : {768u, 512u, 256u}) {
-            const uint32_t t = bs / tl;
-            if (t == 0) continue;
-            int res = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&res, fn, (int)(t * tl), lds) != hipSuccess)
-                res = 0;
-            const uint64_t teams = ncu * (uint64_t)res * t;
-            if (teams > best) { best = teams; block = t * tl; tpw = t; }
-        }
-        return best;
-    };
-    // one batch per team when the smallest R in {1, 2, 4, 6} lets every batch
-    // have a resident team: all loads are issued at once
-    if (g == 1) {
-        for (int R : {1, 2, 4, 6}) {
-            const void *fn = single_fn<T>(tsub, R);
-            if (!fn) break;
-            uint32_t block = 0, tpw = 0;
-            const uint64_t teams = resident(fn, block, tpw);
-            const uint64_t nbat = (n_groups + R - 1) / R;
-            if (teams == 0 || nbat > teams) continue;
-            p->fn = fn;
-            p->R = (uint32_t)R;
-            p->n_batches = (uint32_t)nbat;
-            p->per_team = 1;
-            p->block = block;
-            p->grid = (uint32_t)((nbat + tpw - 1) / tpw);
-            p->n_teams = p->grid * tpw;
-            p->kind = 1;
-            return;
-        }
-    }
-    // otherwise resident teams loop over batches, two batches in flight
-    const void *fn = pipe_fn<T>(tsub, g == 1);
-    uint32_t block = 0, tpw = 0;
-    const uint64_t teams = resident(fn, block, tpw);
-    if (teams == 0) return;                               // no launchable shape: generic kernel
-    const uint64_t R = rows_pipe<T>();
-    const uint64_t nbat = (n_groups + R - 1) / R;
-    const uint64_t per = (nbat + teams - 1) / teams;
-    p->fn = fn;
-    p->R = (uint32_t)R;
+    p->R = 1;
     p->n_batches = (uint32_t)nbat;
-    p->per_team = (uint32_t)per;
-    p->block = block;
-    p->grid = (uint32_t)((nbat + tpw * per - 1) / (tpw * per));
-    p->n_teams = p->grid * tpw;
+    p->per_team = per;
+    p->block = tpw * tl;
+    p->grid = grid;
+    p->n_teams = grid * tpw;
+    p->chunk = chunk;
+    p->red_off = img;
+    p->lds = lds;
     p->kind = 1;
 }
 
@@ -1060,14 +1021,14 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p)
     *p = Plan{};
     if (rows > 0xFFFFFFFFull || cols > 0xFFFFFFFFull) return 0;
     switch (type) {
-    case T_F32: plan_team<T_F32>(rows, cols, n_cu, p); break;
-    case T_F16: plan_team<T_F16>(rows, cols, n_cu, p); break;
-    case T_Q4_0: plan_team<T_Q4_0>(rows, cols, n_cu, p); break;
-    case T_Q5_0: plan_team<T_Q5_0>(rows, cols, n_cu, p); break;
-    case T_Q8_0: plan_team<T_Q8_0>(rows, cols, n_cu, p); break;
-    case T_Q4_K: plan_team<T_Q4_K>(rows, cols, n_cu, p); break;
-    case T_Q5_K: plan_team<T_Q5_K>(rows, cols, n_cu, p); break;
-    case T_Q6_K: plan_team<T_Q6_K>(rows, cols, n_cu, p); break;
+    case T_F32: plan_stream<T_F32>(rows, cols, n_cu, p); break;
+    case T_F16: plan_stream<T_F16>(rows, cols, n_cu, p); break;
+    case T_Q4_0: plan_stream<T_Q4_0>(rows, cols, n_cu, p); break;
+    case T_Q5_0: plan_stream<T_Q5_0>(rows, cols, n_cu, p); break;
+    case T_Q8_0: plan_stream<T_Q8_0>(rows, cols, n_cu, p); break;
+    case T_Q4_K: plan_stream<T_Q4_K>(rows, cols, n_cu, p); break;
+    case T_Q5_K: plan_stream<T_Q5_K>(rows, cols, n_cu, p); break;
+    case T_Q6_K: plan_stream<T_Q6_K>(rows, cols, n_cu, p); break;
     default: return -1;
     }
     return 0;
@@ -1075,37 +1036,19 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p)
 
 // ------------------------------------------------------------ launchers
 
-static int launch_team(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
-                       const void *x, float *y, hipStream_t st)
-{
-    TeamArgs a;
-    a.w = w; a.x = x; a.y = y; a.nbytes = (uint32_t)nbytes; a.group_bytes = (uint32_t)p.group_bytes;
-    a.rows = (uint32_t)rows; a.cols = (uint32_t)cols; a.g = p.g; a.n_groups = p.n_groups;
-    a.ni = p.ni; a.n_teams = p.n_teams; a.per_team = p.per_team; a.wpt = p.wpt;
-    void *args[] = {&a};
-    if (hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) != hipSuccess) return -2;
-    return 0;
-}
-
-// Quant types read x through the fixed-point image: xprep_k builds it in
-// `img` (image_bytes(true, cols) bytes, 16-byte aligned) first.
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
-                size_t cols, const float *x, float *y, uint8_t *img, ihipStream_t *stream)
+                size_t cols, const float *x, float *y, ihipStream_t *stream)
 {
     hipStream_t st = (hipStream_t)stream;
     if (p.kind != 1 || !p.fn) return launch_gemv_generic(type, w, rows, cols, x, y, stream);
-    if (type == T_F16 || type == T_F32) return launch_team(p, w, nbytes, rows, cols, x, y, st);
-    if (!img) return -1;
-    const uint32_t n4 = (uint32_t)(cols / 4);
-    if (type == T_Q4_0)
-        hipLaunchKernelGGL(xprep_k<true>, dim3((n4 + 255) / 256), dim3(256), 0, st, x, (uint32_t)cols, img);
-    else
-        hipLaunchKernelGGL(xprep_k<false>, dim3((n4 + 255) / 256), dim3(256), 0, st, x, (uint32_t)cols, img);
-    if (hipGetLastError() != hipSuccess) return -2;
-    return launch_team(p, w, nbytes, rows, cols, img, y, st);
+    StreamArgs a;
+    a.w = w; a.x = x; a.y = y; a.nbytes = (uint32_t)nbytes; a.group_bytes = (uint32_t)p.group_bytes;
+    a.rows = (uint32_t)rows; a.cols = (uint32_t)cols; a.g = p.g; a.n_groups = p.n_groups;
+    a.ni = p.ni; a.n_teams = p.n_teams; a.per_team = p.per_team; a.wpt = p.wpt;
+    a.chunk = p.chunk; a.red_off = p.red_off;
+    void *args[] = {&a};
+    return hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) == hipSuccess ? 0 : -2;
 }
-
-size_t x_image_bytes(size_t cols) { return image_bytes(true, (uint32_t)cols); }
 
 template <uint32_t T>
 static int launch_generic_t(const uint8_t *w, size_t rows, size_t cols, const float *x, float *y,
