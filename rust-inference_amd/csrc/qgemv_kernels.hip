@@ -287,11 +287,28 @@ template <int N> __device__ __forceinline__ float group_sum(float v)
 // Stage float4 i of x (already loaded into v) as fixed-point planes; each
 // aligned group of 8 lanes holds one 32-element segment and must be active
 // together.
+template <int CTRL> __device__ __forceinline__ uint32_t dppu(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// max(|a|, |b|, |c|, |d|) (v_max3 with abs modifiers; no NaN canonicalisation)
+__device__ __forceinline__ float absmax4(float4 v)
+{
+    float r;
+    asm("v_max3_f32 %0, |%1|, |%2|, |%3|\n\tv_max_f32_e64 %0, |%4|, %0"
+        : "=&v"(r) : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+    return r;
+}
+
 template <bool EVEN_ODD>
 __device__ __forceinline__ void stage_planes1(float4 v, uint32_t i, uint8_t *lds, uint32_t meta)
 {
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m));
+    // non-negative floats order like their bit patterns: max over the 8 lanes
+    // of the segment in integer DPP steps (a NaN element is caught by `bad`)
+    uint32_t mb = __float_as_uint(absmax4(v));
+    mb = max(mb, dppu<0xB1>(mb)); mb = max(mb, dppu<0x4E>(mb)); mb = max(mb, dppu<0x141>(mb));
+    const float m = __uint_as_float(mb);
     float s = (v.x + v.y) + (v.z + v.w);
     s += dpp<0xB1>(s); s += dpp<0x4E>(s);            // 16-element half sums
     const float h = dpp<0x141>(s);                   // the other half's sum
@@ -354,6 +371,13 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
 {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
+// first dot of a chain (VOP3P form with a zero accumulator: no v_mov 0)
+__device__ __forceinline__ int sdot4z(uint32_t a, uint32_t b)
+{
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 // high nibbles as the signed bytes 16*h - 128
 __device__ __forceinline__ uint32_t hi_s(uint32_t w) { return (w & 0xF0F0F0F0u) ^ 0x80808080u; }
 
@@ -366,41 +390,95 @@ __device__ __forceinline__ uint32_t hi_s(uint32_t w) { return (w & 0xF0F0F0F0u) 
 
 template <uint32_t T> struct Item;
 
-// Q4_K (quant.rs:210-228): item = (block, pair p): sub-blocks 2p (low nibbles)
-// and 2p+1 (high nibbles) of qs[32p .. 32p+32].
+// Q4_K (quant.rs:210-228): item = (block, half h): qs[64h .. 64h+64), pairs
+// p = 2h, 2h+1, i.e. sub-blocks 4h .. 4h+3 as slots 0..3 (low nibbles of pair
+// p -> sub-block 2p, high nibbles -> 2p+1).  128 weights per lane per row
+// group halve the per-weight cost of the header, the reduction and the
+// addressing against 64-weight items.
 template <> struct Item<T_Q4_K> {
-    static constexpr uint32_t IE = 64, S = 2, SEG = 32, NRAW = 12, UNIT = 256;
+    static constexpr uint32_t IE = 128, S = 4, SEG = 32, NRAW = 20, UNIT = 256;
     static constexpr bool PLANES = true, EVEN_ODD = false;
     __device__ static uint32_t seg_elem(uint32_t it, uint32_t s)
     {
-        return (it >> 2) * 256u + (it & 3u) * 64u + s * 32u;
+        return (it >> 1) * 256u + (it & 1u) * 128u + s * 32u;
     }
-    __device__ static uint32_t item_byte(uint32_t it) { return (it >> 2) * 144u; }
+    __device__ static uint32_t item_byte(uint32_t it) { return (it >> 1) * 144u; }
     __device__ static void load(const uint8_t *ip, uint32_t it, uint32_t (&r)[NRAW])
     {
         const uint4 h = *(const uint4 *)ip;
-        const uint4 *q = (const uint4 *)(ip + 16u + (it & 3u) * 32u);
-        const uint4 q0 = q[0], q1 = q[1];
+        const uint4 *q = (const uint4 *)(ip + 16u + (it & 1u) * 64u);
+        const uint4 q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
         r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
         r[4] = q0.x; r[5] = q0.y; r[6] = q0.z; r[7] = q0.w;
         r[8] = q1.x; r[9] = q1.y; r[10] = q1.z; r[11] = q1.w;
+        r[12] = q2.x; r[13] = q2.y; r[14] = q2.z; r[15] = q2.w;
+        r[16] = q3.x; r[17] = q3.y; r[18] = q3.z; r[19] = q3.w;
+    }
+    // sum q*x of the four sub-blocks, each in units of 1/k of its segment
+    __device__ static void dots(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, float (&D)[4])
+    {
+        int acc[4][3];
+#pragma unroll
+        for (int pp = 0; pp < 2; pp++) {
+            const uint32_t lo = andm(r[4 + 8 * pp], 0x0F0F0F0Fu), hi = hi_s(r[4 + 8 * pp]);
+#pragma unroll
+            for (int c = 0; c < 3; c++) {
+                acc[2 * pp][c] = sdot4z(lo, x.p[2 * pp][c][0]);
+                acc[2 * pp + 1][c] = sdot4z(hi, x.p[2 * pp + 1][c][0]);
+            }
+        }
+#pragma unroll
+        for (int t = 1; t < 8; t++)
+#pragma unroll
+            for (int pp = 0; pp < 2; pp++) {
+                const uint32_t lo = andm(r[4 + 8 * pp + t], 0x0F0F0F0Fu), hi = hi_s(r[4 + 8 * pp + t]);
+#pragma unroll
+                for (int c = 0; c < 3; c++) {
+                    acc[2 * pp][c] = sdot4(lo, x.p[2 * pp][c][t], acc[2 * pp][c]);
+                    acc[2 * pp + 1][c] = sdot4(hi, x.p[2 * pp + 1][c][t], acc[2 * pp + 1][c]);
+                }
+            }
+#pragma unroll
+        for (int s = 0; s < 4; s += 2) {
+            D[s] = fix3(acc[s][0], acc[s][1], acc[s][2]) * x.ik[s];
+            // high nibbles: (sum (16h - 128) Y + 128 sY) / 16
+            D[s + 1] = __builtin_fmaf(128.0f, x.sy[s + 1], fix3(acc[s + 1][0], acc[s + 1][1], acc[s + 1][2])) *
+                       (x.ik[s + 1] * 0.0625f);
+        }
+    }
+    __device__ static void scales(const uint32_t (&r)[NRAW], uint32_t it, uint32_t (&SC)[2], uint32_t (&MN)[2])
+    {
+        const uint32_t p0 = (it & 1u) * 2u;
+        k4pair(p0, r[1], r[2], r[3], SC[0], MN[0]);
+        k4pair(p0 + 1u, r[1], r[2], r[3], SC[1], MN[1]);
     }
     __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
                                    float (&out)[S])
     {
         const float d = h2f(r[0]), dmin = h2f(r[0] >> 16);
-        uint32_t SC, MN;
-        k4pair(it & 3u, r[1], r[2], r[3], SC, MN);
-        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+        uint32_t SC[2], MN[2];
+        scales(r, it, SC, MN);
+        float D[4];
+        dots(r, x, D);
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const uint32_t lo = andm(r[4 + t], 0x0F0F0F0Fu), hi = hi_s(r[4 + t]);
-            a0 = sdot4(lo, x.p[0][0][t], a0); a1 = sdot4(lo, x.p[0][1][t], a1); a2 = sdot4(lo, x.p[0][2][t], a2);
-            b0 = sdot4(hi, x.p[1][0][t], b0); b1 = sdot4(hi, x.p[1][1][t], b1); b2 = sdot4(hi, x.p[1][2][t], b2);
+        for (int s = 0; s < 4; s++)
+            out[s] = __builtin_fmaf(d * ub(SC[s >> 1], s & 1), D[s], -(dmin * ub(MN[s >> 1], s & 1)) * x.sx[s]);
+    }
+    // sum of the four slots (one row per item)
+    __device__ static float compute_sum(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it)
+    {
+        const float d = h2f(r[0]), dmin = h2f(r[0] >> 16);
+        uint32_t SC[2], MN[2];
+        scales(r, it, SC, MN);
+        float D[4];
+        dots(r, x, D);
+        float u = ub(SC[0], 0) * D[0], mm = ub(MN[0], 0) * x.sx[0];
+#pragma unroll
+        for (int s = 1; s < 4; s++) {
+            u = __builtin_fmaf(ub(SC[s >> 1], s & 1), D[s], u);
+            mm = __builtin_fmaf(ub(MN[s >> 1], s & 1), x.sx[s], mm);
         }
-        const float hb = __builtin_fmaf(128.0f, x.sy[1], fix3(b0, b1, b2));
-        out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
-        out[1] = __builtin_fmaf((d * 0.0625f) * ub(SC, 1), hb * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
+        return __builtin_fmaf(d, u, -dmin * mm);
     }
 };
 
@@ -701,6 +779,10 @@ template <> struct Item<T_F32> {
 // ... (NT = teams in the grid), so at any moment the whole grid streams one
 // contiguous band of the matrix.
 
+// Items that can return the sum of their slots directly (one row per item)
+template <class I, class = void> struct HasSum : std::false_type {};
+template <class I> struct HasSum<I, std::void_t<decltype(&I::compute_sum)>> : std::true_type {};
+
 // x as the kernel stages it in LDS: planes + records (quant types) or padded f32
 __host__ __device__ constexpr uint32_t image_bytes(bool planes, uint32_t cols)
 {
@@ -709,6 +791,11 @@ __host__ __device__ constexpr uint32_t image_bytes(bool planes, uint32_t cols)
 
 constexpr int kMaxWG = 768;        // 12 waves: 3 per SIMD
 constexpr int kStage = 8;          // 16-byte pieces of x each thread loads before the weights
+constexpr int kDepth = 2;          // batches of loads in flight per team
+
+// Largest workgroup of the stream kernel for type T: 128-weight items hold a
+// 96-VGPR x slice and need the register budget of 2 waves per SIMD.
+template <uint32_t T> constexpr int wg_max() { return Item<T>::IE == 128 ? 512 : kMaxWG; }
 
 struct StreamArgs {
     const uint8_t *w;
@@ -721,6 +808,16 @@ struct StreamArgs {
     uint32_t chunk;                // batches per partial-sum flush (TSUB == 0)
     uint32_t red_off;              // LDS byte offset of the partial-sum slots
 };
+
+// y[row] = v as an inline-asm store.  The compiler does not count it among the
+// vector memory operations it waits for, so the waits it places before using
+// a batch's weights stay "all but the later batches" instead of falling back
+// to "everything" after a data-dependent number of stores.  Uncounted stores
+// only make those waits stricter (vmcnt completes in order), never too loose.
+__device__ __forceinline__ void store_y(float *p, float v)
+{
+    asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
 
 // Workgroup barrier that waits for this wave's LDS traffic only: global loads
 // issued before it stay in flight.
@@ -784,20 +881,25 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     const uint32_t team = blockIdx.x * tpw + tw;
     const uint32_t g = G1 ? 1u : a.g;
 
-    // 1. x loads, then the first D batches of weight loads
+    // 1. x loads, then (once x is in) the first D batches of weight loads
     const uint32_t n16 = I::PLANES && !CV ? image_bytes(true, a.cols) / 16u : a.cols / 4u;
     const uint4 *src = (const uint4 *)a.x;
     const uint32_t meta = planes_bytes(a.cols);
+    // Every load below is unconditional (clamped addresses): the compiler's
+    // wait counting stays exact only when no load sits on a conditional path.
     uint4 xv[XS];
 #pragma unroll
     for (int k = 0; k < XS; k++) {
         const uint32_t j = tid + k * blockDim.x;
-        xv[k] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
+        xv[k] = src[j < n16 ? j : n16 - 1u];
     }
+    // x first: issued behind the weight stream of the workgroups that started
+    // earlier, x reaches the late ones after most of the matrix; waiting for
+    // it here (the weights then overlap the conversion) is measurably faster
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t raw[D][R][NR];
 #pragma unroll
-    for (int d = 0; d < D; d++)
-        if ((uint32_t)d < a.per_team) issue<T, R>(a, team, d, it, ib, active, raw[d]);
+    for (int d = 0; d < D; d++) issue<T, R>(a, team, d, it, ib, active, raw[d]);
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
@@ -860,7 +962,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
             float sum = 0.f;
             for (uint32_t wv = 0; wv < a.wpt; wv++)
                 sum += red[((tw * a.wpt + wv) * a.chunk + b) * RED + k];
-            if (gi < g && grp < a.n_groups && row < a.rows) a.y[row] = sum;
+            if (gi < g && grp < a.n_groups && row < a.rows) store_y(a.y + row, sum);
         }
         lds_barrier();
     };
@@ -868,16 +970,25 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
         float v[RED];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t grp = team + (i * R + r) * a.n_teams;
-            const bool ok = active && grp < a.n_groups && grp * a.group_bytes + ib < a.nbytes;
-            float acc[S];
-            I::compute(rw[r], xs, it, acc);
-            if (G1) {
-                float t = 0.f;
+            if constexpr (G1) {
+                // one row per group: rows past the end are computed from the
+                // clamped loads and never written; inactive lanes add zero
+                float t;
+                if constexpr (HasSum<I>::value) {
+                    t = I::compute_sum(rw[r], xs, it);
+                } else {
+                    float acc[S];
+                    I::compute(rw[r], xs, it, acc);
+                    t = 0.f;
 #pragma unroll
-                for (int s = 0; s < S; s++) t += acc[s];
-                v[r] = ok ? t : 0.f;
+                    for (int s = 0; s < S; s++) t += acc[s];
+                }
+                v[r] = active ? t : 0.f;
             } else {
+                const uint32_t grp = team + (i * R + r) * a.n_teams;
+                const bool ok = active && grp < a.n_groups && grp * a.group_bytes + ib < a.nbytes;
+                float acc[S];
+                I::compute(rw[r], xs, it, acc);
 #pragma unroll
                 for (int gi = 0; gi < 8; gi++) {
                     float t = 0.f;
@@ -894,7 +1005,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
                 if (!G1 && gi >= g) continue;
                 const float sum = group_sum<TSUB>(v[k]);
                 const uint32_t grp = team + (i * R + r) * a.n_teams, row = grp * g + gi;
-                if (lt == (uint32_t)TSUB - 1u && grp < a.n_groups && row < a.rows) a.y[row] = sum;
+                if (lt == (uint32_t)TSUB - 1u && grp < a.n_groups && row < a.rows) store_y(a.y + row, sum);
             }
         } else {
             const uint32_t slot = i % a.chunk;
@@ -906,15 +1017,20 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
             if (slot + 1 == a.chunk || i + 1 == a.per_team) flush(i - slot, slot + 1);
         }
     };
-    for (uint32_t i = 0; i < a.per_team; i += D) {
+    // Whole rounds of D batches while a full round follows; then the last
+    // 1..D batches, with no loads (a round's loads past per_team fetch clamped
+    // addresses and are never used)
+    uint32_t i = 0;
+    for (; i + D < a.per_team; i += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            if (i + d < a.per_team) {
-                process(raw[d], i + d);
-                if (i + d + D < a.per_team) issue<T, R>(a, team, i + d + D, it, ib, active, raw[d]);
-            }
+            process(raw[d], i + d);
+            issue<T, R>(a, team, i + d + D, it, ib, active, raw[d]);
         }
     }
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (i + d < a.per_team) process(raw[d], i + d);
 }
 
 // ------------------------------------------------------------ planning
@@ -927,12 +1043,12 @@ static uint32_t gcd_u(uint64_t a, uint64_t b)
 
 template <uint32_t T, bool G1> static const void *stream_fn_g(uint32_t tsub)
 {
-    constexpr int R = 1, D = 2;
+    constexpr int R = 1, D = kDepth, LB = wg_max<T>();
     switch (tsub) {
-    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, kMaxWG>;
-    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, kMaxWG>;
-    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, kMaxWG>;
-    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, kMaxWG>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB>;
+    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB>;
     default: return nullptr;
     }
 }
@@ -958,7 +1074,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     const uint64_t g = unit / gcd_u(cols, unit);
     const uint64_t gel = g * cols;
     const uint64_t ni = gel / I::IE;
-    if (ni > (uint64_t)kMaxWG || g > 8) return;
+    if (ni > (uint64_t)wg_max<T>() || g > 8) return;
     const uint64_t gbytes = gel / block_elems(T) * block_bytes(T);
     const uint64_t n_groups = (rows + g - 1) / g;
     if ((n_groups + 8) * gbytes + kTailPad >= 0xFFFFFFFFull) return;
@@ -973,7 +1089,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     const uint64_t nbat = n_groups;                        // R = 1 row group per batch
     // Full workgroups (768 threads) on every CU when there is enough work;
     // otherwise smaller workgroups, one team batch each, spread over the CUs.
-    const uint32_t tpw_max = tl >= (uint32_t)kMaxWG ? 1u : (uint32_t)kMaxWG / tl;
+    const uint32_t tpw_max = tl >= (uint32_t)wg_max<T>() ? 1u : (uint32_t)wg_max<T>() / tl;
     const uint32_t tpw_min = tl >= 64u ? 1u : 64u / tl;
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, (int)(tpw_max * tl), img + 4096) != hipSuccess)
