@@ -7,11 +7,14 @@ One step = one QuantizedMatrix::mat_vec_mul (src/quant.rs:178) over a
 that every launch misses the 256 MB Infinity Cache and streams from HBM.
 
 value        whole-job GB/s = algorithmic bytes x K / wall time of K back-to-back
-             launches (events bracket the K launches on the library's stream)
-roofline     algorithmic bytes / average kernel duration (events around each
-             launch, a second pass) against 8 TB/s; `traffic` is the HBM bytes
-             per launch that rocprofv3 FETCH_SIZE + WRITE_SIZE measured
-             (profiles/traffic.json), or null
+             launches (the better of eager launches and a HIP-graph replay)
+roofline     algorithmic bytes / average launch duration of the GEMV kernel:
+             HIP events around a HIP-graph replay of K back-to-back launches
+             (one kernel per launch, so rocprofv3 --kernel-trace --stats of the
+             same command gives the same average up to the inter-kernel gaps),
+             against 8 TB/s;
+             `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
+             WRITE_SIZE (profiles/traffic.json, written by --pmc-summary), or null
 cpu_baseline the oracle's restatement of the reference's --cpu loop
              (src/quant.rs:188-205) on one host core, same matrix
 
@@ -115,6 +118,57 @@ def cpu_baseline(oracle, raw, dtype, rows, cols, x, seconds, nbytes):
             "us_per_gemv": round(med * 1e6, 1)}
 
 
+def _pmc_rows(d):
+    """(kernel name, counter value in KiB, grid size) of every dispatch in a rocprofv3 run."""
+    import csv
+    out = []
+    for f in sorted(pathlib.Path(d).rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                out.append((r["Kernel_Name"], float(r["Counter_Value"]), int(r["Grid_Size"])))
+    return out
+
+
+def pmc_summary(args):
+    """profiles/traffic.json from a FETCH_SIZE run and a WRITE_SIZE run of
+    `bench.py ... --copy-probe-mb M`.  Both counters report KiB per dispatch;
+    the copy kernel moves exactly M MiB each way, so its readings give the
+    factor that turns the counters into bytes."""
+    res = {}
+    for key, d in (("fetch", args.pmc_summary[0]), ("write", args.pmc_summary[1])):
+        rows = _pmc_rows(d)
+        gemv = [v for k, v, _ in rows if "gemv_stream" in k]
+        copy = [v for k, v, _ in rows if "elementwise" in k.lower() and "mul" in k.lower()]
+        if not gemv or not copy:
+            raise SystemExit(f"{d}: no gemv or no copy-probe dispatches found")
+        res[key] = (statistics.median(gemv), statistics.median(copy), len(gemv), len(copy))
+    ideal_kib = args.copy_probe_mb * 1024
+    f_scale = ideal_kib / res["fetch"][1]
+    w_scale = ideal_kib / res["write"][1]
+    fetch_b = res["fetch"][0] * f_scale * 1024
+    write_b = res["write"][0] * w_scale * 1024
+    import __graft_entry__ as ge
+    rinf = ge.load_package()
+    dtype = rinf.TYPE_IDS[args.type]
+    alg = alg_bytes(rinf, dtype, args.rows, args.cols)
+    workload = f"{args.type.lower()}_gemv_{args.rows}x{args.cols}"
+    tf = ROOT / "profiles" / "traffic.json"
+    data = json.loads(tf.read_text()) if tf.exists() else {}
+    data[workload] = {
+        "hbm_bytes_per_launch": int(round(fetch_b + write_b)),
+        "fetch_bytes": int(round(fetch_b)), "write_bytes": int(round(write_b)),
+        "algorithmic_bytes": alg, "traffic_over_algorithmic": round((fetch_b + write_b) / alg, 4),
+        "raw_fetch_kib_median": res["fetch"][0], "raw_write_kib_median": res["write"][0],
+        "copy_probe_mib": args.copy_probe_mb,
+        "copy_fetch_kib_median": res["fetch"][1], "copy_write_kib_median": res["write"][1],
+        "fetch_scale": round(f_scale, 5), "write_scale": round(w_scale, 5),
+        "dispatches": {"gemv_fetch": res["fetch"][2], "gemv_write": res["write"][2]},
+    }
+    tf.parent.mkdir(exist_ok=True)
+    tf.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
+    print(json.dumps(data[workload], indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,7 +180,16 @@ def main():
     ap.add_argument("--rotate-mb", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="after timing, run 4 elementwise copies (y = 1.0 * x) of this many MiB: the "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 --pmc runs of this script (FETCH_SIZE, then "
+                         "WRITE_SIZE, each with --copy-probe-mb) into profiles/traffic.json")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -160,13 +223,23 @@ def main():
     wall_ms = min(eager_ms, graph_ms)
     ms_step = wall_ms / args.steps
     value = B / (ms_step * 1e-3) / 1e9
-    kern_ms = statistics.mean(per)
+    # average launch duration: the graph replay is GPU-side back-to-back
+    # (no host launch cost, which a profiler's callbacks inflate for eager launches)
+    kern_ms = graph_ms / args.steps
     achieved = B / (kern_ms * 1e-3) / 1e9
     log(f"eager {eager_ms / args.steps * 1e3:.2f} us/step, graph {graph_ms / args.steps * 1e3:.2f} us/step")
     log(f"wall {wall_ms:.3f} ms / {args.steps} launches = {ms_step * 1e3:.2f} us/step -> "
-        f"{value:.1f} GB/s; per-launch events: mean {kern_ms * 1e3:.2f} us, "
-        f"median {statistics.median(per) * 1e3:.2f} us -> {achieved:.1f} GB/s "
-        f"({achieved / PEAK_GBS:.1%} of 8 TB/s)")
+        f"{value:.1f} GB/s; kernel {kern_ms * 1e3:.2f} us -> {achieved:.1f} GB/s "
+        f"({achieved / PEAK_GBS:.1%} of 8 TB/s); isolated launches with event pairs: median "
+        f"{statistics.median(per) * 1e3:.2f} us")
+    if args.copy_probe_mb > 0:
+        n = args.copy_probe_mb * 2**20 // 4
+        a = torch.ones(n, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(4):
+            torch.mul(a, 1.0, out=b)                    # elementwise: reads M MiB, writes M MiB
+        torch.cuda.synchronize()
+        del a, b
 
     # consistency of the measured launches (parity itself is tests/test_gemv_gpu.py):
     # every copy holds the same bytes, so two launches on different copies
@@ -198,6 +271,7 @@ def main():
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "compute": "int8 dot4 of weight codes with 24-bit fixed-point x digits, f32 scales and accumulation",
         "data": "synthetic (seeded GGUF blocks: f16 scales U[1e-3,2e-2], uniform code bytes; x ~ N(0,1))",
         "config": {"workload": workload, "type": args.type, "rows": rows, "cols": cols,
                    "bytes_per_launch": B, "rotating_copies": ncopy,
@@ -207,7 +281,8 @@ def main():
                    "frac_of_8TBs_wall": round(value / PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel_us_mean": round(kern_ms * 1e3, 3)},
+                     "kernel_us_mean": round(kern_ms * 1e3, 3),
+                     "kernel": "qg::gemv_stream (rust-inference_amd/csrc/qgemv_kernels.hip)"},
         "cpu_baseline": cpu,
     }
     for m in mats:
