@@ -26,6 +26,7 @@ import re
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libqgemv.so"
 HEADER_PATH = HERE.parent / "include" / "qgemv.h"
+HEADERS = (HEADER_PATH, HERE.parent / "include" / "qgmodel.h")
 
 # GGML type ids, src/gguf.rs:43-59
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = (
@@ -81,16 +82,43 @@ _SIGS = {
     "qg_synchronize": (ctypes.c_int, [_P]),
     "qg_stream": (_P, [_P]),
     "qg_device_cu_count": (ctypes.c_int, [_P]),
+    # include/qgmodel.h
+    "qg_model_create": (ctypes.c_int, [_P, _P, ctypes.POINTER(_P)]),
+    "qg_model_destroy": (ctypes.c_int, [_P]),
+    "qg_model_set_matrix": (ctypes.c_int, [_P, _U32, _U32, _P, _SZ, _U32, _SZ, _SZ]),
+    "qg_model_share_matrix": (ctypes.c_int, [_P, _U32, _U32, _P]),
+    "qg_model_set_vector": (ctypes.c_int, [_P, _U32, _U32, _P, _SZ]),
+    "qg_model_reset": (ctypes.c_int, [_P]),
+    "qg_model_seq_len": (ctypes.c_int, [_P, ctypes.POINTER(_SZ)]),
+    "qg_model_forward": (ctypes.c_int, [_P, _U32, _U32, _P]),
+    "qg_model_sample_greedy": (ctypes.c_int, [_P, _P, _SZ, ctypes.c_float, _SZ, ctypes.POINTER(_U32)]),
+    "qg_model_generate": (ctypes.c_int, [_P, _P, _SZ, _SZ, ctypes.c_float, _SZ, _P,
+                                         ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
 }
+
+# include/qgmodel.h slots (names of the GGUF tensors, src/model.rs:197-298)
+M_TOKEN_EMBD, M_LM_HEAD, M_WQ, M_WK, M_WV, M_WO, M_GATE, M_UP, M_DOWN = range(9)
+V_FINAL_NORM, V_ATTN_NORM, V_FFN_NORM, V_BQ, V_BK, V_BV = range(6)
+
+
+class ModelConfig(ctypes.Structure):
+    """qg_model_config: ModelConfig (src/model.rs:34-46)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("embed_dim", "n_layers", "n_heads", "n_kv_heads",
+                                                 "hidden_dim", "vocab_size", "max_seq_len")] + \
+               [("rope_base", ctypes.c_float), ("norm_eps", ctypes.c_float)]
 
 _lib = None
 
 
-def header_symbols(path: pathlib.Path = HEADER_PATH) -> list[str]:
-    """Every function the C ABI header declares."""
-    text = path.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(qg_[a-z0-9_]+)\s*\(", text)))
+def header_symbols(paths=HEADERS) -> list[str]:
+    """Every function the C ABI headers declare."""
+    if isinstance(paths, (str, pathlib.Path)):
+        paths = (paths,)
+    out = set()
+    for path in paths:
+        text = re.sub(r"/\*.*?\*/", "", pathlib.Path(path).read_text(), flags=re.S)
+        out.update(re.findall(r"\b(qg_[a-z0-9_]+)\s*\(", text))
+    return sorted(out)
 
 
 def load_library(path: pathlib.Path | str = LIB_PATH):
@@ -194,9 +222,10 @@ class DeviceMatrix:
         self.ctx, self.h, self.dtype, self.rows, self.cols = ctx, h, dtype, rows, cols
 
     def free(self):
-        if self.h:
+        # a closed context has already freed its matrices (qg_destroy)
+        if self.h and self.ctx.h:
             self.ctx.check(self.ctx.lib.qg_mat_free(self.ctx.h, self.h), "qg_mat_free")
-            self.h = None
+        self.h = None
 
     @property
     def kernel_kind(self) -> int:
@@ -238,6 +267,81 @@ class QuantizedMatrix:
         if len(x) != self.cols or len(out) != self.rows:     # quant.rs:179-180
             raise QgemvError(7, "mat_vec_mul length mismatch")
         gpu.mat_vec_mul(self.data, self.dtype, x, out, self.rows, self.cols)
+
+
+class DeviceModel:
+    """The decode step on device (include/qgmodel.h): Transformer::forward
+    (src/transformer.rs:63-98), greedy Sampler::sample (src/sampler.rs:72-83,
+    109-127) and Model::generate's loop (src/model.rs:357-440)."""
+
+    def __init__(self, ctx: GpuContext, embed_dim: int, n_layers: int, n_heads: int,
+                 n_kv_heads: int, hidden_dim: int, vocab_size: int, max_seq_len: int,
+                 rope_base: float, norm_eps: float):
+        self.ctx = ctx
+        self.cfg = ModelConfig(embed_dim, n_layers, n_heads, n_kv_heads, hidden_dim, vocab_size,
+                               max_seq_len, rope_base, norm_eps)
+        h = _P()
+        ctx.check(ctx.lib.qg_model_create(ctx.h, ctypes.byref(self.cfg), ctypes.byref(h)),
+                  "qg_model_create")
+        self.h = h
+
+    def close(self):
+        # a closed context has already freed its models (qg_destroy)
+        if self.h and self.ctx.h:
+            self.ctx.lib.qg_model_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_matrix(self, which: int, layer: int, raw, dtype: int, rows: int, cols: int):
+        self.ctx.check(self.ctx.lib.qg_model_set_matrix(self.h, which, layer, _ptr(raw), raw.nbytes,
+                                                        dtype, rows, cols), "qg_model_set_matrix")
+
+    def share_matrix(self, which: int, layer: int, mat: DeviceMatrix):
+        self.ctx.check(self.ctx.lib.qg_model_share_matrix(self.h, which, layer, mat.h),
+                       "qg_model_share_matrix")
+
+    def set_vector(self, which: int, layer: int, v):
+        self.ctx.check(self.ctx.lib.qg_model_set_vector(self.h, which, layer, _ptr(v), len(v)),
+                       "qg_model_set_vector")
+
+    def reset(self):
+        self.ctx.check(self.ctx.lib.qg_model_reset(self.h), "qg_model_reset")
+
+    @property
+    def seq_len(self) -> int:
+        n = _SZ()
+        self.ctx.check(self.ctx.lib.qg_model_seq_len(self.h, ctypes.byref(n)), "qg_model_seq_len")
+        return n.value
+
+    def forward(self, token: int, pos: int, logits=None):
+        """logits: numpy float32[vocab] receiving the step's logits, or None."""
+        self.ctx.check(self.ctx.lib.qg_model_forward(self.h, token, pos, _ptr(logits)),
+                       "qg_model_forward")
+
+    def sample_greedy(self, recent, penalty: float = 1.1, window: int = 64) -> int:
+        import numpy as np
+        r = np.ascontiguousarray(recent, dtype=np.uint32)
+        t = _U32()
+        self.ctx.check(self.ctx.lib.qg_model_sample_greedy(self.h, _ptr(r) if len(r) else None, len(r),
+                                                           penalty, window, ctypes.byref(t)),
+                       "qg_model_sample_greedy")
+        return t.value
+
+    def generate(self, prompt, n_new: int, penalty: float = 1.1, window: int = 64):
+        """(new tokens, prefill seconds, decode seconds)."""
+        import numpy as np
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(n_new, 1), np.uint32)
+        a, b = ctypes.c_double(), ctypes.c_double()
+        self.ctx.check(self.ctx.lib.qg_model_generate(self.h, _ptr(p), len(p), n_new, penalty, window,
+                                                      _ptr(out), ctypes.byref(a), ctypes.byref(b)),
+                       "qg_model_generate")
+        return out[:n_new], a.value, b.value
 
 
 def env_flag(name: str) -> bool:

@@ -1,0 +1,47 @@
+// qg_internal.h -- library-internal view of the C ABI's opaque handles,
+// shared by qgemv_api.cpp and the decode-step engine (qg_model.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <set>
+#include <string>
+#include <tuple>
+
+#include "qg_common.h"
+#include "qgemv.h"
+
+struct qg_model;
+
+struct qg_mat {
+    qg_ctx *ctx;
+    uint8_t *d;        // device bytes (nbytes data + kTailPad zeros)
+    size_t nbytes;     // bytes the kernels may treat as data
+    uint32_t type;
+    size_t rows, cols;
+    bool owned;
+    qg::Plan plan;
+};
+
+struct qg_ctx {
+    int device = 0;
+    int n_cu = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    float *h_x = nullptr, *h_y = nullptr;   // pinned staging
+    size_t h_x_cap = 0, h_y_cap = 0;
+    float *d_x = nullptr, *d_y = nullptr;   // device staging
+    size_t d_x_cap = 0, d_y_cap = 0;
+    std::set<qg_mat *> mats;
+    std::set<qg_model *> models;            // decode-step engines on this context
+    std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
+};
+
+struct qg_model;
+// Frees every decode-step engine of the context (qg_model.hip); qg_destroy
+// calls it before freeing the context's matrices.
+void qg_models_free_all(qg_ctx *ctx);
+
+// Records `what` (and the HIP error text) as the context's last error; returns `status`.
+int qg_fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess);

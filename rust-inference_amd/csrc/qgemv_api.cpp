@@ -17,34 +17,10 @@
 #include <tuple>
 
 #include "qg_common.h"
+#include "qg_internal.h"
 #include "qgemv.h"
 
-struct qg_mat {
-    qg_ctx *ctx;
-    uint8_t *d;        // device bytes (nbytes data + kTailPad zeros)
-    size_t nbytes;     // bytes the kernels may treat as data
-    uint32_t type;
-    size_t rows, cols;
-    bool owned;
-    qg::Plan plan;
-};
-
-struct qg_ctx {
-    int device = 0;
-    int n_cu = 0;
-    hipStream_t stream = nullptr;
-    std::string err;
-    float *h_x = nullptr, *h_y = nullptr;   // pinned staging
-    size_t h_x_cap = 0, h_y_cap = 0;
-    float *d_x = nullptr, *d_y = nullptr;   // device staging
-    size_t d_x_cap = 0, d_y_cap = 0;
-    std::set<qg_mat *> mats;
-    std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
-};
-
-namespace {
-
-int fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess)
+int qg_fail(qg_ctx *ctx, int status, const char *what, hipError_t e)
 {
     if (ctx) {
         char buf[256];
@@ -55,6 +31,13 @@ int fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess)
         ctx->err = buf;
     }
     return status;
+}
+
+namespace {
+
+int fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess)
+{
+    return qg_fail(ctx, status, what, e);
 }
 
 #define QG_HIP(ctx, call)                                                   \
@@ -201,6 +184,7 @@ int qg_init(int device, qg_ctx **out)
 
 int qg_destroy(qg_ctx *ctx)
 {
+    if (ctx) qg_models_free_all(ctx);
     if (!ctx) return QG_ERR_INVALID_ARG;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);

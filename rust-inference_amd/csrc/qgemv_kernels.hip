@@ -862,7 +862,7 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 // LDS slots and add them up every `chunk` batches (two workgroup barriers per
 // chunk instead of per batch).
 
-template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB>
+template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D>
 __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 {
     using I = Item<T>;
@@ -899,7 +899,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t raw[D][R][NR];
 #pragma unroll
-    for (int d = 0; d < D; d++) issue<T, R>(a, team, d, it, ib, active, raw[d]);
+    for (int d = 0; d < D0; d++) issue<T, R>(a, team, d, it, ib, active, raw[d]);
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
@@ -949,6 +949,10 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
             }
         }
     }
+
+    // the rest of the ring, now that no conversion work waits behind it
+#pragma unroll
+    for (int d = D0; d < D; d++) issue<T, R>(a, team, d, it, ib, active, raw[d]);
 
     // 3. stream the batches
     float *red = (float *)(lds + a.red_off);

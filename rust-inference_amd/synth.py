@@ -58,3 +58,88 @@ def gen_x(n: int, seed: int) -> np.ndarray:
 def config_seed(index: int) -> int:
     """Seed of BASELINE.json config `index` (0-based)."""
     return 0x5EED0000 + index
+
+
+# ------------------------------------------------------------ whole models
+#
+# BASELINE.json configs 3-5: random-init models of a named architecture in a
+# GGUF quantization mix.  Q4_K_M: attn_v and ffn_down Q6_K, every other
+# matrix Q4_K; the lm_head is Q6_K unless it is tied to token_embd.  RMSNorm
+# weights are f32 1 + N(0, 0.02); q/k/v biases f32 N(0, 0.02).
+
+ARCH = {
+    # embed, layers, heads, kv heads, ffn, vocab, rope base, tied lm_head
+    "qwen2-0.5b": dict(embed_dim=896, n_layers=24, n_heads=14, n_kv_heads=2, hidden_dim=4864,
+                       vocab_size=151936, rope_base=1e6, norm_eps=1e-6, tied=True, bias=True),
+    "qwen2-7b": dict(embed_dim=3584, n_layers=28, n_heads=28, n_kv_heads=4, hidden_dim=18944,
+                     vocab_size=152064, rope_base=1e6, norm_eps=1e-6, tied=False, bias=True),
+    "llama3-8b": dict(embed_dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, hidden_dim=14336,
+                      vocab_size=128256, rope_base=5e5, norm_eps=1e-5, tied=False, bias=False),
+}
+
+MIXES = {
+    # slot -> GGML type; "base" covers every matrix not listed
+    "q4_k_m": dict(base=12, wv=14, down=14, lm_head=14),
+    "q5_k": dict(base=13, lm_head=14),
+    "q8_0": dict(base=8, lm_head=8),
+}
+
+SLOTS = ("token_embd", "lm_head", "wq", "wk", "wv", "wo", "gate", "up", "down")
+
+
+def slot_shape(cfg: dict, slot: str):
+    """(rows, cols) of a matrix slot (src/model.rs:197-298: rows = ne1 = out)."""
+    E, H, V = cfg["embed_dim"], cfg["hidden_dim"], cfg["vocab_size"]
+    hd = E // cfg["n_heads"]
+    q_dim, kv_dim = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    return {"token_embd": (V, E), "lm_head": (V, E), "wq": (q_dim, E), "wk": (kv_dim, E),
+            "wv": (kv_dim, E), "wo": (E, q_dim), "gate": (H, E), "up": (H, E), "down": (E, H)}[slot]
+
+
+def gen_model(cfg: dict, mix: str = "q4_k_m", seed: int = 0):
+    """{"mats": {(slot, layer): (raw, dtype, rows, cols)}, "vecs": {(name, layer): f32}}.
+    Layer is 0 for token_embd / lm_head / final_norm.  A tied lm_head is absent
+    from "mats" (the caller shares token_embd)."""
+    m = MIXES[mix]
+    rng = np.random.default_rng(seed)
+    mats, vecs = {}, {}
+    for slot in SLOTS:
+        if slot == "lm_head" and cfg.get("tied"):
+            continue
+        layers = [0] if slot in ("token_embd", "lm_head") else range(cfg["n_layers"])
+        rows, cols = slot_shape(cfg, slot)
+        dtype = m.get(slot, m["base"])
+        for layer in layers:
+            s = int(rng.integers(0, 2**31))
+            mats[(slot, layer)] = (gen_blocks(dtype, rows, cols, s), dtype, rows, cols)
+    E = cfg["embed_dim"]
+    hd = E // cfg["n_heads"]
+    kv_dim = cfg["n_kv_heads"] * hd
+    vecs[("final_norm", 0)] = (1.0 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    for layer in range(cfg["n_layers"]):
+        vecs[("attn_norm", layer)] = (1.0 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+        vecs[("ffn_norm", layer)] = (1.0 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+        if cfg.get("bias", True):
+            vecs[("bq", layer)] = (0.02 * rng.standard_normal(E)).astype(np.float32)
+            vecs[("bk", layer)] = (0.02 * rng.standard_normal(kv_dim)).astype(np.float32)
+            vecs[("bv", layer)] = (0.02 * rng.standard_normal(kv_dim)).astype(np.float32)
+    return {"mats": mats, "vecs": vecs}
+
+
+def model_bytes(cfg: dict, mix: str = "q4_k_m") -> int:
+    """Quantized weight bytes one decode step reads (tied lm_head read twice)."""
+    m = MIXES[mix]
+    total = 0
+    for slot in SLOTS:
+        rows, cols = slot_shape(cfg, slot)
+        src = "token_embd" if (slot == "lm_head" and cfg.get("tied")) else slot
+        dtype = m.get(src, m["base"])
+        bs, bb, _ = LAYOUT[dtype]
+        nb = -(-(rows * cols) // bs) * bb
+        if slot == "token_embd":
+            total += -(-cols // bs) * bb            # one row per token
+        elif slot == "lm_head":
+            total += nb
+        else:
+            total += nb * cfg["n_layers"]
+    return total

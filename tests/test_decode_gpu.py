@@ -1,0 +1,153 @@
+"""GPU parity of the on-device decode step (include/qgmodel.h) against the
+oracle's restatement of Transformer::forward (oracle/qref_model.c,
+src/transformer.rs:63-98) and of the greedy sampler with repetition penalty
+(src/sampler.rs:72-83, 109-127; src/math.rs:328-339).
+
+Per step, the device logits must agree with the oracle's within normwise
+max|Δ| / max|logits_ref| <= LOGIT_TOL (2 layers) or DEEP_TOL (24 layers), and
+the greedily sampled token ids must be identical.  Both bounds are looser
+than the single-GEMV bound (1e-4) because every step chains ~7 mat-vecs per
+layer plus attention and RMSNorm, whose block reductions add in a different
+order than the reference's sequential loops, and the random-init models
+amplify such differences with depth: their residual stream grows by one to
+two orders of magnitude per layer and their attention scores are large
+enough that the softmax is nearly one-hot, so ulp-level differences in the
+scores move the weights of the other positions.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import normwise_err
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-4
+DEEP_TOL = 1e-3
+
+SMALL = dict(embed_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=512, vocab_size=600,
+             rope_base=1e6, norm_eps=1e-6, tied=False, bias=True)
+
+
+def build(rinf, synth, oracle, ctx, cfg, mix, seed, max_seq):
+    t = synth.gen_model(cfg, mix, seed)
+    dev = rinf.DeviceModel(ctx, cfg["embed_dim"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                           cfg["hidden_dim"], cfg["vocab_size"], max_seq, cfg["rope_base"],
+                           cfg["norm_eps"])
+    ocfg = dict(cfg, max_seq_len=max_seq)
+    ref = oracle.Model(ocfg)
+    slots = {"token_embd": rinf.M_TOKEN_EMBD, "lm_head": rinf.M_LM_HEAD, "wq": rinf.M_WQ,
+             "wk": rinf.M_WK, "wv": rinf.M_WV, "wo": rinf.M_WO, "gate": rinf.M_GATE,
+             "up": rinf.M_UP, "down": rinf.M_DOWN}
+    vslots = {"final_norm": rinf.V_FINAL_NORM, "attn_norm": rinf.V_ATTN_NORM,
+              "ffn_norm": rinf.V_FFN_NORM, "bq": rinf.V_BQ, "bk": rinf.V_BK, "bv": rinf.V_BV}
+    shared = None
+    for (slot, layer), (raw, dtype, rows, cols) in t["mats"].items():
+        if slot == "token_embd" and cfg.get("tied"):
+            shared = ctx.upload(raw, dtype, rows, cols)
+            dev.share_matrix(rinf.M_TOKEN_EMBD, 0, shared)
+            dev.share_matrix(rinf.M_LM_HEAD, 0, shared)
+            ref.set_mat("lm_head", 0, raw, dtype, rows, cols)           # tied (model.rs:221-226)
+        else:
+            dev.set_matrix(slots[slot], layer, raw, dtype, rows, cols)
+        ref.set_mat(slot, layer, raw, dtype, rows, cols)
+    for (name, layer), v in t["vecs"].items():
+        dev.set_vector(vslots[name], layer, v)
+        ref.set_vec(name, layer, v)
+    return dev, ref, shared
+
+
+def run_and_compare(dev, ref, oracle, cfg, prompt, n_new, penalty=1.1, window=64):
+    """Prompt then greedy decode, step by step on both sides."""
+    V = cfg["vocab_size"]
+    logits = np.zeros(V, np.float32)
+    all_ids, errs, out = [], [], []
+    pos = 0
+    for tok in prompt:
+        dev.forward(int(tok), pos, logits)
+        ref_l = ref.forward(int(tok), pos)
+        errs.append(normwise_err(logits, ref_l))
+        all_ids.append(int(tok))
+        pos += 1
+    for _ in range(n_new):
+        recent = all_ids[-64:]
+        t_dev = dev.sample_greedy(recent, penalty, window)
+        rl = ref_l.copy()
+        oracle.repetition_penalty(rl, recent, penalty, window)
+        t_ref = oracle.argmax(rl)
+        assert t_dev == t_ref, f"step {len(out)}: device token {t_dev} != reference {t_ref}"
+        out.append(t_dev)
+        dev.forward(t_dev, pos, logits)
+        ref_l = ref.forward(t_dev, pos)
+        errs.append(normwise_err(logits, ref_l))
+        all_ids.append(t_dev)
+        pos += 1
+    return out, errs
+
+
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k", "q8_0"])
+def test_small_model_logits_and_tokens(rinf, synth, oracle, ctx, mix):
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, mix, 11, 40)
+    prompt = np.random.default_rng(5).integers(0, SMALL["vocab_size"], 8)
+    out, errs = run_and_compare(dev, ref, oracle, SMALL, prompt, 16)
+    print(f"{mix}: max logits err {max(errs):.2e}, tokens {out}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    assert dev.seq_len == 24
+    dev.close()
+
+
+def test_generate_matches_stepwise(rinf, synth, oracle, ctx):
+    """qg_model_generate (Model::generate's loop) gives the tokens of the
+    step-by-step run and of the reference sampler."""
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, "q4_k_m", 12, 40)
+    prompt = np.random.default_rng(6).integers(0, SMALL["vocab_size"], 6)
+    toks, t_pre, t_dec = dev.generate(prompt, 12)
+    dev.reset()
+    ref.reset()
+    step, _ = run_and_compare(dev, ref, oracle, SMALL, prompt, 12)
+    assert list(toks) == step
+    assert t_pre > 0 and t_dec > 0
+    dev.close()
+
+
+def test_qwen2_05b_shape_config3(rinf, synth, oracle, ctx):
+    """Qwen2-0.5B architecture, Q4_K_M, tied lm_head,
+    token_embd Q4_K at cols = 896 (rows straddle superblocks: the
+    dequantize_row placement of quant.rs:152-174 is in the loop)."""
+    cfg = synth.ARCH["qwen2-0.5b"]
+    dev, ref, shared = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", synth.config_seed(2), 48)
+    prompt = np.random.default_rng(synth.config_seed(2)).integers(0, cfg["vocab_size"], 8)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 8)
+    print(f"qwen2-0.5b: max logits err {max(errs):.2e}, tokens {out}", flush=True)
+    assert max(errs) <= DEEP_TOL
+    dev.close()
+    shared.free()
+
+
+def test_errors(rinf, synth, ctx):
+    dev = rinf.DeviceModel(ctx, 256, 1, 4, 2, 512, 100, 4, 1e6, 1e-6)
+    with pytest.raises(rinf.QgemvError) as e:
+        dev.forward(0, 0)                                   # matrices not set
+    assert e.value.status == 1
+    t = synth.gen_model(dict(SMALL, n_layers=1, vocab_size=100), "q4_k_m", 3)
+    slots = {"token_embd": rinf.M_TOKEN_EMBD, "lm_head": rinf.M_LM_HEAD, "wq": rinf.M_WQ,
+             "wk": rinf.M_WK, "wv": rinf.M_WV, "wo": rinf.M_WO, "gate": rinf.M_GATE,
+             "up": rinf.M_UP, "down": rinf.M_DOWN}
+    with pytest.raises(rinf.QgemvError) as e:
+        raw, dtype, rows, cols = t["mats"][("wq", 0)]
+        dev.set_matrix(rinf.M_WQ, 0, raw, dtype, rows, cols + 256)   # wrong shape
+    for (slot, layer), (raw, dtype, rows, cols) in t["mats"].items():
+        dev.set_matrix(slots[slot], layer, raw, dtype, rows, cols)
+    dev.set_vector(rinf.V_FINAL_NORM, 0, np.ones(256, np.float32))
+    with pytest.raises(rinf.QgemvError) as e:
+        dev.forward(100, 0)                                 # token >= vocab
+    assert e.value.status == 7
+    for p in range(4):
+        dev.forward(1, p)
+    with pytest.raises(rinf.QgemvError) as e:
+        dev.forward(1, 4)                                   # KV cache full (kv_cache.rs:54-59)
+    assert e.value.status == 7
+    dev.reset()
+    dev.forward(1, 0)
+    dev.close()
