@@ -9,10 +9,10 @@ that every launch misses the 256 MB Infinity Cache and streams from HBM.
 value        whole-job GB/s = algorithmic bytes x K / wall time of K back-to-back
              launches (the better of eager launches and a HIP-graph replay)
 roofline     algorithmic bytes / average launch duration of the GEMV kernel:
-             HIP events around a HIP-graph replay of K back-to-back launches
-             (one kernel per launch, so rocprofv3 --kernel-trace --stats of the
-             same command gives the same average up to the inter-kernel gaps),
-             against 8 TB/s;
+             HIP events around K back-to-back launches, eager or replayed from
+             a HIP graph, whichever is faster (one kernel per launch, so
+             rocprofv3 --kernel-trace --stats of the same command gives the
+             same average up to the inter-kernel gaps), against 8 TB/s;
              `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
              WRITE_SIZE (profiles/traffic.json, written by --pmc-summary), or null
 cpu_baseline the oracle's restatement of the reference's --cpu loop
@@ -118,6 +118,64 @@ def cpu_baseline(oracle, raw, dtype, rows, cols, x, seconds, nbytes):
             "us_per_gemv": round(med * 1e6, 1)}
 
 
+def decode_run(rinf, synth, ctx, args):
+    """greedy decode of a random-init model of
+    `args.decode` in the `args.decode_mix` GGUF mix, all GEMVs on this GPU.
+    Prompt tokens are processed one by one as the reference does
+    (src/model.rs:357-363), then `decode_tokens` greedy steps with the
+    reference's repetition penalty 1.1 over the last 64 tokens."""
+    import numpy as np
+    cfg = synth.ARCH[args.decode]
+    seed = synth.config_seed(3)
+    t0 = time.perf_counter()
+    t = synth.gen_model(cfg, args.decode_mix, seed)
+    max_seq = args.decode_prompt + args.decode_tokens + 1
+    dev = rinf.DeviceModel(ctx, cfg["embed_dim"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                           cfg["hidden_dim"], cfg["vocab_size"], max_seq, cfg["rope_base"],
+                           cfg["norm_eps"])
+    slots = {"token_embd": rinf.M_TOKEN_EMBD, "lm_head": rinf.M_LM_HEAD, "wq": rinf.M_WQ,
+             "wk": rinf.M_WK, "wv": rinf.M_WV, "wo": rinf.M_WO, "gate": rinf.M_GATE,
+             "up": rinf.M_UP, "down": rinf.M_DOWN}
+    vslots = {"final_norm": rinf.V_FINAL_NORM, "attn_norm": rinf.V_ATTN_NORM,
+              "ffn_norm": rinf.V_FFN_NORM, "bq": rinf.V_BQ, "bk": rinf.V_BK, "bv": rinf.V_BV}
+    shared = None
+    for (slot, layer), (raw, dtype, rows, cols) in list(t["mats"].items()):
+        if slot == "token_embd" and cfg.get("tied"):
+            shared = ctx.upload(raw, dtype, rows, cols)
+            dev.share_matrix(rinf.M_TOKEN_EMBD, 0, shared)
+            dev.share_matrix(rinf.M_LM_HEAD, 0, shared)
+        else:
+            dev.set_matrix(slots[slot], layer, raw, dtype, rows, cols)
+        del t["mats"][(slot, layer)]
+    for (name, layer), v in t["vecs"].items():
+        dev.set_vector(vslots[name], layer, v)
+    setup_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab_size"], args.decode_prompt)
+    dev.generate(prompt[:4], 4)                           # warm-up (kernels, clocks)
+    toks, pre_s, dec_s = dev.generate(prompt, args.decode_tokens)
+    dev.close()
+    if shared is not None:
+        shared.free()
+    tok_s = args.decode_tokens / dec_s
+    wbytes = synth.model_bytes(cfg, args.decode_mix)
+    E = cfg["embed_dim"]
+    kv_dim = cfg["n_kv_heads"] * (E // cfg["n_heads"])
+    mean_pos = args.decode_prompt + (args.decode_tokens + 1) / 2
+    kv_bytes = 2 * cfg["n_layers"] * mean_pos * kv_dim * 4
+    per_tok = wbytes + kv_bytes
+    log(f"decode {args.decode} {args.decode_mix}: {tok_s:.1f} tok/s ({dec_s * 1e3 / args.decode_tokens:.3f} "
+        f"ms/token), {per_tok / 1e9:.3f} GB/token -> {per_tok * tok_s / 1e9:.1f} GB/s; prefill "
+        f"{args.decode_prompt / pre_s:.1f} tok/s; set-up {setup_s:.1f} s")
+    return {"model": f"{args.decode} ({args.decode_mix}, random init, synthetic)",
+            "prompt_tokens": args.decode_prompt, "decode_tokens": args.decode_tokens,
+            "tok_s": round(tok_s, 2), "ms_per_token": round(dec_s * 1e3 / args.decode_tokens, 4),
+            "prefill_tok_s": round(args.decode_prompt / pre_s, 2),
+            "bytes_per_token": int(per_tok), "weight_bytes_per_token": int(wbytes),
+            "achieved_GBs": round(per_tok * tok_s / 1e9, 2),
+            "frac_of_8TBs": round(per_tok * tok_s / 8e12, 4),
+            "first_tokens": [int(v) for v in toks[:8]]}
+
+
 def _pmc_rows(d):
     """(kernel name, counter value in KiB, grid size) of every dispatch in a rocprofv3 run."""
     import csv
@@ -180,6 +238,13 @@ def main():
     ap.add_argument("--rotate-mb", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode", default="qwen2-7b",
+                    help="architecture of the synthetic decode run (synth.ARCH key; 'none' skips it)")
+    ap.add_argument("--decode-mix", default="q4_k_m")
+    ap.add_argument("--decode-prompt", type=int, default=64)
+    ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the decode leg (prints its JSON object)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after timing, run 4 elementwise copies (y = 1.0 * x) of this many MiB: the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -211,6 +276,10 @@ def main():
     ncopy = max(2, -(-args.rotate_mb * 2**20 // nb))
 
     ctx = rinf.GpuContext(0)
+    if args.decode_only:
+        print(json.dumps(decode_run(rinf, synth, ctx, args)), flush=True)
+        ctx.close()
+        return
     log(f"device CUs={ctx.cu_count}; {args.type} {rows}x{cols}: {nb} weight bytes, "
         f"{B} algorithmic bytes/launch, {ncopy} rotating copies ({ncopy * nb / 2**20:.0f} MiB)")
     raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
@@ -223,9 +292,9 @@ def main():
     wall_ms = min(eager_ms, graph_ms)
     ms_step = wall_ms / args.steps
     value = B / (ms_step * 1e-3) / 1e9
-    # average launch duration: the graph replay is GPU-side back-to-back
-    # (no host launch cost, which a profiler's callbacks inflate for eager launches)
-    kern_ms = graph_ms / args.steps
+    # average launch duration: the faster of the eager and graph-replay
+    # back-to-back loops (a profiler's callbacks inflate the eager one)
+    kern_ms = wall_ms / args.steps
     achieved = B / (kern_ms * 1e-3) / 1e9
     log(f"eager {eager_ms / args.steps * 1e3:.2f} us/step, graph {graph_ms / args.steps * 1e3:.2f} us/step")
     log(f"wall {wall_ms:.3f} ms / {args.steps} launches = {ms_step * 1e3:.2f} us/step -> "
@@ -267,6 +336,10 @@ def main():
         cpu = cpu_baseline(oracle, raw, dtype, rows, cols, x, args.cpu_seconds, B)
         log(f"cpu_baseline: {cpu['value']} GB/s ({cpu['us_per_gemv']} us/GEMV)")
 
+    decode = None
+    if args.decode != "none":
+        decode = decode_run(rinf, synth, ctx, args)
+
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
@@ -284,6 +357,7 @@ def main():
                      "kernel_us_mean": round(kern_ms * 1e3, 3),
                      "kernel": "qg::gemv_stream (rust-inference_amd/csrc/qgemv_kernels.hip)"},
         "cpu_baseline": cpu,
+        "decode": decode,
     }
     for m in mats:
         m.free()
