@@ -79,6 +79,19 @@ int qg_mat_kernel_kind(const qg_mat *mat);
  * Asynchronous on `stream`. */
 int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, void *stream);
 
+/* RmsNorm then mat_vec_mul, as every projection input of a decode step is
+ * formed: y = W · (rmsnorm(xa + xb) * nw) (src/math.rs:237-257 as called by
+ * src/rmsnorm.rs:14-29, the residual add of src/transformer.rs:31-46, then
+ * src/quant.rs:178-206).  d_xb may be NULL (x = xa); d_sum_out, if not NULL,
+ * receives xa + xb and must not overlap xa or xb.  xa, xb, nw, sum_out: cols
+ * floats; y: rows floats; all device pointers, asynchronous on `stream`.
+ * With 16-byte aligned vectors, a non-NULL d_xb and a stream-kernel matrix
+ * the norm runs inside the mat-vec kernel; otherwise a separate RMSNorm kernel
+ * writes the context's scratch vector first, so such calls on one context
+ * must not overlap on different streams. */
+int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const float *d_xb,
+                       const float *d_nw, float eps, float *d_sum_out, float *d_y, void *stream);
+
 /* Host-buffer drop-in for QuantizedMatrix::mat_vec_mul(x, out, Some(gpu))
  * (src/quant.rs:178-186): synchronous; stages x/y through pinned buffers
  * allocated once per context.  x: cols floats, y: rows floats. */

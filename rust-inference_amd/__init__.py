@@ -74,6 +74,7 @@ _SIGS = {
                                    ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "qg_mat_kernel_kind": (ctypes.c_int, [_P]),
     "qg_matvec_dev": (ctypes.c_int, [_P, _P, _P, _P, _P]),
+    "qg_matvec_norm_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
     "qg_gpu_mat_vec_mul": (ctypes.c_int, [_P, _P, _SZ, _U32, _P, _P, _SZ, _SZ]),
     "qg_dequant_dev": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -236,6 +237,16 @@ class DeviceMatrix:
         rc = self.ctx.lib.qg_matvec_dev(self.ctx.h, self.h, _ptr(d_x), _ptr(d_y),
                                         ctypes.c_void_p(stream) if stream else None)
         self.ctx.check(rc, "qg_matvec_dev")
+
+    def matvec_norm_dev(self, d_xa, d_xb, d_nw, eps, d_y, d_sum_out=None, stream=None):
+        """y = W · (rmsnorm(xa + xb) * nw); torch device tensors (float32),
+        d_xb / d_sum_out may be None."""
+        rc = self.ctx.lib.qg_matvec_norm_dev(self.ctx.h, self.h, _ptr(d_xa),
+                                             _ptr(d_xb) if d_xb is not None else None, _ptr(d_nw),
+                                             float(eps),
+                                             _ptr(d_sum_out) if d_sum_out is not None else None,
+                                             _ptr(d_y), ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_matvec_norm_dev")
 
     def matvec_host(self, x, y):
         self.ctx.check(self.ctx.lib.qg_matvec_host(self.ctx.h, self.h, _ptr(x), _ptr(y)),

@@ -57,6 +57,7 @@ struct Plan {
     uint32_t red_off;      // LDS offset of the partial-sum slots
     uint32_t lds;          // dynamic LDS bytes
     const void *fn;        // kernel chosen for this matrix
+    const void *fn_norm;   // the same kernel with the fused RMSNorm input
 };
 
 }  // namespace qg
@@ -67,6 +68,12 @@ namespace qg {
 int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p);
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
                 size_t cols, const float *x, float *y, ihipStream_t *stream);
+// y = W · (rmsnorm(xa + xb) * nw) with the stream kernel (kind 1 plans only;
+// -1 otherwise); sum_out (may be NULL) receives xa + xb.  xa, xb, nw,
+// sum_out: cols floats, 16-byte aligned.
+int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                     const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
+                     float *y, ihipStream_t *stream);
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                         const float *x, float *y, ihipStream_t *stream);
 int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,
@@ -74,4 +81,7 @@ int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *ou
 int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                           size_t row, float *out, ihipStream_t *stream);
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
+// out = rmsnorm(a (+ b)) * w in one workgroup; sum_out (may be NULL) = a + b.
+int launch_rmsnorm(const float *a, const float *b, float *sum_out, const float *w, float *out, size_t n,
+                   float eps, ihipStream_t *stream);
 }  // namespace qg

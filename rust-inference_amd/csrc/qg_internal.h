@@ -33,6 +33,8 @@ struct qg_ctx {
     size_t h_x_cap = 0, h_y_cap = 0;
     float *d_x = nullptr, *d_y = nullptr;   // device staging
     size_t d_x_cap = 0, d_y_cap = 0;
+    float *d_norm = nullptr;                // normalised x of qg_matvec_norm_dev's two-kernel path
+    size_t d_norm_cap = 0;
     std::set<qg_mat *> mats;
     std::set<qg_model *> models;            // decode-step engines on this context
     std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
@@ -42,6 +44,13 @@ struct qg_model;
 // Frees every decode-step engine of the context (qg_model.hip); qg_destroy
 // calls it before freeing the context's matrices.
 void qg_models_free_all(qg_ctx *ctx);
+
+// y = W · (rmsnorm(xa + xb) * nw), sum_out (may be NULL) = xa + xb (xb may be
+// NULL: then xa alone).  The stream kernel does the norm in its prologue when
+// the plan and the pointers allow; otherwise a one-workgroup RMSNorm kernel
+// writes `scratch` (cols floats) and the mat-vec reads it.  Asynchronous.
+int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float *xb, const float *nw,
+                   float eps, float *sum_out, float *y, float *scratch, hipStream_t stream);
 
 // Records `what` (and the HIP error text) as the context's last error; returns `status`.
 int qg_fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess);

@@ -60,27 +60,6 @@ __device__ float block_max(float v, float *red)
     return t;
 }
 
-// out = rmsnorm(a (+ b)) * w; with b, also sum_out = a + b (the residual).
-__global__ void __launch_bounds__(kBlock) rmsnorm_k(const float *__restrict__ a, const float *__restrict__ b,
-                                                    float *__restrict__ sum_out, const float *__restrict__ w,
-                                                    float *__restrict__ out, uint32_t n, float eps)
-{
-    __shared__ float red[kBlock / 64];
-    float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float x = b ? a[i] + b[i] : a[i];
-        if (sum_out) sum_out[i] = x;
-        ss += x * x;
-    }
-    ss = block_sum(ss, red);
-    const float rms = sqrtf(ss / (float)n + eps);
-    const float scale = 1.0f / rms;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float x = b ? a[i] + b[i] : a[i];
-        out[i] = x * scale * w[i];
-    }
-}
-
 // One thread per (2i, 2i+1) pair of q (q_dim/2 pairs) and of k/v (kv_dim/2).
 __global__ void __launch_bounds__(256) qkv_post_k(float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, const float *__restrict__ bq,
@@ -148,6 +127,62 @@ __global__ void __launch_bounds__(256) attention_k(const float *__restrict__ q, 
         for (uint32_t j = 0; j < seq; j++) acc += sc[j] * vc[(size_t)j * kv_dim + kvh + d];
         out[h * hd + d] = acc;
     }
+}
+
+// Same result for head dimensions hd = 64 * E (E = 1, 2, 4): one workgroup of
+// four waves per query head.  Wave w takes positions j = w, w + 4, ...; its
+// lanes split the head dimension (lane owns d = lane + 64e), so every key and
+// value row is one coalesced 4E-byte-per-lane read and each score is a wave
+// reduction.  The four per-wave partial outputs are added through LDS.
+template <int E>
+__global__ void __launch_bounds__(256) attention_wave_k(const float *__restrict__ q, const float *__restrict__ kc,
+                                                        const float *__restrict__ vc, float *__restrict__ out,
+                                                        uint32_t seq, uint32_t kv_dim, uint32_t n_rep, float scale)
+{
+    constexpr uint32_t HD = 64 * E;
+    extern __shared__ float sm[];                 // sc[seq], part[4][HD]
+    __shared__ float red[4];
+    float *sc = sm, *part = sm + seq;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t h = blockIdx.x, kvh = (h / n_rep) * HD;
+    float qv[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) qv[e] = q[h * HD + lane + 64 * e];
+    float mx = -INFINITY;
+    for (uint32_t j = wave; j < seq; j += 4) {
+        const float *kr = kc + (size_t)j * kv_dim + kvh;
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; e++) s += qv[e] * kr[lane + 64 * e];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        s = s * scale;
+        if (lane == 0) sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = block_max(mx, red);                      // (barrier inside: sc complete)
+    float sum = 0.f;
+    for (uint32_t j = threadIdx.x; j < seq; j += blockDim.x) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);
+    const float inv = 1.0f / sum;
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) acc[e] = 0.f;
+    for (uint32_t j = wave; j < seq; j += 4) {
+        const float p = sc[j] * inv;
+        const float *vr = vc + (size_t)j * kv_dim + kvh;
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[e] += p * vr[lane + 64 * e];
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) part[wave * HD + lane + 64 * e] = acc[e];
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x)
+        out[h * HD + d] = (part[d] + part[HD + d]) + (part[2 * HD + d] + part[3 * HD + d]);
 }
 
 __device__ __forceinline__ float silu1(float x)
@@ -242,6 +277,7 @@ struct qg_model {
     float *h0 = nullptr, *h1 = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *ao = nullptr, *ao2 = nullptr, *g = nullptr, *u = nullptr, *hb = nullptr, *fo = nullptr;
     float *logits = nullptr;
+    float *zeros = nullptr;               // the residual addend of the first layer
     uint32_t *d_recent = nullptr, *d_token = nullptr;
     uint32_t *h_recent = nullptr, *h_token = nullptr;   // pinned
     std::vector<void *> allocs;
@@ -309,6 +345,15 @@ int gemv(qg_model *m, const qg_mat *a, const float *x, float *y)
     return QG_OK;
 }
 
+// y = A · (rmsnorm(xa + xb) * nw); sum_out (may be NULL) receives xa + xb.
+// The GEMV's own prologue does the norm when the matrix runs on the stream
+// kernel; otherwise a separate RMSNorm kernel writes m->xn first.
+int gemv_norm(qg_model *m, const qg_mat *A, const float *xa, const float *xb, const float *nw,
+              float *sum_out, float *y)
+{
+    return qg_norm_matvec(m->ctx, A, xa, xb, nw, m->cfg.norm_eps, sum_out, y, m->xn, m->ctx->stream);
+}
+
 int launched(qg_model *m, const char *what)
 {
     hipError_t e = hipGetLastError();
@@ -361,6 +406,7 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
         (rc = dalloc(m, &m->ao, m->q_dim)) || (rc = dalloc(m, &m->ao2, E)) ||
         (rc = dalloc(m, &m->g, H)) || (rc = dalloc(m, &m->u, H)) || (rc = dalloc(m, &m->hb, H)) ||
         (rc = dalloc(m, &m->fo, E)) || (rc = dalloc(m, &m->logits, c.vocab_size)) ||
+        (rc = dalloc(m, &m->zeros, E > H ? E : H)) ||
         (rc = dalloc(m, &m->d_recent, kRecentMax)) || (rc = dalloc(m, &m->d_token, 1))) {
         free_model(m);
         return rc;
@@ -514,41 +560,45 @@ int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits)
     const float scale = 1.0f / sqrtf((float)m->hd);                      // attention.rs:99
     const size_t att_lds = (m->hd + slot + 1) * sizeof(float);
     for (uint32_t l = 0; l < c.n_layers; l++) {
-        // h0 = residual stream entering the layer (h1 + fo after the first)
-        if (l == 0)
-            hipLaunchKernelGGL(qgm::rmsnorm_k, dim3(1), dim3(qgm::kBlock), 0, st, m->h0, nullptr, nullptr,
-                               m->vec[QG_V_ATTN_NORM][l], m->xn, E, c.norm_eps);
-        else
-            hipLaunchKernelGGL(qgm::rmsnorm_k, dim3(1), dim3(qgm::kBlock), 0, st, m->h1, m->fo, m->h0,
-                               m->vec[QG_V_ATTN_NORM][l], m->xn, E, c.norm_eps);
-        if ((rc = launched(m, "rmsnorm"))) return rc;
-        if ((rc = gemv(m, m->w[QG_M_WQ - 2][l], m->xn, m->q)) || (rc = gemv(m, m->w[QG_M_WK - 2][l], m->xn, m->k)) ||
-            (rc = gemv(m, m->w[QG_M_WV - 2][l], m->xn, m->v)))
+        // the residual stream entering the layer is h0 (layer 0: the
+        // embedding) or h1 + fo, which the Q GEMV also stores to h0
+        const float *na = l == 0 ? m->h0 : m->h1, *nb = l == 0 ? m->zeros : m->fo;
+        const float *anorm = m->vec[QG_V_ATTN_NORM][l];
+        if ((rc = gemv_norm(m, m->w[QG_M_WQ - 2][l], na, nb, anorm, l == 0 ? nullptr : m->h0, m->q)) ||
+            (rc = gemv_norm(m, m->w[QG_M_WK - 2][l], na, nb, anorm, nullptr, m->k)) ||
+            (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
             return rc;
         float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
         const uint32_t pairs = (m->q_dim > m->kv_dim ? m->q_dim : m->kv_dim) / 2;
         hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
                            m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
                            m->sin_t, m->q_dim, m->kv_dim, m->hd, pos, slot);
-        hipLaunchKernelGGL(qgm::attention_k, dim3(c.n_heads), dim3(256), att_lds, st, m->q, kc, vc, m->ao,
-                           slot + 1, m->hd, m->kv_dim, m->n_rep, scale);
+        const size_t wlds = (slot + 1 + 4 * (size_t)m->hd) * sizeof(float);
+        if (m->hd == 64)
+            hipLaunchKernelGGL(qgm::attention_wave_k<1>, dim3(c.n_heads), dim3(256), wlds, st, m->q, kc, vc,
+                               m->ao, slot + 1, m->kv_dim, m->n_rep, scale);
+        else if (m->hd == 128)
+            hipLaunchKernelGGL(qgm::attention_wave_k<2>, dim3(c.n_heads), dim3(256), wlds, st, m->q, kc, vc,
+                               m->ao, slot + 1, m->kv_dim, m->n_rep, scale);
+        else if (m->hd == 256)
+            hipLaunchKernelGGL(qgm::attention_wave_k<4>, dim3(c.n_heads), dim3(256), wlds, st, m->q, kc, vc,
+                               m->ao, slot + 1, m->kv_dim, m->n_rep, scale);
+        else
+            hipLaunchKernelGGL(qgm::attention_k, dim3(c.n_heads), dim3(256), att_lds, st, m->q, kc, vc, m->ao,
+                               slot + 1, m->hd, m->kv_dim, m->n_rep, scale);
         if ((rc = launched(m, "attention"))) return rc;
         if ((rc = gemv(m, m->w[QG_M_WO - 2][l], m->ao, m->ao2))) return rc;
-        // h1 = h0 + attention output; xn = ffn_norm(h1)
-        hipLaunchKernelGGL(qgm::rmsnorm_k, dim3(1), dim3(qgm::kBlock), 0, st, m->h0, m->ao2, m->h1,
-                           m->vec[QG_V_FFN_NORM][l], m->xn, E, c.norm_eps);
-        if ((rc = launched(m, "rmsnorm"))) return rc;
-        if ((rc = gemv(m, m->w[QG_M_GATE - 2][l], m->xn, m->g)) || (rc = gemv(m, m->w[QG_M_UP - 2][l], m->xn, m->u)))
+        // h1 = h0 + attention output (stored by the gate GEMV); MLP input = ffn_norm(h1)
+        const float *fnorm = m->vec[QG_V_FFN_NORM][l];
+        if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
+            (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u)))
             return rc;
         hipLaunchKernelGGL(qgm::silu_mul_k, dim3((H + 255) / 256), dim3(256), 0, st, m->g, m->u, m->hb, H);
         if ((rc = launched(m, "silu*up"))) return rc;
         if ((rc = gemv(m, m->w[QG_M_DOWN - 2][l], m->hb, m->fo))) return rc;
     }
-    // final norm of h1 + fo (transformer.rs:87-97), lm_head
-    hipLaunchKernelGGL(qgm::rmsnorm_k, dim3(1), dim3(qgm::kBlock), 0, st, m->h1, m->fo, m->h0, m->final_norm,
-                       m->xn, E, c.norm_eps);
-    if ((rc = launched(m, "final rmsnorm"))) return rc;
-    if ((rc = gemv(m, m->lm, m->xn, m->logits))) return rc;
+    // final norm of h1 + fo (transformer.rs:87-97) inside the lm_head GEMV
+    if ((rc = gemv_norm(m, m->lm, m->h1, m->fo, m->final_norm, nullptr, m->logits))) return rc;
     m->seq += 1;
     if (logits) {
         QGM_HIP(m, hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float),

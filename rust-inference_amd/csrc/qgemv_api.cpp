@@ -137,6 +137,33 @@ int check_mat(qg_ctx *ctx, const qg_mat *mat)
 
 }  // namespace
 
+int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float *xb, const float *nw,
+                   float eps, float *sum_out, float *y, float *scratch, hipStream_t st)
+{
+    ihipStream_t *sti = (ihipStream_t *)st;
+    const size_t cols = mat->cols;
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    int lr = -1;
+    if (cols == 0) {                                   // empty x: out.fill(0.0), quant.rs:189
+        lr = qg::launch_fill(y, mat->rows, 0.0f, sti);
+        return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
+    }
+    if (xb && a16(xa) && a16(xb) && a16(nw) && (!sum_out || a16(sum_out)))
+        lr = qg::launch_gemv_norm(mat->plan, mat->d, mat->nbytes, mat->rows, cols, xa, xb, nw, eps, sum_out,
+                                  y, sti);
+    if (lr == -1) {
+        // two kernels: RMSNorm into scratch, then the mat-vec
+        lr = qg::launch_rmsnorm(xa, xb, sum_out, nw, scratch, cols, eps, sti);
+        if (lr == 0) {
+            if (mat->plan.kind == 1 && a16(scratch))
+                lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, cols, scratch, y, sti);
+            else
+                lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, cols, scratch, y, sti);
+        }
+    }
+    return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
+}
+
 extern "C" {
 
 const char *qg_status_string(int s)
@@ -193,6 +220,7 @@ int qg_destroy(qg_ctx *ctx)
     if (ctx->h_y) (void)hipHostFree(ctx->h_y);
     if (ctx->d_x) (void)hipFree(ctx->d_x);
     if (ctx->d_y) (void)hipFree(ctx->d_y);
+    if (ctx->d_norm) (void)hipFree(ctx->d_norm);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QG_OK;
@@ -278,6 +306,26 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
                                      (ihipStream_t *)st);
     if (lr != 0) return fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError());
     return QG_OK;
+}
+
+int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const float *d_xb,
+                       const float *d_nw, float eps, float *d_sum_out, float *d_y, void *stream)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    if (mat->rows == 0 && !d_sum_out) return QG_OK;
+    const size_t n = mat->cols;
+    if (!d_y || (n > 0 && (!d_xa || !d_nw))) return fail(ctx, QG_ERR_INVALID_ARG, "xa, nw or y is NULL");
+    auto a4 = [](const void *p) { return ((uintptr_t)p & 3u) == 0; };
+    if (!a4(d_xa) || !a4(d_xb) || !a4(d_nw) || !a4(d_sum_out) || !a4(d_y))
+        return fail(ctx, QG_ERR_INVALID_ARG, "vectors not 4-byte aligned");
+    // sum_out is written while xa and xb are still being read
+    auto overlap = [n](const float *p, const float *q) { return p && q && p < q + n && q < p + n; };
+    if (overlap(d_sum_out, d_xa) || overlap(d_sum_out, d_xb))
+        return fail(ctx, QG_ERR_INVALID_ARG, "sum_out overlaps xa or xb");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if ((rc = grow_device(ctx, &ctx->d_norm, &ctx->d_norm_cap, n))) return rc;
+    return qg_norm_matvec(ctx, mat, d_xa, d_xb, d_nw, eps, d_sum_out, d_y, ctx->d_norm, pick(ctx, stream));
 }
 
 int qg_matvec_host(qg_ctx *ctx, const qg_mat *mat, const float *x, float *y)

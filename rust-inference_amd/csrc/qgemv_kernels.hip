@@ -200,6 +200,36 @@ __global__ void fill_k(float *out, uint64_t n, float v)
         out[i] = v;
 }
 
+// out = rmsnorm(a (+ b)) * w (math.rs:237-257); with b, sum_out (may be
+// NULL) receives a + b.  One workgroup of kNormBlock threads.
+constexpr int kNormBlock = 1024;
+__global__ void __launch_bounds__(kNormBlock) rmsnorm_k(const float *__restrict__ a,
+                                                        const float *__restrict__ b,
+                                                        float *__restrict__ sum_out,
+                                                        const float *__restrict__ w,
+                                                        float *__restrict__ out, uint32_t n, float eps)
+{
+    __shared__ float red[kNormBlock / 64];
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float x = b ? a[i] + b[i] : a[i];
+        if (sum_out) sum_out[i] = x;
+        ss += x * x;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (uint32_t i = 0; i < blockDim.x / 64u; i++) tot += red[i];
+    const float rms = sqrtf(tot / (float)n + eps);
+    const float scale = 1.0f / rms;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float x = b ? a[i] + b[i] : a[i];
+        out[i] = x * scale * w[i];
+    }
+}
+
 // ------------------------------------------------------- generic GEMV
 
 __device__ __forceinline__ float wave_sum(float v)
@@ -807,7 +837,21 @@ struct StreamArgs {
     uint32_t wpt;                  // waves per team (TSUB == 0)
     uint32_t chunk;                // batches per partial-sum flush (TSUB == 0)
     uint32_t red_off;              // LDS byte offset of the partial-sum slots
+    // fused RMSNorm of the input (NORM kernels): x = rmsnorm(x + xb) * nw
+    const float *xb;               // second addend (the residual branch), cols floats
+    const float *nw;               // norm weights, cols floats
+    float *sum_out;                // if not NULL, workgroup 0 stores x + xb here
+    float eps;
 };
+
+// 16 bytes of v to p as an inline-asm store (not counted by the compiler's
+// wait bookkeeping, like store_y)
+__device__ __forceinline__ void store16(float *p, float4 v)
+{
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v r = {v.x, v.y, v.z, v.w};
+    asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(p), "v"(r) : "memory");
+}
 
 // y[row] = v as an inline-asm store.  The compiler does not count it among the
 // vector memory operations it waits for, so the waits it places before using
@@ -862,7 +906,12 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 // LDS slots and add them up every `chunk` batches (two workgroup barriers per
 // chunk instead of per batch).
 
-template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D>
+// NORM: the input is rmsnorm(a.x + a.xb) * a.nw (math.rs:237-257, with the
+// residual add of transformer.rs:31-46 folded in): every workgroup loads both
+// addends and the weights, reduces the sum of squares itself and converts the
+// normalised vector; workgroup 0 also stores the residual sum.
+template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
+          bool NORM = false>
 __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 {
     using I = Item<T>;
@@ -888,10 +937,16 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     // Every load below is unconditional (clamped addresses): the compiler's
     // wait counting stays exact only when no load sits on a conditional path.
     uint4 xv[XS];
+    uint4 bvv[NORM ? XS : 1], wvv[NORM ? XS : 1];
+    const uint4 *srcb = (const uint4 *)a.xb, *srcw = (const uint4 *)a.nw;
 #pragma unroll
     for (int k = 0; k < XS; k++) {
-        const uint32_t j = tid + k * blockDim.x;
-        xv[k] = src[j < n16 ? j : n16 - 1u];
+        const uint32_t j = tid + k * blockDim.x, jc = j < n16 ? j : n16 - 1u;
+        xv[k] = src[jc];
+        if constexpr (NORM) {
+            bvv[k] = srcb[jc];
+            wvv[k] = srcw[jc];
+        }
     }
     // x first: issued behind the weight stream of the workgroups that started
     // earlier, x reaches the late ones after most of the matrix; waiting for
@@ -907,12 +962,62 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
         if constexpr (CV) stage_planes1<I::EVEN_ODD>(__builtin_bit_cast(float4, v), j, lds, meta);
         else l4[I::PLANES ? j : j + (j >> 4)] = v;
     };
+    if constexpr (NORM) {
+        // x = a + b; sum of squares in element order within each thread
+        const bool w0 = blockIdx.x == 0 && a.sum_out;
+        auto addv = [](uint4 p, uint4 q) {
+            const float4 u = __builtin_bit_cast(float4, p), v = __builtin_bit_cast(float4, q);
+            return make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+        };
+        auto sq = [](float s, float4 x) {
+            s += x.x * x.x; s += x.y * x.y; s += x.z * x.z; s += x.w * x.w;
+            return s;
+        };
+        float ss = 0.f;
 #pragma unroll
-    for (int k = 0; k < XS; k++) {
-        const uint32_t j = tid + k * blockDim.x;
-        if (j < n16) put(xv[k], j);
+        for (int k = 0; k < XS; k++) {
+            const uint32_t j = tid + k * blockDim.x;
+            if (j < n16) {
+                const float4 x = addv(xv[k], bvv[k]);
+                if (w0) store16(a.sum_out + 4 * j, x);
+                ss = sq(ss, x);
+                xv[k] = __builtin_bit_cast(uint4, x);
+            }
+        }
+        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) {
+            const float4 x = addv(src[j], srcb[j]);
+            if (w0) store16(a.sum_out + 4 * j, x);
+            ss = sq(ss, x);
+        }
+        __shared__ float nred[LB / 64];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63u) == 0) nred[tid >> 6] = ss;
+        __syncthreads();
+        float tot = 0.f;
+        for (uint32_t i = 0; i < (blockDim.x + 63u) / 64u; i++) tot += nred[i];
+        const float rms = sqrtf(tot / (float)a.cols + a.eps);
+        const float scale = 1.0f / rms;
+        auto nrm = [&](float4 x, uint4 wq) {
+            const float4 w = __builtin_bit_cast(float4, wq);
+            return __builtin_bit_cast(uint4, make_float4(x.x * scale * w.x, x.y * scale * w.y,
+                                                         x.z * scale * w.z, x.w * scale * w.w));
+        };
+#pragma unroll
+        for (int k = 0; k < XS; k++) {
+            const uint32_t j = tid + k * blockDim.x;
+            if (j < n16) put(nrm(__builtin_bit_cast(float4, xv[k]), wvv[k]), j);
+        }
+        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x)
+            put(nrm(addv(src[j], srcb[j]), srcw[j]), j);
+    } else {
+#pragma unroll
+        for (int k = 0; k < XS; k++) {
+            const uint32_t j = tid + k * blockDim.x;
+            if (j < n16) put(xv[k], j);
+        }
+        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(src[j], j);
     }
-    for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(src[j], j);
     lds_barrier();
 
     using XT = typename std::conditional<I::PLANES, XP<S, SEG>, XF<S, SEG>>::type;
@@ -1045,14 +1150,14 @@ static uint32_t gcd_u(uint64_t a, uint64_t b)
     return (uint32_t)a;
 }
 
-template <uint32_t T, bool G1> static const void *stream_fn_g(uint32_t tsub)
+template <uint32_t T, bool G1, bool NORM> static const void *stream_fn_g(uint32_t tsub)
 {
     constexpr int R = 1, D = kDepth, LB = wg_max<T>();
     switch (tsub) {
-    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB>;
-    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB>;
-    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB>;
-    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, NORM>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, NORM>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, NORM>;
+    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB, D, NORM>;
     default: return nullptr;
     }
 }
@@ -1085,7 +1190,10 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     uint32_t tsub = 0, wpt = 1, tl;
     if (ni <= 64) { tsub = 16; while (tsub < ni) tsub <<= 1; tl = tsub; }
     else { wpt = (uint32_t)((ni + 63) / 64); tl = 64 * wpt; }
-    const void *fn = g == 1 ? stream_fn_g<T, true>(tsub) : stream_fn_g<T, false>(tsub);
+    const void *fn = g == 1 ? stream_fn_g<T, true, false>(tsub) : stream_fn_g<T, false, false>(tsub);
+    // fused-norm variant for the quant types (F16/F32 x tiles leave no registers for it)
+    const void *fn_norm = !I::PLANES ? nullptr
+                        : g == 1 ? stream_fn_g<T, true, I::PLANES>(tsub) : stream_fn_g<T, false, I::PLANES>(tsub);
     if (!fn) return;
     const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
     const uint32_t img = (image_bytes(I::PLANES, (uint32_t)cols) + 15u) & ~15u;
@@ -1106,9 +1214,12 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     } else {
         const uint64_t t = (nbat + ncu - 1) / ncu;         // teams per CU
         tpw = (uint32_t)(t < tpw_min ? tpw_min : t > tpw_max ? tpw_max : t);
+        // whole waves only: the workgroup reductions count blockDim / 64 waves
+        tpw = (tpw + tpw_min - 1) / tpw_min * tpw_min;
         per = 1;
     }
     const uint32_t grid = (uint32_t)((nbat + (uint64_t)tpw * per - 1) / ((uint64_t)tpw * per));
+    if ((tpw * tl) % 64u != 0) return;
     // partial-sum slots for a chunk of batches (several-wave teams)
     const uint32_t nw = tpw * tl / 64u;
     const uint32_t room = (uint32_t)max_lds_bytes() > img ? (uint32_t)max_lds_bytes() - img : 0u;
@@ -1117,6 +1228,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     const uint32_t lds = img + (tsub == 0 ? nw * chunk * red * 4u : 0u);
     if (lds > (uint32_t)max_lds_bytes()) return;
     p->fn = fn;
+    p->fn_norm = fn_norm;
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
     p->ts = tl;
@@ -1156,18 +1268,37 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p)
 
 // ------------------------------------------------------------ launchers
 
+static StreamArgs stream_args(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                               const float *x, float *y)
+{
+    StreamArgs a{};
+    a.w = w; a.x = x; a.y = y; a.nbytes = (uint32_t)nbytes; a.group_bytes = (uint32_t)p.group_bytes;
+    a.rows = (uint32_t)rows; a.cols = (uint32_t)cols; a.g = p.g; a.n_groups = p.n_groups;
+    a.ni = p.ni; a.n_teams = p.n_teams; a.per_team = p.per_team; a.wpt = p.wpt;
+    a.chunk = p.chunk; a.red_off = p.red_off;
+    return a;
+}
+
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
                 size_t cols, const float *x, float *y, ihipStream_t *stream)
 {
     hipStream_t st = (hipStream_t)stream;
     if (p.kind != 1 || !p.fn) return launch_gemv_generic(type, w, rows, cols, x, y, stream);
-    StreamArgs a;
-    a.w = w; a.x = x; a.y = y; a.nbytes = (uint32_t)nbytes; a.group_bytes = (uint32_t)p.group_bytes;
-    a.rows = (uint32_t)rows; a.cols = (uint32_t)cols; a.g = p.g; a.n_groups = p.n_groups;
-    a.ni = p.ni; a.n_teams = p.n_teams; a.per_team = p.per_team; a.wpt = p.wpt;
-    a.chunk = p.chunk; a.red_off = p.red_off;
+    StreamArgs a = stream_args(p, w, nbytes, rows, cols, x, y);
     void *args[] = {&a};
     return hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) == hipSuccess ? 0 : -2;
+}
+
+int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                     const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
+                     float *y, ihipStream_t *stream)
+{
+    if (p.kind != 1 || !p.fn_norm || cols % 4 != 0) return -1;
+    StreamArgs a = stream_args(p, w, nbytes, rows, cols, xa, y);
+    a.xb = xb; a.nw = nw; a.sum_out = sum_out; a.eps = eps;
+    void *args[] = {&a};
+    return hipLaunchKernel(p.fn_norm, dim3(p.grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
+                   hipSuccess ? 0 : -2;
 }
 
 template <uint32_t T>
@@ -1263,6 +1394,16 @@ int launch_fill(float *out, size_t n, float v, ihipStream_t *stream)
     if (n == 0) return 0;
     hipLaunchKernelGGL(fill_k, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, out,
                        (uint64_t)n, v);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_rmsnorm(const float *a, const float *b, float *sum_out, const float *w, float *out, size_t n,
+                   float eps, ihipStream_t *stream)
+{
+    if (n == 0) return 0;
+    if (n > 0xFFFFFFFFull) return -1;
+    hipLaunchKernelGGL(rmsnorm_k, dim3(1), dim3(kNormBlock), 0, (hipStream_t)stream, a, b, sum_out, w, out,
+                       (uint32_t)n, eps);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -58,8 +58,11 @@ def build(rinf, synth, oracle, ctx, cfg, mix, seed, max_seq):
     return dev, ref, shared
 
 
-def run_and_compare(dev, ref, oracle, cfg, prompt, n_new, penalty=1.1, window=64):
-    """Prompt then greedy decode, step by step on both sides."""
+def run_and_compare(dev, ref, oracle, cfg, prompt, n_new, penalty=1.1, window=64, tie_tol=0.0):
+    """Prompt then greedy decode, step by step on both sides.  A different
+    greedy choice is accepted only as a near-tie: the reference's penalised
+    logits of the two tokens differ by at most tie_tol * max|logits|; both
+    sides then continue with the reference's token."""
     V = cfg["vocab_size"]
     logits = np.zeros(V, np.float32)
     all_ids, errs, out = [], [], []
@@ -76,17 +79,20 @@ def run_and_compare(dev, ref, oracle, cfg, prompt, n_new, penalty=1.1, window=64
         rl = ref_l.copy()
         oracle.repetition_penalty(rl, recent, penalty, window)
         t_ref = oracle.argmax(rl)
-        assert t_dev == t_ref, f"step {len(out)}: device token {t_dev} != reference {t_ref}"
-        out.append(t_dev)
-        dev.forward(t_dev, pos, logits)
-        ref_l = ref.forward(t_dev, pos)
+        if t_dev != t_ref:
+            gap = abs(float(rl[t_ref]) - float(rl[t_dev])) / float(np.max(np.abs(rl)))
+            print(f"step {len(out)}: near-tie {t_dev} vs {t_ref}, relative gap {gap:.2e}", flush=True)
+            assert gap <= tie_tol, f"step {len(out)}: device token {t_dev} != reference {t_ref} (gap {gap:.2e})"
+        out.append(t_ref)
+        dev.forward(t_ref, pos, logits)
+        ref_l = ref.forward(t_ref, pos)
         errs.append(normwise_err(logits, ref_l))
-        all_ids.append(t_dev)
+        all_ids.append(t_ref)
         pos += 1
     return out, errs
 
 
-@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k", "q8_0"])
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k", "q8_0", "f16"])
 def test_small_model_logits_and_tokens(rinf, synth, oracle, ctx, mix):
     dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, mix, 11, 40)
     prompt = np.random.default_rng(5).integers(0, SMALL["vocab_size"], 8)
@@ -94,6 +100,16 @@ def test_small_model_logits_and_tokens(rinf, synth, oracle, ctx, mix):
     print(f"{mix}: max logits err {max(errs):.2e}, tokens {out}", flush=True)
     assert max(errs) <= LOGIT_TOL
     assert dev.seq_len == 24
+    dev.close()
+
+
+def test_head_dim_96_general_attention(rinf, synth, oracle, ctx):
+    """head_dim 96 (not a multiple of 64) takes the general attention kernel."""
+    cfg = dict(SMALL, embed_dim=384, hidden_dim=768)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q8_0", 13, 24)
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab_size"], 5)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 6)
+    assert max(errs) <= LOGIT_TOL
     dev.close()
 
 

@@ -41,9 +41,11 @@ def ref_gemv(oracle, raw, dtype, rows, cols, x):
 # BASELINE.json configs[1] (per-type sweep at Qwen2-0.5B shapes) plus the
 # row-group cases: cols % 256 in {32, 64, 128} and cols % 64 == 32.
 # Multi-wave teams (rows of more than 64 items: 14336 and 18944 columns),
-# rows that do not fill the last batch.
+# rows that do not fill the last batch; 1200 and 1700 row groups of short
+# teams (5 and 7 teams of 16 lanes per CU).
 SHAPES = [(896, 896), (128, 896), (896, 4864), (33, 96), (40, 160), (24, 192), (10, 640),
-          (7, 4096), (3, 14336), (37, 18944), (129, 3584), (70, 14336), (21, 8320)]
+          (7, 4096), (3, 14336), (37, 18944), (129, 3584), (70, 14336), (21, 8320), (1200, 256),
+          (1700, 256)]
 
 
 @pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])

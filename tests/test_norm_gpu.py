@@ -1,0 +1,101 @@
+"""GPU parity of qg_matvec_norm_dev (include/qgemv.h): RmsNorm of xa + xb
+followed by the mat-vec (src/math.rs:237-257, src/transformer.rs:31-46,
+src/quant.rs:178-206) against the oracle's rmsnorm + mat_vec_mul.
+
+y within GEMV_TOL normwise of the oracle; sum_out (xa + xb) bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import GEMV_TOL, normwise_err
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [0, 1, 2, 6, 8, 12, 13, 14]
+NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 6: "Q5_0", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}
+EPS = 1e-6
+
+# Qwen2-0.5B / 7B projection shapes (cols = embed), the lm_head of the tied
+# 0.5B model, small matrices, and row-group counts of 1025..1792 with short
+# teams (5..7 teams of 16 lanes per CU: workgroups that are not whole waves
+# unless the planner rounds them up).
+SHAPES = [(896, 896), (128, 896), (4864, 896), (600, 256), (256, 256), (3584, 3584), (1200, 256),
+          (1500, 512), (1700, 256)]
+
+
+def run(ctx, rinf, m, xa, xb, nw, rows, cols, with_sum=True, offset=0):
+    import torch
+    dev = lambda a: torch.from_numpy(a).cuda()
+    pad = torch.zeros(cols + offset, dtype=torch.float32, device="cuda")
+    pad[offset:] = dev(xa)
+    dxa = pad[offset:]
+    dxb = dev(xb) if xb is not None else None
+    dnw = dev(nw)
+    dy = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    ds = torch.full((cols,), float("nan"), dtype=torch.float32, device="cuda") if with_sum else None
+    torch.cuda.synchronize()
+    m.matvec_norm_dev(dxa, dxb, dnw, EPS, dy, ds, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return dy.cpu().numpy(), (ds.cpu().numpy() if with_sum else None)
+
+
+def inputs(synth, rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    xa = (rng.standard_normal(cols) * 3).astype(np.float32)
+    xb = rng.standard_normal(cols).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    return xa, xb, nw
+
+
+@pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{r}x{c}" for r, c in SHAPES])
+def test_norm_matvec_parity(ctx, rinf, oracle, synth, dtype, shape):
+    rows, cols = shape
+    seed = synth.config_seed(1) + 31 * rows + cols
+    raw = synth.gen_blocks(dtype, rows, cols, seed)
+    xa, xb, nw = inputs(synth, rows, cols, seed)
+    m = ctx.upload(raw, dtype, rows, cols)
+    y, s = run(ctx, rinf, m, xa, xb, nw, rows, cols)
+    kind = m.kernel_kind
+    m.free()
+    x = (xa + xb).astype(np.float32)
+    ref = oracle.mat_vec_mul_rows(raw, dtype, rows, cols, oracle.rmsnorm(x, nw, EPS))
+    err = normwise_err(y, ref)
+    print(f"{NAMES[dtype]} {rows}x{cols} kernel={kind} err={err:.2e}", flush=True)
+    assert np.array_equal(s.view(np.uint32), x.view(np.uint32))
+    assert err <= GEMV_TOL
+
+
+@pytest.mark.parametrize("dtype", [12, 14, 8], ids=["Q4_K", "Q6_K", "Q8_0"])
+def test_norm_matvec_variants(ctx, rinf, oracle, synth, dtype):
+    """No xb, no sum_out, and an x that is not 16-byte aligned (the
+    two-kernel path) give the same values as the fused kernel."""
+    rows, cols = 896, 896
+    seed = synth.config_seed(1) + dtype
+    raw = synth.gen_blocks(dtype, rows, cols, seed)
+    xa, xb, nw = inputs(synth, rows, cols, seed)
+    m = ctx.upload(raw, dtype, rows, cols)
+    fused, _ = run(ctx, rinf, m, xa, xb, nw, rows, cols, with_sum=False)
+    x = (xa + xb).astype(np.float32)
+    shifted, s = run(ctx, rinf, m, x, None, nw, rows, cols, offset=1)
+    alone, _ = run(ctx, rinf, m, x, None, nw, rows, cols)
+    m.free()
+    ref = oracle.mat_vec_mul_rows(raw, dtype, rows, cols, oracle.rmsnorm(x, nw, EPS))
+    for y in (fused, shifted, alone):
+        assert normwise_err(y, ref) <= GEMV_TOL
+    assert np.array_equal(s, x)
+
+
+def test_norm_matvec_errors(ctx, rinf, synth):
+    import torch
+    rows, cols = 64, 256
+    m = ctx.upload(synth.gen_blocks(12, rows, cols, 5), 12, rows, cols)
+    xa = torch.zeros(cols, dtype=torch.float32, device="cuda")
+    nw = torch.ones(cols, dtype=torch.float32, device="cuda")
+    y = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    with pytest.raises(rinf.QgemvError) as e:
+        m.matvec_norm_dev(xa, None, nw, EPS, y, xa)            # sum_out overlaps xa
+    assert e.value.status == 1                                 # QG_ERR_INVALID_ARG
+    m.free()
