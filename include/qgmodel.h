@@ -64,6 +64,12 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
 int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_mat *mat);
 int qg_model_set_vector(qg_model *m, uint32_t which, uint32_t layer, const float *v, size_t n);
 
+/* No counterpart in the reference: replay each forward pass (and generate's
+ * sample + forward step) from a HIP graph captured on first use (enable != 0,
+ * the default), or enqueue the kernels one by one (enable == 0).  Both run the
+ * same kernels on the same data and give bit-identical results. */
+int qg_model_use_graphs(qg_model *m, int enable);
+
 /* KVCache::clear for every layer (src/kv_cache.rs:232). */
 int qg_model_reset(qg_model *m);
 /* Number of positions currently in the caches. */

@@ -89,6 +89,7 @@ _SIGS = {
     "qg_model_set_matrix": (ctypes.c_int, [_P, _U32, _U32, _P, _SZ, _U32, _SZ, _SZ]),
     "qg_model_share_matrix": (ctypes.c_int, [_P, _U32, _U32, _P]),
     "qg_model_set_vector": (ctypes.c_int, [_P, _U32, _U32, _P, _SZ]),
+    "qg_model_use_graphs": (ctypes.c_int, [_P, ctypes.c_int]),
     "qg_model_reset": (ctypes.c_int, [_P]),
     "qg_model_seq_len": (ctypes.c_int, [_P, ctypes.POINTER(_SZ)]),
     "qg_model_forward": (ctypes.c_int, [_P, _U32, _U32, _P]),
@@ -319,6 +320,10 @@ class DeviceModel:
     def set_vector(self, which: int, layer: int, v):
         self.ctx.check(self.ctx.lib.qg_model_set_vector(self.h, which, layer, _ptr(v), len(v)),
                        "qg_model_set_vector")
+
+    def use_graphs(self, enable: bool):
+        """HIP graph replay of the forward pass (default) or one launch per kernel."""
+        self.ctx.check(self.ctx.lib.qg_model_use_graphs(self.h, int(bool(enable))), "qg_model_use_graphs")
 
     def reset(self):
         self.ctx.check(self.ctx.lib.qg_model_reset(self.h), "qg_model_reset")

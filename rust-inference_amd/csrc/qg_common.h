@@ -80,6 +80,9 @@ int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *ou
                    ihipStream_t *stream);
 int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                           size_t row, float *out, ihipStream_t *stream);
+// the same with the row index read from device memory when the kernel runs
+int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
+                              float *out, ihipStream_t *stream);
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
 // out = rmsnorm(a (+ b)) * w in one workgroup; sum_out (may be NULL) = a + b.
 int launch_rmsnorm(const float *a, const float *b, float *sum_out, const float *w, float *out, size_t n,

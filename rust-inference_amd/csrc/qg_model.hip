@@ -3,19 +3,27 @@
 //
 // Every tensor stays in HBM for the whole generation: the quantized weights
 // (raw GGUF blocks, mat-vec'd by the library's GEMV), norms and biases, the
-// f32 KV caches, the activations and the logits.  Per token the host only
-// enqueues kernels; the one device->host transfer is the sampled token id.
+// f32 KV caches, the activations, the logits and the token history.  The
+// per-token values (token id, position, cache slot) live in a device-side
+// Step record that the kernels read when they run, so one forward pass is a
+// fixed sequence of launches: it is captured once as a HIP graph and replayed
+// per token.  In generate, the sampler appends its token to the history and
+// advances the Step itself, so a decode step needs no host round trip.
 //
 // Kernels (all f32, -ffp-contract=off: every product and sum is rounded where
-// the reference rounds it, except that block reductions add in tree order):
-//   rmsnorm_k        math.rs:237-273 (RmsNorm::forward), optionally fused
+// the reference rounds it, except that reductions add in tree order and the
+// attention softmax is split over position ranges):
+//   RMSNorm          math.rs:237-257 (RmsNorm::forward), inside the next GEMV
 //                    with the residual add of transformer.rs:31-46
 //   qkv_post_k       attention.rs:68-90: bias add, RoPE on q and k
 //                    (rope.rs:88-96, pairs 2i/2i+1), KV append (kv_cache.rs:52-73)
-//   attention_k      attention.rs:92-121: scores, softmax (math.rs:104-118),
-//                    weighted sum of v, one workgroup per query head
+//   attn_split_k     attention.rs:92-121 over one range of positions for the
+//   attn_combine_k   query heads of one kv head; then the ranges' partial
+//                    softmax sums are merged (math.rs:104-118 rescaled)
+//   attention_k      the same in one workgroup per head (head_dim % 64 != 0)
 //   silu_mul_k       mlp.rs:36-41, silu as math.rs:137-146
-//   sample_greedy_k  sampler.rs:109-127 then math.rs:328-339
+//   sample_part_k    sampler.rs:109-127 then math.rs:328-339 over one range
+//   sample_final_k   of the logits per workgroup; then the first maximum
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -30,13 +38,68 @@
 
 namespace qgm {
 
-constexpr int kBlock = 1024;
+constexpr uint32_t kRecentMax = 64;       // model.rs:370-374 passes the last 64 tokens
+constexpr uint32_t kSampleWG = 256;       // partial-argmax workgroups
+constexpr uint32_t kMaxGroup = 8;         // query heads per attention workgroup
+constexpr uint32_t kMaxSplit = 64;        // position ranges per head
+constexpr uint32_t kMinLen = 8;           // positions per range (the last may hold fewer)
 
-// Sum over the workgroup (every thread gets the total).
+// Positions per range for seq cached positions; ranges = ceil(seq / len).
+__host__ __device__ __forceinline__ uint32_t range_len(uint32_t seq, uint32_t nsplit)
+{
+    const uint32_t l = (seq + nsplit - 1) / nsplit;
+    return l > kMinLen ? l : kMinLen;
+}
+
+// Per-token state read by the kernels: the token fed to the next forward
+// pass, its position (RoPE) and its cache slot (number of cached positions).
+struct Step {
+    uint32_t token, pos, slot, pad;
+};
+
+// Sum / max over the 64 lanes of a full wave, returned to every lane.
+// DPP steps (gfx9 controls: quad_perm 0xB1 / 0x4E, row_half_mirror 0x141,
+// row_mirror 0x140, row_bcast15 0x142 into rows 1 and 3, row_bcast31 0x143
+// into rows 2 and 3) leave the total in lane 63; rows outside a step's row
+// mask are left as they are.
+template <int CTRL, int ROW_MASK = 0xF> __device__ __forceinline__ float dppf(float v, float old)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                 0xF, false));
+}
+
+__device__ __forceinline__ float lane63(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dppf<0xB1>(v, 0.f);
+    v += dppf<0x4E>(v, 0.f);
+    v += dppf<0x141>(v, 0.f);
+    v += dppf<0x140>(v, 0.f);
+    v += dppf<0x142, 0xA>(v, 0.f);
+    v += dppf<0x143, 0xC>(v, 0.f);
+    return lane63(v);
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dppf<0xB1>(v, v));
+    v = fmaxf(v, dppf<0x4E>(v, v));
+    v = fmaxf(v, dppf<0x141>(v, v));
+    v = fmaxf(v, dppf<0x140>(v, v));
+    v = fmaxf(v, dppf<0x142, 0xA>(v, v));
+    v = fmaxf(v, dppf<0x143, 0xC>(v, v));
+    return lane63(v);
+}
+
+// Sum / max over a workgroup of whole waves (every thread gets the result).
 __device__ float block_sum(float v, float *red)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = wave_sum(v);
     const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[w] = v;
@@ -46,11 +109,9 @@ __device__ float block_sum(float v, float *red)
     return t;
 }
 
-// Max over the workgroup ignoring NaN (f32::max), every thread gets it.
 __device__ float block_max(float v, float *red)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = wave_max(v);
     const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[w] = v;
@@ -66,10 +127,11 @@ __global__ void __launch_bounds__(256) qkv_post_k(float *__restrict__ q, const f
                                                   const float *__restrict__ bk, const float *__restrict__ bv,
                                                   float *__restrict__ kc, float *__restrict__ vc,
                                                   const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                                                  uint32_t q_dim, uint32_t kv_dim, uint32_t hd, uint32_t pos,
-                                                  uint32_t slot)
+                                                  uint32_t q_dim, uint32_t kv_dim, uint32_t hd,
+                                                  const Step *__restrict__ st)
 {
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x, half = hd / 2;
+    const uint32_t pos = st->pos, slot = st->slot;
     const uint32_t i0 = 2 * t;
     if (i0 < q_dim) {
         const uint32_t j = (i0 % hd) / 2;
@@ -90,15 +152,145 @@ __global__ void __launch_bounds__(256) qkv_post_k(float *__restrict__ q, const f
     }
 }
 
-// One workgroup per query head; LDS: hd floats of q, seq floats of scores.
+// Attention over positions [j0, j1) of the seq = slot + 1 cached ones, for
+// the `grp` query heads h0 .. h0 + grp - 1 that share one kv head
+// (head_dim = 64 * E).  Workgroup (head group, range): 4 waves, each lane
+// owns dimensions lane + 64 e, so every K and V row is one coalesced read
+// shared by the group's heads.  Writes the unnormalised partial output
+// sum_j exp(s_j - m) v_j and (m, l = sum_j exp(s_j - m)) of its range;
+// workgroups whose range starts past seq exit.
+template <int E>
+__global__ void __launch_bounds__(256) attn_split_k(const float *__restrict__ q, const float *__restrict__ kc,
+                                                    const float *__restrict__ vc, float *__restrict__ part,
+                                                    float *__restrict__ ml, const Step *__restrict__ st,
+                                                    uint32_t kv_dim, uint32_t n_rep, uint32_t grp,
+                                                    uint32_t nsplit, uint32_t lmax, float scale)
+{
+    constexpr uint32_t HD = 64 * E;
+    extern __shared__ float sm[];             // sc[grp][lmax], pr[4][grp][HD]
+    float *sc = sm, *pr = sm + grp * lmax;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t split = blockIdx.x % nsplit, h0 = (blockIdx.x / nsplit) * grp;
+    const uint32_t kvo = (h0 / n_rep) * HD;
+    const uint32_t seq = st->slot + 1;
+    const uint32_t len = range_len(seq, nsplit);           // <= lmax while seq <= max_seq_len
+    const uint32_t j0 = split * len, j1 = min(seq, j0 + len);
+    if (j0 >= seq) return;
+    float qv[kMaxGroup][E];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxGroup; r++)
+#pragma unroll
+        for (int e = 0; e < E; e++) qv[r][e] = r < grp ? q[(h0 + r) * HD + lane + 64 * e] : 0.f;
+    // scores (attention.rs:101-109)
+    for (uint32_t j = j0 + wave; j < j1; j += 4) {
+        const float *kr = kc + (size_t)j * kv_dim + kvo;
+        float kv[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) kv[e] = kr[lane + 64 * e];
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxGroup; r++) {
+            if (r >= grp) break;
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; e++) s += qv[r][e] * kv[e];
+            s = wave_sum(s);
+            if (lane == 0) sc[r * lmax + (j - j0)] = s * scale;
+        }
+    }
+    __syncthreads();
+    // range max and exp sum per head (math.rs:104-113 over this range)
+    const uint32_t cnt = j1 - j0;
+    for (uint32_t r = wave; r < grp; r += 4) {
+        float mx = -INFINITY;
+        for (uint32_t t = lane; t < cnt; t += 64) mx = fmaxf(mx, sc[r * lmax + t]);
+        mx = wave_max(mx);
+        float sum = 0.f;
+        for (uint32_t t = lane; t < cnt; t += 64) {
+            const float ex = expf(sc[r * lmax + t] - mx);
+            sc[r * lmax + t] = ex;
+            sum += ex;
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) {
+            float *o = ml + ((size_t)(h0 + r) * nsplit + split) * 2;
+            o[0] = mx;
+            o[1] = sum;
+        }
+    }
+    __syncthreads();
+    // weighted sum of v (attention.rs:113-119 over this range)
+    float acc[kMaxGroup][E];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxGroup; r++)
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[r][e] = 0.f;
+    for (uint32_t j = j0 + wave; j < j1; j += 4) {
+        const float *vr = vc + (size_t)j * kv_dim + kvo;
+        float vv[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) vv[e] = vr[lane + 64 * e];
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxGroup; r++) {
+            if (r >= grp) break;
+            const float p = sc[r * lmax + (j - j0)];
+#pragma unroll
+            for (int e = 0; e < E; e++) acc[r][e] += p * vv[e];
+        }
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxGroup; r++) {
+        if (r >= grp) break;
+#pragma unroll
+        for (int e = 0; e < E; e++) pr[(wave * grp + r) * HD + lane + 64 * e] = acc[r][e];
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < grp * HD; i += blockDim.x) {
+        const uint32_t r = i / HD, d = i % HD;
+        const float s = (pr[r * HD + d] + pr[(grp + r) * HD + d]) + (pr[(2 * grp + r) * HD + d] +
+                                                                     pr[(3 * grp + r) * HD + d]);
+        part[((size_t)(h0 + r) * nsplit + split) * HD + d] = s;
+    }
+}
+
+// out[h] = sum_s w_s part_s with w_s = exp(m_s - max m) / sum_s exp(m_s - max m) l_s:
+// the softmax-weighted sum of v over all positions.  One workgroup per head;
+// wave 0 derives the weights of the ranges in use.
+__global__ void __launch_bounds__(256) attn_combine_k(const float *__restrict__ part, const float *__restrict__ ml,
+                                                      float *__restrict__ out, const Step *__restrict__ st,
+                                                      uint32_t hd, uint32_t nsplit)
+{
+    __shared__ float wt[kMaxSplit];
+    const uint32_t h = blockIdx.x, seq = st->slot + 1;
+    const uint32_t len = range_len(seq, nsplit), nr = (seq + len - 1) / len;
+    const float *m = ml + (size_t)h * nsplit * 2;
+    if (threadIdx.x < 64) {
+        const uint32_t s = threadIdx.x;
+        const float ms = s < nr ? m[2 * s] : -INFINITY, ls = s < nr ? m[2 * s + 1] : 0.f;
+        const float mx = wave_max(ms);
+        const float w = s < nr ? expf(ms - mx) : 0.f;
+        const float l = wave_sum(w * ls);
+        wt[s] = w / l;
+    }
+    __syncthreads();
+    const float *p = part + (size_t)h * nsplit * hd;
+    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+        float acc = 0.f;
+        for (uint32_t s = 0; s < nr; s++) acc += wt[s] * p[(size_t)s * hd + d];
+        out[h * hd + d] = acc;
+    }
+}
+
+// One workgroup per query head for any even head_dim; LDS: hd floats of q,
+// max_seq_len floats of scores.
 __global__ void __launch_bounds__(256) attention_k(const float *__restrict__ q, const float *__restrict__ kc,
                                                    const float *__restrict__ vc, float *__restrict__ out,
-                                                   uint32_t seq, uint32_t hd, uint32_t kv_dim, uint32_t n_rep,
-                                                   float scale)
+                                                   const Step *__restrict__ st, uint32_t hd, uint32_t kv_dim,
+                                                   uint32_t n_rep, float scale)
 {
     extern __shared__ float sm[];
     __shared__ float red[4];
     float *qs = sm, *sc = sm + hd;
+    const uint32_t seq = st->slot + 1;
     const uint32_t h = blockIdx.x, kvh = (h / n_rep) * hd;
     for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[h * hd + d];
     __syncthreads();
@@ -129,62 +321,6 @@ __global__ void __launch_bounds__(256) attention_k(const float *__restrict__ q, 
     }
 }
 
-// Same result for head dimensions hd = 64 * E (E = 1, 2, 4): one workgroup of
-// four waves per query head.  Wave w takes positions j = w, w + 4, ...; its
-// lanes split the head dimension (lane owns d = lane + 64e), so every key and
-// value row is one coalesced 4E-byte-per-lane read and each score is a wave
-// reduction.  The four per-wave partial outputs are added through LDS.
-template <int E>
-__global__ void __launch_bounds__(256) attention_wave_k(const float *__restrict__ q, const float *__restrict__ kc,
-                                                        const float *__restrict__ vc, float *__restrict__ out,
-                                                        uint32_t seq, uint32_t kv_dim, uint32_t n_rep, float scale)
-{
-    constexpr uint32_t HD = 64 * E;
-    extern __shared__ float sm[];                 // sc[seq], part[4][HD]
-    __shared__ float red[4];
-    float *sc = sm, *part = sm + seq;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t h = blockIdx.x, kvh = (h / n_rep) * HD;
-    float qv[E];
-#pragma unroll
-    for (int e = 0; e < E; e++) qv[e] = q[h * HD + lane + 64 * e];
-    float mx = -INFINITY;
-    for (uint32_t j = wave; j < seq; j += 4) {
-        const float *kr = kc + (size_t)j * kv_dim + kvh;
-        float s = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; e++) s += qv[e] * kr[lane + 64 * e];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-        s = s * scale;
-        if (lane == 0) sc[j] = s;
-        mx = fmaxf(mx, s);
-    }
-    mx = block_max(mx, red);                      // (barrier inside: sc complete)
-    float sum = 0.f;
-    for (uint32_t j = threadIdx.x; j < seq; j += blockDim.x) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
-    }
-    sum = block_sum(sum, red);
-    const float inv = 1.0f / sum;
-    float acc[E];
-#pragma unroll
-    for (int e = 0; e < E; e++) acc[e] = 0.f;
-    for (uint32_t j = wave; j < seq; j += 4) {
-        const float p = sc[j] * inv;
-        const float *vr = vc + (size_t)j * kv_dim + kvh;
-#pragma unroll
-        for (int e = 0; e < E; e++) acc[e] += p * vr[lane + 64 * e];
-    }
-#pragma unroll
-    for (int e = 0; e < E; e++) part[wave * HD + lane + 64 * e] = acc[e];
-    __syncthreads();
-    for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x)
-        out[h * HD + d] = (part[d] + part[HD + d]) + (part[2 * HD + d] + part[3 * HD + d]);
-}
-
 __device__ __forceinline__ float silu1(float x)
 {
     if (x >= 0.0f) {
@@ -202,30 +338,53 @@ __global__ void __launch_bounds__(256) silu_mul_k(const float *__restrict__ g, c
     if (i < n) h[i] = silu1(g[i]) * u[i];
 }
 
-// Repetition penalty over recent[0..n_recent) in order, then the first index
-// of the maximum (NaN never wins; a NaN at index 0 returns 0, as the
-// reference's strict ">" scan does).
-__global__ void __launch_bounds__(kBlock) sample_greedy_k(float *__restrict__ logits, uint32_t n,
-                                                          const uint32_t *__restrict__ recent,
-                                                          uint32_t n_recent, float penalty,
-                                                          uint32_t *__restrict__ token)
+// Greedy sampler.  The recent tokens are either an explicit list (recent,
+// n_recent) or, in generate, the last min(window, 64) entries of the token
+// history hist[0 .. slot + 1).
+struct SampleArgs {
+    float *logits;
+    uint32_t n;
+    const uint32_t *recent;
+    uint32_t n_recent;
+    uint32_t *hist;              // generate: history (NULL: explicit list)
+    uint32_t window;
+    float penalty;
+    Step *st;
+    float *pv;                   // per-workgroup maximum and its index
+    uint32_t *pi;
+    uint32_t *token;             // the sampled token
+};
+
+// (value, index) of the first maximum over [lo, hi) after the repetition
+// penalty of the tokens in this range (applied in list order, each
+// occurrence again, as sampler.rs:109-127).  NaN never wins.
+__global__ void __launch_bounds__(256) sample_part_k(SampleArgs a)
 {
-    __shared__ float bv[kBlock / 64];
-    __shared__ uint32_t bi[kBlock / 64];
-    if (threadIdx.x == 0 && penalty != 1.0f) {
-        for (uint32_t r = 0; r < n_recent; r++) {
-            const uint32_t t = recent[r];
-            if (t < n) {
-                const float l = logits[t];
-                logits[t] = l > 0.0f ? l / penalty : l * penalty;
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const uint32_t per = (a.n + gridDim.x - 1) / gridDim.x;
+    const uint32_t lo = blockIdx.x * per, hi = min(a.n, lo + per);
+    const uint32_t *rc = a.recent;
+    uint32_t nr = a.n_recent;
+    if (a.hist) {
+        const uint32_t cnt = a.st->slot + 1, w = min(min(a.window, kRecentMax), cnt);
+        rc = a.hist + (cnt - w);
+        nr = w;
+    }
+    if (threadIdx.x == 0 && a.penalty != 1.0f) {          // sampler.rs:76-78
+        for (uint32_t r = 0; r < nr; r++) {
+            const uint32_t t = rc[r];
+            if (t >= lo && t < hi) {
+                const float l = a.logits[t];
+                a.logits[t] = l > 0.0f ? l / a.penalty : l * a.penalty;
             }
         }
     }
     __syncthreads();
     float best = -INFINITY;
     uint32_t idx = 0xFFFFFFFFu;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = logits[i];
+    for (uint32_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        const float v = a.logits[i];
         if (v > best || (idx == 0xFFFFFFFFu && v == best)) { best = v; idx = i; }
     }
     // (value, index) max with the smaller index on ties
@@ -247,8 +406,43 @@ __global__ void __launch_bounds__(kBlock) sample_greedy_k(float *__restrict__ lo
             if (bi[i] == 0xFFFFFFFFu) continue;
             if (id == 0xFFFFFFFFu || bv[i] > b || (bv[i] == b && bi[i] < id)) { b = bv[i]; id = bi[i]; }
         }
-        const float l0 = logits[0];
-        *token = (l0 != l0 || id == 0xFFFFFFFFu) ? 0u : id;
+        a.pv[blockIdx.x] = b;
+        a.pi[blockIdx.x] = id;
+    }
+}
+
+// The first maximum over the ranges (math.rs:328-339: a NaN at index 0
+// returns 0, as the reference's strict ">" scan does).  In generate the token
+// is appended to the history and becomes the next step's token.
+__global__ void __launch_bounds__(64) sample_final_k(SampleArgs a, uint32_t nparts)
+{
+    if (threadIdx.x != 0) return;
+    float b = -INFINITY;
+    uint32_t id = 0xFFFFFFFFu;
+    for (uint32_t i = 0; i < nparts; i++) {
+        if (a.pi[i] == 0xFFFFFFFFu) continue;
+        if (id == 0xFFFFFFFFu || a.pv[i] > b) { b = a.pv[i]; id = a.pi[i]; }
+    }
+    const float l0 = a.logits[0];
+    const uint32_t tok = (l0 != l0 || id == 0xFFFFFFFFu) ? 0u : id;
+    *a.token = tok;
+    if (a.hist) {
+        Step *s = a.st;
+        const uint32_t n = s->slot + 1;
+        a.hist[n] = tok;
+        s->slot = n;
+        s->pos += 1;
+        s->token = tok;
+    }
+}
+
+// Prefill: the next step feeds the next history token.
+__global__ void advance_k(Step *st, const uint32_t *hist)
+{
+    if (threadIdx.x == 0) {
+        st->slot += 1;
+        st->pos += 1;
+        st->token = hist[st->slot];
     }
 }
 
@@ -258,13 +452,15 @@ __global__ void __launch_bounds__(kBlock) sample_greedy_k(float *__restrict__ lo
 
 namespace {
 constexpr int kSlots = 7;                 // WQ .. DOWN
-constexpr size_t kRecentMax = 64;         // model.rs:370-374 passes the last 64 tokens
+constexpr uint32_t kRing = 256;           // pinned Step records for host-fed forwards
 }
 
 struct qg_model {
     qg_ctx *ctx = nullptr;
     qg_model_config cfg{};
     uint32_t hd = 0, q_dim = 0, kv_dim = 0, n_rep = 0;
+    uint32_t att_grp = 0, att_nsplit = 0, att_lmax = 0;   // split attention (head_dim % 64 == 0)
+    size_t att_lds = 0;
     qg_mat *tok = nullptr, *lm = nullptr;
     bool tok_owned = false, lm_owned = false;
     std::vector<qg_mat *> w[kSlots];
@@ -278,8 +474,19 @@ struct qg_model {
     float *ao = nullptr, *ao2 = nullptr, *g = nullptr, *u = nullptr, *hb = nullptr, *fo = nullptr;
     float *logits = nullptr;
     float *zeros = nullptr;               // the residual addend of the first layer
-    uint32_t *d_recent = nullptr, *d_token = nullptr;
+    float *att_part = nullptr, *att_ml = nullptr;
+    float *s_pv = nullptr;
+    uint32_t *s_pi = nullptr;
+    uint32_t *d_recent = nullptr, *d_token = nullptr, *d_hist = nullptr;
+    qgm::Step *d_step = nullptr;
     uint32_t *h_recent = nullptr, *h_token = nullptr;   // pinned
+    qgm::Step *h_steps = nullptr;                       // pinned ring
+    uint32_t ring = 0;
+    bool use_graphs = true;
+    hipGraphExec_t g_fwd = nullptr;       // forward pass
+    hipGraphExec_t g_dec = nullptr;       // sample + advance + forward (generate)
+    float g_dec_penalty = 0.f;
+    uint32_t g_dec_window = 0;
     std::vector<void *> allocs;
 };
 
@@ -308,9 +515,17 @@ template <class T> int dalloc(qg_model *m, T **p, size_t n)
     return QG_OK;
 }
 
+void drop_graphs(qg_model *m)
+{
+    if (m->g_fwd) (void)hipGraphExecDestroy(m->g_fwd);
+    if (m->g_dec) (void)hipGraphExecDestroy(m->g_dec);
+    m->g_fwd = m->g_dec = nullptr;
+}
+
 void free_model(qg_model *m)
 {
     m->ctx->models.erase(m);
+    drop_graphs(m);
     for (int s = 0; s < kSlots; s++)
         for (size_t l = 0; l < m->w[s].size(); l++)
             if (m->w[s][l] && m->owned[s][l]) qg_mat_free(m->ctx, m->w[s][l]);
@@ -319,6 +534,7 @@ void free_model(qg_model *m)
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->h_recent) (void)hipHostFree(m->h_recent);
     if (m->h_token) (void)hipHostFree(m->h_token);
+    if (m->h_steps) (void)hipHostFree(m->h_steps);
     delete m;
 }
 
@@ -369,6 +585,159 @@ bool complete(const qg_model *m)
     return true;
 }
 
+// Transformer::forward (transformer.rs:63-98) for the token, position and
+// slot in m->d_step; enqueues kernels only (also used under graph capture).
+int enqueue_forward(qg_model *m)
+{
+    const qg_model_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    ihipStream_t *sti = (ihipStream_t *)st;
+    const uint32_t E = c.embed_dim, H = c.hidden_dim;
+    int rc;
+    // embedding row into a zeroed buffer (transformer.rs:74-75, quant.rs:152-174)
+    if (qg::launch_fill(m->h0, E, 0.0f, sti) ||
+        qg::launch_dequantize_row_dev(m->tok->type, m->tok->d, m->tok->rows, m->tok->cols, &m->d_step->token,
+                                      m->h0, sti))
+        return mfail(m, QG_ERR_HIP, "embedding", hipGetLastError());
+    const size_t kv_layer = (size_t)c.max_seq_len * m->kv_dim;
+    const float scale = 1.0f / sqrtf((float)m->hd);                      // attention.rs:99
+    const uint32_t pairs = (m->q_dim > m->kv_dim ? m->q_dim : m->kv_dim) / 2;
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        // the residual stream entering the layer is h0 (layer 0: the
+        // embedding) or h1 + fo, which the Q GEMV also stores to h0
+        const float *na = l == 0 ? m->h0 : m->h1, *nb = l == 0 ? m->zeros : m->fo;
+        const float *anorm = m->vec[QG_V_ATTN_NORM][l];
+        if ((rc = gemv_norm(m, m->w[QG_M_WQ - 2][l], na, nb, anorm, l == 0 ? nullptr : m->h0, m->q)) ||
+            (rc = gemv_norm(m, m->w[QG_M_WK - 2][l], na, nb, anorm, nullptr, m->k)) ||
+            (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
+            return rc;
+        float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
+        hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
+                           m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
+                           m->sin_t, m->q_dim, m->kv_dim, m->hd, m->d_step);
+        if (m->att_grp) {
+            const dim3 grid(c.n_heads / m->att_grp * m->att_nsplit);
+            if (m->hd == 64)
+                hipLaunchKernelGGL(qgm::attn_split_k<1>, grid, dim3(256), m->att_lds, st, m->q, kc, vc,
+                                   m->att_part, m->att_ml, m->d_step, m->kv_dim, m->n_rep, m->att_grp,
+                                   m->att_nsplit, m->att_lmax, scale);
+            else if (m->hd == 128)
+                hipLaunchKernelGGL(qgm::attn_split_k<2>, grid, dim3(256), m->att_lds, st, m->q, kc, vc,
+                                   m->att_part, m->att_ml, m->d_step, m->kv_dim, m->n_rep, m->att_grp,
+                                   m->att_nsplit, m->att_lmax, scale);
+            else
+                hipLaunchKernelGGL(qgm::attn_split_k<4>, grid, dim3(256), m->att_lds, st, m->q, kc, vc,
+                                   m->att_part, m->att_ml, m->d_step, m->kv_dim, m->n_rep, m->att_grp,
+                                   m->att_nsplit, m->att_lmax, scale);
+            hipLaunchKernelGGL(qgm::attn_combine_k, dim3(c.n_heads), dim3(256), 0, st, m->att_part, m->att_ml,
+                               m->ao, m->d_step, m->hd, m->att_nsplit);
+        } else {
+            hipLaunchKernelGGL(qgm::attention_k, dim3(c.n_heads), dim3(256), m->att_lds, st, m->q, kc, vc, m->ao,
+                               m->d_step, m->hd, m->kv_dim, m->n_rep, scale);
+        }
+        if ((rc = launched(m, "attention"))) return rc;
+        if ((rc = gemv(m, m->w[QG_M_WO - 2][l], m->ao, m->ao2))) return rc;
+        // h1 = h0 + attention output (stored by the gate GEMV); MLP input = ffn_norm(h1)
+        const float *fnorm = m->vec[QG_V_FFN_NORM][l];
+        if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
+            (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u)))
+            return rc;
+        hipLaunchKernelGGL(qgm::silu_mul_k, dim3((H + 255) / 256), dim3(256), 0, st, m->g, m->u, m->hb, H);
+        if ((rc = launched(m, "silu*up"))) return rc;
+        if ((rc = gemv(m, m->w[QG_M_DOWN - 2][l], m->hb, m->fo))) return rc;
+    }
+    // final norm of h1 + fo (transformer.rs:87-97) inside the lm_head GEMV
+    return gemv_norm(m, m->lm, m->h1, m->fo, m->final_norm, nullptr, m->logits);
+}
+
+qgm::SampleArgs sample_args(qg_model *m, uint32_t n_recent, float penalty, bool generate, uint32_t window)
+{
+    qgm::SampleArgs a{};
+    a.logits = m->logits;
+    a.n = m->cfg.vocab_size;
+    a.recent = m->d_recent;
+    a.n_recent = n_recent;
+    a.hist = generate ? m->d_hist : nullptr;
+    a.window = window;
+    a.penalty = penalty;
+    a.st = m->d_step;
+    a.pv = m->s_pv;
+    a.pi = m->s_pi;
+    a.token = m->d_token;
+    return a;
+}
+
+int enqueue_sample(qg_model *m, const qgm::SampleArgs &a)
+{
+    hipStream_t st = m->ctx->stream;
+    hipLaunchKernelGGL(qgm::sample_part_k, dim3(qgm::kSampleWG), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(qgm::sample_final_k, dim3(1), dim3(64), 0, st, a, qgm::kSampleWG);
+    return launched(m, "sample");
+}
+
+// generate's decode step: sample from the last logits, append and advance,
+// then the forward pass of the sampled token
+int enqueue_decode(qg_model *m)
+{
+    int rc = enqueue_sample(m, sample_args(m, 0, m->g_dec_penalty, true, m->g_dec_window));
+    return rc ? rc : enqueue_forward(m);
+}
+
+int capture(qg_model *m, int (*fn)(qg_model *), hipGraphExec_t *out)
+{
+    hipStream_t st = m->ctx->stream;
+    QGM_HIP(m, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int rc = fn(m);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return mfail(m, QG_ERR_HIP, "hipStreamEndCapture", e);
+    const hipError_t e2 = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e2 != hipSuccess) { *out = nullptr; return mfail(m, QG_ERR_HIP, "hipGraphInstantiate", e2); }
+    return QG_OK;
+}
+
+int run_forward(qg_model *m)
+{
+    if (!m->use_graphs) return enqueue_forward(m);
+    int rc;
+    if (!m->g_fwd && (rc = capture(m, enqueue_forward, &m->g_fwd))) return rc;
+    QGM_HIP(m, hipGraphLaunch(m->g_fwd, m->ctx->stream));
+    return QG_OK;
+}
+
+int run_decode(qg_model *m, float penalty, uint32_t window)
+{
+    if (m->g_dec && (m->g_dec_penalty != penalty || m->g_dec_window != window)) {
+        (void)hipGraphExecDestroy(m->g_dec);
+        m->g_dec = nullptr;
+    }
+    m->g_dec_penalty = penalty;
+    m->g_dec_window = window;
+    if (!m->use_graphs) return enqueue_decode(m);
+    int rc;
+    if (!m->g_dec && (rc = capture(m, enqueue_decode, &m->g_dec))) return rc;
+    QGM_HIP(m, hipGraphLaunch(m->g_dec, m->ctx->stream));
+    return QG_OK;
+}
+
+// host-fed Step record (pinned ring; the stream is drained before a slot is reused)
+int put_step(qg_model *m, uint32_t token, uint32_t pos, uint32_t slot)
+{
+    if (m->ring == kRing) {
+        QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
+        m->ring = 0;
+    }
+    qgm::Step *s = m->h_steps + m->ring++;
+    *s = qgm::Step{token, pos, slot, 0};
+    QGM_HIP(m, hipMemcpyAsync(m->d_step, s, sizeof(qgm::Step), hipMemcpyHostToDevice, m->ctx->stream));
+    return QG_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -393,12 +762,41 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
     m->q_dim = c.n_heads * hd;
     m->kv_dim = n_kv * hd;
     m->n_rep = c.n_heads / n_kv;
+    // attention layout: workgroups of grp query heads (a divisor of n_rep, at
+    // most 8) times up to 64 position ranges of at least 8 positions, about
+    // 256 workgroups in all at long sequences
+    constexpr size_t kLdsMax = 65536;
+    if (hd == 64 || hd == 128 || hd == 256) {
+        uint32_t grp = 1;
+        for (uint32_t d = 1; d <= qgm::kMaxGroup; d++)
+            if (m->n_rep % d == 0) grp = d;
+        const uint32_t groups = c.n_heads / grp;
+        uint32_t ns = (256 + groups - 1) / groups;
+        ns = ns < 1 ? 1 : ns > qgm::kMaxSplit ? qgm::kMaxSplit : ns;
+        const uint32_t lmax = qgm::range_len(c.max_seq_len, ns);
+        const size_t lds = ((size_t)grp * lmax + 4ull * grp * hd) * sizeof(float);
+        if (lds > kLdsMax) {
+            delete m;
+            return qg_fail(ctx, QG_ERR_SHAPE, "max_seq_len too large for the attention kernel");
+        }
+        m->att_grp = grp;
+        m->att_nsplit = ns;
+        m->att_lmax = lmax;
+        m->att_lds = lds;
+    } else {
+        m->att_lds = ((size_t)hd + c.max_seq_len) * sizeof(float);
+        if (m->att_lds > kLdsMax) {
+            delete m;
+            return qg_fail(ctx, QG_ERR_SHAPE, "max_seq_len too large for this head_dim");
+        }
+    }
     const size_t L = c.n_layers, E = c.embed_dim, H = c.hidden_dim;
     for (int s = 0; s < kSlots; s++) { m->w[s].assign(L, nullptr); m->owned[s].assign(L, false); }
     int rc;
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) { free_model(m); return qg_fail(ctx, QG_ERR_HIP, "hipSetDevice", e); }
     const size_t kvn = L * (size_t)c.max_seq_len * m->kv_dim;
+    const size_t npart = m->att_grp ? (size_t)c.n_heads * m->att_nsplit : 1;
     if ((rc = dalloc(m, &m->final_norm, E)) || (rc = dalloc(m, &m->kc, kvn)) ||
         (rc = dalloc(m, &m->vc, kvn)) || (rc = dalloc(m, &m->h0, E)) || (rc = dalloc(m, &m->h1, E)) ||
         (rc = dalloc(m, &m->xn, E > H ? E : H)) || (rc = dalloc(m, &m->q, m->q_dim)) ||
@@ -406,8 +804,11 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
         (rc = dalloc(m, &m->ao, m->q_dim)) || (rc = dalloc(m, &m->ao2, E)) ||
         (rc = dalloc(m, &m->g, H)) || (rc = dalloc(m, &m->u, H)) || (rc = dalloc(m, &m->hb, H)) ||
         (rc = dalloc(m, &m->fo, E)) || (rc = dalloc(m, &m->logits, c.vocab_size)) ||
-        (rc = dalloc(m, &m->zeros, E > H ? E : H)) ||
-        (rc = dalloc(m, &m->d_recent, kRecentMax)) || (rc = dalloc(m, &m->d_token, 1))) {
+        (rc = dalloc(m, &m->zeros, E > H ? E : H)) || (rc = dalloc(m, &m->att_part, npart * hd)) ||
+        (rc = dalloc(m, &m->att_ml, npart * 2)) || (rc = dalloc(m, &m->s_pv, qgm::kSampleWG)) ||
+        (rc = dalloc(m, &m->s_pi, qgm::kSampleWG)) || (rc = dalloc(m, &m->d_recent, qgm::kRecentMax)) ||
+        (rc = dalloc(m, &m->d_token, 1)) || (rc = dalloc(m, &m->d_hist, (size_t)c.max_seq_len + 1)) ||
+        (rc = dalloc(m, &m->d_step, 1))) {
         free_model(m);
         return rc;
     }
@@ -431,8 +832,10 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
     if ((rc = dalloc(m, &m->cos_t, np)) || (rc = dalloc(m, &m->sin_t, np))) { free_model(m); return rc; }
     if ((e = hipMemcpy(m->cos_t, ct.data(), np * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess ||
         (e = hipMemcpy(m->sin_t, st.data(), np * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess ||
-        (e = hipHostMalloc((void **)&m->h_recent, kRecentMax * sizeof(uint32_t), hipHostMallocDefault)) != hipSuccess ||
-        (e = hipHostMalloc((void **)&m->h_token, sizeof(uint32_t), hipHostMallocDefault)) != hipSuccess) {
+        (e = hipHostMalloc((void **)&m->h_recent, qgm::kRecentMax * sizeof(uint32_t), hipHostMallocDefault)) !=
+            hipSuccess ||
+        (e = hipHostMalloc((void **)&m->h_token, sizeof(uint32_t), hipHostMallocDefault)) != hipSuccess ||
+        (e = hipHostMalloc((void **)&m->h_steps, kRing * sizeof(qgm::Step), hipHostMallocDefault)) != hipSuccess) {
         free_model(m);
         return qg_fail(ctx, QG_ERR_HIP, "model set-up", e);
     }
@@ -463,6 +866,8 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
     qg_mat *mat = nullptr;
     int rc = qg_upload(m->ctx, raw, nbytes, ggml_type, rows, cols, &mat);
     if (rc) return rc;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    drop_graphs(m);
     qg_mat **dst;
     bool *own;
     if (which == QG_M_TOKEN_EMBD) { dst = &m->tok; own = &m->tok_owned; }
@@ -488,6 +893,10 @@ int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_
     if (er == 0) return mfail(m, QG_ERR_INVALID_ARG, "matrix slot");
     if (mat->rows != er || mat->cols != ec || mat->ctx != m->ctx)
         return mfail(m, QG_ERR_SHAPE, "matrix shape does not match the config");
+    const bool per_layer = which >= QG_M_WQ;
+    if (per_layer && layer >= m->cfg.n_layers) return mfail(m, QG_ERR_INVALID_ARG, "layer");
+    (void)hipStreamSynchronize(m->ctx->stream);
+    drop_graphs(m);
     qg_mat *mm = const_cast<qg_mat *>(mat);
     if (which == QG_M_TOKEN_EMBD) {
         if (m->tok && m->tok_owned) qg_mat_free(m->ctx, m->tok);
@@ -496,7 +905,6 @@ int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_
         if (m->lm && m->lm_owned) qg_mat_free(m->ctx, m->lm);
         m->lm = mm; m->lm_owned = false;
     } else {
-        if (layer >= m->cfg.n_layers) return mfail(m, QG_ERR_INVALID_ARG, "layer");
         const int s = (int)which - QG_M_WQ;
         if (m->w[s][layer] && m->owned[s][layer]) qg_mat_free(m->ctx, m->w[s][layer]);
         m->w[s][layer] = mm;
@@ -520,7 +928,15 @@ int qg_model_set_vector(qg_model *m, uint32_t which, uint32_t layer, const float
     }
     if (n != want) return mfail(m, QG_ERR_SHAPE, "vector length does not match the config");
     QGM_HIP(m, hipSetDevice(m->ctx->device));
+    QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
     QGM_HIP(m, hipMemcpy(dst, v, n * sizeof(float), hipMemcpyHostToDevice));
+    return QG_OK;
+}
+
+int qg_model_use_graphs(qg_model *m, int enable)
+{
+    if (!m) return QG_ERR_INVALID_ARG;
+    m->use_graphs = enable != 0;
     return QG_OK;
 }
 
@@ -547,63 +963,13 @@ int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits)
     if (m->seq >= c.max_seq_len || pos >= c.max_seq_len)
         return mfail(m, QG_ERR_SHAPE, "KV cache full (max_seq_len)");   // kv_cache.rs:54-59
     QGM_HIP(m, hipSetDevice(m->ctx->device));
-    hipStream_t st = m->ctx->stream;
-    ihipStream_t *sti = (ihipStream_t *)st;
-    const uint32_t E = c.embed_dim, H = c.hidden_dim;
     int rc;
-    // embedding row into a zeroed buffer (transformer.rs:74-75, quant.rs:152-174)
-    if (qg::launch_fill(m->h0, E, 0.0f, sti) || qg::launch_dequantize_row(m->tok->type, m->tok->d, m->tok->rows,
-                                                                           m->tok->cols, token, m->h0, sti))
-        return mfail(m, QG_ERR_HIP, "embedding", hipGetLastError());
-    const uint32_t slot = (uint32_t)m->seq;
-    const size_t kv_layer = (size_t)c.max_seq_len * m->kv_dim;
-    const float scale = 1.0f / sqrtf((float)m->hd);                      // attention.rs:99
-    const size_t att_lds = (m->hd + slot + 1) * sizeof(float);
-    for (uint32_t l = 0; l < c.n_layers; l++) {
-        // the residual stream entering the layer is h0 (layer 0: the
-        // embedding) or h1 + fo, which the Q GEMV also stores to h0
-        const float *na = l == 0 ? m->h0 : m->h1, *nb = l == 0 ? m->zeros : m->fo;
-        const float *anorm = m->vec[QG_V_ATTN_NORM][l];
-        if ((rc = gemv_norm(m, m->w[QG_M_WQ - 2][l], na, nb, anorm, l == 0 ? nullptr : m->h0, m->q)) ||
-            (rc = gemv_norm(m, m->w[QG_M_WK - 2][l], na, nb, anorm, nullptr, m->k)) ||
-            (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
-            return rc;
-        float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
-        const uint32_t pairs = (m->q_dim > m->kv_dim ? m->q_dim : m->kv_dim) / 2;
-        hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
-                           m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
-                           m->sin_t, m->q_dim, m->kv_dim, m->hd, pos, slot);
-        const size_t wlds = (slot + 1 + 4 * (size_t)m->hd) * sizeof(float);
-        if (m->hd == 64)
-            hipLaunchKernelGGL(qgm::attention_wave_k<1>, dim3(c.n_heads), dim3(256), wlds, st, m->q, kc, vc,
-                               m->ao, slot + 1, m->kv_dim, m->n_rep, scale);
-        else if (m->hd == 128)
-            hipLaunchKernelGGL(qgm::attention_wave_k<2>, dim3(c.n_heads), dim3(256), wlds, st, m->q, kc, vc,
-                               m->ao, slot + 1, m->kv_dim, m->n_rep, scale);
-        else if (m->hd == 256)
-            hipLaunchKernelGGL(qgm::attention_wave_k<4>, dim3(c.n_heads), dim3(256), wlds, st, m->q, kc, vc,
-                               m->ao, slot + 1, m->kv_dim, m->n_rep, scale);
-        else
-            hipLaunchKernelGGL(qgm::attention_k, dim3(c.n_heads), dim3(256), att_lds, st, m->q, kc, vc, m->ao,
-                               slot + 1, m->hd, m->kv_dim, m->n_rep, scale);
-        if ((rc = launched(m, "attention"))) return rc;
-        if ((rc = gemv(m, m->w[QG_M_WO - 2][l], m->ao, m->ao2))) return rc;
-        // h1 = h0 + attention output (stored by the gate GEMV); MLP input = ffn_norm(h1)
-        const float *fnorm = m->vec[QG_V_FFN_NORM][l];
-        if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
-            (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u)))
-            return rc;
-        hipLaunchKernelGGL(qgm::silu_mul_k, dim3((H + 255) / 256), dim3(256), 0, st, m->g, m->u, m->hb, H);
-        if ((rc = launched(m, "silu*up"))) return rc;
-        if ((rc = gemv(m, m->w[QG_M_DOWN - 2][l], m->hb, m->fo))) return rc;
-    }
-    // final norm of h1 + fo (transformer.rs:87-97) inside the lm_head GEMV
-    if ((rc = gemv_norm(m, m->lm, m->h1, m->fo, m->final_norm, nullptr, m->logits))) return rc;
+    if ((rc = put_step(m, token, pos, (uint32_t)m->seq)) || (rc = run_forward(m))) return rc;
     m->seq += 1;
     if (logits) {
         QGM_HIP(m, hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float),
-                                  hipMemcpyDeviceToHost, st));
-        QGM_HIP(m, hipStreamSynchronize(st));
+                                  hipMemcpyDeviceToHost, m->ctx->stream));
+        QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
     }
     return QG_OK;
 }
@@ -615,17 +981,16 @@ int qg_model_sample_greedy(qg_model *m, const uint32_t *recent, size_t n_recent,
     // sampler.rs:109-116: the last `window` of the recent tokens
     size_t start = n_recent > window ? n_recent - window : 0;
     size_t n = n_recent - start;
-    if (n > kRecentMax) { start += n - kRecentMax; n = kRecentMax; }
+    if (n > qgm::kRecentMax) { start += n - qgm::kRecentMax; n = qgm::kRecentMax; }
     hipStream_t st = m->ctx->stream;
     QGM_HIP(m, hipSetDevice(m->ctx->device));
     if (n) {
+        QGM_HIP(m, hipStreamSynchronize(st));                 // h_recent is reused
         std::memcpy(m->h_recent, recent + start, n * sizeof(uint32_t));
         QGM_HIP(m, hipMemcpyAsync(m->d_recent, m->h_recent, n * sizeof(uint32_t), hipMemcpyHostToDevice, st));
     }
     // sampler.rs:76-78: no penalty pass without recent tokens or with penalty 1
-    hipLaunchKernelGGL(qgm::sample_greedy_k, dim3(1), dim3(qgm::kBlock), 0, st, m->logits, m->cfg.vocab_size,
-                       m->d_recent, (uint32_t)n, n ? penalty : 1.0f, m->d_token);
-    int rc = launched(m, "sample");
+    int rc = enqueue_sample(m, sample_args(m, (uint32_t)n, n ? penalty : 1.0f, false, 0));
     if (rc) return rc;
     QGM_HIP(m, hipMemcpyAsync(m->h_token, m->d_token, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     QGM_HIP(m, hipStreamSynchronize(st));
@@ -638,27 +1003,39 @@ int qg_model_generate(qg_model *m, const uint32_t *prompt, size_t n_prompt, size
 {
     if (!m || (n_prompt && !prompt) || (n_new && !out_tokens)) return QG_ERR_INVALID_ARG;
     if (n_prompt == 0 && n_new > 0) return mfail(m, QG_ERR_INVALID_ARG, "generation needs a prompt");
+    if (!complete(m)) return mfail(m, QG_ERR_INVALID_ARG, "model matrices / final norm not all set");
+    const qg_model_config &c = m->cfg;
+    if (n_prompt + n_new > c.max_seq_len) return mfail(m, QG_ERR_SHAPE, "KV cache full (max_seq_len)");
+    for (size_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= c.vocab_size) return mfail(m, QG_ERR_SHAPE, "token id >= vocab_size");
     using clk = std::chrono::steady_clock;
-    std::vector<uint32_t> all(prompt, prompt + n_prompt);
+    hipStream_t st = m->ctx->stream;
+    QGM_HIP(m, hipSetDevice(m->ctx->device));
+    QGM_HIP(m, hipStreamSynchronize(st));
     m->seq = 0;                                                     // fresh caches (model.rs:341-346)
-    auto t0 = clk::now();
+    if (n_prompt == 0) return QG_OK;
+    QGM_HIP(m, hipMemcpy(m->d_hist, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice));
+    // model.rs:370-374 passes the last 64 tokens; the sampler keeps `window` of them
+    const uint32_t win = window > qgm::kRecentMax ? qgm::kRecentMax : (uint32_t)window;
     int rc;
-    for (size_t p = 0; p < n_prompt; p++)
-        if ((rc = qg_model_forward(m, prompt[p], (uint32_t)p, nullptr))) return rc;
-    QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
-    auto t1 = clk::now();
-    size_t pos = n_prompt;
-    for (size_t s = 0; s < n_new; s++) {
-        const size_t nr = all.size() > kRecentMax ? kRecentMax : all.size();   // model.rs:370-374
-        uint32_t tok;
-        if ((rc = qg_model_sample_greedy(m, all.data() + all.size() - nr, nr, penalty, window, &tok))) return rc;
-        out_tokens[s] = tok;
-        if ((rc = qg_model_forward(m, tok, (uint32_t)pos, nullptr))) return rc;
-        all.push_back(tok);
-        pos++;
+    auto t0 = clk::now();
+    if ((rc = put_step(m, prompt[0], 0, 0))) return rc;
+    for (size_t p = 0; p < n_prompt; p++) {
+        if ((rc = run_forward(m))) return rc;
+        if (p + 1 < n_prompt) {
+            hipLaunchKernelGGL(qgm::advance_k, dim3(1), dim3(64), 0, st, m->d_step, m->d_hist);
+            if ((rc = launched(m, "advance"))) return rc;
+        }
     }
-    QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
+    QGM_HIP(m, hipStreamSynchronize(st));
+    auto t1 = clk::now();
+    for (size_t s = 0; s < n_new; s++)
+        if ((rc = run_decode(m, penalty, win))) return rc;
+    QGM_HIP(m, hipStreamSynchronize(st));
     auto t2 = clk::now();
+    m->seq = n_prompt + n_new;
+    if (n_new)
+        QGM_HIP(m, hipMemcpy(out_tokens, m->d_hist + n_prompt, n_new * sizeof(uint32_t), hipMemcpyDeviceToHost));
     if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
     if (decode_s) *decode_s = std::chrono::duration<double>(t2 - t1).count();
     return QG_OK;

@@ -170,13 +170,19 @@ __global__ void __launch_bounds__(256) dequant_k(const uint8_t *__restrict__ w, 
         out[f] = elem<T>(w + (f / BS) * BB, (uint32_t)(f % BS));
 }
 
-// quant.rs:152-174: writes only the positions the reference writes.
+// quant.rs:152-174: writes only the positions the reference writes.  The
+// row is `row`, or *d_row when d_row is not NULL (a row index that lives in
+// device memory, e.g. the token id of a decode step); rows past the end write
+// nothing.
 template <uint32_t T>
 __global__ void __launch_bounds__(256) deq_row_k(const uint8_t *__restrict__ w, uint64_t rows,
-                                                 uint64_t cols, uint64_t row,
+                                                 uint64_t cols, uint64_t row_arg,
+                                                 const uint32_t *__restrict__ d_row,
                                                  float *__restrict__ out)
 {
     constexpr uint64_t BS = block_elems(T), BB = block_bytes(T);
+    const uint64_t row = d_row ? (uint64_t)*d_row : row_arg;
+    if (row >= rows) return;
     const uint64_t nbpr = (cols + BS - 1) / BS;
     const uint64_t start_block = row * cols / BS, col_off = row * cols % BS;
     const uint64_t total = rows * cols;
@@ -1361,32 +1367,44 @@ int launch_dequant(uint32_t type, const uint8_t *w, size_t n, float *out, ihipSt
 }
 
 template <uint32_t T>
-static int launch_deq_row_t(const uint8_t *w, size_t rows, size_t cols, size_t row, float *out,
-                            hipStream_t st)
+static int launch_deq_row_t(const uint8_t *w, size_t rows, size_t cols, size_t row, const uint32_t *d_row,
+                            float *out, hipStream_t st)
 {
     const uint64_t bs = block_elems(T);
     const uint64_t n = (cols + bs - 1) / bs * bs;
     hipLaunchKernelGGL((deq_row_k<T>), dim3(grid_for(n)), dim3(256), 0, st, w, (uint64_t)rows,
-                       (uint64_t)cols, (uint64_t)row, out);
+                       (uint64_t)cols, (uint64_t)row, d_row, out);
     return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+static int launch_dequantize_row_any(uint32_t type, const uint8_t *w, size_t rows, size_t cols, size_t row,
+                              const uint32_t *d_row, float *out, ihipStream_t *stream)
+{
+    hipStream_t st = (hipStream_t)stream;
+    if (cols == 0) return 0;
+    switch (type) {
+    case T_F32: return launch_deq_row_t<T_F32>(w, rows, cols, row, d_row, out, st);
+    case T_F16: return launch_deq_row_t<T_F16>(w, rows, cols, row, d_row, out, st);
+    case T_Q4_0: return launch_deq_row_t<T_Q4_0>(w, rows, cols, row, d_row, out, st);
+    case T_Q5_0: return launch_deq_row_t<T_Q5_0>(w, rows, cols, row, d_row, out, st);
+    case T_Q8_0: return launch_deq_row_t<T_Q8_0>(w, rows, cols, row, d_row, out, st);
+    case T_Q4_K: return launch_deq_row_t<T_Q4_K>(w, rows, cols, row, d_row, out, st);
+    case T_Q5_K: return launch_deq_row_t<T_Q5_K>(w, rows, cols, row, d_row, out, st);
+    case T_Q6_K: return launch_deq_row_t<T_Q6_K>(w, rows, cols, row, d_row, out, st);
+    default: return -1;
+    }
 }
 
 int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t cols, size_t row,
                           float *out, ihipStream_t *stream)
 {
-    hipStream_t st = (hipStream_t)stream;
-    if (cols == 0) return 0;
-    switch (type) {
-    case T_F32: return launch_deq_row_t<T_F32>(w, rows, cols, row, out, st);
-    case T_F16: return launch_deq_row_t<T_F16>(w, rows, cols, row, out, st);
-    case T_Q4_0: return launch_deq_row_t<T_Q4_0>(w, rows, cols, row, out, st);
-    case T_Q5_0: return launch_deq_row_t<T_Q5_0>(w, rows, cols, row, out, st);
-    case T_Q8_0: return launch_deq_row_t<T_Q8_0>(w, rows, cols, row, out, st);
-    case T_Q4_K: return launch_deq_row_t<T_Q4_K>(w, rows, cols, row, out, st);
-    case T_Q5_K: return launch_deq_row_t<T_Q5_K>(w, rows, cols, row, out, st);
-    case T_Q6_K: return launch_deq_row_t<T_Q6_K>(w, rows, cols, row, out, st);
-    default: return -1;
-    }
+    return launch_dequantize_row_any(type, w, rows, cols, row, nullptr, out, stream);
+}
+
+int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
+                              float *out, ihipStream_t *stream)
+{
+    return launch_dequantize_row_any(type, w, rows, cols, 0, d_row, out, stream);
 }
 
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream)

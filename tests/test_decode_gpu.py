@@ -113,6 +113,70 @@ def test_head_dim_96_general_attention(rinf, synth, oracle, ctx):
     dev.close()
 
 
+@pytest.mark.parametrize("embed,heads,kv", [(512, 4, 2), (512, 2, 1), (448, 7, 1)],
+                         ids=["hd128", "hd256", "hd64-rep7"])
+def test_head_layouts(rinf, synth, oracle, ctx, embed, heads, kv):
+    """Split attention for head_dim 64 / 128 / 256 and 7 query heads per kv head."""
+    cfg = dict(SMALL, embed_dim=embed, n_heads=heads, n_kv_heads=kv, hidden_dim=2 * embed)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q8_0", 17, 32)
+    prompt = np.random.default_rng(8).integers(0, cfg["vocab_size"], 9)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 12)
+    print(f"{embed}/{heads}/{kv}: max logits err {max(errs):.2e}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    dev.close()
+
+
+def test_long_sequence(rinf, synth, oracle, ctx):
+    """~100 cached positions: every attention range holds several of them."""
+    cfg = dict(SMALL, n_layers=1)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", 19, 512)
+    prompt = np.random.default_rng(9).integers(0, cfg["vocab_size"], 90)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 12)
+    print(f"long: max logits err {max(errs):.2e}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    dev.close()
+
+
+def test_graph_replay_matches_eager(rinf, synth, oracle, ctx):
+    """Graph replays give the logits of one-launch-per-kernel execution, bit for
+    bit, with other GPU work and synchronisations between the replays."""
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, "q4_k_m", 21, 40)
+    raw = synth.gen_blocks(12, 64, 256, 3)
+    other = ctx.upload(raw, 12, 64, 256)
+    x = synth.gen_x(256, 3)
+    y = np.zeros(64, np.float32)
+    toks = np.random.default_rng(10).integers(0, SMALL["vocab_size"], 10)
+    runs = []
+    for graphs in (False, True):
+        dev.use_graphs(graphs)
+        dev.reset()
+        steps = []
+        for p, t in enumerate(toks):
+            lg = np.zeros(SMALL["vocab_size"], np.float32)
+            dev.forward(int(t), p, lg)
+            other.matvec_host(x, y)                 # eager work between replays
+            steps.append(lg)
+        runs.append(steps)
+    for a, b in zip(*runs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    other.free()
+    dev.close()
+
+
+def test_generate_graph_and_eager(rinf, synth, oracle, ctx):
+    """generate's on-device sample + forward loop: same tokens with and without graphs."""
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, "q5_k", 23, 40)
+    prompt = np.random.default_rng(11).integers(0, SMALL["vocab_size"], 7)
+    dev.use_graphs(False)
+    eager, _, _ = dev.generate(prompt, 14)
+    dev.use_graphs(True)
+    graph, _, _ = dev.generate(prompt, 14)
+    again, _, _ = dev.generate(prompt, 14)
+    assert list(eager) == list(graph) == list(again)
+    assert dev.seq_len == 21
+    dev.close()
+
+
 def test_generate_matches_stepwise(rinf, synth, oracle, ctx):
     """qg_model_generate (Model::generate's loop) gives the tokens of the
     step-by-step run and of the reference sampler."""
