@@ -92,6 +92,16 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
 int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const float *d_xb,
                        const float *d_nw, float eps, float *d_sum_out, float *d_y, void *stream);
 
+/* The MLP's down projection input formed and consumed in one pass:
+ * y = W · (silu(g) * u) (src/mlp.rs:36-45, silu as src/math.rs:137-146, then
+ * src/quant.rs:178-206).  g, u: cols floats; y: rows floats; device pointers,
+ * asynchronous on `stream`.  With 16-byte aligned g and u and a stream-kernel
+ * matrix the product is formed inside the mat-vec kernel; otherwise a
+ * separate kernel writes the context's scratch vector first (calls on one
+ * context must then not overlap on different streams). */
+int qg_matvec_silu_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_g, const float *d_u, float *d_y,
+                       void *stream);
+
 /* Host-buffer drop-in for QuantizedMatrix::mat_vec_mul(x, out, Some(gpu))
  * (src/quant.rs:178-186): synchronous; stages x/y through pinned buffers
  * allocated once per context.  x: cols floats, y: rows floats. */

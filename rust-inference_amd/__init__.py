@@ -75,6 +75,7 @@ _SIGS = {
     "qg_mat_kernel_kind": (ctypes.c_int, [_P]),
     "qg_matvec_dev": (ctypes.c_int, [_P, _P, _P, _P, _P]),
     "qg_matvec_norm_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
+    "qg_matvec_silu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, _P]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
     "qg_gpu_mat_vec_mul": (ctypes.c_int, [_P, _P, _SZ, _U32, _P, _P, _SZ, _SZ]),
     "qg_dequant_dev": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -248,6 +249,12 @@ class DeviceMatrix:
                                              _ptr(d_sum_out) if d_sum_out is not None else None,
                                              _ptr(d_y), ctypes.c_void_p(stream) if stream else None)
         self.ctx.check(rc, "qg_matvec_norm_dev")
+
+    def matvec_silu_dev(self, d_g, d_u, d_y, stream=None):
+        """y = W · (silu(g) * u); torch device tensors (float32)."""
+        rc = self.ctx.lib.qg_matvec_silu_dev(self.ctx.h, self.h, _ptr(d_g), _ptr(d_u), _ptr(d_y),
+                                             ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_matvec_silu_dev")
 
     def matvec_host(self, x, y):
         self.ctx.check(self.ctx.lib.qg_matvec_host(self.ctx.h, self.h, _ptr(x), _ptr(y)),

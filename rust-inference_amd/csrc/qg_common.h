@@ -58,6 +58,7 @@ struct Plan {
     uint32_t lds;          // dynamic LDS bytes
     const void *fn;        // kernel chosen for this matrix
     const void *fn_norm;   // the same kernel with the fused RMSNorm input
+    const void *fn_silu;   // the same kernel with the silu(g) * u input
 };
 
 }  // namespace qg
@@ -74,6 +75,10 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
 int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
                      const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
                      float *y, ihipStream_t *stream);
+// y = W · (silu(g) * u) with the stream kernel (kind 1 plans only; -1
+// otherwise).  g, u: cols floats, 16-byte aligned.
+int launch_gemv_silu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                     const float *g, const float *u, float *y, ihipStream_t *stream);
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                         const float *x, float *y, ihipStream_t *stream);
 int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,
@@ -84,6 +89,8 @@ int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t c
 int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
                               float *out, ihipStream_t *stream);
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
+// out = silu(g) * u elementwise
+int launch_silu_mul(const float *g, const float *u, float *out, size_t n, ihipStream_t *stream);
 // out = rmsnorm(a (+ b)) * w in one workgroup; sum_out (may be NULL) = a + b.
 int launch_rmsnorm(const float *a, const float *b, float *sum_out, const float *w, float *out, size_t n,
                    float eps, ihipStream_t *stream);

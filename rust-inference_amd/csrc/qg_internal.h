@@ -52,5 +52,15 @@ void qg_models_free_all(qg_ctx *ctx);
 int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float *xb, const float *nw,
                    float eps, float *sum_out, float *y, float *scratch, hipStream_t stream);
 
+// y = W · (silu(g) * u): the product inside the stream kernel's prologue, or
+// a separate kernel into `scratch` (cols floats) when that does not apply.
+int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *u, float *y, float *scratch,
+                   hipStream_t stream);
+
+// One owned matrix whose rows are the rows of parts[0], parts[1], ... (same
+// type and cols; every part but the last a whole number of blocks): device
+// copies of the parts' blocks, one after the other.  Synchronous.
+int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out);
+
 // Records `what` (and the HIP error text) as the context's last error; returns `status`.
 int qg_fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess);

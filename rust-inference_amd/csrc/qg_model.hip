@@ -21,7 +21,8 @@
 //   attn_combine_k   query heads of one kv head; then the ranges' partial
 //                    softmax sums are merged (math.rs:104-118 rescaled)
 //   attention_k      the same in one workgroup per head (head_dim % 64 != 0)
-//   silu_mul_k       mlp.rs:36-41, silu as math.rs:137-146
+//   SiLU * up        mlp.rs:36-43, silu as math.rs:137-146, inside the down
+//                    GEMV (a separate kernel where that does not apply)
 //   sample_part_k    sampler.rs:109-127 then math.rs:328-339 over one range
 //   sample_final_k   of the logits per workgroup; then the first maximum
 #include <hip/hip_runtime.h>
@@ -321,23 +322,6 @@ __global__ void __launch_bounds__(256) attention_k(const float *__restrict__ q, 
     }
 }
 
-__device__ __forceinline__ float silu1(float x)
-{
-    if (x >= 0.0f) {
-        const float e = expf(-x);
-        return x / (1.0f + e);
-    }
-    const float e = expf(x);
-    return x * e / (1.0f + e);
-}
-
-__global__ void __launch_bounds__(256) silu_mul_k(const float *__restrict__ g, const float *__restrict__ u,
-                                                  float *__restrict__ h, uint32_t n)
-{
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) h[i] = silu1(g[i]) * u[i];
-}
-
 // Greedy sampler.  The recent tokens are either an explicit list (recent,
 // n_recent) or, in generate, the last min(window, 64) entries of the token
 // history hist[0 .. slot + 1).
@@ -475,6 +459,13 @@ struct qg_model {
     float *logits = nullptr;
     float *zeros = nullptr;               // the residual addend of the first layer
     float *att_part = nullptr, *att_ml = nullptr;
+    // per layer: [Q;K;V] (n = 3) or [Q;K] (n = 2) stacked into one matrix
+    // when the parts share a type, and [gate;up]; the outputs q,k,v and g,u
+    // are contiguous, so one mat-vec fills them.  Built before the first
+    // forward pass after any matrix change.
+    std::vector<qg_mat *> f_qkv, f_gu;
+    std::vector<uint8_t> f_qkv_n;
+    bool fused_ready = false;
     float *s_pv = nullptr;
     uint32_t *s_pi = nullptr;
     uint32_t *d_recent = nullptr, *d_token = nullptr, *d_hist = nullptr;
@@ -522,10 +513,46 @@ void drop_graphs(qg_model *m)
     m->g_fwd = m->g_dec = nullptr;
 }
 
+void drop_fused(qg_model *m)
+{
+    for (qg_mat *&p : m->f_qkv) if (p) { qg_mat_free(m->ctx, p); p = nullptr; }
+    for (qg_mat *&p : m->f_gu) if (p) { qg_mat_free(m->ctx, p); p = nullptr; }
+    for (uint8_t &n : m->f_qkv_n) n = 0;
+    m->fused_ready = false;
+}
+
+// parts stack into one matrix: same type and cols, all but the last a whole
+// number of blocks
+bool stackable(qg_mat *const *p, int n)
+{
+    for (int i = 0; i < n; i++) {
+        if (p[i]->type != p[0]->type || p[i]->cols != p[0]->cols) return false;
+        if (i + 1 < n && (p[i]->rows * p[i]->cols) % qg::block_elems(p[i]->type) != 0) return false;
+    }
+    return true;
+}
+
+int prepare(qg_model *m)
+{
+    if (m->fused_ready) return QG_OK;
+    for (uint32_t l = 0; l < m->cfg.n_layers; l++) {
+        qg_mat *qkv[3] = {m->w[QG_M_WQ - 2][l], m->w[QG_M_WK - 2][l], m->w[QG_M_WV - 2][l]};
+        const int n = stackable(qkv, 3) ? 3 : stackable(qkv, 2) ? 2 : 0;
+        int rc;
+        if (n && (rc = qg_stack_mats(m->ctx, qkv, n, &m->f_qkv[l]))) return rc;
+        m->f_qkv_n[l] = (uint8_t)n;
+        qg_mat *gu[2] = {m->w[QG_M_GATE - 2][l], m->w[QG_M_UP - 2][l]};
+        if (stackable(gu, 2) && (rc = qg_stack_mats(m->ctx, gu, 2, &m->f_gu[l]))) return rc;
+    }
+    m->fused_ready = true;
+    return QG_OK;
+}
+
 void free_model(qg_model *m)
 {
     m->ctx->models.erase(m);
     drop_graphs(m);
+    drop_fused(m);
     for (int s = 0; s < kSlots; s++)
         for (size_t l = 0; l < m->w[s].size(); l++)
             if (m->w[s][l] && m->owned[s][l]) qg_mat_free(m->ctx, m->w[s][l]);
@@ -592,7 +619,7 @@ int enqueue_forward(qg_model *m)
     const qg_model_config &c = m->cfg;
     hipStream_t st = m->ctx->stream;
     ihipStream_t *sti = (ihipStream_t *)st;
-    const uint32_t E = c.embed_dim, H = c.hidden_dim;
+    const uint32_t E = c.embed_dim;
     int rc;
     // embedding row into a zeroed buffer (transformer.rs:74-75, quant.rs:152-174)
     if (qg::launch_fill(m->h0, E, 0.0f, sti) ||
@@ -607,10 +634,19 @@ int enqueue_forward(qg_model *m)
         // embedding) or h1 + fo, which the Q GEMV also stores to h0
         const float *na = l == 0 ? m->h0 : m->h1, *nb = l == 0 ? m->zeros : m->fo;
         const float *anorm = m->vec[QG_V_ATTN_NORM][l];
-        if ((rc = gemv_norm(m, m->w[QG_M_WQ - 2][l], na, nb, anorm, l == 0 ? nullptr : m->h0, m->q)) ||
-            (rc = gemv_norm(m, m->w[QG_M_WK - 2][l], na, nb, anorm, nullptr, m->k)) ||
-            (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
+        float *res = l == 0 ? nullptr : m->h0;
+        const int nq = m->f_qkv_n[l];
+        if (nq == 3) {
+            if ((rc = gemv_norm(m, m->f_qkv[l], na, nb, anorm, res, m->q))) return rc;
+        } else if (nq == 2) {
+            if ((rc = gemv_norm(m, m->f_qkv[l], na, nb, anorm, res, m->q)) ||
+                (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
+                return rc;
+        } else if ((rc = gemv_norm(m, m->w[QG_M_WQ - 2][l], na, nb, anorm, res, m->q)) ||
+                   (rc = gemv_norm(m, m->w[QG_M_WK - 2][l], na, nb, anorm, nullptr, m->k)) ||
+                   (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v))) {
             return rc;
+        }
         float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
         hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
                            m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
@@ -639,12 +675,14 @@ int enqueue_forward(qg_model *m)
         if ((rc = gemv(m, m->w[QG_M_WO - 2][l], m->ao, m->ao2))) return rc;
         // h1 = h0 + attention output (stored by the gate GEMV); MLP input = ffn_norm(h1)
         const float *fnorm = m->vec[QG_V_FFN_NORM][l];
-        if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
-            (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u)))
+        if (m->f_gu[l]) {
+            if ((rc = gemv_norm(m, m->f_gu[l], m->h0, m->ao2, fnorm, m->h1, m->g))) return rc;
+        } else if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
+                   (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u))) {
             return rc;
-        hipLaunchKernelGGL(qgm::silu_mul_k, dim3((H + 255) / 256), dim3(256), 0, st, m->g, m->u, m->hb, H);
-        if ((rc = launched(m, "silu*up"))) return rc;
-        if ((rc = gemv(m, m->w[QG_M_DOWN - 2][l], m->hb, m->fo))) return rc;
+        }
+        // down(silu(g) * u) (mlp.rs:36-45): the product inside the down GEMV's prologue
+        if ((rc = qg_silu_matvec(m->ctx, m->w[QG_M_DOWN - 2][l], m->g, m->u, m->fo, m->hb, st))) return rc;
     }
     // final norm of h1 + fo (transformer.rs:87-97) inside the lm_head GEMV
     return gemv_norm(m, m->lm, m->h1, m->fo, m->final_norm, nullptr, m->logits);
@@ -703,8 +741,9 @@ int capture(qg_model *m, int (*fn)(qg_model *), hipGraphExec_t *out)
 
 int run_forward(qg_model *m)
 {
-    if (!m->use_graphs) return enqueue_forward(m);
     int rc;
+    if ((rc = prepare(m))) return rc;
+    if (!m->use_graphs) return enqueue_forward(m);
     if (!m->g_fwd && (rc = capture(m, enqueue_forward, &m->g_fwd))) return rc;
     QGM_HIP(m, hipGraphLaunch(m->g_fwd, m->ctx->stream));
     return QG_OK;
@@ -718,8 +757,9 @@ int run_decode(qg_model *m, float penalty, uint32_t window)
     }
     m->g_dec_penalty = penalty;
     m->g_dec_window = window;
-    if (!m->use_graphs) return enqueue_decode(m);
     int rc;
+    if ((rc = prepare(m))) return rc;
+    if (!m->use_graphs) return enqueue_decode(m);
     if (!m->g_dec && (rc = capture(m, enqueue_decode, &m->g_dec))) return rc;
     QGM_HIP(m, hipGraphLaunch(m->g_dec, m->ctx->stream));
     return QG_OK;
@@ -799,10 +839,9 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
     const size_t npart = m->att_grp ? (size_t)c.n_heads * m->att_nsplit : 1;
     if ((rc = dalloc(m, &m->final_norm, E)) || (rc = dalloc(m, &m->kc, kvn)) ||
         (rc = dalloc(m, &m->vc, kvn)) || (rc = dalloc(m, &m->h0, E)) || (rc = dalloc(m, &m->h1, E)) ||
-        (rc = dalloc(m, &m->xn, E > H ? E : H)) || (rc = dalloc(m, &m->q, m->q_dim)) ||
-        (rc = dalloc(m, &m->k, m->kv_dim)) || (rc = dalloc(m, &m->v, m->kv_dim)) ||
+        (rc = dalloc(m, &m->xn, E > H ? E : H)) || (rc = dalloc(m, &m->q, m->q_dim + 2 * (size_t)m->kv_dim)) ||
         (rc = dalloc(m, &m->ao, m->q_dim)) || (rc = dalloc(m, &m->ao2, E)) ||
-        (rc = dalloc(m, &m->g, H)) || (rc = dalloc(m, &m->u, H)) || (rc = dalloc(m, &m->hb, H)) ||
+        (rc = dalloc(m, &m->g, 2 * H)) || (rc = dalloc(m, &m->hb, H)) ||
         (rc = dalloc(m, &m->fo, E)) || (rc = dalloc(m, &m->logits, c.vocab_size)) ||
         (rc = dalloc(m, &m->zeros, E > H ? E : H)) || (rc = dalloc(m, &m->att_part, npart * hd)) ||
         (rc = dalloc(m, &m->att_ml, npart * 2)) || (rc = dalloc(m, &m->s_pv, qgm::kSampleWG)) ||
@@ -812,6 +851,12 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
         free_model(m);
         return rc;
     }
+    m->k = m->q + m->q_dim;                 // q, k, v and g, u are contiguous
+    m->v = m->k + m->kv_dim;
+    m->u = m->g + H;
+    m->f_qkv.assign(L, nullptr);
+    m->f_gu.assign(L, nullptr);
+    m->f_qkv_n.assign(L, 0);
     for (int s = 1; s < 6; s++) {
         m->vec[s].assign(L, nullptr);
         const size_t n = s <= 2 ? E : s == 3 ? m->q_dim : m->kv_dim;
@@ -868,6 +913,7 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
     if (rc) return rc;
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
+    drop_fused(m);
     qg_mat **dst;
     bool *own;
     if (which == QG_M_TOKEN_EMBD) { dst = &m->tok; own = &m->tok_owned; }
@@ -897,6 +943,7 @@ int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_
     if (per_layer && layer >= m->cfg.n_layers) return mfail(m, QG_ERR_INVALID_ARG, "layer");
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
+    drop_fused(m);
     qg_mat *mm = const_cast<qg_mat *>(mat);
     if (which == QG_M_TOKEN_EMBD) {
         if (m->tok && m->tok_owned) qg_mat_free(m->ctx, m->tok);

@@ -15,6 +15,7 @@
 #include <set>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "qg_common.h"
 #include "qg_internal.h"
@@ -162,6 +163,70 @@ int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float 
         }
     }
     return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
+}
+
+int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *u, float *y, float *scratch,
+                   hipStream_t st)
+{
+    ihipStream_t *sti = (ihipStream_t *)st;
+    const size_t cols = mat->cols;
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    int lr = -1;
+    if (cols == 0) {                                   // empty x: out.fill(0.0), quant.rs:189
+        lr = qg::launch_fill(y, mat->rows, 0.0f, sti);
+        return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
+    }
+    if (a16(g) && a16(u)) lr = qg::launch_gemv_silu(mat->plan, mat->d, mat->nbytes, mat->rows, cols, g, u, y, sti);
+    if (lr == -1) {
+        lr = qg::launch_silu_mul(g, u, scratch, cols, sti);
+        if (lr == 0) {
+            if (mat->plan.kind == 1 && a16(scratch))
+                lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, cols, scratch, y, sti);
+            else
+                lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, cols, scratch, y, sti);
+        }
+    }
+    return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
+}
+
+int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out)
+{
+    *out = nullptr;
+    if (!ctx || n < 1) return QG_ERR_INVALID_ARG;
+    const uint32_t type = parts[0]->type;
+    const size_t cols = parts[0]->cols;
+    size_t rows = 0, total = 0;
+    std::vector<size_t> need(n);
+    for (int i = 0; i < n; i++) {
+        const qg_mat *p = parts[i];
+        if (p->type != type || p->cols != cols) return fail(ctx, QG_ERR_SHAPE, "stacked parts differ");
+        if (required_bytes(type, p->rows, cols, &need[i]) != QG_OK)
+            return fail(ctx, QG_ERR_SHAPE, "stacked part shape");
+        // every part but the last ends on a block boundary, so the stacked
+        // blocks are the blocks of the stacked matrix
+        if (i + 1 < n && (p->rows * cols) % qg::block_elems(type) != 0)
+            return fail(ctx, QG_ERR_SHAPE, "stacked part does not end on a block");
+        rows += p->rows;
+        total += need[i];
+    }
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    uint8_t *d = nullptr;
+    hipError_t e = hipMalloc((void **)&d, total + qg::kTailPad);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc", e);
+    size_t off = 0;
+    for (int i = 0; i < n && e == hipSuccess; i++) {
+        e = hipMemcpyAsync(d + off, parts[i]->d, need[i], hipMemcpyDeviceToDevice, ctx->stream);
+        off += need[i];
+    }
+    if (e == hipSuccess) e = hipMemsetAsync(d + total, 0, qg::kTailPad, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return fail(ctx, QG_ERR_HIP, "stacking copies", e);
+    }
+    int rc = new_mat(ctx, d, total, type, rows, cols, true, out);
+    if (rc) (void)hipFree(d);
+    return rc;
 }
 
 extern "C" {
@@ -326,6 +391,21 @@ int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const 
     QG_HIP(ctx, hipSetDevice(ctx->device));
     if ((rc = grow_device(ctx, &ctx->d_norm, &ctx->d_norm_cap, n))) return rc;
     return qg_norm_matvec(ctx, mat, d_xa, d_xb, d_nw, eps, d_sum_out, d_y, ctx->d_norm, pick(ctx, stream));
+}
+
+int qg_matvec_silu_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_g, const float *d_u, float *d_y,
+                       void *stream)
+{
+    int rc = check_mat(ctx, mat);
+    if (rc) return rc;
+    if (mat->rows == 0) return QG_OK;
+    const size_t n = mat->cols;
+    if (!d_y || (n > 0 && (!d_g || !d_u))) return fail(ctx, QG_ERR_INVALID_ARG, "g, u or y is NULL");
+    auto a4 = [](const void *p) { return ((uintptr_t)p & 3u) == 0; };
+    if (!a4(d_g) || !a4(d_u) || !a4(d_y)) return fail(ctx, QG_ERR_INVALID_ARG, "vectors not 4-byte aligned");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if ((rc = grow_device(ctx, &ctx->d_norm, &ctx->d_norm_cap, n))) return rc;
+    return qg_silu_matvec(ctx, mat, d_g, d_u, d_y, ctx->d_norm, pick(ctx, stream));
 }
 
 int qg_matvec_host(qg_ctx *ctx, const qg_mat *mat, const float *x, float *y)

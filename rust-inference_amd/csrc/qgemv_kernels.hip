@@ -199,6 +199,19 @@ __global__ void __launch_bounds__(256) deq_row_k(const uint8_t *__restrict__ w, 
     }
 }
 
+constexpr int kProPlain = 0, kProNorm = 1, kProSilu = 2;
+
+// silu(x) = x / (1 + exp(-x)), in the two branches of math.rs:137-146
+__device__ __forceinline__ float silu1(float x)
+{
+    if (x >= 0.0f) {
+        const float e = expf(-x);
+        return x / (1.0f + e);
+    }
+    const float e = expf(x);
+    return x * e / (1.0f + e);
+}
+
 __global__ void fill_k(float *out, uint64_t n, float v)
 {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -234,6 +247,14 @@ __global__ void __launch_bounds__(kNormBlock) rmsnorm_k(const float *__restrict_
         const float x = b ? a[i] + b[i] : a[i];
         out[i] = x * scale * w[i];
     }
+}
+
+// out = silu(g) * u elementwise (mlp.rs:36-43)
+__global__ void __launch_bounds__(256) silu_mul_k(const float *__restrict__ g, const float *__restrict__ u,
+                                                  float *__restrict__ out, uint64_t n)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = silu1(g[i]) * u[i];
 }
 
 // ------------------------------------------------------- generic GEMV
@@ -912,14 +933,19 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 // LDS slots and add them up every `chunk` batches (two workgroup barriers per
 // chunk instead of per batch).
 
-// NORM: the input is rmsnorm(a.x + a.xb) * a.nw (math.rs:237-257, with the
-// residual add of transformer.rs:31-46 folded in): every workgroup loads both
-// addends and the weights, reduces the sum of squares itself and converts the
-// normalised vector; workgroup 0 also stores the residual sum.
+// Input prologues (PRO):
+//   kProNorm: the input is rmsnorm(a.x + a.xb) * a.nw (math.rs:237-257, with
+//             the residual add of transformer.rs:31-46 folded in): every
+//             workgroup loads both addends and the weights, reduces the sum of
+//             squares itself and converts the normalised vector; workgroup 0
+//             also stores the residual sum.
+//   kProSilu: the input is silu(a.x) * a.xb, elementwise (mlp.rs:36-43 with
+//             math.rs:137-146).
 template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
-          bool NORM = false>
+          int PRO = kProPlain>
 __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 {
+    constexpr bool NORM = PRO == kProNorm, TWO = PRO != kProPlain;
     using I = Item<T>;
     constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
     constexpr int RED = G1 ? R : R * 8;
@@ -943,16 +969,14 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     // Every load below is unconditional (clamped addresses): the compiler's
     // wait counting stays exact only when no load sits on a conditional path.
     uint4 xv[XS];
-    uint4 bvv[NORM ? XS : 1], wvv[NORM ? XS : 1];
+    uint4 bvv[TWO ? XS : 1], wvv[NORM ? XS : 1];
     const uint4 *srcb = (const uint4 *)a.xb, *srcw = (const uint4 *)a.nw;
 #pragma unroll
     for (int k = 0; k < XS; k++) {
         const uint32_t j = tid + k * blockDim.x, jc = j < n16 ? j : n16 - 1u;
         xv[k] = src[jc];
-        if constexpr (NORM) {
-            bvv[k] = srcb[jc];
-            wvv[k] = srcw[jc];
-        }
+        if constexpr (TWO) bvv[k] = srcb[jc];
+        if constexpr (NORM) wvv[k] = srcw[jc];
     }
     // x first: issued behind the weight stream of the workgroups that started
     // earlier, x reaches the late ones after most of the matrix; waiting for
@@ -1016,6 +1040,18 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
         }
         for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x)
             put(nrm(addv(src[j], srcb[j]), srcw[j]), j);
+    } else if constexpr (PRO == kProSilu) {
+        auto sm = [](uint4 gq, uint4 uq) {
+            const float4 g = __builtin_bit_cast(float4, gq), u = __builtin_bit_cast(float4, uq);
+            return __builtin_bit_cast(uint4, make_float4(silu1(g.x) * u.x, silu1(g.y) * u.y,
+                                                         silu1(g.z) * u.z, silu1(g.w) * u.w));
+        };
+#pragma unroll
+        for (int k = 0; k < XS; k++) {
+            const uint32_t j = tid + k * blockDim.x;
+            if (j < n16) put(sm(xv[k], bvv[k]), j);
+        }
+        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(sm(src[j], srcb[j]), j);
     } else {
 #pragma unroll
         for (int k = 0; k < XS; k++) {
@@ -1156,14 +1192,14 @@ static uint32_t gcd_u(uint64_t a, uint64_t b)
     return (uint32_t)a;
 }
 
-template <uint32_t T, bool G1, bool NORM> static const void *stream_fn_g(uint32_t tsub)
+template <uint32_t T, bool G1, int PRO> static const void *stream_fn_g(uint32_t tsub)
 {
     constexpr int R = 1, D = kDepth, LB = wg_max<T>();
     switch (tsub) {
-    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, NORM>;
-    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, NORM>;
-    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, NORM>;
-    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB, D, NORM>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, PRO>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, PRO>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, PRO>;
+    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB, D, PRO>;
     default: return nullptr;
     }
 }
@@ -1196,10 +1232,11 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     uint32_t tsub = 0, wpt = 1, tl;
     if (ni <= 64) { tsub = 16; while (tsub < ni) tsub <<= 1; tl = tsub; }
     else { wpt = (uint32_t)((ni + 63) / 64); tl = 64 * wpt; }
-    const void *fn = g == 1 ? stream_fn_g<T, true, false>(tsub) : stream_fn_g<T, false, false>(tsub);
-    // fused-norm variant for the quant types (F16/F32 x tiles leave no registers for it)
-    const void *fn_norm = !I::PLANES ? nullptr
-                        : g == 1 ? stream_fn_g<T, true, I::PLANES>(tsub) : stream_fn_g<T, false, I::PLANES>(tsub);
+    const void *fn = g == 1 ? stream_fn_g<T, true, kProPlain>(tsub) : stream_fn_g<T, false, kProPlain>(tsub);
+    // prologue variants for the quant types (F16/F32 x tiles leave no registers for them)
+    constexpr int PN = I::PLANES ? kProNorm : kProPlain, PS = I::PLANES ? kProSilu : kProPlain;
+    const void *fn_norm = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
+    const void *fn_silu = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
     if (!fn) return;
     const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
     const uint32_t img = (image_bytes(I::PLANES, (uint32_t)cols) + 15u) & ~15u;
@@ -1235,6 +1272,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     if (lds > (uint32_t)max_lds_bytes()) return;
     p->fn = fn;
     p->fn_norm = fn_norm;
+    p->fn_silu = fn_silu;
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
     p->ts = tl;
@@ -1293,6 +1331,17 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
     StreamArgs a = stream_args(p, w, nbytes, rows, cols, x, y);
     void *args[] = {&a};
     return hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) == hipSuccess ? 0 : -2;
+}
+
+int launch_gemv_silu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                     const float *g, const float *u, float *y, ihipStream_t *stream)
+{
+    if (p.kind != 1 || !p.fn_silu || cols % 4 != 0) return -1;
+    StreamArgs a = stream_args(p, w, nbytes, rows, cols, g, y);
+    a.xb = u;
+    void *args[] = {&a};
+    return hipLaunchKernel(p.fn_silu, dim3(p.grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
+                   hipSuccess ? 0 : -2;
 }
 
 int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
@@ -1412,6 +1461,13 @@ int launch_fill(float *out, size_t n, float v, ihipStream_t *stream)
     if (n == 0) return 0;
     hipLaunchKernelGGL(fill_k, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, out,
                        (uint64_t)n, v);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_silu_mul(const float *g, const float *u, float *out, size_t n, ihipStream_t *stream)
+{
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(silu_mul_k, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, g, u, out, (uint64_t)n);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

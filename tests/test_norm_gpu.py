@@ -1,6 +1,9 @@
-"""GPU parity of qg_matvec_norm_dev (include/qgemv.h): RmsNorm of xa + xb
-followed by the mat-vec (src/math.rs:237-257, src/transformer.rs:31-46,
-src/quant.rs:178-206) against the oracle's rmsnorm + mat_vec_mul.
+"""GPU parity of the mat-vecs with an input prologue (include/qgemv.h):
+qg_matvec_norm_dev, RmsNorm of xa + xb then the mat-vec (src/math.rs:237-257,
+src/transformer.rs:31-46, src/quant.rs:178-206), against the oracle's rmsnorm
++ mat_vec_mul; qg_matvec_silu_dev, silu(g) * u then the mat-vec
+(src/mlp.rs:36-45, src/math.rs:137-146), against the oracle's silu + product
++ mat_vec_mul.
 
 y within GEMV_TOL normwise of the oracle; sum_out (xa + xb) bit-exact.
 """
@@ -99,3 +102,29 @@ def test_norm_matvec_errors(ctx, rinf, synth):
         m.matvec_norm_dev(xa, None, nw, EPS, y, xa)            # sum_out overlaps xa
     assert e.value.status == 1                                 # QG_ERR_INVALID_ARG
     m.free()
+
+
+@pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
+@pytest.mark.parametrize("shape", [(3584, 18944), (896, 4864), (256, 512), (1200, 256)],
+                         ids=["3584x18944", "896x4864", "256x512", "1200x256"])
+def test_silu_matvec_parity(ctx, rinf, oracle, synth, dtype, shape):
+    import torch
+    rows, cols = shape
+    seed = synth.config_seed(1) + 17 * rows + cols
+    raw = synth.gen_blocks(dtype, rows, cols, seed)
+    rng = np.random.default_rng(seed)
+    g = (rng.standard_normal(cols) * 4).astype(np.float32)
+    u = rng.standard_normal(cols).astype(np.float32)
+    m = ctx.upload(raw, dtype, rows, cols)
+    dg, du = torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()
+    dy = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    m.matvec_silu_dev(dg, du, dy, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy()
+    m.free()
+    x = np.array([oracle.silu(float(v)) for v in g], np.float32) * u
+    ref = oracle.mat_vec_mul_rows(raw, dtype, rows, cols, x.astype(np.float32))
+    err = normwise_err(y, ref)
+    print(f"silu {NAMES[dtype]} {rows}x{cols} err={err:.2e}", flush=True)
+    assert err <= GEMV_TOL
