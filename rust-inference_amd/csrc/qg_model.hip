@@ -397,16 +397,25 @@ __global__ void __launch_bounds__(256) sample_part_k(SampleArgs a)
 
 // The first maximum over the ranges (math.rs:328-339: a NaN at index 0
 // returns 0, as the reference's strict ">" scan does).  In generate the token
-// is appended to the history and becomes the next step's token.
+// is appended to the history and becomes the next step's token.  One wave:
+// lane l scans ranges l, l + 64, ... in order; ranges hold increasing indices,
+// so ties go to the smaller index.
 __global__ void __launch_bounds__(64) sample_final_k(SampleArgs a, uint32_t nparts)
 {
-    if (threadIdx.x != 0) return;
     float b = -INFINITY;
     uint32_t id = 0xFFFFFFFFu;
-    for (uint32_t i = 0; i < nparts; i++) {
-        if (a.pi[i] == 0xFFFFFFFFu) continue;
-        if (id == 0xFFFFFFFFu || a.pv[i] > b) { b = a.pv[i]; id = a.pi[i]; }
+    for (uint32_t i = threadIdx.x; i < nparts; i += 64) {
+        const float v = a.pv[i];
+        const uint32_t j = a.pi[i];
+        if (j != 0xFFFFFFFFu && (id == 0xFFFFFFFFu || v > b)) { b = v; id = j; }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(b, o, 64);
+        const uint32_t oi = __shfl_xor(id, o, 64);
+        if (oi != 0xFFFFFFFFu && (id == 0xFFFFFFFFu || ov > b || (ov == b && oi < id))) { b = ov; id = oi; }
+    }
+    if (threadIdx.x != 0) return;
     const float l0 = a.logits[0];
     const uint32_t tok = (l0 != l0 || id == 0xFFFFFFFFu) ? 0u : id;
     *a.token = tok;
@@ -639,6 +648,8 @@ int enqueue_forward(qg_model *m)
         if (nq == 3) {
             if ((rc = gemv_norm(m, m->f_qkv[l], na, nb, anorm, res, m->q))) return rc;
         } else if (nq == 2) {
+            // (running V beside [Q;K] as a graph branch on a second stream
+            // measured slower than one after the other)
             if ((rc = gemv_norm(m, m->f_qkv[l], na, nb, anorm, res, m->q)) ||
                 (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
                 return rc;

@@ -176,7 +176,11 @@ int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *
         lr = qg::launch_fill(y, mat->rows, 0.0f, sti);
         return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
     }
-    if (a16(g) && a16(u)) lr = qg::launch_gemv_silu(mat->plan, mat->d, mat->nbytes, mat->rows, cols, g, u, y, sti);
+    // every workgroup of the fused kernel forms the whole product itself:
+    // cheaper than a second kernel for short rows only
+    constexpr size_t kFuseMaxCols = 8192;
+    if (cols <= kFuseMaxCols && a16(g) && a16(u))
+        lr = qg::launch_gemv_silu(mat->plan, mat->d, mat->nbytes, mat->rows, cols, g, u, y, sti);
     if (lr == -1) {
         lr = qg::launch_silu_mul(g, u, scratch, cols, sti);
         if (lr == 0) {
