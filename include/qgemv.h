@@ -95,10 +95,10 @@ int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const 
 /* The MLP's down projection input formed and consumed in one pass:
  * y = W · (silu(g) * u) (src/mlp.rs:36-45, silu as src/math.rs:137-146, then
  * src/quant.rs:178-206).  g, u: cols floats; y: rows floats; device pointers,
- * asynchronous on `stream`.  With 16-byte aligned g and u and a stream-kernel
- * matrix the product is formed inside the mat-vec kernel; otherwise a
- * separate kernel writes the context's scratch vector first (calls on one
- * context must then not overlap on different streams). */
+ * asynchronous on `stream`.  With 16-byte aligned g and u, at most 8192 cols
+ * and a stream-kernel matrix the product is formed inside the mat-vec kernel;
+ * otherwise a separate kernel writes the context's scratch vector first
+ * (calls on one context must then not overlap on different streams). */
 int qg_matvec_silu_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_g, const float *d_u, float *d_y,
                        void *stream);
 

@@ -26,7 +26,7 @@ import re
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libqgemv.so"
 HEADER_PATH = HERE.parent / "include" / "qgemv.h"
-HEADERS = (HEADER_PATH, HERE.parent / "include" / "qgmodel.h")
+HEADERS = (HEADER_PATH, HERE.parent / "include" / "qgmodel.h", HERE.parent / "include" / "qggguf.h")
 
 # GGML type ids, src/gguf.rs:43-59
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = (
@@ -84,6 +84,28 @@ _SIGS = {
     "qg_synchronize": (ctypes.c_int, [_P]),
     "qg_stream": (_P, [_P]),
     "qg_device_cu_count": (ctypes.c_int, [_P]),
+    # include/qggguf.h
+    "qg_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "qg_gguf_close": (ctypes.c_int, [_P]),
+    "qg_gguf_last_error": (ctypes.c_char_p, [_P]),
+    "qg_gguf_open_error": (ctypes.c_char_p, []),
+    "qg_gguf_version": (ctypes.c_int, [_P, ctypes.POINTER(_U32)]),
+    "qg_gguf_data_offset": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64)]),
+    "qg_gguf_metadata_count": (ctypes.c_int, [_P, ctypes.POINTER(_SZ)]),
+    "qg_gguf_metadata_type": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(_U32)]),
+    "qg_gguf_get_u64": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "qg_gguf_get_f32": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+    "qg_gguf_get_string": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)]),
+    "qg_gguf_get_array_info": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(_U32),
+                                              ctypes.POINTER(ctypes.c_uint64)]),
+    "qg_gguf_tensor_count": (ctypes.c_int, [_P, ctypes.POINTER(_SZ)]),
+    "qg_gguf_find_tensor": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(_SZ)]),
+    "qg_gguf_tensor_info": (ctypes.c_int, [_P, _SZ, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U32),
+                                           ctypes.POINTER(_U32), ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_SZ)]),
+    "qg_gguf_tensor_data": (ctypes.c_int, [_P, _SZ, ctypes.POINTER(_P), ctypes.POINTER(_SZ)]),
+    "qg_gguf_model_config": (ctypes.c_int, [_P, _U32, _P]),
+    "qg_model_load_gguf": (ctypes.c_int, [_P, ctypes.c_char_p, _U32, ctypes.POINTER(_P)]),
     # include/qgmodel.h
     "qg_model_create": (ctypes.c_int, [_P, _P, ctypes.POINTER(_P)]),
     "qg_model_destroy": (ctypes.c_int, [_P]),
@@ -288,6 +310,113 @@ class QuantizedMatrix:
         gpu.mat_vec_mul(self.data, self.dtype, x, out, self.rows, self.cols)
 
 
+class GgufError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what}: {STATUS.get(status, status)}")
+        self.status = status
+
+
+class GgufFile:
+    """GGUF v3 file (include/qggguf.h; GgufFile, src/gguf.rs:244-357), mapped
+    read-only.  Needs only the host part of libqgemv.so (no GPU)."""
+
+    def __init__(self, path):
+        self.lib = load_library()
+        h = _P()
+        rc = self.lib.qg_gguf_open(str(path).encode(), ctypes.byref(h))
+        if rc:
+            raise GgufError(rc, f"qg_gguf_open: {self.lib.qg_gguf_open_error().decode()}")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.qg_gguf_close(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _q(self, rc, what):
+        if rc:
+            raise GgufError(rc, what)
+
+    @property
+    def version(self) -> int:
+        v = _U32()
+        self._q(self.lib.qg_gguf_version(self.h, ctypes.byref(v)), "version")
+        return v.value
+
+    @property
+    def data_offset(self) -> int:
+        v = ctypes.c_uint64()
+        self._q(self.lib.qg_gguf_data_offset(self.h, ctypes.byref(v)), "data_offset")
+        return v.value
+
+    def metadata_count(self) -> int:
+        n = _SZ()
+        self._q(self.lib.qg_gguf_metadata_count(self.h, ctypes.byref(n)), "metadata_count")
+        return n.value
+
+    def metadata_type(self, key: str):
+        t = _U32()
+        rc = self.lib.qg_gguf_metadata_type(self.h, key.encode(), ctypes.byref(t))
+        return None if rc else t.value
+
+    def get_u64(self, key: str):
+        """MetadataValue::to_u64 (None when absent or of another type)."""
+        v = ctypes.c_uint64()
+        return None if self.lib.qg_gguf_get_u64(self.h, key.encode(), ctypes.byref(v)) else v.value
+
+    def get_f32(self, key: str):
+        v = ctypes.c_float()
+        return None if self.lib.qg_gguf_get_f32(self.h, key.encode(), ctypes.byref(v)) else v.value
+
+    def get_string(self, key: str):
+        n = _SZ()
+        if self.lib.qg_gguf_get_string(self.h, key.encode(), None, 0, ctypes.byref(n)):
+            return None
+        buf = ctypes.create_string_buffer(n.value + 1)
+        self._q(self.lib.qg_gguf_get_string(self.h, key.encode(), buf, n.value + 1, ctypes.byref(n)), key)
+        return buf.raw[: n.value].decode()
+
+    def get_array_info(self, key: str):
+        t, c = _U32(), ctypes.c_uint64()
+        if self.lib.qg_gguf_get_array_info(self.h, key.encode(), ctypes.byref(t), ctypes.byref(c)):
+            return None
+        return t.value, c.value
+
+    def tensors(self):
+        """[(name, ggml type, dims (ne0 first), offset, bytes the loader reads)]."""
+        n = _SZ()
+        self._q(self.lib.qg_gguf_tensor_count(self.h, ctypes.byref(n)), "tensor_count")
+        out = []
+        for i in range(n.value):
+            name, t, nd = ctypes.c_char_p(), _U32(), _U32()
+            dims, off, nb = (ctypes.c_uint64 * 4)(), ctypes.c_uint64(), _SZ()
+            self._q(self.lib.qg_gguf_tensor_info(self.h, i, ctypes.byref(name), ctypes.byref(t), ctypes.byref(nd),
+                                                 dims, ctypes.byref(off), ctypes.byref(nb)), "tensor_info")
+            out.append((name.value.decode(), t.value, tuple(dims[: min(nd.value, 4)]), off.value, nb.value))
+        return out
+
+    def tensor_bytes(self, name: str):
+        """A copy of the tensor's bytes (numpy uint8), or None if absent."""
+        import numpy as np
+        i = _SZ()
+        if self.lib.qg_gguf_find_tensor(self.h, name.encode(), ctypes.byref(i)):
+            return None
+        p, nb = _P(), _SZ()
+        self._q(self.lib.qg_gguf_tensor_data(self.h, i.value, ctypes.byref(p), ctypes.byref(nb)), name)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint8)), (nb.value,)).copy()
+
+    def model_config(self, max_seq_len: int = 0) -> dict:
+        cfg = ModelConfig()
+        self._q(self.lib.qg_gguf_model_config(self.h, max_seq_len, ctypes.byref(cfg)), "model_config")
+        return {k: getattr(cfg, k) for k, _ in ModelConfig._fields_}
+
+
 class DeviceModel:
     """The decode step on device (include/qgmodel.h): Transformer::forward
     (src/transformer.rs:63-98), greedy Sampler::sample (src/sampler.rs:72-83,
@@ -303,6 +432,21 @@ class DeviceModel:
         ctx.check(ctx.lib.qg_model_create(ctx.h, ctypes.byref(self.cfg), ctypes.byref(h)),
                   "qg_model_create")
         self.h = h
+
+    @classmethod
+    def load_gguf(cls, ctx: GpuContext, path, max_seq_len: int = 0):
+        """Model::load's weights from a GGUF file (qg_model_load_gguf)."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        h = _P()
+        ctx.check(ctx.lib.qg_model_load_gguf(ctx.h, str(path).encode(), max_seq_len, ctypes.byref(h)),
+                  "qg_model_load_gguf")
+        self.h = h
+        g = GgufFile(path)
+        c = g.model_config(max_seq_len)
+        g.close()
+        self.cfg = ModelConfig(*[c[k] for k, _ in ModelConfig._fields_])
+        return self
 
     def close(self):
         # a closed context has already freed its models (qg_destroy)

@@ -62,5 +62,8 @@ int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *
 // copies of the parts' blocks, one after the other.  Synchronous.
 int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out);
 
+// lm_head = the model's token_embd device matrix (a tied output, model.rs:224-226).
+int qg_model_tie_lm_head(qg_model *m);
+
 // Records `what` (and the HIP error text) as the context's last error; returns `status`.
 int qg_fail(qg_ctx *ctx, int status, const char *what, hipError_t e = hipSuccess);

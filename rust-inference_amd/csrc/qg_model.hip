@@ -566,7 +566,7 @@ void free_model(qg_model *m)
         for (size_t l = 0; l < m->w[s].size(); l++)
             if (m->w[s][l] && m->owned[s][l]) qg_mat_free(m->ctx, m->w[s][l]);
     if (m->tok && m->tok_owned) qg_mat_free(m->ctx, m->tok);
-    if (m->lm && m->lm_owned) qg_mat_free(m->ctx, m->lm);
+    if (m->lm && m->lm_owned && m->lm != m->tok) qg_mat_free(m->ctx, m->lm);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->h_recent) (void)hipHostFree(m->h_recent);
     if (m->h_token) (void)hipHostFree(m->h_token);
@@ -925,6 +925,12 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
     drop_fused(m);
+    if (which == QG_M_TOKEN_EMBD && m->tok && m->lm == m->tok) {
+        // a tied lm_head keeps the old token_embd copy
+        m->lm_owned = m->tok_owned;
+        m->tok = nullptr;
+        m->tok_owned = false;
+    }
     qg_mat **dst;
     bool *own;
     if (which == QG_M_TOKEN_EMBD) { dst = &m->tok; own = &m->tok_owned; }
@@ -936,7 +942,7 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
         m->owned[s][layer] = true;
         return QG_OK;
     }
-    if (*dst && *own) qg_mat_free(m->ctx, *dst);
+    if (*dst && *own && !(which == QG_M_LM_HEAD && *dst == m->tok)) qg_mat_free(m->ctx, *dst);
     *dst = mat;
     *own = true;
     return QG_OK;
@@ -956,11 +962,16 @@ int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_
     drop_graphs(m);
     drop_fused(m);
     qg_mat *mm = const_cast<qg_mat *>(mat);
+    if (which == QG_M_TOKEN_EMBD && m->tok && m->lm == m->tok && m->tok != mm) {
+        m->lm_owned = m->tok_owned;                        // a tied lm_head keeps the old copy
+        m->tok = nullptr;
+        m->tok_owned = false;
+    }
     if (which == QG_M_TOKEN_EMBD) {
         if (m->tok && m->tok_owned) qg_mat_free(m->ctx, m->tok);
         m->tok = mm; m->tok_owned = false;
     } else if (which == QG_M_LM_HEAD) {
-        if (m->lm && m->lm_owned) qg_mat_free(m->ctx, m->lm);
+        if (m->lm && m->lm_owned && m->lm != m->tok) qg_mat_free(m->ctx, m->lm);
         m->lm = mm; m->lm_owned = false;
     } else {
         const int s = (int)which - QG_M_WQ;
@@ -1100,6 +1111,17 @@ int qg_model_generate(qg_model *m, const uint32_t *prompt, size_t n_prompt, size
 }
 
 }  // extern "C"
+
+int qg_model_tie_lm_head(qg_model *m)
+{
+    if (!m || !m->tok) return QG_ERR_INVALID_ARG;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    drop_graphs(m);
+    if (m->lm && m->lm_owned && m->lm != m->tok) qg_mat_free(m->ctx, m->lm);
+    m->lm = m->tok;
+    m->lm_owned = false;
+    return QG_OK;
+}
 
 void qg_models_free_all(qg_ctx *ctx)
 {
