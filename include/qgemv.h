@@ -92,6 +92,29 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
 int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const float *d_xb,
                        const float *d_nw, float eps, float *d_sum_out, float *d_y, void *stream);
 
+/* The MLP's gate and up projections with the SiLU product, from the norm of
+ * the residual stream: h[j] = silu(gate_j · x) * (up_j · x) with
+ * x = rmsnorm(xa + xb) * nw (src/mlp.rs:31-43 with silu as
+ * src/math.rs:137-146, its input as in qg_matvec_norm_dev).  gu is the stacked
+ * [gate; up] matrix (qg_mat_stack; 2 * H rows, gate rows first); h: H floats;
+ * xa, xb, nw, sum_out as in qg_matvec_norm_dev.  With 16-byte aligned
+ * vectors, a non-NULL d_xb, a quantized type and short whole-block rows
+ * (cols <= 8192 for Q4_K, <= 4096 for Q5_K, Q6_K, Q8_0, Q4_0, Q5_0) one
+ * kernel computes each gate row and its up row back to back and writes h
+ * only; otherwise the [gate; up] outputs go to a context
+ * scratch vector first (calls on one context must then not overlap on
+ * different streams).  QG_ERR_SHAPE for an odd row count. */
+int qg_matvec_norm_glu_dev(qg_ctx *ctx, const qg_mat *gu, const float *d_xa, const float *d_xb,
+                           const float *d_nw, float eps, float *d_sum_out, float *d_h, void *stream);
+
+/* One matrix whose rows are those of parts[0], parts[1], ... in order (the
+ * same GGML type and cols; every part but the last a whole number of blocks),
+ * as model.rs keeps wq/wk/wv and ffn_gate/ffn_up as separate
+ * QuantizedMatrix values (src/model.rs:231-298) -- the stacked copy lets one
+ * launch stream them together.  Synchronous device copies; the parts stay
+ * valid.  Free with qg_mat_free. */
+int qg_mat_stack(qg_ctx *ctx, qg_mat *const *parts, int n_parts, qg_mat **out);
+
 /* The MLP's down projection input formed and consumed in one pass:
  * y = W · (silu(g) * u) (src/mlp.rs:36-45, silu as src/math.rs:137-146, then
  * src/quant.rs:178-206).  g, u: cols floats; y: rows floats; device pointers,

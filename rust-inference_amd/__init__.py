@@ -76,6 +76,8 @@ _SIGS = {
     "qg_matvec_dev": (ctypes.c_int, [_P, _P, _P, _P, _P]),
     "qg_matvec_norm_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_matvec_silu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, _P]),
+    "qg_matvec_norm_glu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
+    "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
     "qg_gpu_mat_vec_mul": (ctypes.c_int, [_P, _P, _SZ, _U32, _P, _P, _SZ, _SZ]),
     "qg_dequant_dev": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -233,6 +235,15 @@ class GpuContext:
         self.check(rc, "qg_upload")
         return DeviceMatrix(self, m, dtype, rows, cols)
 
+    def stack(self, parts) -> "DeviceMatrix":
+        """One matrix with the rows of `parts` (DeviceMatrix, same type and
+        cols) in order (qg_mat_stack)."""
+        arr = (_P * len(parts))(*[p.h for p in parts])
+        m = _P()
+        rc = self.lib.qg_mat_stack(self.h, arr, len(parts), ctypes.byref(m))
+        self.check(rc, "qg_mat_stack")
+        return DeviceMatrix(self, m, parts[0].dtype, sum(p.rows for p in parts), parts[0].cols)
+
     def mat_vec_mul(self, weight_data, dtype: int, x, out, rows: int, cols: int):
         """src/gpu_backend.rs:429-437 signature; host numpy arrays in and out."""
         rc = self.lib.qg_gpu_mat_vec_mul(self.h, _ptr(weight_data), weight_data.nbytes, dtype,
@@ -271,6 +282,16 @@ class DeviceMatrix:
                                              _ptr(d_sum_out) if d_sum_out is not None else None,
                                              _ptr(d_y), ctypes.c_void_p(stream) if stream else None)
         self.ctx.check(rc, "qg_matvec_norm_dev")
+
+    def matvec_norm_glu_dev(self, d_xa, d_xb, d_nw, eps, d_h, d_sum_out=None, stream=None):
+        """h = silu(gate · x) * (up · x), x = rmsnorm(xa + xb) * nw, for this
+        [gate; up] matrix; torch device tensors (float32)."""
+        rc = self.ctx.lib.qg_matvec_norm_glu_dev(self.ctx.h, self.h, _ptr(d_xa),
+                                                 _ptr(d_xb) if d_xb is not None else None, _ptr(d_nw),
+                                                 float(eps),
+                                                 _ptr(d_sum_out) if d_sum_out is not None else None,
+                                                 _ptr(d_h), ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_matvec_norm_glu_dev")
 
     def matvec_silu_dev(self, d_g, d_u, d_y, stream=None):
         """y = W · (silu(g) * u); torch device tensors (float32)."""

@@ -59,6 +59,7 @@ struct Plan {
     const void *fn;        // kernel chosen for this matrix
     const void *fn_norm;   // the same kernel with the fused RMSNorm input
     const void *fn_silu;   // the same kernel with the silu(g) * u input
+    const void *fn_norm_glu;  // RMSNorm input, [gate; up] rows paired into silu(g) * u
 };
 
 }  // namespace qg
@@ -75,6 +76,12 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
 int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
                      const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
                      float *y, ihipStream_t *stream);
+// W = [gate; up] (rows = 2 * half, one row per group, teams of one wave or
+// less; -1 otherwise): y[j] = silu(gate_j · x) * (up_j · x) for j < half,
+// x = rmsnorm(xa + xb) * nw as in launch_gemv_norm.
+int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                         const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
+                         float *y, ihipStream_t *stream);
 // y = W · (silu(g) * u) with the stream kernel (kind 1 plans only; -1
 // otherwise).  g, u: cols floats, 16-byte aligned.
 int launch_gemv_silu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,

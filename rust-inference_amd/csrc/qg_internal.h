@@ -35,6 +35,8 @@ struct qg_ctx {
     size_t d_x_cap = 0, d_y_cap = 0;
     float *d_norm = nullptr;                // normalised x of qg_matvec_norm_dev's two-kernel path
     size_t d_norm_cap = 0;
+    float *d_glu = nullptr;                 // gate and up outputs of qg_matvec_norm_glu_dev's unfused path
+    size_t d_glu_cap = 0;
     std::set<qg_mat *> mats;
     std::set<qg_model *> models;            // decode-step engines on this context
     std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
@@ -56,6 +58,14 @@ int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float 
 // a separate kernel into `scratch` (cols floats) when that does not apply.
 int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *u, float *y, float *scratch,
                    hipStream_t stream);
+
+// h = silu(gate · x) * (up · x), x = rmsnorm(xa + xb) * nw, for the stacked
+// gu = [gate; up] (rows = 2 * rows(h)): one stream kernel that pairs the rows
+// when the plan and pointers allow; otherwise the norm mat-vec of gu into
+// gu_out (rows floats; its norm scratch is `scratch`, cols floats) and a
+// silu * up kernel.  Asynchronous.
+int qg_norm_glu_matvec(qg_ctx *ctx, const qg_mat *gu, const float *xa, const float *xb, const float *nw,
+                       float eps, float *sum_out, float *h, float *gu_out, float *scratch, hipStream_t stream);
 
 // One owned matrix whose rows are the rows of parts[0], parts[1], ... (same
 // type and cols; every part but the last a whole number of blocks): device

@@ -15,14 +15,17 @@
 // attention softmax is split over position ranges):
 //   RMSNorm          math.rs:237-257 (RmsNorm::forward), inside the next GEMV
 //                    with the residual add of transformer.rs:31-46
-//   qkv_post_k       attention.rs:68-90: bias add, RoPE on q and k
-//                    (rope.rs:88-96, pairs 2i/2i+1), KV append (kv_cache.rs:52-73)
-//   attn_split_k     attention.rs:92-121 over one range of positions for the
-//   attn_combine_k   query heads of one kv head; then the ranges' partial
-//                    softmax sums are merged (math.rs:104-118 rescaled)
-//   attention_k      the same in one workgroup per head (head_dim % 64 != 0)
-//   SiLU * up        mlp.rs:36-43, silu as math.rs:137-146, inside the down
-//                    GEMV (a separate kernel where that does not apply)
+//   attn_rope_split_k  attention.rs:66-121 for head_dim 64/128/256: bias
+//                    add, RoPE on q and k (rope.rs:88-96, pairs 2i/2i+1), KV
+//   attn_combine_k   append (kv_cache.rs:52-73), then attention over one range
+//                    of positions for the query heads of one kv head; then the
+//                    ranges' partial softmax sums are merged (math.rs:104-118
+//                    rescaled)
+//   qkv_post_k       the bias add, RoPE and KV append alone, and
+//   attention_k      attention in one workgroup per head (other head_dim)
+//   SiLU * up        mlp.rs:31-43, silu as math.rs:137-146, in the epilogue
+//                    of the [gate; up] GEMV (gate and up rows paired), else
+//                    inside the down GEMV's prologue or a separate kernel
 //   sample_part_k    sampler.rs:109-127 then math.rs:328-339 over one range
 //   sample_final_k   of the logits per workgroup; then the first maximum
 #include <hip/hip_runtime.h>
@@ -153,103 +156,211 @@ __global__ void __launch_bounds__(256) qkv_post_k(float *__restrict__ q, const f
     }
 }
 
-// Attention over positions [j0, j1) of the seq = slot + 1 cached ones, for
-// the `grp` query heads h0 .. h0 + grp - 1 that share one kv head
-// (head_dim = 64 * E).  Workgroup (head group, range): 4 waves, each lane
-// owns dimensions lane + 64 e, so every K and V row is one coalesced read
-// shared by the group's heads.  Writes the unnormalised partial output
-// sum_j exp(s_j - m) v_j and (m, l = sum_j exp(s_j - m)) of its range;
+// Arguments of the split attention kernel.
+struct AttnArgs {
+    const float *q, *k, *v;          // this token's projections, before bias and RoPE
+    const float *bq, *bk, *bv;
+    float *kc, *vc;                  // the layer's cache, [max_seq_len][kv_dim]
+    const float *cos_t, *sin_t;      // [max_seq_len][head_dim / 2]
+    float *part, *ml;                // per (head, range): partial output, (max, sum)
+    const Step *st;
+    uint32_t kv_dim, n_rep, grp, nsplit;
+    float scale;
+};
+
+// Element d of a head after RoPE (rope.rs: the pair (2i, 2i+1) turned by
+// pos * theta_i); `self` is element d, `other` its partner d ^ 1, cs / sn the
+// position's rows of the tables.  The same expressions as qkv_post_k.
+__device__ __forceinline__ float rope1(float self, float other, uint32_t d, float c, float s)
+{
+    // even d: self c - other s; odd d: other s + self c (= self c + other s)
+    const float p0 = self * c, p1 = other * s;
+    return p0 + ((d & 1u) ? p1 : -p1);
+}
+
+// Attention of the token at st->pos over positions [j0, j1) of the
+// seq = slot + 1 cached ones, for the `grp` query heads h0 .. h0 + grp - 1
+// that share one kv head (head_dim = 64 * E), with the projections'
+// post-processing folded in: q, k, v biases (attention.rs:66-76), RoPE of q
+// and k (attention.rs:78-87) and the cache append at `slot`
+// (attention.rs:89-90, kv_cache.rs:52-73).  The range that holds `slot` uses
+// this token's k and v from registers, and its first head group of each kv
+// head stores them to the cache, so no other workgroup reads the slot being
+// written.
+//
+// (Merging the ranges in the last workgroup to finish, behind a device-scope
+// counter, measured slower than the separate merge kernel: the fences that
+// make the partial sums visible across the XCDs' L2 caches cost more than the
+// launch.)
+//
+// Workgroup (head group, range): 4 waves, each lane owns dimensions
+// lane + 64 e (every K and V row is one coalesced read shared by the group's
+// heads).  A wave takes positions j0 + wave + 4 p in chunks of kPW, all K and
+// V rows of a chunk loaded before any use, with a running (max, sum, output)
+// per head (the softmax of attention.rs:101-119 over the wave's positions);
+// the four waves are merged in LDS.  Writes the unnormalised partial output
+// sum_j exp(s_j - m) v_j and (m, l = sum_j exp(s_j - m)) of the range;
 // workgroups whose range starts past seq exit.
+// Positions per wave per chunk: the chunk's code is unrolled over heads and
+// positions, and a larger chunk made the kernel slower (straight-line code
+// fetched cold by every workgroup) while short ranges fill only one chunk.
+constexpr uint32_t kPW = 2;
 template <int E>
-__global__ void __launch_bounds__(256) attn_split_k(const float *__restrict__ q, const float *__restrict__ kc,
-                                                    const float *__restrict__ vc, float *__restrict__ part,
-                                                    float *__restrict__ ml, const Step *__restrict__ st,
-                                                    uint32_t kv_dim, uint32_t n_rep, uint32_t grp,
-                                                    uint32_t nsplit, uint32_t lmax, float scale)
+__global__ void __launch_bounds__(256) attn_rope_split_k(AttnArgs a)
 {
     constexpr uint32_t HD = 64 * E;
-    extern __shared__ float sm[];             // sc[grp][lmax], pr[4][grp][HD]
-    float *sc = sm, *pr = sm + grp * lmax;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t split = blockIdx.x % nsplit, h0 = (blockIdx.x / nsplit) * grp;
-    const uint32_t kvo = (h0 / n_rep) * HD;
-    const uint32_t seq = st->slot + 1;
-    const uint32_t len = range_len(seq, nsplit);           // <= lmax while seq <= max_seq_len
+    __shared__ float sacc[4][kMaxGroup][HD];
+    __shared__ float sml[4][kMaxGroup][2];
+    // wave index as a uniform value: the position loop's bounds depend on it,
+    // and a per-lane value would turn every branch on them into exec masking
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t grp = a.grp, split = blockIdx.x % a.nsplit, h0 = (blockIdx.x / a.nsplit) * grp;
+    const uint32_t kvo = (h0 / a.n_rep) * HD;
+    // Every load below is unconditional (clamped indices, selects after the
+    // loads): a load behind a branch waits for everything issued before it.
+    // The projections do not depend on the step record, so they are in flight
+    // while it arrives.
+    float qv[kMaxGroup][E], kn[E], vn[E];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxGroup; r++)
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const uint32_t i = (h0 + (r < grp ? r : 0u)) * HD + lane + 64 * e;
+            qv[r][e] = a.q[i] + a.bq[i];
+        }
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        kn[e] = a.k[kvo + lane + 64 * e] + a.bk[kvo + lane + 64 * e];
+        vn[e] = a.v[kvo + lane + 64 * e] + a.bv[kvo + lane + 64 * e];
+    }
+    const uint32_t pos = a.st->pos, slot = a.st->slot, seq = slot + 1;
+    const uint32_t len = range_len(seq, a.nsplit);
     const uint32_t j0 = split * len, j1 = min(seq, j0 + len);
+    // K and V rows of this wave's positions j0 + wave + 4 p, kPW at a time,
+    // clamped into the cache rows that exist (a workgroup past seq loads and
+    // exits); the next chunk is in flight while one is used
+    float kk[kPW][E], vv[kPW][E], nk[kPW][E], nv[kPW][E];
+    auto load = [&](uint32_t b, float (&ko)[kPW][E], float (&vo)[kPW][E]) {
+#pragma unroll
+        for (uint32_t p = 0; p < kPW; p++) {
+            const uint32_t j = min(b + 4 * p, slot);
+            const float *kr = a.kc + (size_t)j * a.kv_dim + kvo, *vr = a.vc + (size_t)j * a.kv_dim + kvo;
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                ko[p][e] = kr[lane + 64 * e];
+                vo[p][e] = vr[lane + 64 * e];
+            }
+        }
+    };
+    uint32_t base = j0 + wave;
+    load(base, kk, vv);
+    // cos / sin of this lane's pairs (the table rows of `pos`)
+    float cv[E], sv[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        cv[e] = a.cos_t[(size_t)pos * (HD / 2) + ((lane + 64 * e) >> 1)];
+        sv[e] = a.sin_t[(size_t)pos * (HD / 2) + ((lane + 64 * e) >> 1)];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxGroup; r++)
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const float o = __shfl_xor(qv[r][e], 1, 64);
+            qv[r][e] = r < grp ? rope1(qv[r][e], o, lane + 64 * e, cv[e], sv[e]) : 0.f;
+        }
+#pragma unroll
+    for (int e = 0; e < E; e++) kn[e] = rope1(kn[e], __shfl_xor(kn[e], 1, 64), lane + 64 * e, cv[e], sv[e]);
     if (j0 >= seq) return;
-    float qv[kMaxGroup][E];
+    const bool has_new = j1 == seq;
+    if (has_new && h0 % a.n_rep == 0 && wave == 0) {
+        float *kr = a.kc + (size_t)slot * a.kv_dim + kvo, *vr = a.vc + (size_t)slot * a.kv_dim + kvo;
 #pragma unroll
-    for (uint32_t r = 0; r < kMaxGroup; r++)
-#pragma unroll
-        for (int e = 0; e < E; e++) qv[r][e] = r < grp ? q[(h0 + r) * HD + lane + 64 * e] : 0.f;
-    // scores (attention.rs:101-109)
-    for (uint32_t j = j0 + wave; j < j1; j += 4) {
-        const float *kr = kc + (size_t)j * kv_dim + kvo;
-        float kv[E];
-#pragma unroll
-        for (int e = 0; e < E; e++) kv[e] = kr[lane + 64 * e];
-#pragma unroll
-        for (uint32_t r = 0; r < kMaxGroup; r++) {
-            if (r >= grp) break;
-            float s = 0.f;
-#pragma unroll
-            for (int e = 0; e < E; e++) s += qv[r][e] * kv[e];
-            s = wave_sum(s);
-            if (lane == 0) sc[r * lmax + (j - j0)] = s * scale;
+        for (int e = 0; e < E; e++) {
+            kr[lane + 64 * e] = kn[e];
+            vr[lane + 64 * e] = vn[e];
         }
     }
-    __syncthreads();
-    // range max and exp sum per head (math.rs:104-113 over this range)
-    const uint32_t cnt = j1 - j0;
-    for (uint32_t r = wave; r < grp; r += 4) {
-        float mx = -INFINITY;
-        for (uint32_t t = lane; t < cnt; t += 64) mx = fmaxf(mx, sc[r * lmax + t]);
-        mx = wave_max(mx);
-        float sum = 0.f;
-        for (uint32_t t = lane; t < cnt; t += 64) {
-            const float ex = expf(sc[r * lmax + t] - mx);
-            sc[r * lmax + t] = ex;
-            sum += ex;
-        }
-        sum = wave_sum(sum);
-        if (lane == 0) {
-            float *o = ml + ((size_t)(h0 + r) * nsplit + split) * 2;
-            o[0] = mx;
-            o[1] = sum;
-        }
-    }
-    __syncthreads();
-    // weighted sum of v (attention.rs:113-119 over this range)
-    float acc[kMaxGroup][E];
+    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][E];
 #pragma unroll
-    for (uint32_t r = 0; r < kMaxGroup; r++)
+    for (uint32_t r = 0; r < kMaxGroup; r++) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
 #pragma unroll
         for (int e = 0; e < E; e++) acc[r][e] = 0.f;
-    for (uint32_t j = j0 + wave; j < j1; j += 4) {
-        const float *vr = vc + (size_t)j * kv_dim + kvo;
-        float vv[E];
+    }
+    for (; base < j1; base += 4 * kPW) {
+        const uint32_t np = min((j1 - base + 3) / 4, kPW);   // this wave's positions in the chunk
+        if (base + 4 * kPW < j1) load(base + 4 * kPW, nk, nv);
+        // the slot being appended comes from registers (its cache row is written above)
 #pragma unroll
-        for (int e = 0; e < E; e++) vv[e] = vr[lane + 64 * e];
+        for (uint32_t p = 0; p < kPW; p++)
+            if (base + 4 * p == slot)
+#pragma unroll
+                for (int e = 0; e < E; e++) { kk[p][e] = kn[e]; vv[p][e] = vn[e]; }
 #pragma unroll
         for (uint32_t r = 0; r < kMaxGroup; r++) {
             if (r >= grp) break;
-            const float p = sc[r * lmax + (j - j0)];
+            float sc[kPW], cm = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < E; e++) acc[r][e] += p * vv[e];
+            for (uint32_t p = 0; p < kPW; p++) {
+                if (p >= np) break;
+                float t = 0.f;
+#pragma unroll
+                for (int e = 0; e < E; e++) t += qv[r][e] * kk[p][e];
+                sc[p] = wave_sum(t) * a.scale;
+                cm = fmaxf(cm, sc[p]);
+            }
+            const float mn = fmaxf(m[r], cm);
+            const float al = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
+            float ls = 0.f, o[E];
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] = 0.f;
+#pragma unroll
+            for (uint32_t p = 0; p < kPW; p++) {
+                if (p >= np) break;
+                const float ex = expf(sc[p] - mn);
+                ls += ex;
+#pragma unroll
+                for (int e = 0; e < E; e++) o[e] += ex * vv[p][e];
+            }
+            l[r] = l[r] * al + ls;
+#pragma unroll
+            for (int e = 0; e < E; e++) acc[r][e] = acc[r][e] * al + o[e];
+            m[r] = mn;
         }
+#pragma unroll
+        for (uint32_t p = 0; p < kPW; p++)
+#pragma unroll
+            for (int e = 0; e < E; e++) { kk[p][e] = nk[p][e]; vv[p][e] = nv[p][e]; }
     }
 #pragma unroll
     for (uint32_t r = 0; r < kMaxGroup; r++) {
         if (r >= grp) break;
 #pragma unroll
-        for (int e = 0; e < E; e++) pr[(wave * grp + r) * HD + lane + 64 * e] = acc[r][e];
+        for (int e = 0; e < E; e++) sacc[wave][r][lane + 64 * e] = acc[r][e];
+        if (lane == 0) { sml[wave][r][0] = m[r]; sml[wave][r][1] = l[r]; }
     }
     __syncthreads();
+    // merge the waves: weights exp(m_w - M) (0 for a wave without positions)
     for (uint32_t i = threadIdx.x; i < grp * HD; i += blockDim.x) {
         const uint32_t r = i / HD, d = i % HD;
-        const float s = (pr[r * HD + d] + pr[(grp + r) * HD + d]) + (pr[(2 * grp + r) * HD + d] +
-                                                                     pr[(3 * grp + r) * HD + d]);
-        part[((size_t)(h0 + r) * nsplit + split) * HD + d] = s;
+        float mx = sml[0][r][0];
+#pragma unroll
+        for (int w = 1; w < 4; w++) mx = fmaxf(mx, sml[w][r][0]);
+        float sum = 0.f, lsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = sml[w][r][0];
+            const float f = mw == -INFINITY ? 0.f : expf(mw - mx);
+            sum += f * sacc[w][r][d];
+            lsum += f * sml[w][r][1];
+        }
+        const size_t o = (size_t)(h0 + r) * a.nsplit + split;
+        a.part[o * HD + d] = sum;
+        if (d == 0) {
+            a.ml[2 * o] = mx;
+            a.ml[2 * o + 1] = lsum;
+        }
     }
 }
 
@@ -452,8 +563,8 @@ struct qg_model {
     qg_ctx *ctx = nullptr;
     qg_model_config cfg{};
     uint32_t hd = 0, q_dim = 0, kv_dim = 0, n_rep = 0;
-    uint32_t att_grp = 0, att_nsplit = 0, att_lmax = 0;   // split attention (head_dim % 64 == 0)
-    size_t att_lds = 0;
+    uint32_t att_grp = 0, att_nsplit = 0;   // split attention (head_dim 64, 128, 256)
+    size_t att_lds = 0;                     // LDS of the one-workgroup-per-head kernel
     qg_mat *tok = nullptr, *lm = nullptr;
     bool tok_owned = false, lm_owned = false;
     std::vector<qg_mat *> w[kSlots];
@@ -659,26 +770,27 @@ int enqueue_forward(qg_model *m)
             return rc;
         }
         float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
-        hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
-                           m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
-                           m->sin_t, m->q_dim, m->kv_dim, m->hd, m->d_step);
         if (m->att_grp) {
+            qgm::AttnArgs aa{};
+            aa.q = m->q; aa.k = m->k; aa.v = m->v;
+            aa.bq = m->vec[QG_V_BQ][l]; aa.bk = m->vec[QG_V_BK][l]; aa.bv = m->vec[QG_V_BV][l];
+            aa.kc = kc; aa.vc = vc; aa.cos_t = m->cos_t; aa.sin_t = m->sin_t;
+            aa.part = m->att_part; aa.ml = m->att_ml; aa.st = m->d_step;
+            aa.kv_dim = m->kv_dim; aa.n_rep = m->n_rep; aa.grp = m->att_grp; aa.nsplit = m->att_nsplit;
+            aa.scale = scale;
             const dim3 grid(c.n_heads / m->att_grp * m->att_nsplit);
             if (m->hd == 64)
-                hipLaunchKernelGGL(qgm::attn_split_k<1>, grid, dim3(256), m->att_lds, st, m->q, kc, vc,
-                                   m->att_part, m->att_ml, m->d_step, m->kv_dim, m->n_rep, m->att_grp,
-                                   m->att_nsplit, m->att_lmax, scale);
+                hipLaunchKernelGGL(qgm::attn_rope_split_k<1>, grid, dim3(256), 0, st, aa);
             else if (m->hd == 128)
-                hipLaunchKernelGGL(qgm::attn_split_k<2>, grid, dim3(256), m->att_lds, st, m->q, kc, vc,
-                                   m->att_part, m->att_ml, m->d_step, m->kv_dim, m->n_rep, m->att_grp,
-                                   m->att_nsplit, m->att_lmax, scale);
+                hipLaunchKernelGGL(qgm::attn_rope_split_k<2>, grid, dim3(256), 0, st, aa);
             else
-                hipLaunchKernelGGL(qgm::attn_split_k<4>, grid, dim3(256), m->att_lds, st, m->q, kc, vc,
-                                   m->att_part, m->att_ml, m->d_step, m->kv_dim, m->n_rep, m->att_grp,
-                                   m->att_nsplit, m->att_lmax, scale);
+                hipLaunchKernelGGL(qgm::attn_rope_split_k<4>, grid, dim3(256), 0, st, aa);
             hipLaunchKernelGGL(qgm::attn_combine_k, dim3(c.n_heads), dim3(256), 0, st, m->att_part, m->att_ml,
                                m->ao, m->d_step, m->hd, m->att_nsplit);
         } else {
+            hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
+                               m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
+                               m->sin_t, m->q_dim, m->kv_dim, m->hd, m->d_step);
             hipLaunchKernelGGL(qgm::attention_k, dim3(c.n_heads), dim3(256), m->att_lds, st, m->q, kc, vc, m->ao,
                                m->d_step, m->hd, m->kv_dim, m->n_rep, scale);
         }
@@ -687,11 +799,17 @@ int enqueue_forward(qg_model *m)
         // h1 = h0 + attention output (stored by the gate GEMV); MLP input = ffn_norm(h1)
         const float *fnorm = m->vec[QG_V_FFN_NORM][l];
         if (m->f_gu[l]) {
-            if ((rc = gemv_norm(m, m->f_gu[l], m->h0, m->ao2, fnorm, m->h1, m->g))) return rc;
-        } else if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
-                   (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u))) {
-            return rc;
+            // silu(gate) * up (mlp.rs:31-43) paired in the [gate; up] kernel
+            // (or its outputs in g, u and a product kernel), then down
+            if ((rc = qg_norm_glu_matvec(m->ctx, m->f_gu[l], m->h0, m->ao2, fnorm, c.norm_eps, m->h1, m->hb, m->g,
+                                         m->xn, st)) ||
+                (rc = gemv(m, m->w[QG_M_DOWN - 2][l], m->hb, m->fo)))
+                return rc;
+            continue;
         }
+        if ((rc = gemv_norm(m, m->w[QG_M_GATE - 2][l], m->h0, m->ao2, fnorm, m->h1, m->g)) ||
+            (rc = gemv_norm(m, m->w[QG_M_UP - 2][l], m->h0, m->ao2, fnorm, nullptr, m->u)))
+            return rc;
         // down(silu(g) * u) (mlp.rs:36-45): the product inside the down GEMV's prologue
         if ((rc = qg_silu_matvec(m->ctx, m->w[QG_M_DOWN - 2][l], m->g, m->u, m->fo, m->hb, st))) return rc;
     }
@@ -815,7 +933,7 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
     m->n_rep = c.n_heads / n_kv;
     // attention layout: workgroups of grp query heads (a divisor of n_rep, at
     // most 8) times up to 64 position ranges of at least 8 positions, about
-    // 256 workgroups in all at long sequences
+    // 256 workgroups in all at long sequences; any max_seq_len
     constexpr size_t kLdsMax = 65536;
     if (hd == 64 || hd == 128 || hd == 256) {
         uint32_t grp = 1;
@@ -824,16 +942,8 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
         const uint32_t groups = c.n_heads / grp;
         uint32_t ns = (256 + groups - 1) / groups;
         ns = ns < 1 ? 1 : ns > qgm::kMaxSplit ? qgm::kMaxSplit : ns;
-        const uint32_t lmax = qgm::range_len(c.max_seq_len, ns);
-        const size_t lds = ((size_t)grp * lmax + 4ull * grp * hd) * sizeof(float);
-        if (lds > kLdsMax) {
-            delete m;
-            return qg_fail(ctx, QG_ERR_SHAPE, "max_seq_len too large for the attention kernel");
-        }
         m->att_grp = grp;
         m->att_nsplit = ns;
-        m->att_lmax = lmax;
-        m->att_lds = lds;
     } else {
         m->att_lds = ((size_t)hd + c.max_seq_len) * sizeof(float);
         if (m->att_lds > kLdsMax) {

@@ -193,6 +193,24 @@ int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *
     return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
 }
 
+int qg_norm_glu_matvec(qg_ctx *ctx, const qg_mat *gu, const float *xa, const float *xb, const float *nw,
+                       float eps, float *sum_out, float *h, float *gu_out, float *scratch, hipStream_t st)
+{
+    ihipStream_t *sti = (ihipStream_t *)st;
+    const size_t half = gu->rows / 2;
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    int lr = -1;
+    if (gu->cols > 0 && xb && a16(xa) && a16(xb) && a16(nw) && (!sum_out || a16(sum_out)))
+        lr = qg::launch_gemv_norm_glu(gu->plan, gu->d, gu->nbytes, gu->rows, gu->cols, xa, xb, nw, eps, sum_out,
+                                      h, sti);
+    if (lr == -1) {
+        int rc = qg_norm_matvec(ctx, gu, xa, xb, nw, eps, sum_out, gu_out, scratch, st);
+        if (rc) return rc;
+        lr = qg::launch_silu_mul(gu_out, gu_out + half, h, half, sti);
+    }
+    return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
+}
+
 int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out)
 {
     *out = nullptr;
@@ -290,6 +308,7 @@ int qg_destroy(qg_ctx *ctx)
     if (ctx->d_x) (void)hipFree(ctx->d_x);
     if (ctx->d_y) (void)hipFree(ctx->d_y);
     if (ctx->d_norm) (void)hipFree(ctx->d_norm);
+    if (ctx->d_glu) (void)hipFree(ctx->d_glu);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QG_OK;
@@ -395,6 +414,41 @@ int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const 
     QG_HIP(ctx, hipSetDevice(ctx->device));
     if ((rc = grow_device(ctx, &ctx->d_norm, &ctx->d_norm_cap, n))) return rc;
     return qg_norm_matvec(ctx, mat, d_xa, d_xb, d_nw, eps, d_sum_out, d_y, ctx->d_norm, pick(ctx, stream));
+}
+
+int qg_matvec_norm_glu_dev(qg_ctx *ctx, const qg_mat *gu, const float *d_xa, const float *d_xb,
+                           const float *d_nw, float eps, float *d_sum_out, float *d_h, void *stream)
+{
+    int rc = check_mat(ctx, gu);
+    if (rc) return rc;
+    if (gu->rows % 2 != 0) return fail(ctx, QG_ERR_SHAPE, "[gate; up] matrix with an odd row count");
+    if (gu->rows == 0 && !d_sum_out) return QG_OK;
+    const size_t n = gu->cols;
+    if (!d_h || (n > 0 && (!d_xa || !d_nw))) return fail(ctx, QG_ERR_INVALID_ARG, "xa, nw or h is NULL");
+    auto a4 = [](const void *p) { return ((uintptr_t)p & 3u) == 0; };
+    if (!a4(d_xa) || !a4(d_xb) || !a4(d_nw) || !a4(d_sum_out) || !a4(d_h))
+        return fail(ctx, QG_ERR_INVALID_ARG, "vectors not 4-byte aligned");
+    auto overlap = [n](const float *p, const float *q) { return p && q && p < q + n && q < p + n; };
+    if (overlap(d_sum_out, d_xa) || overlap(d_sum_out, d_xb))
+        return fail(ctx, QG_ERR_INVALID_ARG, "sum_out overlaps xa or xb");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if ((rc = grow_device(ctx, &ctx->d_norm, &ctx->d_norm_cap, n)) ||
+        (rc = grow_device(ctx, &ctx->d_glu, &ctx->d_glu_cap, gu->rows)))
+        return rc;
+    return qg_norm_glu_matvec(ctx, gu, d_xa, d_xb, d_nw, eps, d_sum_out, d_h, ctx->d_glu, ctx->d_norm,
+                              pick(ctx, stream));
+}
+
+int qg_mat_stack(qg_ctx *ctx, qg_mat *const *parts, int n_parts, qg_mat **out)
+{
+    if (!out) return fail(ctx, QG_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (!ctx || !parts || n_parts < 1) return fail(ctx, QG_ERR_INVALID_ARG, "no parts");
+    for (int i = 0; i < n_parts; i++) {
+        int rc = check_mat(ctx, parts[i]);
+        if (rc) return rc;
+    }
+    return qg_stack_mats(ctx, parts, n_parts, out);
 }
 
 int qg_matvec_silu_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_g, const float *d_u, float *d_y,

@@ -869,6 +869,9 @@ struct StreamArgs {
     const float *nw;               // norm weights, cols floats
     float *sum_out;                // if not NULL, workgroup 0 stores x + xb here
     float eps;
+    // gate/up pairs (GLU kernels): the matrix is [gate; up] with glu_half rows
+    // each; y[j] = silu(gate_j . x) * (up_j . x), glu_half floats
+    uint32_t glu_half;
 };
 
 // 16 bytes of v to p as an inline-asm store (not counted by the compiler's
@@ -901,15 +904,23 @@ __device__ __forceinline__ void lds_barrier()
 // unconditional (row groups past the end read the matrix's first bytes and
 // are masked out later) so that all of them are in flight together.  Byte
 // offsets fit in 32 bits (the planner sends larger matrices elsewhere).
-template <uint32_t T, int R>
+// GLU (R = 1): batches alternate gate row j and up row j, j = t + (i/2)*NT.
+template <uint32_t T, int R, bool GLU = false>
 __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t i, uint32_t it,
                                       uint32_t ib, bool active, uint32_t (&raw)[R][Item<T>::NRAW])
 {
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const uint32_t grp = t + (i * R + r) * a.n_teams;
+        uint32_t grp, lim;
+        if constexpr (GLU) {
+            lim = t + (i >> 1) * a.n_teams;
+            grp = lim + (i & 1u) * a.glu_half;
+        } else {
+            grp = t + (i * R + r) * a.n_teams;
+            lim = grp;
+        }
         const uint32_t off = grp * a.group_bytes + ib;
-        const bool ok = active && grp < a.n_groups && off < a.nbytes;
+        const bool ok = active && lim < (GLU ? a.glu_half : a.n_groups) && off < a.nbytes;
         Item<T>::load(a.w + (ok ? off : 0u), it, raw[r]);
     }
 }
@@ -941,10 +952,14 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 //             also stores the residual sum.
 //   kProSilu: the input is silu(a.x) * a.xb, elementwise (mlp.rs:36-43 with
 //             math.rs:137-146).
+// GLU: y[j] = silu(gate_j . x) * (up_j . x) over the [gate; up] matrix
+// (mlp.rs:31-43), the two dot products of a pair run by one team in
+// consecutive batches (one-wave-or-less teams, one row per group).
 template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
-          int PRO = kProPlain>
+          int PRO = kProPlain, bool GLU = false>
 __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 {
+    static_assert(!GLU || (G1 && R == 1 && TSUB != 0 && D % 2 == 0), "GLU pairs need single-row teams");
     constexpr bool NORM = PRO == kProNorm, TWO = PRO != kProPlain;
     using I = Item<T>;
     constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
@@ -984,7 +999,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t raw[D][R][NR];
 #pragma unroll
-    for (int d = 0; d < D0; d++) issue<T, R>(a, team, d, it, ib, active, raw[d]);
+    for (int d = 0; d < D0; d++) issue<T, R, GLU>(a, team, d, it, ib, active, raw[d]);
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
@@ -1099,7 +1114,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 
     // the rest of the ring, now that no conversion work waits behind it
 #pragma unroll
-    for (int d = D0; d < D; d++) issue<T, R>(a, team, d, it, ib, active, raw[d]);
+    for (int d = D0; d < D; d++) issue<T, R, GLU>(a, team, d, it, ib, active, raw[d]);
 
     // 3. stream the batches
     float *red = (float *)(lds + a.red_off);
@@ -1117,6 +1132,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
         }
         lds_barrier();
     };
+    float gate = 0.f;              // GLU: the gate dot product of the pair in progress
     auto process = [&](const uint32_t (&rw)[R][NR], uint32_t i) {
         float v[RED];
 #pragma unroll
@@ -1149,7 +1165,12 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
                 }
             }
         }
-        if constexpr (TSUB != 0) {
+        if constexpr (GLU) {
+            const float sum = group_sum<TSUB>(v[0]);
+            const uint32_t j = team + (i >> 1) * a.n_teams;
+            if ((i & 1u) == 0) gate = sum;
+            else if (lt == (uint32_t)TSUB - 1u && j < a.glu_half) store_y(a.y + j, silu1(gate) * sum);
+        } else if constexpr (TSUB != 0) {
 #pragma unroll
             for (int k = 0; k < RED; k++) {
                 const uint32_t r = G1 ? k : k / 8, gi = G1 ? 0 : k % 8;
@@ -1176,7 +1197,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 #pragma unroll
         for (int d = 0; d < D; d++) {
             process(raw[d], i + d);
-            issue<T, R>(a, team, i + d + D, it, ib, active, raw[d]);
+            issue<T, R, GLU>(a, team, i + d + D, it, ib, active, raw[d]);
         }
     }
 #pragma unroll
@@ -1200,6 +1221,19 @@ template <uint32_t T, bool G1, int PRO> static const void *stream_fn_g(uint32_t 
     case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, PRO>;
     case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, PRO>;
     case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB, D, PRO>;
+    default: return nullptr;
+    }
+}
+
+// [gate; up] kernels with the RMSNorm prologue (one-row groups, teams of one
+// wave or less)
+template <uint32_t T> static const void *stream_fn_glu(uint32_t tsub)
+{
+    constexpr int R = 1, D = kDepth, LB = wg_max<T>();
+    switch (tsub) {
+    case 16: return (const void *)gemv_stream<T, 16, R, D, true, true, kStage, LB, D, kProNorm, true>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, true, true, kStage, LB, D, kProNorm, true>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, true, true, kStage, LB, D, kProNorm, true>;
     default: return nullptr;
     }
 }
@@ -1237,6 +1271,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     constexpr int PN = I::PLANES ? kProNorm : kProPlain, PS = I::PLANES ? kProSilu : kProPlain;
     const void *fn_norm = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
     const void *fn_silu = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
+    const void *fn_norm_glu = I::PLANES && g == 1 ? stream_fn_glu<T>(tsub) : nullptr;
     if (!fn) return;
     const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
     const uint32_t img = (image_bytes(I::PLANES, (uint32_t)cols) + 15u) & ~15u;
@@ -1273,6 +1308,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     p->fn = fn;
     p->fn_norm = fn_norm;
     p->fn_silu = fn_silu;
+    p->fn_norm_glu = fn_norm_glu;
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
     p->ts = tl;
@@ -1353,6 +1389,26 @@ int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows
     a.xb = xb; a.nw = nw; a.sum_out = sum_out; a.eps = eps;
     void *args[] = {&a};
     return hipLaunchKernel(p.fn_norm, dim3(p.grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
+                   hipSuccess ? 0 : -2;
+}
+
+// Teams keep the plan's batches per team, rounded up to whole (gate, up)
+// pairs; the grid covers the glu_half pairs.
+int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                         const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
+                         float *y, ihipStream_t *stream)
+{
+    if (p.kind != 1 || !p.fn_norm_glu || p.g != 1 || p.tsub == 0 || rows % 2 != 0 || cols % 4 != 0) return -1;
+    const uint32_t half = (uint32_t)(rows / 2), tpw = p.block / p.ts;
+    const uint32_t pairs = (p.per_team + 1) / 2;
+    const uint32_t grid = (half + tpw * pairs - 1) / (tpw * pairs);
+    StreamArgs a = stream_args(p, w, nbytes, rows, cols, xa, y);
+    a.n_teams = grid * tpw;
+    a.per_team = 2 * pairs;
+    a.glu_half = half;
+    a.xb = xb; a.nw = nw; a.sum_out = sum_out; a.eps = eps;
+    void *args[] = {&a};
+    return hipLaunchKernel(p.fn_norm_glu, dim3(grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
                    hipSuccess ? 0 : -2;
 }
 

@@ -137,6 +137,23 @@ def test_long_sequence(rinf, synth, oracle, ctx):
     dev.close()
 
 
+@pytest.mark.parametrize("embed", [256, 512], ids=["hd64", "hd128"])
+def test_long_ranges(rinf, synth, oracle, ctx, embed):
+    """~600 cached positions over 64 ranges of 10: a wave runs two chunks of
+    positions, and the appended slot sits in a later chunk of its range.  At
+    this length a few steps' softmax is nearly one-hot (ulp-level score
+    differences reach 1e-4 in the logits), so the maximum is held to
+    DEEP_TOL and the typical step to 1e-5."""
+    cfg = dict(SMALL, n_layers=1, embed_dim=embed, hidden_dim=2 * embed)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q8_0", 23, 640)
+    prompt = np.random.default_rng(10).integers(0, cfg["vocab_size"], 590)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 12)
+    print(f"ranges {embed}: max logits err {max(errs):.2e}, median {np.median(errs):.2e}", flush=True)
+    assert max(errs) <= DEEP_TOL
+    assert np.median(errs) <= 1e-5
+    dev.close()
+
+
 def test_graph_replay_matches_eager(rinf, synth, oracle, ctx):
     """Graph replays give the logits of one-launch-per-kernel execution, bit for
     bit, with other GPU work and synchronisations between the replays."""

@@ -128,3 +128,105 @@ def test_silu_matvec_parity(ctx, rinf, oracle, synth, dtype, shape):
     err = normwise_err(y, ref)
     print(f"silu {NAMES[dtype]} {rows}x{cols} err={err:.2e}", flush=True)
     assert err <= GEMV_TOL
+
+
+GLU_SHAPES = [(t, s) for t in TYPES for s in [(600, 256), (1200, 256), (4864, 896), (40, 512)]] + \
+    [(t, s) for t in (12, 13, 14, 8, 2, 6) for s in [(18944, 3584), (14336, 4096)]]
+
+
+def glu_inputs(synth, dtype, H, cols, seed):
+    gate = synth.gen_blocks(dtype, H, cols, seed)
+    up = synth.gen_blocks(dtype, H, cols, seed + 1)
+    return gate, up
+
+
+@pytest.mark.parametrize("dtype,shape", GLU_SHAPES, ids=[f"{NAMES[t]}-{h}x{c}" for t, (h, c) in GLU_SHAPES])
+def test_norm_glu_matvec_parity(ctx, rinf, oracle, synth, dtype, shape):
+    """qg_matvec_norm_glu_dev on qg_mat_stack([gate, up]): h = silu(gate.x) *
+    (up.x) with x = rmsnorm(xa + xb) * nw (mlp.rs:31-43) within GEMV_TOL of
+    the oracle; within a few ulp of silu applied to the stacked matrix's own
+    norm mat-vec (the pairing kernel forms the same dot products); sum_out
+    bit-exact."""
+    import torch
+    H, cols = shape
+    seed = synth.config_seed(1) + 7 * H + cols + dtype
+    gate, up = glu_inputs(synth, dtype, H, cols, seed)
+    xa, xb, nw = inputs(synth, H, cols, seed)
+    mg, mu = ctx.upload(gate, dtype, H, cols), ctx.upload(up, dtype, H, cols)
+    gu = ctx.stack([mg, mu])
+    mg.free()
+    mu.free()
+    assert (gu.rows, gu.cols) == (2 * H, cols)
+    dev = lambda a: torch.from_numpy(a).cuda()
+    dxa, dxb, dnw = dev(xa), dev(xb), dev(nw)
+    dh = torch.full((H,), float("nan"), dtype=torch.float32, device="cuda")
+    ds = torch.full((cols,), float("nan"), dtype=torch.float32, device="cuda")
+    dy = torch.full((2 * H,), float("nan"), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    gu.matvec_norm_glu_dev(dxa, dxb, dnw, EPS, dh, ds, stream)
+    gu.matvec_norm_dev(dxa, dxb, dnw, EPS, dy, None, stream)
+    torch.cuda.synchronize()
+    h, s, y = dh.cpu().numpy(), ds.cpu().numpy(), dy.cpu().numpy().astype(np.float64)
+    kind = gu.kernel_kind
+    gu.free()
+    x = (xa + xb).astype(np.float32)
+    assert np.array_equal(s.view(np.uint32), x.view(np.uint32))
+    xn = oracle.rmsnorm(x, nw, EPS)
+    g_ref = oracle.mat_vec_mul_rows(gate, dtype, H, cols, xn)
+    u_ref = oracle.mat_vec_mul_rows(up, dtype, H, cols, xn)
+    ref = np.array([oracle.silu(float(v)) for v in g_ref], np.float32) * u_ref
+    err = normwise_err(h, ref)
+    # silu in float64 of the device's own gate/up values
+    g64, u64 = y[:H], y[H:]
+    own = g64 / (1.0 + np.exp(-g64)) * u64
+    ulp = np.abs(h - own) / np.maximum(np.abs(own), 1e-30)
+    print(f"glu {NAMES[dtype]} {H}x{cols} kernel={kind} err={err:.2e} max rel vs own {ulp.max():.1e}", flush=True)
+    assert err <= GEMV_TOL
+    assert ulp.max() <= 6e-7
+
+
+def test_glu_and_stack_errors(ctx, rinf, synth):
+    import torch
+    m = ctx.upload(synth.gen_blocks(8, 65, 256, 3), 8, 65, 256)
+    xa = torch.zeros(256, dtype=torch.float32, device="cuda")
+    h = torch.zeros(65, dtype=torch.float32, device="cuda")
+    with pytest.raises(rinf.QgemvError) as e:
+        m.matvec_norm_glu_dev(xa, xa, xa, EPS, h)              # odd row count
+    assert e.value.status == 7                                 # QG_ERR_SHAPE
+    # a first part that does not end on a block boundary
+    a = ctx.upload(synth.gen_blocks(12, 1, 288, 4), 12, 1, 288)
+    b = ctx.upload(synth.gen_blocks(12, 1, 288, 5), 12, 1, 288)
+    c = ctx.upload(synth.gen_blocks(8, 1, 288, 6), 8, 1, 288)
+    with pytest.raises(rinf.QgemvError) as e:
+        ctx.stack([a, b])
+    assert e.value.status == 7
+    with pytest.raises(rinf.QgemvError) as e:
+        ctx.stack([c, a])                                      # types differ
+    assert e.value.status == 7
+    for x in (m, a, b, c):
+        x.free()
+
+
+@pytest.mark.parametrize("dtype", [12, 14, 8, 1], ids=["Q4_K", "Q6_K", "Q8_0", "F16"])
+def test_stacked_matvec_bit_exact(ctx, rinf, synth, dtype):
+    """qg_mat_stack([A, B, C]) · x is A · x, B · x, C · x one after the other,
+    bit for bit (rows are formed by the same per-row code)."""
+    import torch
+    cols, rows = 1024, (512, 128, 300)
+    parts = [synth.gen_blocks(dtype, r, cols, 60 + i) for i, r in enumerate(rows)]
+    mats = [ctx.upload(p, dtype, r, cols) for p, r in zip(parts, rows)]
+    st = ctx.stack(mats)
+    x = torch.from_numpy(np.random.default_rng(9).standard_normal(cols).astype(np.float32)).cuda()
+    ys = [torch.zeros(r, dtype=torch.float32, device="cuda") for r in rows]
+    y = torch.zeros(sum(rows), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    for m, yy in zip(mats, ys):
+        m.matvec_dev(x, yy, stream)
+    st.matvec_dev(x, y, stream)
+    torch.cuda.synchronize()
+    cat = torch.cat(ys).cpu().numpy()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), cat.view(np.uint32))
+    for m in mats + [st]:
+        m.free()
