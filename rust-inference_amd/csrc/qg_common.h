@@ -82,6 +82,15 @@ int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows
 int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
                          const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
                          float *y, ihipStream_t *stream);
+// y1 = W1 · x and y2 = W2 · x, x = rmsnorm(xa + xb) * nw, in one launch (two
+// matrices with the same cols, one row per group, teams of one wave or less,
+// supported type pairs Q4_K/Q5_K with Q6_K; -1 otherwise).  sum_out (may be
+// NULL) receives xa + xb.  n_cu: the device's compute units (both parts are
+// sized to be resident together).
+int launch_gemv_norm_pair(uint32_t t1, const Plan &p1, const uint8_t *w1, size_t nbytes1, size_t rows1, float *y1,
+                          uint32_t t2, const Plan &p2, const uint8_t *w2, size_t nbytes2, size_t rows2, float *y2,
+                          size_t cols, const float *xa, const float *xb, const float *nw, float eps,
+                          float *sum_out, int n_cu, ihipStream_t *stream);
 // y = W · (silu(g) * u) with the stream kernel (kind 1 plans only; -1
 // otherwise).  g, u: cols floats, 16-byte aligned.
 int launch_gemv_silu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,

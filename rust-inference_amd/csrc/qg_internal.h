@@ -67,6 +67,14 @@ int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *
 int qg_norm_glu_matvec(qg_ctx *ctx, const qg_mat *gu, const float *xa, const float *xb, const float *nw,
                        float eps, float *sum_out, float *h, float *gu_out, float *scratch, hipStream_t stream);
 
+// y1 = W1 · x, y2 = W2 · x with x = rmsnorm(xa + xb) * nw (same cols): one
+// launch when the pair is supported and the pointers are 16-byte aligned;
+// otherwise two qg_norm_matvec calls (scratch: cols floats).  sum_out (may be
+// NULL) = xa + xb.  Asynchronous.
+int qg_norm_pair_matvec(qg_ctx *ctx, const qg_mat *m1, const qg_mat *m2, const float *xa, const float *xb,
+                        const float *nw, float eps, float *sum_out, float *y1, float *y2, float *scratch,
+                        hipStream_t stream);
+
 // One owned matrix whose rows are the rows of parts[0], parts[1], ... (same
 // type and cols; every part but the last a whole number of blocks): device
 // copies of the parts' blocks, one after the other.  Synchronous.

@@ -759,10 +759,11 @@ int enqueue_forward(qg_model *m)
         if (nq == 3) {
             if ((rc = gemv_norm(m, m->f_qkv[l], na, nb, anorm, res, m->q))) return rc;
         } else if (nq == 2) {
-            // (running V beside [Q;K] as a graph branch on a second stream
-            // measured slower than one after the other)
-            if ((rc = gemv_norm(m, m->f_qkv[l], na, nb, anorm, res, m->q)) ||
-                (rc = gemv_norm(m, m->w[QG_M_WV - 2][l], na, nb, anorm, nullptr, m->v)))
+            // [Q;K] and V (another type) in one launch where the pair is
+            // supported (a graph branch on a second stream measured slower
+            // than one launch after the other)
+            if ((rc = qg_norm_pair_matvec(m->ctx, m->f_qkv[l], m->w[QG_M_WV - 2][l], na, nb, anorm, c.norm_eps, res,
+                                          m->q, m->v, m->xn, st)))
                 return rc;
         } else if ((rc = gemv_norm(m, m->w[QG_M_WQ - 2][l], na, nb, anorm, res, m->q)) ||
                    (rc = gemv_norm(m, m->w[QG_M_WK - 2][l], na, nb, anorm, nullptr, m->k)) ||

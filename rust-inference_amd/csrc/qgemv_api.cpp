@@ -211,6 +211,22 @@ int qg_norm_glu_matvec(qg_ctx *ctx, const qg_mat *gu, const float *xa, const flo
     return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
 }
 
+int qg_norm_pair_matvec(qg_ctx *ctx, const qg_mat *m1, const qg_mat *m2, const float *xa, const float *xb,
+                        const float *nw, float eps, float *sum_out, float *y1, float *y2, float *scratch,
+                        hipStream_t st)
+{
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    int lr = -1;
+    if (m1->cols == m2->cols && m1->cols > 0 && xb && a16(xa) && a16(xb) && a16(nw) && (!sum_out || a16(sum_out)))
+        lr = qg::launch_gemv_norm_pair(m1->type, m1->plan, m1->d, m1->nbytes, m1->rows, y1, m2->type, m2->plan,
+                                       m2->d, m2->nbytes, m2->rows, y2, m1->cols, xa, xb, nw, eps, sum_out,
+                                       ctx->n_cu, (ihipStream_t *)st);
+    if (lr == 0) return QG_OK;
+    if (lr != -1) return fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError());
+    int rc = qg_norm_matvec(ctx, m1, xa, xb, nw, eps, sum_out, y1, scratch, st);
+    return rc ? rc : qg_norm_matvec(ctx, m2, xa, xb, nw, eps, nullptr, y2, scratch, st);
+}
+
 int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out)
 {
     *out = nullptr;

@@ -17,6 +17,9 @@
 //                     team streams its row groups
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
+
 #include <type_traits>
 
 #include "qg_common.h"
@@ -955,9 +958,12 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 // GLU: y[j] = silu(gate_j . x) * (up_j . x) over the [gate; up] matrix
 // (mlp.rs:31-43), the two dot products of a pair run by one team in
 // consecutive batches (one-wave-or-less teams, one row per group).
+//
+// stream_body runs workgroup `bid` of such a launch; gemv_stream is the
+// kernel of one matrix, gemv_stream_pair runs two matrices in one grid.
 template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
           int PRO = kProPlain, bool GLU = false>
-__global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
+__device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 {
     static_assert(!GLU || (G1 && R == 1 && TSUB != 0 && D % 2 == 0), "GLU pairs need single-row teams");
     constexpr bool NORM = PRO == kProNorm, TWO = PRO != kProPlain;
@@ -974,7 +980,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     const bool active = lt < a.ni;
     const uint32_t it = active ? lt : 0u;
     const uint32_t ib = I::item_byte(it);
-    const uint32_t team = blockIdx.x * tpw + tw;
+    const uint32_t team = bid * tpw + tw;
     const uint32_t g = G1 ? 1u : a.g;
 
     // 1. x loads, then (once x is in) the first D batches of weight loads
@@ -1009,7 +1015,7 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
     };
     if constexpr (NORM) {
         // x = a + b; sum of squares in element order within each thread
-        const bool w0 = blockIdx.x == 0 && a.sum_out;
+        const bool w0 = bid == 0 && a.sum_out;
         auto addv = [](uint4 p, uint4 q) {
             const float4 u = __builtin_bit_cast(float4, p), v = __builtin_bit_cast(float4, q);
             return make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
@@ -1203,6 +1209,27 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 #pragma unroll
     for (int d = 0; d < D; d++)
         if (i + d < a.per_team) process(raw[d], i + d);
+}
+
+template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
+          int PRO = kProPlain, bool GLU = false>
+__global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
+{
+    stream_body<T, TSUB, R, D, G1, CONV, XS, LB, D0, PRO, GLU>(a, blockIdx.x);
+}
+
+// Two matrices with the same input, each with its own type and plan, in one
+// launch: workgroups [0, grid1) run a1 (type T1, teams of TS1 lanes), the rest
+// run a2 (T2, TS2) -- for a projection whose parts have different types
+// ([Q;K] Q4_K beside V Q6_K in the Q4_K_M mix), so the small part does not
+// pay a launch and an x staging of its own.  RMSNorm prologue, one-row groups.
+template <uint32_t T1, int TS1, uint32_t T2, int TS2, int LB>
+__global__ void __launch_bounds__(LB) gemv_stream_pair(StreamArgs a1, StreamArgs a2, uint32_t grid1)
+{
+    if (blockIdx.x < grid1)
+        stream_body<T1, TS1, 1, kDepth, true, true, kStage, LB, kDepth, kProNorm>(a1, blockIdx.x);
+    else
+        stream_body<T2, TS2, 1, kDepth, true, true, kStage, LB, kDepth, kProNorm>(a2, blockIdx.x - grid1);
 }
 
 // ------------------------------------------------------------ planning
@@ -1410,6 +1437,83 @@ int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t 
     void *args[] = {&a};
     return hipLaunchKernel(p.fn_norm_glu, dim3(grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
                    hipSuccess ? 0 : -2;
+}
+
+// ------------------------------------------------------ pairs of matrices
+
+constexpr int kPairBlock = 512;
+
+template <uint32_t T1, uint32_t T2> static const void *pair_fn(uint32_t ts1, uint32_t ts2)
+{
+    constexpr int LB = kPairBlock;
+    if (ts1 == 16 && ts2 == 16) return (const void *)gemv_stream_pair<T1, 16, T2, 16, LB>;
+    if (ts1 == 16 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 16, T2, 32, LB>;
+    if (ts1 == 32 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 32, T2, 32, LB>;
+    if (ts1 == 32 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 32, T2, 64, LB>;
+    if (ts1 == 64 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 64, T2, 64, LB>;
+    return nullptr;
+}
+
+static bool pair_part_ok(const Plan &p)
+{
+    return p.kind == 1 && p.g == 1 && p.tsub != 0 && kPairBlock % p.ts == 0;
+}
+
+// Workgroups of kPairBlock threads for a part of n_batches batches, per
+// batches per team.
+static uint32_t pair_grid(const Plan &p, uint32_t per)
+{
+    const uint32_t tpw = kPairBlock / p.ts;
+    return (p.n_batches + tpw * per - 1) / (tpw * per);
+}
+
+// Resident workgroups of a pair kernel per CU (queried once per kernel).
+static int pair_occupancy(const void *fn, uint32_t lds)
+{
+    static std::mutex mu;
+    static std::map<std::pair<const void *, uint32_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({fn, lds});
+    if (it != cache.end()) return it->second;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kPairBlock, lds) != hipSuccess || occ < 1) occ = 1;
+    cache[{fn, lds}] = occ;
+    return occ;
+}
+
+int launch_gemv_norm_pair(uint32_t t1, const Plan &p1, const uint8_t *w1, size_t nbytes1, size_t rows1, float *y1,
+                          uint32_t t2, const Plan &p2, const uint8_t *w2, size_t nbytes2, size_t rows2, float *y2,
+                          size_t cols, const float *xa, const float *xb, const float *nw, float eps,
+                          float *sum_out, int n_cu, ihipStream_t *stream)
+{
+    const void *fn = nullptr;
+    if (t1 == T_Q4_K && t2 == T_Q6_K) fn = pair_fn<T_Q4_K, T_Q6_K>(p1.tsub, p2.tsub);
+    else if (t1 == T_Q5_K && t2 == T_Q6_K) fn = pair_fn<T_Q5_K, T_Q6_K>(p1.tsub, p2.tsub);
+    if (!fn || cols % 4 != 0 || !pair_part_ok(p1) || !pair_part_ok(p2)) return -1;
+    const uint32_t lds = p1.lds > p2.lds ? p1.lds : p2.lds;
+    // both parts resident at once (a part that waits for the other's
+    // workgroups to finish costs as much as a second launch): more batches
+    // per team for the part with more workgroups until they fit
+    const uint64_t slots = (uint64_t)(n_cu > 0 ? n_cu : 256) * (uint64_t)pair_occupancy(fn, lds);
+    uint32_t per1 = p1.per_team ? p1.per_team : 1u, per2 = p2.per_team ? p2.per_team : 1u;
+    uint32_t g1 = pair_grid(p1, per1), g2 = pair_grid(p2, per2);
+    while ((uint64_t)g1 + g2 > slots && (g1 > 1 || g2 > 1)) {
+        if (g1 >= g2) g1 = pair_grid(p1, ++per1);
+        else g2 = pair_grid(p2, ++per2);
+    }
+    StreamArgs a1 = stream_args(p1, w1, nbytes1, rows1, cols, xa, y1);
+    StreamArgs a2 = stream_args(p2, w2, nbytes2, rows2, cols, xa, y2);
+    a1.n_teams = g1 * (kPairBlock / p1.ts);
+    a2.n_teams = g2 * (kPairBlock / p2.ts);
+    a1.per_team = per1;
+    a2.per_team = per2;
+    a1.xb = a2.xb = xb;
+    a1.nw = a2.nw = nw;
+    a1.eps = a2.eps = eps;
+    a1.sum_out = sum_out;
+    void *args[] = {&a1, &a2, &g1};
+    return hipLaunchKernel(fn, dim3(g1 + g2), dim3(kPairBlock), args, lds, (hipStream_t)stream) == hipSuccess ? 0
+                                                                                                             : -2;
 }
 
 template <uint32_t T>
