@@ -81,6 +81,7 @@ MIXES = {
     # slot -> GGML type; "base" covers every matrix not listed
     "q4_k_m": dict(base=12, wv=14, down=14, lm_head=14),
     "q5_k": dict(base=13, lm_head=14),
+    "q5_k_m": dict(base=13, wv=14, down=14, lm_head=14),
     "q8_0": dict(base=8, lm_head=8),
     "f16": dict(base=1, lm_head=1),          # no fused-norm kernel: separate RMSNorm path
 }

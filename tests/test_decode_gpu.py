@@ -154,15 +154,16 @@ def test_long_ranges(rinf, synth, oracle, ctx, embed):
     dev.close()
 
 
-def test_qwen2_7b_layer_shape(rinf, synth, oracle, ctx):
-    """One layer of the Qwen2-7B shape in the Q4_K_M mix: [Q;K] (Q4_K) and V
-    (Q6_K) in one launch, gate/up paired at 3584 cols, 7 query heads per kv
-    head of dim 128."""
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m"])
+def test_qwen2_7b_layer_shape(rinf, synth, oracle, ctx, mix):
+    """One layer of the Qwen2-7B shape: [Q;K] (Q4_K or Q5_K) and V (Q6_K) in
+    one launch, gate/up paired at 3584 cols, 7 query heads per kv head of dim
+    128."""
     cfg = dict(SMALL, n_layers=1, embed_dim=3584, n_heads=28, n_kv_heads=4, hidden_dim=1024)
-    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", 29, 64)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, mix, 29, 64)
     prompt = np.random.default_rng(12).integers(0, cfg["vocab_size"], 12)
     out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 8)
-    print(f"7b layer: max logits err {max(errs):.2e}, median {np.median(errs):.2e}", flush=True)
+    print(f"7b layer {mix}: max logits err {max(errs):.2e}, median {np.median(errs):.2e}", flush=True)
     assert max(errs) <= DEEP_TOL
     assert np.median(errs) <= 1e-5
     dev.close()
