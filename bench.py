@@ -101,21 +101,60 @@ def time_gemv(ctx, torch, mats, dx, dy, steps, warmup):
     return eager, graph, per
 
 
-def cpu_baseline(oracle, raw, dtype, rows, cols, x, seconds, nbytes):
-    """Single-thread CPU port of the reference's --cpu loop, bounded sample."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def _time_loop(fn, seconds):
     times = []
     t_end = time.perf_counter() + seconds
     while True:
         t0 = time.perf_counter()
-        oracle.mat_vec_mul(raw, dtype, rows, cols, x)
+        fn()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() >= t_end and len(times) >= 3:
-            break
-    med = statistics.median(times)
-    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{len(times)} full Q4_K {rows}x{cols} GEMVs (median {med * 1e3:.1f} ms each) "
-                      f"through oracle/qref.c's restatement of src/quant.rs:188-205, one thread",
-            "us_per_gemv": round(med * 1e6, 1)}
+        if time.perf_counter() >= t_end and len(times) >= 5:
+            return times
+
+
+def cpu_baseline(oracle, raw, dtype, rows, cols, x, seconds, nbytes):
+    """Both reference CPU paths, restated in oracle/qref.c, single-threaded and
+    pinned to one core (the reference has no threads): (A) the --cpu loop of
+    QuantizedMatrix::mat_vec_mul (src/quant.rs:188-205), reported as `value`,
+    and (B) fallback_cpu (src/gpu_backend.rs:543-567: dequantize, then
+    mat_vec_mul_transposed), reported beside it.  Bounded sample: about
+    `seconds` of CPU work for (A) and a third of that for (B)."""
+    pinned = None
+    if hasattr(os, "sched_getaffinity"):
+        old = os.sched_getaffinity(0)
+        core = min(old)
+        try:
+            os.sched_setaffinity(0, {core})
+            pinned = core
+        except OSError:
+            old = None
+    try:
+        ta = _time_loop(lambda: oracle.mat_vec_mul(raw, dtype, rows, cols, x), seconds)
+        tb = _time_loop(lambda: oracle.fallback_cpu(raw, dtype, rows, cols, x), seconds / 3)
+    finally:
+        if pinned is not None and old:
+            os.sched_setaffinity(0, old)
+    ma, mb = statistics.median(ta), statistics.median(tb)
+    where = f"core {pinned} of {os.cpu_count()} ({_cpu_model()})" if pinned is not None else \
+        f"1 thread, unpinned, of {os.cpu_count()} ({_cpu_model()})"
+    return {"value": round(nbytes / ma / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{len(ta)} full Q4_K {rows}x{cols} GEMVs (median {ma * 1e3:.1f} ms each) through "
+                      f"oracle/qref.c's restatement of src/quant.rs:188-205, one thread on {where}",
+            "us_per_gemv": round(ma * 1e6, 1),
+            "fallback_cpu": {"value": round(nbytes / mb / 1e9, 4), "unit": "GB/s",
+                             "us_per_gemv": round(mb * 1e6, 1), "runs": len(tb),
+                             "path": "src/gpu_backend.rs:543-567 (dequantize + mat_vec_mul_transposed)"}}
 
 
 def decode_run(rinf, synth, ctx, args):
