@@ -98,10 +98,10 @@ int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const 
  * src/math.rs:137-146, its input as in qg_matvec_norm_dev).  gu is the stacked
  * [gate; up] matrix (qg_mat_stack; 2 * H rows, gate rows first); h: H floats;
  * xa, xb, nw, sum_out as in qg_matvec_norm_dev.  With 16-byte aligned
- * vectors, a non-NULL d_xb, a quantized type and short whole-block rows
- * (cols <= 8192 for Q4_K, <= 4096 for Q5_K, Q6_K, Q8_0, Q4_0, Q5_0) one
- * kernel computes each gate row and its up row back to back and writes h
- * only; otherwise the [gate; up] outputs go to a context
+ * vectors, a non-NULL d_xb, a quantized type and short rows (row groups of
+ * at most 64 items: cols <= 8192 for Q4_K and <= 4096 for the other quant
+ * types when a row is whole blocks) one kernel computes each gate row and its
+ * up row back to back and writes h only; otherwise the [gate; up] outputs go to a context
  * scratch vector first (calls on one context must then not overlap on
  * different streams).  QG_ERR_SHAPE for an odd row count. */
 int qg_matvec_norm_glu_dev(qg_ctx *ctx, const qg_mat *gu, const float *d_xa, const float *d_xb,

@@ -76,15 +76,16 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
 int launch_gemv_norm(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
                      const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
                      float *y, ihipStream_t *stream);
-// W = [gate; up] (rows = 2 * half, one row per group, teams of one wave or
-// less; -1 otherwise): y[j] = silu(gate_j · x) * (up_j · x) for j < half,
-// x = rmsnorm(xa + xb) * nw as in launch_gemv_norm.
+// W = [gate; up] (each half a whole number of row groups, teams of one wave
+// or less; -1 otherwise): y[r] = silu(gate_r · x) * (up_r · x) for
+// r < rows / 2, x = rmsnorm(xa + xb) * nw as in launch_gemv_norm.
 int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
                          const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
                          float *y, ihipStream_t *stream);
 // y1 = W1 · x and y2 = W2 · x, x = rmsnorm(xa + xb) * nw, in one launch (two
-// matrices with the same cols, one row per group, teams of one wave or less,
-// supported type pairs Q4_K/Q5_K with Q6_K; -1 otherwise).  sum_out (may be
+// matrices with the same cols, teams of one wave or less, both with one row
+// per group or both with several, supported type pairs Q4_K/Q5_K with Q6_K;
+// -1 otherwise).  sum_out (may be
 // NULL) receives xa + xb.  n_cu: the device's compute units (both parts are
 // sized to be resident together).
 int launch_gemv_norm_pair(uint32_t t1, const Plan &p1, const uint8_t *w1, size_t nbytes1, size_t rows1, float *y1,

@@ -872,8 +872,8 @@ struct StreamArgs {
     const float *nw;               // norm weights, cols floats
     float *sum_out;                // if not NULL, workgroup 0 stores x + xb here
     float eps;
-    // gate/up pairs (GLU kernels): the matrix is [gate; up] with glu_half rows
-    // each; y[j] = silu(gate_j . x) * (up_j . x), glu_half floats
+    // gate/up pairs (GLU kernels): the matrix is [gate; up] with glu_half row
+    // groups each; y[r] = silu(gate_r . x) * (up_r . x), rows / 2 floats
     uint32_t glu_half;
 };
 
@@ -907,7 +907,8 @@ __device__ __forceinline__ void lds_barrier()
 // unconditional (row groups past the end read the matrix's first bytes and
 // are masked out later) so that all of them are in flight together.  Byte
 // offsets fit in 32 bits (the planner sends larger matrices elsewhere).
-// GLU (R = 1): batches alternate gate row j and up row j, j = t + (i/2)*NT.
+// GLU (R = 1): batches alternate gate row group j and up row group j,
+// j = t + (i/2)*NT.
 template <uint32_t T, int R, bool GLU = false>
 __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t i, uint32_t it,
                                       uint32_t ib, bool active, uint32_t (&raw)[R][Item<T>::NRAW])
@@ -955,9 +956,9 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 //             also stores the residual sum.
 //   kProSilu: the input is silu(a.x) * a.xb, elementwise (mlp.rs:36-43 with
 //             math.rs:137-146).
-// GLU: y[j] = silu(gate_j . x) * (up_j . x) over the [gate; up] matrix
-// (mlp.rs:31-43), the two dot products of a pair run by one team in
-// consecutive batches (one-wave-or-less teams, one row per group).
+// GLU: y[r] = silu(gate_r . x) * (up_r . x) over the [gate; up] matrix
+// (mlp.rs:31-43): one team runs row group j of gate and row group j of up in
+// consecutive batches (teams of one wave or less).
 //
 // stream_body runs workgroup `bid` of such a launch; gemv_stream is the
 // kernel of one matrix, gemv_stream_pair runs two matrices in one grid.
@@ -965,7 +966,7 @@ template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB
           int PRO = kProPlain, bool GLU = false>
 __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 {
-    static_assert(!GLU || (G1 && R == 1 && TSUB != 0 && D % 2 == 0), "GLU pairs need single-row teams");
+    static_assert(!GLU || (R == 1 && TSUB != 0 && D % 2 == 0), "GLU pairs need teams of a wave or less");
     constexpr bool NORM = PRO == kProNorm, TWO = PRO != kProPlain;
     using I = Item<T>;
     constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
@@ -1138,7 +1139,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
         }
         lds_barrier();
     };
-    float gate = 0.f;              // GLU: the gate dot product of the pair in progress
+    float gate[G1 ? 1 : 8] = {};   // GLU: the gate dot products of the pair in progress
     auto process = [&](const uint32_t (&rw)[R][NR], uint32_t i) {
         float v[RED];
 #pragma unroll
@@ -1158,8 +1159,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
                 }
                 v[r] = active ? t : 0.f;
             } else {
-                const uint32_t grp = team + (i * R + r) * a.n_teams;
-                const bool ok = active && grp < a.n_groups && grp * a.group_bytes + ib < a.nbytes;
+                uint32_t grp, lim, lim_n;
+                if constexpr (GLU) {
+                    lim = team + (i >> 1) * a.n_teams;
+                    grp = lim + (i & 1u) * a.glu_half;
+                    lim_n = a.glu_half;
+                } else {
+                    grp = team + (i * R + r) * a.n_teams;
+                    lim = grp;
+                    lim_n = a.n_groups;
+                }
+                const bool ok = active && lim < lim_n && grp * a.group_bytes + ib < a.nbytes;
                 float acc[S];
                 I::compute(rw[r], xs, it, acc);
 #pragma unroll
@@ -1172,10 +1182,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
             }
         }
         if constexpr (GLU) {
-            const float sum = group_sum<TSUB>(v[0]);
+            // group j of each half: rows j*g + gi of gate, then of up
             const uint32_t j = team + (i >> 1) * a.n_teams;
-            if ((i & 1u) == 0) gate = sum;
-            else if (lt == (uint32_t)TSUB - 1u && j < a.glu_half) store_y(a.y + j, silu1(gate) * sum);
+#pragma unroll
+            for (int gi = 0; gi < (G1 ? 1 : 8); gi++) {
+                if (!G1 && (uint32_t)gi >= g) continue;
+                const float sum = group_sum<TSUB>(v[gi]);
+                const uint32_t row = j * g + gi;
+                if ((i & 1u) == 0) gate[gi] = sum;
+                else if (lt == (uint32_t)TSUB - 1u && j < a.glu_half && row < a.rows / 2u)
+                    store_y(a.y + row, silu1(gate[gi]) * sum);
+            }
         } else if constexpr (TSUB != 0) {
 #pragma unroll
             for (int k = 0; k < RED; k++) {
@@ -1222,14 +1239,15 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 // launch: workgroups [0, grid1) run a1 (type T1, teams of TS1 lanes), the rest
 // run a2 (T2, TS2) -- for a projection whose parts have different types
 // ([Q;K] Q4_K beside V Q6_K in the Q4_K_M mix), so the small part does not
-// pay a launch and an x staging of its own.  RMSNorm prologue, one-row groups.
-template <uint32_t T1, int TS1, uint32_t T2, int TS2, int LB>
+// pay a launch and an x staging of its own.  RMSNorm prologue; G1A / G1B:
+// one row per group in that part.
+template <uint32_t T1, int TS1, bool G1A, uint32_t T2, int TS2, bool G1B, int LB>
 __global__ void __launch_bounds__(LB) gemv_stream_pair(StreamArgs a1, StreamArgs a2, uint32_t grid1)
 {
     if (blockIdx.x < grid1)
-        stream_body<T1, TS1, 1, kDepth, true, true, kStage, LB, kDepth, kProNorm>(a1, blockIdx.x);
+        stream_body<T1, TS1, 1, kDepth, G1A, true, kStage, LB, kDepth, kProNorm>(a1, blockIdx.x);
     else
-        stream_body<T2, TS2, 1, kDepth, true, true, kStage, LB, kDepth, kProNorm>(a2, blockIdx.x - grid1);
+        stream_body<T2, TS2, 1, kDepth, G1B, true, kStage, LB, kDepth, kProNorm>(a2, blockIdx.x - grid1);
 }
 
 // ------------------------------------------------------------ planning
@@ -1252,15 +1270,14 @@ template <uint32_t T, bool G1, int PRO> static const void *stream_fn_g(uint32_t 
     }
 }
 
-// [gate; up] kernels with the RMSNorm prologue (one-row groups, teams of one
-// wave or less)
-template <uint32_t T> static const void *stream_fn_glu(uint32_t tsub)
+// [gate; up] kernels with the RMSNorm prologue (teams of one wave or less)
+template <uint32_t T, bool G1> static const void *stream_fn_glu(uint32_t tsub)
 {
     constexpr int R = 1, D = kDepth, LB = wg_max<T>();
     switch (tsub) {
-    case 16: return (const void *)gemv_stream<T, 16, R, D, true, true, kStage, LB, D, kProNorm, true>;
-    case 32: return (const void *)gemv_stream<T, 32, R, D, true, true, kStage, LB, D, kProNorm, true>;
-    case 64: return (const void *)gemv_stream<T, 64, R, D, true, true, kStage, LB, D, kProNorm, true>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, kProNorm, true>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, kProNorm, true>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, kProNorm, true>;
     default: return nullptr;
     }
 }
@@ -1298,7 +1315,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     constexpr int PN = I::PLANES ? kProNorm : kProPlain, PS = I::PLANES ? kProSilu : kProPlain;
     const void *fn_norm = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
     const void *fn_silu = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
-    const void *fn_norm_glu = I::PLANES && g == 1 ? stream_fn_glu<T>(tsub) : nullptr;
+    const void *fn_norm_glu = !I::PLANES ? nullptr : g == 1 ? stream_fn_glu<T, true>(tsub) : stream_fn_glu<T, false>(tsub);
     if (!fn) return;
     const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
     const uint32_t img = (image_bytes(I::PLANES, (uint32_t)cols) + 15u) & ~15u;
@@ -1425,8 +1442,9 @@ int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t 
                          const float *xa, const float *xb, const float *nw, float eps, float *sum_out,
                          float *y, ihipStream_t *stream)
 {
-    if (p.kind != 1 || !p.fn_norm_glu || p.g != 1 || p.tsub == 0 || rows % 2 != 0 || cols % 4 != 0) return -1;
-    const uint32_t half = (uint32_t)(rows / 2), tpw = p.block / p.ts;
+    // each half a whole number of row groups
+    if (p.kind != 1 || !p.fn_norm_glu || p.tsub == 0 || rows % (2u * p.g) != 0 || cols % 4 != 0) return -1;
+    const uint32_t half = (uint32_t)(rows / 2 / p.g), tpw = p.block / p.ts;
     const uint32_t pairs = (p.per_team + 1) / 2;
     const uint32_t grid = (half + tpw * pairs - 1) / (tpw * pairs);
     StreamArgs a = stream_args(p, w, nbytes, rows, cols, xa, y);
@@ -1443,20 +1461,29 @@ int launch_gemv_norm_glu(const Plan &p, const uint8_t *w, size_t nbytes, size_t 
 
 constexpr int kPairBlock = 512;
 
-template <uint32_t T1, uint32_t T2> static const void *pair_fn(uint32_t ts1, uint32_t ts2)
+template <uint32_t T1, uint32_t T2, bool G1> static const void *pair_fn_g(uint32_t ts1, uint32_t ts2)
 {
     constexpr int LB = kPairBlock;
-    if (ts1 == 16 && ts2 == 16) return (const void *)gemv_stream_pair<T1, 16, T2, 16, LB>;
-    if (ts1 == 16 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 16, T2, 32, LB>;
-    if (ts1 == 32 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 32, T2, 32, LB>;
-    if (ts1 == 32 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 32, T2, 64, LB>;
-    if (ts1 == 64 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 64, T2, 64, LB>;
+    if (ts1 == 16 && ts2 == 16) return (const void *)gemv_stream_pair<T1, 16, G1, T2, 16, G1, LB>;
+    if (ts1 == 16 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 16, G1, T2, 32, G1, LB>;
+    if (ts1 == 32 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 32, G1, T2, 32, G1, LB>;
+    if (ts1 == 32 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 32, G1, T2, 64, G1, LB>;
+    if (ts1 == 64 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 64, G1, T2, 64, G1, LB>;
+    return nullptr;
+}
+
+// Both parts one-row groups, or both multi-row groups (the 896-column rows of
+// Qwen2-0.5B: two rows per group for the K-quants).
+template <uint32_t T1, uint32_t T2> static const void *pair_fn(const Plan &p1, const Plan &p2)
+{
+    if (p1.g == 1 && p2.g == 1) return pair_fn_g<T1, T2, true>(p1.tsub, p2.tsub);
+    if (p1.g > 1 && p2.g > 1) return pair_fn_g<T1, T2, false>(p1.tsub, p2.tsub);
     return nullptr;
 }
 
 static bool pair_part_ok(const Plan &p)
 {
-    return p.kind == 1 && p.g == 1 && p.tsub != 0 && kPairBlock % p.ts == 0;
+    return p.kind == 1 && p.tsub != 0 && kPairBlock % p.ts == 0;
 }
 
 // Workgroups of kPairBlock threads for a part of n_batches batches, per
@@ -1487,8 +1514,8 @@ int launch_gemv_norm_pair(uint32_t t1, const Plan &p1, const uint8_t *w1, size_t
                           float *sum_out, int n_cu, ihipStream_t *stream)
 {
     const void *fn = nullptr;
-    if (t1 == T_Q4_K && t2 == T_Q6_K) fn = pair_fn<T_Q4_K, T_Q6_K>(p1.tsub, p2.tsub);
-    else if (t1 == T_Q5_K && t2 == T_Q6_K) fn = pair_fn<T_Q5_K, T_Q6_K>(p1.tsub, p2.tsub);
+    if (t1 == T_Q4_K && t2 == T_Q6_K) fn = pair_fn<T_Q4_K, T_Q6_K>(p1, p2);
+    else if (t1 == T_Q5_K && t2 == T_Q6_K) fn = pair_fn<T_Q5_K, T_Q6_K>(p1, p2);
     if (!fn || cols % 4 != 0 || !pair_part_ok(p1) || !pair_part_ok(p2)) return -1;
     const uint32_t lds = p1.lds > p2.lds ? p1.lds : p2.lds;
     // both parts resident at once (a part that waits for the other's

@@ -130,7 +130,10 @@ def test_silu_matvec_parity(ctx, rinf, oracle, synth, dtype, shape):
     assert err <= GEMV_TOL
 
 
-GLU_SHAPES = [(t, s) for t in TYPES for s in [(600, 256), (1200, 256), (4864, 896), (40, 512)]] + \
+# (4864, 896): two rows per group for the K-quants; (64, 288) and (1000, 288):
+# eight rows per group (rows of 9 segments of 32)
+GLU_SHAPES = [(t, s) for t in TYPES for s in [(600, 256), (1200, 256), (4864, 896), (40, 512), (64, 288),
+                                            (1000, 288)]] + \
     [(t, s) for t in (12, 13, 14, 8, 2, 6) for s in [(18944, 3584), (14336, 4096)]]
 
 
