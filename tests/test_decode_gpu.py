@@ -237,6 +237,20 @@ def test_qwen2_05b_shape_config3(rinf, synth, oracle, ctx):
     shared.free()
 
 
+def test_qwen2_7b_full_config4(rinf, synth, oracle, ctx):
+    """BASELINE.json configs[3] at full size: the 28-layer Qwen2-7B
+    architecture in the Q4_K_M mix (the bench's decode model, same seed),
+    4 prompt tokens then 4 greedy steps, logits and tokens against the
+    oracle's CPU forward pass."""
+    cfg = synth.ARCH["qwen2-7b"]
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", synth.config_seed(3), 16)
+    prompt = np.random.default_rng(synth.config_seed(3)).integers(0, cfg["vocab_size"], 4)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 4)
+    print(f"qwen2-7b: max logits err {max(errs):.2e}, tokens {out}", flush=True)
+    assert max(errs) <= DEEP_TOL
+    dev.close()
+
+
 def test_errors(rinf, synth, ctx):
     dev = rinf.DeviceModel(ctx, 256, 1, 4, 2, 512, 100, 4, 1e6, 1e-6)
     with pytest.raises(rinf.QgemvError) as e:
