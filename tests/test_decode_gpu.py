@@ -237,16 +237,18 @@ def test_qwen2_05b_shape_config3(rinf, synth, oracle, ctx):
     shared.free()
 
 
-def test_qwen2_7b_full_config4(rinf, synth, oracle, ctx):
-    """BASELINE.json configs[3] at full size: the 28-layer Qwen2-7B
-    architecture in the Q4_K_M mix (the bench's decode model, same seed),
-    4 prompt tokens then 4 greedy steps, logits and tokens against the
-    oracle's CPU forward pass."""
-    cfg = synth.ARCH["qwen2-7b"]
-    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", synth.config_seed(3), 16)
-    prompt = np.random.default_rng(synth.config_seed(3)).integers(0, cfg["vocab_size"], 4)
+@pytest.mark.parametrize("arch,mix,cidx", [("qwen2-7b", "q4_k_m", 3), ("llama3-8b", "q4_k_m", 4),
+                                           ("llama3-8b", "q5_k", 4), ("llama3-8b", "q8_0", 4)])
+def test_full_size_models(rinf, synth, oracle, ctx, arch, mix, cidx):
+    """BASELINE.json configs[3] and [4] at full size: the 28-layer Qwen2-7B
+    model of the bench (Q4_K_M, same seed) and the 32-layer Llama-3-8B in the
+    Q4_K_M, Q5_K and Q8_0 mixes; 4 prompt tokens then 4 greedy steps, logits
+    and tokens against the oracle's CPU forward pass."""
+    cfg = synth.ARCH[arch]
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, mix, synth.config_seed(cidx), 16)
+    prompt = np.random.default_rng(synth.config_seed(cidx)).integers(0, cfg["vocab_size"], 4)
     out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 4)
-    print(f"qwen2-7b: max logits err {max(errs):.2e}, tokens {out}", flush=True)
+    print(f"{arch} {mix}: max logits err {max(errs):.2e}, tokens {out}", flush=True)
     assert max(errs) <= DEEP_TOL
     dev.close()
 
