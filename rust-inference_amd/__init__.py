@@ -235,6 +235,16 @@ class GpuContext:
         self.check(rc, "qg_upload")
         return DeviceMatrix(self, m, dtype, rows, cols)
 
+    def wrap_device(self, d_raw, dtype: int, rows: int, cols: int) -> "DeviceMatrix":
+        """A matrix over GGUF-layout bytes already in device memory (a torch
+        uint8 tensor, 16-byte aligned, with >= 512 readable bytes after the
+        data); not copied, so the tensor must outlive the handle (qg_wrap_device)."""
+        m = _P()
+        rc = self.lib.qg_wrap_device(self.h, _ptr(d_raw), nbytes_for(dtype, rows, cols), dtype, rows, cols,
+                                     ctypes.byref(m))
+        self.check(rc, "qg_wrap_device")
+        return DeviceMatrix(self, m, dtype, rows, cols)
+
     def stack(self, parts) -> "DeviceMatrix":
         """One matrix with the rows of `parts` (DeviceMatrix, same type and
         cols) in order (qg_mat_stack)."""

@@ -60,6 +60,7 @@ struct Plan {
     const void *fn_norm;   // the same kernel with the fused RMSNorm input
     const void *fn_silu;   // the same kernel with the silu(g) * u input
     const void *fn_norm_glu;  // RMSNorm input, [gate; up] rows paired into silu(g) * u
+    bool rp;               // the kernels read the repacked layout (launch_repack)
 };
 
 }  // namespace qg
@@ -67,7 +68,14 @@ struct Plan {
 // Launchers implemented in qgemv_kernels.hip (C++ linkage, library-internal).
 struct ihipStream_t;
 namespace qg {
-int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p);
+// rp: plan the kernels of the repacked layout where the type has one (Q4_K,
+// Q6_K with whole row groups; Plan::rp tells whether it applied).
+int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool rp = false);
+// Whether make_plan(..., rp = true) would give a repacked-layout plan.
+bool repack_eligible(uint32_t type, const Plan &p, size_t rows);
+// dst = the repacked layout of src's n_groups row groups (same size); both
+// device pointers; asynchronous.
+int launch_repack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst, ihipStream_t *stream);
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
                 size_t cols, const float *x, float *y, ihipStream_t *stream);
 // y = W · (rmsnorm(xa + xb) * nw) with the stream kernel (kind 1 plans only;

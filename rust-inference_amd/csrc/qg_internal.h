@@ -16,13 +16,18 @@ struct qg_model;
 
 struct qg_mat {
     qg_ctx *ctx;
-    uint8_t *d;        // device bytes (nbytes data + kTailPad zeros)
+    uint8_t *d;        // device bytes in the GGUF layout (nbytes data + kTailPad zeros)
+    uint8_t *d_rp;     // the same bytes in the repacked layout, or NULL (owned)
     size_t nbytes;     // bytes the kernels may treat as data
     uint32_t type;
     size_t rows, cols;
     bool owned;
-    qg::Plan plan;
+    qg::Plan plan;     // plan.rp: the stream kernels read d_rp
 };
+
+// The bytes the stream GEMV kernels read (the dequant and generic kernels
+// always read d).
+inline const uint8_t *qg_gemv_bytes(const qg_mat *m) { return m->plan.rp ? m->d_rp : m->d; }
 
 struct qg_ctx {
     int device = 0;

@@ -702,7 +702,7 @@ void slot_shape(const qg_model *m, uint32_t which, size_t *rows, size_t *cols)
 
 int gemv(qg_model *m, const qg_mat *a, const float *x, float *y)
 {
-    if (qg::launch_gemv(a->type, a->plan, a->d, a->nbytes, a->rows, a->cols, x, y,
+    if (qg::launch_gemv(a->type, a->plan, qg_gemv_bytes(a), a->nbytes, a->rows, a->cols, x, y,
                         (ihipStream_t *)m->ctx->stream) != 0)
         return mfail(m, QG_ERR_HIP, "GEMV launch", hipGetLastError());
     return QG_OK;

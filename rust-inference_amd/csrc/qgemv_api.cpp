@@ -107,9 +107,34 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
     m->rows = rows;
     m->cols = cols;
     m->owned = owned;
+    m->d_rp = nullptr;
     if (qg::make_plan(type, rows, cols, ctx->n_cu, &m->plan) != 0) {
         delete m;
         return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
+    }
+    // Owned Q4_K / Q6_K matrices also get the repacked layout the stream
+    // kernels read with contiguous loads (a permutation of the same bytes;
+    // d keeps the GGUF layout for the dequant and generic kernels).  Bytes
+    // wrapped from caller memory keep the GGUF-layout kernels.
+    if (owned && qg::repack_eligible(type, m->plan, rows)) {
+        uint8_t *r = nullptr;
+        hipError_t e = hipMalloc((void **)&r, nbytes + qg::kTailPad);
+        if (e != hipSuccess) {
+            delete m;
+            return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc repacked matrix", e);
+        }
+        qg::Plan rp_plan;
+        int lr = qg::launch_repack(type, m->plan, d, r, (ihipStream_t *)ctx->stream);
+        if (lr == 0) e = hipMemsetAsync(r + nbytes, 0, qg::kTailPad, ctx->stream);
+        if (lr == 0 && e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (lr != 0 || e != hipSuccess || qg::make_plan(type, rows, cols, ctx->n_cu, &rp_plan, true) != 0 ||
+            !rp_plan.rp) {
+            (void)hipFree(r);
+            delete m;
+            return fail(ctx, QG_ERR_HIP, "repacking the matrix", e != hipSuccess ? e : hipGetLastError());
+        }
+        m->d_rp = r;
+        m->plan = rp_plan;
     }
     ctx->mats.insert(m);
     *out = m;
@@ -119,6 +144,7 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
 void drop_mat(qg_ctx *ctx, qg_mat *m)
 {
     if (m->owned && m->d) (void)hipFree(m->d);
+    if (m->d_rp) (void)hipFree(m->d_rp);
     ctx->mats.erase(m);
     for (auto it = ctx->keyed.begin(); it != ctx->keyed.end();) {
         if (it->second == m)
@@ -150,14 +176,14 @@ int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float 
         return lr ? fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError()) : QG_OK;
     }
     if (xb && a16(xa) && a16(xb) && a16(nw) && (!sum_out || a16(sum_out)))
-        lr = qg::launch_gemv_norm(mat->plan, mat->d, mat->nbytes, mat->rows, cols, xa, xb, nw, eps, sum_out,
+        lr = qg::launch_gemv_norm(mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, cols, xa, xb, nw, eps, sum_out,
                                   y, sti);
     if (lr == -1) {
         // two kernels: RMSNorm into scratch, then the mat-vec
         lr = qg::launch_rmsnorm(xa, xb, sum_out, nw, scratch, cols, eps, sti);
         if (lr == 0) {
             if (mat->plan.kind == 1 && a16(scratch))
-                lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, cols, scratch, y, sti);
+                lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, cols, scratch, y, sti);
             else
                 lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, cols, scratch, y, sti);
         }
@@ -180,12 +206,12 @@ int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *
     // cheaper than a second kernel for short rows only
     constexpr size_t kFuseMaxCols = 8192;
     if (cols <= kFuseMaxCols && a16(g) && a16(u))
-        lr = qg::launch_gemv_silu(mat->plan, mat->d, mat->nbytes, mat->rows, cols, g, u, y, sti);
+        lr = qg::launch_gemv_silu(mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, cols, g, u, y, sti);
     if (lr == -1) {
         lr = qg::launch_silu_mul(g, u, scratch, cols, sti);
         if (lr == 0) {
             if (mat->plan.kind == 1 && a16(scratch))
-                lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, cols, scratch, y, sti);
+                lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, cols, scratch, y, sti);
             else
                 lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, cols, scratch, y, sti);
         }
@@ -201,7 +227,7 @@ int qg_norm_glu_matvec(qg_ctx *ctx, const qg_mat *gu, const float *xa, const flo
     auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     int lr = -1;
     if (gu->cols > 0 && xb && a16(xa) && a16(xb) && a16(nw) && (!sum_out || a16(sum_out)))
-        lr = qg::launch_gemv_norm_glu(gu->plan, gu->d, gu->nbytes, gu->rows, gu->cols, xa, xb, nw, eps, sum_out,
+        lr = qg::launch_gemv_norm_glu(gu->plan, qg_gemv_bytes(gu), gu->nbytes, gu->rows, gu->cols, xa, xb, nw, eps, sum_out,
                                       h, sti);
     if (lr == -1) {
         int rc = qg_norm_matvec(ctx, gu, xa, xb, nw, eps, sum_out, gu_out, scratch, st);
@@ -218,8 +244,8 @@ int qg_norm_pair_matvec(qg_ctx *ctx, const qg_mat *m1, const qg_mat *m2, const f
     auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     int lr = -1;
     if (m1->cols == m2->cols && m1->cols > 0 && xb && a16(xa) && a16(xb) && a16(nw) && (!sum_out || a16(sum_out)))
-        lr = qg::launch_gemv_norm_pair(m1->type, m1->plan, m1->d, m1->nbytes, m1->rows, y1, m2->type, m2->plan,
-                                       m2->d, m2->nbytes, m2->rows, y2, m1->cols, xa, xb, nw, eps, sum_out,
+        lr = qg::launch_gemv_norm_pair(m1->type, m1->plan, qg_gemv_bytes(m1), m1->nbytes, m1->rows, y1, m2->type, m2->plan,
+                                       qg_gemv_bytes(m2), m2->nbytes, m2->rows, y2, m1->cols, xa, xb, nw, eps, sum_out,
                                        ctx->n_cu, (ihipStream_t *)st);
     if (lr == 0) return QG_OK;
     if (lr != -1) return fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError());
@@ -403,7 +429,7 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
     if (mat->cols == 0)                                   // out.fill(0.0), quant.rs:189
         lr = qg::launch_fill(d_y, mat->rows, 0.0f, (ihipStream_t *)st);
     else if (mat->plan.kind == 1 && ((uintptr_t)d_x & 15u) == 0)
-        lr = qg::launch_gemv(mat->type, mat->plan, mat->d, mat->nbytes, mat->rows, mat->cols, d_x,
+        lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, mat->cols, d_x,
                              d_y, (ihipStream_t *)st);
     else
         lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, mat->cols, d_x, d_y,

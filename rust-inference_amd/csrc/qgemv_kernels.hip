@@ -474,6 +474,21 @@ template <> struct Item<T_Q4_K> {
         r[12] = q2.x; r[13] = q2.y; r[14] = q2.z; r[15] = q2.w;
         r[16] = q3.x; r[17] = q3.y; r[18] = q3.z; r[19] = q3.w;
     }
+    // The same registers from the repacked row group (repack_k): the nb = ni/2
+    // block headers, then piece k (16 bytes) of item it at nb*16 + (k*ni + it)*16,
+    // so every load instruction of a wave reads one contiguous range.
+    __device__ static void load_rp(const uint8_t *grp, uint32_t it, uint32_t ni, uint32_t (&r)[NRAW])
+    {
+        const uint4 h = *(const uint4 *)(grp + (it >> 1) * 16u);
+        const uint8_t *q = grp + (ni >> 1) * 16u + it * 16u;
+        const uint4 q0 = *(const uint4 *)q, q1 = *(const uint4 *)(q + ni * 16u);
+        const uint4 q2 = *(const uint4 *)(q + 2u * ni * 16u), q3 = *(const uint4 *)(q + 3u * ni * 16u);
+        r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
+        r[4] = q0.x; r[5] = q0.y; r[6] = q0.z; r[7] = q0.w;
+        r[8] = q1.x; r[9] = q1.y; r[10] = q1.z; r[11] = q1.w;
+        r[12] = q2.x; r[13] = q2.y; r[14] = q2.z; r[15] = q2.w;
+        r[16] = q3.x; r[17] = q3.y; r[18] = q3.z; r[19] = q3.w;
+    }
     // sum q*x of the four sub-blocks, each in units of 1/k of its segment
     __device__ static void dots(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, float (&D)[4])
     {
@@ -625,8 +640,27 @@ template <> struct Item<T_Q6_K> {
         r[13] = __builtin_amdgcn_alignbyte(S2, S1, sh);
         r[14] = D >> (8u * sh);
     }
-    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
-                                   float (&out)[S])
+    // The same registers from the repacked row group (repack_k): pieces A, B
+    // and H of every item piece-major (ni x 16 bytes each), then the item's
+    // four scale bytes sc[8n + i + 2k] (ni x 4), then each block's d (nb x 2).
+    // r[12] then holds the four scales in bytes 0..3.
+    __device__ static void load_rp(const uint8_t *grp, uint32_t it, uint32_t ni, uint32_t (&r)[NRAW])
+    {
+        const uint4 A = *(const uint4 *)(grp + it * 16u);
+        const uint4 B = *(const uint4 *)(grp + (ni + it) * 16u);
+        const uint4 H = *(const uint4 *)(grp + (2u * ni + it) * 16u);
+        r[12] = *(const uint32_t *)(grp + 48u * ni + it * 4u);
+        r[14] = *(const uint16_t *)(grp + 52u * ni + (it >> 2) * 2u);
+        r[0] = A.x; r[1] = A.y; r[2] = A.z; r[3] = A.w;
+        r[4] = B.x; r[5] = B.y; r[6] = B.z; r[7] = B.w;
+        r[8] = H.x; r[9] = H.y; r[10] = H.z; r[11] = H.w;
+        r[13] = 0u;
+    }
+    // sum q*x per 16-weight slot k with scale sc_k (RP: scales as load_rp
+    // leaves them; otherwise as load does)
+    template <bool RP>
+    __device__ static void compute_t(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                     float (&out)[S])
     {
         const float d = h2f(r[14]);
         const uint32_t i8 = (it & 1u) * 8u;
@@ -647,10 +681,21 @@ template <> struct Item<T_Q6_K> {
         }
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            // sc[8n + i + 2k]: byte (i + 2(k&1)) of dword r[12 + k/2]
-            const int sc = __builtin_amdgcn_sbfe((int)r[12 + (k >> 1)], (int)(i8 + 16u * (k & 1)), 8);
+            // sc[8n + i + 2k]: byte (i + 2(k&1)) of dword r[12 + k/2], or byte k of r[12] (RP)
+            const int sc = RP ? __builtin_amdgcn_sbfe((int)r[12], 8 * k, 8)
+                              : __builtin_amdgcn_sbfe((int)r[12 + (k >> 1)], (int)(i8 + 16u * (k & 1)), 8);
             out[k] = (d * (float)sc) * __builtin_fmaf(-32.0f, x.sx[k], fix3(u0[k], u1[k], s2[k]) * x.ik[k]);
         }
+    }
+    __device__ static void compute(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                   float (&out)[S])
+    {
+        compute_t<false>(r, x, it, out);
+    }
+    __device__ static void compute_rp(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                      float (&out)[S])
+    {
+        compute_t<true>(r, x, it, out);
     }
 };
 
@@ -909,7 +954,8 @@ __device__ __forceinline__ void lds_barrier()
 // offsets fit in 32 bits (the planner sends larger matrices elsewhere).
 // GLU (R = 1): batches alternate gate row group j and up row group j,
 // j = t + (i/2)*NT.
-template <uint32_t T, int R, bool GLU = false>
+// RP: the matrix is in the repacked layout (repack_k), read with load_rp.
+template <uint32_t T, int R, bool GLU = false, bool RP = false>
 __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t i, uint32_t it,
                                       uint32_t ib, bool active, uint32_t (&raw)[R][Item<T>::NRAW])
 {
@@ -923,10 +969,28 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
             grp = t + (i * R + r) * a.n_teams;
             lim = grp;
         }
-        const uint32_t off = grp * a.group_bytes + ib;
-        const bool ok = active && lim < (GLU ? a.glu_half : a.n_groups) && off < a.nbytes;
-        Item<T>::load(a.w + (ok ? off : 0u), it, raw[r]);
+        if constexpr (RP) {
+            // whole row groups only (the repack requires them)
+            const bool ok = active && lim < (GLU ? a.glu_half : a.n_groups);
+            Item<T>::load_rp(a.w + (ok ? grp * a.group_bytes : 0u), it, a.ni, raw[r]);
+        } else {
+            const uint32_t off = grp * a.group_bytes + ib;
+            const bool ok = active && lim < (GLU ? a.glu_half : a.n_groups) && off < a.nbytes;
+            Item<T>::load(a.w + (ok ? off : 0u), it, raw[r]);
+        }
     }
+}
+
+template <class I, class = void> struct HasRp : std::false_type {};
+template <class I> struct HasRp<I, std::void_t<decltype(&I::compute_rp)>> : std::true_type {};
+
+// per-slot sums of an item (the repacked layout's register form where it differs)
+template <class I, bool RP, class XT>
+__device__ __forceinline__ void item_compute(const uint32_t (&r)[I::NRAW], const XT &x, uint32_t it,
+                                             float (&acc)[I::S])
+{
+    if constexpr (RP && HasRp<I>::value) I::compute_rp(r, x, it, acc);
+    else I::compute(r, x, it, acc);
 }
 
 // CONV: a.x is x itself (f32) and the workgroup converts it to the
@@ -963,7 +1027,7 @@ __device__ __forceinline__ void issue(const StreamArgs &a, uint32_t t, uint32_t 
 // stream_body runs workgroup `bid` of such a launch; gemv_stream is the
 // kernel of one matrix, gemv_stream_pair runs two matrices in one grid.
 template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
-          int PRO = kProPlain, bool GLU = false>
+          int PRO = kProPlain, bool GLU = false, bool RP = false>
 __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 {
     static_assert(!GLU || (R == 1 && TSUB != 0 && D % 2 == 0), "GLU pairs need teams of a wave or less");
@@ -1006,7 +1070,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t raw[D][R][NR];
 #pragma unroll
-    for (int d = 0; d < D0; d++) issue<T, R, GLU>(a, team, d, it, ib, active, raw[d]);
+    for (int d = 0; d < D0; d++) issue<T, R, GLU, RP>(a, team, d, it, ib, active, raw[d]);
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
@@ -1121,7 +1185,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 
     // the rest of the ring, now that no conversion work waits behind it
 #pragma unroll
-    for (int d = D0; d < D; d++) issue<T, R, GLU>(a, team, d, it, ib, active, raw[d]);
+    for (int d = D0; d < D; d++) issue<T, R, GLU, RP>(a, team, d, it, ib, active, raw[d]);
 
     // 3. stream the batches
     float *red = (float *)(lds + a.red_off);
@@ -1152,7 +1216,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
                     t = I::compute_sum(rw[r], xs, it);
                 } else {
                     float acc[S];
-                    I::compute(rw[r], xs, it, acc);
+                    item_compute<I, RP>(rw[r], xs, it, acc);
                     t = 0.f;
 #pragma unroll
                     for (int s = 0; s < S; s++) t += acc[s];
@@ -1171,7 +1235,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
                 }
                 const bool ok = active && lim < lim_n && grp * a.group_bytes + ib < a.nbytes;
                 float acc[S];
-                I::compute(rw[r], xs, it, acc);
+                item_compute<I, RP>(rw[r], xs, it, acc);
 #pragma unroll
                 for (int gi = 0; gi < 8; gi++) {
                     float t = 0.f;
@@ -1220,7 +1284,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 #pragma unroll
         for (int d = 0; d < D; d++) {
             process(raw[d], i + d);
-            issue<T, R, GLU>(a, team, i + d + D, it, ib, active, raw[d]);
+            issue<T, R, GLU, RP>(a, team, i + d + D, it, ib, active, raw[d]);
         }
     }
 #pragma unroll
@@ -1229,10 +1293,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 }
 
 template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
-          int PRO = kProPlain, bool GLU = false>
+          int PRO = kProPlain, bool GLU = false, bool RP = false>
 __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 {
-    stream_body<T, TSUB, R, D, G1, CONV, XS, LB, D0, PRO, GLU>(a, blockIdx.x);
+    stream_body<T, TSUB, R, D, G1, CONV, XS, LB, D0, PRO, GLU, RP>(a, blockIdx.x);
 }
 
 // Two matrices with the same input, each with its own type and plan, in one
@@ -1241,13 +1305,13 @@ __global__ void __launch_bounds__(LB) gemv_stream(StreamArgs a)
 // ([Q;K] Q4_K beside V Q6_K in the Q4_K_M mix), so the small part does not
 // pay a launch and an x staging of its own.  RMSNorm prologue; G1A / G1B:
 // one row per group in that part.
-template <uint32_t T1, int TS1, bool G1A, uint32_t T2, int TS2, bool G1B, int LB>
+template <uint32_t T1, int TS1, bool G1A, bool RPA, uint32_t T2, int TS2, bool G1B, bool RPB, int LB>
 __global__ void __launch_bounds__(LB) gemv_stream_pair(StreamArgs a1, StreamArgs a2, uint32_t grid1)
 {
     if (blockIdx.x < grid1)
-        stream_body<T1, TS1, 1, kDepth, G1A, true, kStage, LB, kDepth, kProNorm>(a1, blockIdx.x);
+        stream_body<T1, TS1, 1, kDepth, G1A, true, kStage, LB, kDepth, kProNorm, false, RPA>(a1, blockIdx.x);
     else
-        stream_body<T2, TS2, 1, kDepth, G1B, true, kStage, LB, kDepth, kProNorm>(a2, blockIdx.x - grid1);
+        stream_body<T2, TS2, 1, kDepth, G1B, true, kStage, LB, kDepth, kProNorm, false, RPB>(a2, blockIdx.x - grid1);
 }
 
 // ------------------------------------------------------------ planning
@@ -1258,29 +1322,33 @@ static uint32_t gcd_u(uint64_t a, uint64_t b)
     return (uint32_t)a;
 }
 
-template <uint32_t T, bool G1, int PRO> static const void *stream_fn_g(uint32_t tsub)
+template <uint32_t T, bool G1, int PRO, bool RP = false> static const void *stream_fn_g(uint32_t tsub)
 {
     constexpr int R = 1, D = kDepth, LB = wg_max<T>();
     switch (tsub) {
-    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, PRO>;
-    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, PRO>;
-    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, PRO>;
-    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB, D, PRO>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, PRO, false, RP>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, PRO, false, RP>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, PRO, false, RP>;
+    case 0: return (const void *)gemv_stream<T, 0, R, D, G1, true, kStage, LB, D, PRO, false, RP>;
     default: return nullptr;
     }
 }
 
 // [gate; up] kernels with the RMSNorm prologue (teams of one wave or less)
-template <uint32_t T, bool G1> static const void *stream_fn_glu(uint32_t tsub)
+template <uint32_t T, bool G1, bool RP = false> static const void *stream_fn_glu(uint32_t tsub)
 {
     constexpr int R = 1, D = kDepth, LB = wg_max<T>();
     switch (tsub) {
-    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, kProNorm, true>;
-    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, kProNorm, true>;
-    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, kProNorm, true>;
+    case 16: return (const void *)gemv_stream<T, 16, R, D, G1, true, kStage, LB, D, kProNorm, true, RP>;
+    case 32: return (const void *)gemv_stream<T, 32, R, D, G1, true, kStage, LB, D, kProNorm, true, RP>;
+    case 64: return (const void *)gemv_stream<T, 64, R, D, G1, true, kStage, LB, D, kProNorm, true, RP>;
     default: return nullptr;
     }
 }
+
+// Types the upload repacks (repack_k): their items take 5 load instructions or
+// more in the GGUF layout.
+template <uint32_t T> constexpr bool repackable() { return T == T_Q4_K || T == T_Q6_K; }
 
 static int max_lds_bytes()
 {
@@ -1294,7 +1362,7 @@ static int max_lds_bytes()
 // Stream kernel plan (kind 1); leaves kind 0 (generic kernel) where it does
 // not apply: cols % 32 != 0, row groups longer than 768 items, more than 8
 // rows per group, byte offsets past 32 bits, or x larger than LDS.
-template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu, Plan *p)
+template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu, bool rp, Plan *p)
 {
     using I = Item<T>;
     p->kind = 0;
@@ -1310,12 +1378,24 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     uint32_t tsub = 0, wpt = 1, tl;
     if (ni <= 64) { tsub = 16; while (tsub < ni) tsub <<= 1; tl = tsub; }
     else { wpt = (uint32_t)((ni + 63) / 64); tl = 64 * wpt; }
-    const void *fn = g == 1 ? stream_fn_g<T, true, kProPlain>(tsub) : stream_fn_g<T, false, kProPlain>(tsub);
     // prologue variants for the quant types (F16/F32 x tiles leave no registers for them)
     constexpr int PN = I::PLANES ? kProNorm : kProPlain, PS = I::PLANES ? kProSilu : kProPlain;
-    const void *fn_norm = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
-    const void *fn_silu = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
-    const void *fn_norm_glu = !I::PLANES ? nullptr : g == 1 ? stream_fn_glu<T, true>(tsub) : stream_fn_glu<T, false>(tsub);
+    const void *fn = nullptr, *fn_norm = nullptr, *fn_silu = nullptr, *fn_norm_glu = nullptr;
+    rp = rp && repackable<T>() && rows % g == 0;
+    if constexpr (repackable<T>()) {
+        if (rp) {
+            fn = g == 1 ? stream_fn_g<T, true, kProPlain, true>(tsub) : stream_fn_g<T, false, kProPlain, true>(tsub);
+            fn_norm = g == 1 ? stream_fn_g<T, true, PN, true>(tsub) : stream_fn_g<T, false, PN, true>(tsub);
+            fn_silu = g == 1 ? stream_fn_g<T, true, PS, true>(tsub) : stream_fn_g<T, false, PS, true>(tsub);
+            fn_norm_glu = g == 1 ? stream_fn_glu<T, true, true>(tsub) : stream_fn_glu<T, false, true>(tsub);
+        }
+    }
+    if (!rp) {
+        fn = g == 1 ? stream_fn_g<T, true, kProPlain>(tsub) : stream_fn_g<T, false, kProPlain>(tsub);
+        fn_norm = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
+        fn_silu = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
+        fn_norm_glu = !I::PLANES ? nullptr : g == 1 ? stream_fn_glu<T, true>(tsub) : stream_fn_glu<T, false>(tsub);
+    }
     if (!fn) return;
     const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;
     const uint32_t img = (image_bytes(I::PLANES, (uint32_t)cols) + 15u) & ~15u;
@@ -1353,6 +1433,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     p->fn_norm = fn_norm;
     p->fn_silu = fn_silu;
     p->fn_norm_glu = fn_norm_glu;
+    p->rp = rp;
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
     p->ts = tl;
@@ -1372,22 +1453,87 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     p->kind = 1;
 }
 
-int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p)
+int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool rp)
 {
     *p = Plan{};
     if (rows > 0xFFFFFFFFull || cols > 0xFFFFFFFFull) return 0;
     switch (type) {
-    case T_F32: plan_stream<T_F32>(rows, cols, n_cu, p); break;
-    case T_F16: plan_stream<T_F16>(rows, cols, n_cu, p); break;
-    case T_Q4_0: plan_stream<T_Q4_0>(rows, cols, n_cu, p); break;
-    case T_Q5_0: plan_stream<T_Q5_0>(rows, cols, n_cu, p); break;
-    case T_Q8_0: plan_stream<T_Q8_0>(rows, cols, n_cu, p); break;
-    case T_Q4_K: plan_stream<T_Q4_K>(rows, cols, n_cu, p); break;
-    case T_Q5_K: plan_stream<T_Q5_K>(rows, cols, n_cu, p); break;
-    case T_Q6_K: plan_stream<T_Q6_K>(rows, cols, n_cu, p); break;
+    case T_F32: plan_stream<T_F32>(rows, cols, n_cu, false, p); break;
+    case T_F16: plan_stream<T_F16>(rows, cols, n_cu, false, p); break;
+    case T_Q4_0: plan_stream<T_Q4_0>(rows, cols, n_cu, false, p); break;
+    case T_Q5_0: plan_stream<T_Q5_0>(rows, cols, n_cu, false, p); break;
+    case T_Q8_0: plan_stream<T_Q8_0>(rows, cols, n_cu, false, p); break;
+    case T_Q4_K: plan_stream<T_Q4_K>(rows, cols, n_cu, rp, p); break;
+    case T_Q5_K: plan_stream<T_Q5_K>(rows, cols, n_cu, false, p); break;
+    case T_Q6_K: plan_stream<T_Q6_K>(rows, cols, n_cu, rp, p); break;
     default: return -1;
     }
     return 0;
+}
+
+bool repack_eligible(uint32_t type, const Plan &p, size_t rows)
+{
+    return (type == T_Q4_K || type == T_Q6_K) && p.kind == 1 && p.g > 0 && rows % p.g == 0;
+}
+
+// The repacked layout of a whole number of row groups, group by group (the
+// same bytes, permuted so that a wave's loads of one piece are contiguous):
+//   Q4_K (ni = 2 nb items of 128 weights): the nb 16-byte block headers, then
+//        piece k (bytes 16k..16k+15 of the item's 64 quant bytes) of item it
+//        at nb*16 + (k*ni + it)*16;
+//   Q6_K (ni = 4 nb items of 64 weights; item it = block it/4, half
+//        n = (it/2)&1, i = it&1): ql[64n+16i..+16] at it*16,
+//        ql[64n+32+16i..+16] at (ni+it)*16, qh[32n+16i..+16] at (2ni+it)*16,
+//        the scales sc[8n+i+2k], k = 0..3, at 48ni + 4it + k, d at 52ni + 2b.
+// One thread per item.
+template <uint32_t T>
+__global__ void __launch_bounds__(256) repack_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                uint64_t n_items, uint32_t ni, uint32_t group_bytes)
+{
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_items) return;
+    const uint64_t gidx = idx / ni;
+    const uint32_t it = (uint32_t)(idx - gidx * ni);
+    const uint8_t *sg = src + gidx * group_bytes;
+    uint8_t *dg = dst + gidx * group_bytes;
+    if constexpr (T == T_Q4_K) {
+        const uint8_t *b = sg + (it >> 1) * 144u;
+        if ((it & 1u) == 0)
+            for (int j = 0; j < 16; j++) dg[(it >> 1) * 16u + j] = b[j];
+        for (uint32_t k = 0; k < 4; k++)
+            for (int j = 0; j < 16; j++) dg[(ni >> 1) * 16u + (k * ni + it) * 16u + j] = b[16u + (it & 1u) * 64u + 16u * k + j];
+    } else {
+        const uint8_t *b = sg + (it >> 2) * 210u;
+        const uint32_t n = (it >> 1) & 1u, i = it & 1u;
+        for (int j = 0; j < 16; j++) {
+            dg[it * 16u + j] = b[64u * n + 16u * i + j];
+            dg[(ni + it) * 16u + j] = b[64u * n + 32u + 16u * i + j];
+            dg[(2u * ni + it) * 16u + j] = b[128u + 32u * n + 16u * i + j];
+        }
+        for (uint32_t k = 0; k < 4; k++) dg[48u * ni + 4u * it + k] = b[192u + 8u * n + i + 2u * k];
+        if ((it & 3u) == 0) {
+            dg[52u * ni + (it >> 2) * 2u] = b[208];
+            dg[52u * ni + (it >> 2) * 2u + 1u] = b[209];
+        }
+    }
+}
+
+int launch_repack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst, ihipStream_t *stream)
+{
+    if (p.kind != 1 || p.ni == 0) return -1;
+    const uint64_t n_items = (uint64_t)p.n_groups * p.ni;
+    if (n_items == 0) return 0;
+    const uint64_t blocks = (n_items + 255) / 256;
+    if (blocks > 0x7FFFFFFFull) return -1;
+    if (type == T_Q4_K)
+        hipLaunchKernelGGL(repack_k<T_Q4_K>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
+                           n_items, p.ni, (uint32_t)p.group_bytes);
+    else if (type == T_Q6_K)
+        hipLaunchKernelGGL(repack_k<T_Q6_K>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
+                           n_items, p.ni, (uint32_t)p.group_bytes);
+    else
+        return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 // ------------------------------------------------------------ launchers
@@ -1464,18 +1610,22 @@ constexpr int kPairBlock = 512;
 template <uint32_t T1, uint32_t T2, bool G1> static const void *pair_fn_g(uint32_t ts1, uint32_t ts2)
 {
     constexpr int LB = kPairBlock;
-    if (ts1 == 16 && ts2 == 16) return (const void *)gemv_stream_pair<T1, 16, G1, T2, 16, G1, LB>;
-    if (ts1 == 16 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 16, G1, T2, 32, G1, LB>;
-    if (ts1 == 32 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 32, G1, T2, 32, G1, LB>;
-    if (ts1 == 32 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 32, G1, T2, 64, G1, LB>;
-    if (ts1 == 64 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 64, G1, T2, 64, G1, LB>;
+    constexpr bool R1 = repackable<T1>(), R2 = repackable<T2>();
+    if (ts1 == 16 && ts2 == 16) return (const void *)gemv_stream_pair<T1, 16, G1, R1, T2, 16, G1, R2, LB>;
+    if (ts1 == 16 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 16, G1, R1, T2, 32, G1, R2, LB>;
+    if (ts1 == 32 && ts2 == 32) return (const void *)gemv_stream_pair<T1, 32, G1, R1, T2, 32, G1, R2, LB>;
+    if (ts1 == 32 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 32, G1, R1, T2, 64, G1, R2, LB>;
+    if (ts1 == 64 && ts2 == 64) return (const void *)gemv_stream_pair<T1, 64, G1, R1, T2, 64, G1, R2, LB>;
     return nullptr;
 }
 
 // Both parts one-row groups, or both multi-row groups (the 896-column rows of
-// Qwen2-0.5B: two rows per group for the K-quants).
+// Qwen2-0.5B: two rows per group for the K-quants); the repackable types in
+// their repacked layout (matrices wrapped from caller memory are not, and
+// take two launches).
 template <uint32_t T1, uint32_t T2> static const void *pair_fn(const Plan &p1, const Plan &p2)
 {
+    if (p1.rp != repackable<T1>() || p2.rp != repackable<T2>()) return nullptr;
     if (p1.g == 1 && p2.g == 1) return pair_fn_g<T1, T2, true>(p1.tsub, p2.tsub);
     if (p1.g > 1 && p2.g > 1) return pair_fn_g<T1, T2, false>(p1.tsub, p2.tsub);
     return nullptr;

@@ -63,6 +63,44 @@ def test_gemv_parity(ctx, oracle, synth, dtype, shape):
     assert err <= GEMV_TOL
 
 
+WRAP_SHAPES = [(896, 896), (128, 896), (4096, 14336), (37, 18944), (1200, 256), (21, 8320), (64, 288)]
+
+
+@pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
+@pytest.mark.parametrize("shape", WRAP_SHAPES, ids=[f"{r}x{c}" for r, c in WRAP_SHAPES])
+def test_wrapped_bytes_match_upload(ctx, oracle, synth, dtype, shape):
+    """qg_wrap_device keeps the GGUF layout (its kernels read the file's
+    blocks), qg_upload of Q4_K/Q6_K also keeps a repacked copy for the stream
+    kernels: both give the same y, bit for bit, and the oracle's within
+    GEMV_TOL; the plain and the RMSNorm-prologue kernels of both layouts."""
+    import torch
+    rows, cols = shape
+    seed = synth.config_seed(1) + rows * 13 + cols + dtype
+    raw = synth.gen_blocks(dtype, rows, cols, seed)
+    x = synth.gen_x(cols, seed)
+    buf = torch.zeros(raw.nbytes + 1024, dtype=torch.uint8, device="cuda")
+    buf[:raw.nbytes] = torch.from_numpy(raw.view(np.uint8).reshape(-1)).cuda()
+    up = ctx.upload(raw, dtype, rows, cols)
+    wr = ctx.wrap_device(buf, dtype, rows, cols)
+    dx = torch.from_numpy(x).cuda()
+    nw = torch.from_numpy((1 + 0.1 * np.random.default_rng(seed).standard_normal(cols)).astype(np.float32)).cuda()
+    ys = [torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(4)]
+    st = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    up.matvec_dev(dx, ys[0], st)
+    wr.matvec_dev(dx, ys[1], st)
+    up.matvec_norm_dev(dx, dx, nw, 1e-6, ys[2], None, st)
+    wr.matvec_norm_dev(dx, dx, nw, 1e-6, ys[3], None, st)
+    torch.cuda.synchronize()
+    y = [t.cpu().numpy() for t in ys]
+    wr.free()
+    up.free()
+    del buf
+    assert np.array_equal(y[0].view(np.uint32), y[1].view(np.uint32))
+    assert np.array_equal(y[2].view(np.uint32), y[3].view(np.uint32))
+    assert normwise_err(y[0], ref_gemv(oracle, raw, dtype, rows, cols, x)) <= GEMV_TOL
+
+
 def test_config1_q4k_straddle(ctx, oracle, synth):
     """Q4_K 4864x896 (superblocks straddle row pairs)."""
     rows, cols, dtype = 4864, 896, 12

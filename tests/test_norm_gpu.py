@@ -189,6 +189,39 @@ def test_norm_glu_matvec_parity(ctx, rinf, oracle, synth, dtype, shape):
     assert ulp.max() <= 6e-7
 
 
+@pytest.mark.parametrize("dtype", [12, 14, 13, 8], ids=["Q4_K", "Q6_K", "Q5_K", "Q8_0"])
+@pytest.mark.parametrize("shape", [(1024, 3584), (4864, 896)], ids=["1024x3584", "4864x896"])
+def test_glu_wrapped_layout_matches(ctx, rinf, synth, dtype, shape):
+    """The paired [gate; up] kernel over GGUF-layout bytes wrapped from device
+    memory gives the same h, bit for bit, as over the uploaded (for Q4_K/Q6_K
+    repacked) stacked matrix."""
+    import torch
+    H, cols = shape
+    seed = 99 + H + dtype
+    gate, up = glu_inputs(synth, dtype, H, cols, seed)
+    both = np.concatenate([gate.view(np.uint8).reshape(-1), up.view(np.uint8).reshape(-1)])
+    xa, xb, nw = inputs(synth, H, cols, seed)
+    buf = torch.zeros(both.nbytes + 1024, dtype=torch.uint8, device="cuda")
+    buf[:both.nbytes] = torch.from_numpy(both).cuda()
+    wr = ctx.wrap_device(buf, dtype, 2 * H, cols)
+    mg, mu = ctx.upload(gate, dtype, H, cols), ctx.upload(up, dtype, H, cols)
+    gu = ctx.stack([mg, mu])
+    dev = lambda a: torch.from_numpy(a).cuda()
+    dxa, dxb, dnw = dev(xa), dev(xb), dev(nw)
+    h1 = torch.full((H,), float("nan"), dtype=torch.float32, device="cuda")
+    h2 = torch.full((H,), float("nan"), dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    gu.matvec_norm_glu_dev(dxa, dxb, dnw, EPS, h1, None, st)
+    wr.matvec_norm_glu_dev(dxa, dxb, dnw, EPS, h2, None, st)
+    torch.cuda.synchronize()
+    a, b = h1.cpu().numpy(), h2.cpu().numpy()
+    for m in (wr, gu, mg, mu):
+        m.free()
+    del buf
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_glu_and_stack_errors(ctx, rinf, synth):
     import torch
     m = ctx.upload(synth.gen_blocks(8, 65, 256, 3), 8, 65, 256)
