@@ -1052,22 +1052,31 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     const uint32_t n16 = I::PLANES && !CV ? image_bytes(true, a.cols) / 16u : a.cols / 4u;
     const uint4 *src = (const uint4 *)a.x;
     const uint32_t meta = planes_bytes(a.cols);
-    // Every load below is unconditional (clamped addresses): the compiler's
-    // wait counting stays exact only when no load sits on a conditional path.
+    // The weight loads are unconditional (clamped addresses): the compiler's
+    // wait counting stays exact only when no such load sits on a conditional
+    // path.  The x loads are the exception: only the ceil(n16 / blockDim)
+    // pieces the shape needs are issued (a uniform branch; each surplus load
+    // costs address-unit time, and with a 3584-wide x and three input vectors
+    // 18 of 24 would be surplus), and the wait below, visible to the
+    // compiler as a wait for every load, closes them before any weight load.
     uint4 xv[XS];
     uint4 bvv[TWO ? XS : 1], wvv[NORM ? XS : 1];
     const uint4 *srcb = (const uint4 *)a.xb, *srcw = (const uint4 *)a.nw;
+    const uint32_t nxs = (n16 + blockDim.x - 1u) / blockDim.x;
 #pragma unroll
     for (int k = 0; k < XS; k++) {
-        const uint32_t j = tid + k * blockDim.x, jc = j < n16 ? j : n16 - 1u;
-        xv[k] = src[jc];
-        if constexpr (TWO) bvv[k] = srcb[jc];
-        if constexpr (NORM) wvv[k] = srcw[jc];
+        if ((uint32_t)k < nxs) {
+            const uint32_t j = tid + k * blockDim.x, jc = j < n16 ? j : n16 - 1u;
+            xv[k] = src[jc];
+            if constexpr (TWO) bvv[k] = srcb[jc];
+            if constexpr (NORM) wvv[k] = srcw[jc];
+        }
     }
     // x first: issued behind the weight stream of the workgroups that started
     // earlier, x reaches the late ones after most of the matrix; waiting for
-    // it here (the weights then overlap the conversion) is measurably faster
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // it here (the weights then overlap the conversion) is measurably faster.
+    // 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     uint32_t raw[D][R][NR];
 #pragma unroll
     for (int d = 0; d < D0; d++) issue<T, R, GLU, RP>(a, team, d, it, ib, active, raw[d]);
