@@ -373,8 +373,10 @@ __device__ __forceinline__ void stage_planes1(float4 v, uint32_t i, uint8_t *lds
     s += dpp<0xB1>(s); s += dpp<0x4E>(s);            // 16-element half sums
     const float h = dpp<0x141>(s);                   // the other half's sum
     const bool bad = !__builtin_isfinite(s + h);
-    // k capped at 2^64 for tiny segments
-    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.8446744e19f) : 0.f;
+    // k capped at 2^100 (1/k stays a normal float; full precision for
+    // m >= kFix * 2^-100, about 3e-24 -- RMSNorm inputs are converted before
+    // the 1/rms scaling, so their segments may be far below 1)
+    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.2676506e30f) : 0.f;
     const float ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
     // Yb = Y + 0x8080: byte 2 is e2; bytes 0 and 1 are e0 and e1 with the top bit flipped
     const int off = 0x8080 - kMagicBits;
@@ -1087,8 +1089,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
         if constexpr (CV) stage_planes1<I::EVEN_ODD>(__builtin_bit_cast(float4, v), j, lds, meta);
         else l4[I::PLANES ? j : j + (j >> 4)] = v;
     };
+    // kProNorm: 1 / rms, applied to every segment's 1/k and sums after the
+    // barrier that publishes the planes (see below)
+    float nscale = 1.0f;
+    __shared__ float nred[NORM ? LB / 64 : 1];
     if constexpr (NORM) {
-        // x = a + b; sum of squares in element order within each thread
+        // x = a + b.  A segment's digits do not depend on a factor common to
+        // its elements (k adapts to the segment maximum), so the planes are
+        // converted from (a + b) * w at once, like a plain x, and the sum of
+        // squares only has to be complete when the lanes read their slices:
+        // no barrier between the weight issue and the conversion.
+        static_assert(CV, "the RMSNorm prologue converts x itself");
         const bool w0 = bid == 0 && a.sum_out;
         auto addv = [](uint4 p, uint4 q) {
             const float4 u = __builtin_bit_cast(float4, p), v = __builtin_bit_cast(float4, q);
@@ -1098,6 +1109,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
             s += x.x * x.x; s += x.y * x.y; s += x.z * x.z; s += x.w * x.w;
             return s;
         };
+        auto mulw = [](float4 x, uint4 wq) {
+            const float4 w = __builtin_bit_cast(float4, wq);
+            return __builtin_bit_cast(uint4, make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w));
+        };
         float ss = 0.f;
 #pragma unroll
         for (int k = 0; k < XS; k++) {
@@ -1106,35 +1121,17 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
                 const float4 x = addv(xv[k], bvv[k]);
                 if (w0) store16(a.sum_out + 4 * j, x);
                 ss = sq(ss, x);
-                xv[k] = __builtin_bit_cast(uint4, x);
+                put(mulw(x, wvv[k]), j);
             }
         }
         for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) {
             const float4 x = addv(src[j], srcb[j]);
             if (w0) store16(a.sum_out + 4 * j, x);
             ss = sq(ss, x);
+            put(mulw(x, srcw[j]), j);
         }
-        __shared__ float nred[LB / 64];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if ((tid & 63u) == 0) nred[tid >> 6] = ss;
-        __syncthreads();
-        float tot = 0.f;
-        for (uint32_t i = 0; i < (blockDim.x + 63u) / 64u; i++) tot += nred[i];
-        const float rms = sqrtf(tot / (float)a.cols + a.eps);
-        const float scale = 1.0f / rms;
-        auto nrm = [&](float4 x, uint4 wq) {
-            const float4 w = __builtin_bit_cast(float4, wq);
-            return __builtin_bit_cast(uint4, make_float4(x.x * scale * w.x, x.y * scale * w.y,
-                                                         x.z * scale * w.z, x.w * scale * w.w));
-        };
-#pragma unroll
-        for (int k = 0; k < XS; k++) {
-            const uint32_t j = tid + k * blockDim.x;
-            if (j < n16) put(nrm(__builtin_bit_cast(float4, xv[k]), wvv[k]), j);
-        }
-        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x)
-            put(nrm(addv(src[j], srcb[j]), srcw[j]), j);
+        ss = group_sum<64>(ss);
+        if ((tid & 63u) == 63u) nred[tid >> 6] = ss;
     } else if constexpr (PRO == kProSilu) {
         auto sm = [](uint4 gq, uint4 uq) {
             const float4 g = __builtin_bit_cast(float4, gq), u = __builtin_bit_cast(float4, uq);
@@ -1156,6 +1153,12 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
         for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(src[j], j);
     }
     lds_barrier();
+    if constexpr (NORM) {
+        float tot = 0.f;
+        for (uint32_t i = 0; i < (blockDim.x + 63u) / 64u; i++) tot += nred[i];
+        const float rms = sqrtf(tot / (float)a.cols + a.eps);
+        nscale = 1.0f / rms;
+    }
 
     using XT = typename std::conditional<I::PLANES, XP<S, SEG>, XF<S, SEG>>::type;
     XT xs;
@@ -1180,6 +1183,11 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
             xs.ik[s] = m.x;
             xs.sx[s] = SEG == 32 ? m.y + m.z : (h ? m.z : m.y);
             xs.sy[s] = m.w;
+            if constexpr (NORM) {
+                // the digits are those of x * rms; x = (digits / k) / rms
+                xs.ik[s] *= nscale;
+                xs.sx[s] *= nscale;
+            }
         } else {
             const uint32_t j = c / 4;
             const float4 *xp = xl4 + j + (j >> 4);
@@ -1401,9 +1409,12 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     }
     if (!rp) {
         fn = g == 1 ? stream_fn_g<T, true, kProPlain>(tsub) : stream_fn_g<T, false, kProPlain>(tsub);
-        fn_norm = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
-        fn_silu = !I::PLANES ? nullptr : g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
-        fn_norm_glu = !I::PLANES ? nullptr : g == 1 ? stream_fn_glu<T, true>(tsub) : stream_fn_glu<T, false>(tsub);
+        // input prologues for the fixed-point types only
+        if constexpr (I::PLANES) {
+            fn_norm = g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
+            fn_silu = g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
+            fn_norm_glu = g == 1 ? stream_fn_glu<T, true>(tsub) : stream_fn_glu<T, false>(tsub);
+        }
     }
     if (!fn) return;
     const uint64_t ncu = n_cu > 0 ? (uint64_t)n_cu : 256;

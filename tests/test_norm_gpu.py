@@ -91,6 +91,40 @@ def test_norm_matvec_variants(ctx, rinf, oracle, synth, dtype):
     assert np.array_equal(s, x)
 
 
+@pytest.mark.parametrize("dtype", [12, 14, 8], ids=["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("scale", [1e-15, 1e15], ids=["1e-15", "1e15"])
+def test_norm_matvec_input_scale(ctx, rinf, oracle, synth, dtype, scale):
+    """RmsNorm removes the scale of xa + xb (eps negligible here), so inputs
+    at 1e-15 and 1e15 stay within GEMV_TOL of the oracle and of the unscaled
+    result.  The kernel converts (xa + xb) * nw to fixed point before the
+    1/rms factor; at 1e-15 the segment maxima (about 1e-14) need 1/k below
+    2^-64 for full precision."""
+    rows, cols = 1024, 3584
+    eps = 1e-37
+    seed = synth.config_seed(1) + 5 * dtype + 3
+    raw = synth.gen_blocks(dtype, rows, cols, seed)
+    xa, xb, nw = inputs(synth, rows, cols, seed)
+    m = ctx.upload(raw, dtype, rows, cols)
+    outs = {}
+    for s in (1.0, scale):
+        xas, xbs = (xa * np.float32(s)).astype(np.float32), (xb * np.float32(s)).astype(np.float32)
+        import torch
+        dev = lambda a: torch.from_numpy(a).cuda()
+        dy = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        m.matvec_norm_dev(dev(xas), dev(xbs), dev(nw), eps, dy, None, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        y = dy.cpu().numpy()
+        x = (xas + xbs).astype(np.float32)
+        ref = oracle.mat_vec_mul_rows(raw, dtype, rows, cols, oracle.rmsnorm(x, nw, eps))
+        err = normwise_err(y, ref)
+        print(f"{NAMES[dtype]} scale {s:g} err={err:.2e}", flush=True)
+        assert err <= GEMV_TOL
+        outs[s] = y
+    m.free()
+    assert normwise_err(outs[scale], outs[1.0]) <= GEMV_TOL
+
+
 def test_norm_matvec_errors(ctx, rinf, synth):
     import torch
     rows, cols = 64, 256
