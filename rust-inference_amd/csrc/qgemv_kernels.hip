@@ -344,9 +344,6 @@ template <int N> __device__ __forceinline__ float group_sum(float v)
     return v;
 }
 
-// Stage float4 i of x (already loaded into v) as fixed-point planes; each
-// aligned group of 8 lanes holds one 32-element segment and must be active
-// together.
 template <int CTRL> __device__ __forceinline__ uint32_t dppu(uint32_t v)
 {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
@@ -361,56 +358,83 @@ __device__ __forceinline__ float absmax4(float4 v)
     return r;
 }
 
+// Stage 16 consecutive elements of x, half h = c & 1 of segment g = c >> 1
+// (q: its four float4), as fixed-point planes and the segment record; the two
+// halves of a segment sit in adjacent lanes (c even in the even lane) that
+// are active together, and each reduction over the segment is one DPP swap
+// between them.  The sums use fixed trees: a half's sum of x is
+// (t0 + t1) + (t2 + t3) with t_i = (x0 + x1) + (x2 + x3) over float4 i, and
+// sY adds the float4s' exact integer sums the same way, then the two halves.
 template <bool EVEN_ODD>
-__device__ __forceinline__ void stage_planes1(float4 v, uint32_t i, uint8_t *lds, uint32_t meta)
+__device__ __forceinline__ void stage_planes16(const uint4 (&q)[4], uint32_t c, uint8_t *lds, uint32_t meta)
 {
-    // non-negative floats order like their bit patterns: max over the 8 lanes
-    // of the segment in integer DPP steps (a NaN element is caught by `bad`)
-    uint32_t mb = __float_as_uint(absmax4(v));
-    mb = max(mb, dppu<0xB1>(mb)); mb = max(mb, dppu<0x4E>(mb)); mb = max(mb, dppu<0x141>(mb));
+    float4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = __builtin_bit_cast(float4, q[i]);
+    const uint32_t h = c & 1u, g = c >> 1;
+    uint32_t mb = max(max(__float_as_uint(absmax4(v[0])), __float_as_uint(absmax4(v[1]))),
+                      max(__float_as_uint(absmax4(v[2])), __float_as_uint(absmax4(v[3]))));
+    mb = max(mb, dppu<0xB1>(mb));
     const float m = __uint_as_float(mb);
-    float s = (v.x + v.y) + (v.z + v.w);
-    s += dpp<0xB1>(s); s += dpp<0x4E>(s);            // 16-element half sums
-    const float h = dpp<0x141>(s);                   // the other half's sum
-    const bool bad = !__builtin_isfinite(s + h);
-    // k capped at 2^100 (1/k stays a normal float; full precision for
-    // m >= kFix * 2^-100, about 3e-24 -- RMSNorm inputs are converted before
-    // the 1/rms scaling, so their segments may be far below 1)
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) t[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float s = (t[0] + t[1]) + (t[2] + t[3]);   // this half's sum
+    const float o = dpp<0xB1>(s);                    // the other half's
+    const bool bad = !__builtin_isfinite(s + o);
     const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.2676506e30f) : 0.f;
     const float ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
-    // Yb = Y + 0x8080: byte 2 is e2; bytes 0 and 1 are e0 and e1 with the top bit flipped
     const int off = 0x8080 - kMagicBits;
-    const uint32_t Y0 = (uint32_t)(__float_as_int(__builtin_fmaf(v.x, k, kMagic)) + off);
-    const uint32_t Y1 = (uint32_t)(__float_as_int(__builtin_fmaf(v.y, k, kMagic)) + off);
-    const uint32_t Y2 = (uint32_t)(__float_as_int(__builtin_fmaf(v.z, k, kMagic)) + off);
-    const uint32_t Y3 = (uint32_t)(__float_as_int(__builtin_fmaf(v.w, k, kMagic)) + off);
-    const int sy_part = EVEN_ODD ? (int)(Y1 + Y3) - 2 * 0x8080 : (int)((Y0 + Y1) + (Y2 + Y3)) - 4 * 0x8080;
-    float sy = (float)sy_part;
-    sy += dpp<0xB1>(sy); sy += dpp<0x4E>(sy); sy += dpp<0x141>(sy);
-    const uint32_t g = i >> 3, j = i & 7u;
+    uint32_t Y[4][4];
+    float f[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        Y[i][0] = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].x, k, kMagic)) + off);
+        Y[i][1] = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].y, k, kMagic)) + off);
+        Y[i][2] = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].z, k, kMagic)) + off);
+        Y[i][3] = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].w, k, kMagic)) + off);
+        f[i] = (float)(EVEN_ODD ? (int)(Y[i][1] + Y[i][3]) - 2 * 0x8080
+                                : (int)((Y[i][0] + Y[i][1]) + (Y[i][2] + Y[i][3])) - 4 * 0x8080);
+    }
+    float sy = (f[0] + f[1]) + (f[2] + f[3]);
+    sy += dpp<0xB1>(sy);
     uint8_t *seg = lds + plane_off(g);
     if (!EVEN_ODD) {
-        const uint32_t P01 = __builtin_amdgcn_perm(Y1, Y0, 0x05010400u);   // Y0.b0 Y1.b0 Y0.b1 Y1.b1
-        const uint32_t P23 = __builtin_amdgcn_perm(Y3, Y2, 0x05010400u);
-        const uint32_t Q01 = __builtin_amdgcn_perm(Y1, Y0, 0x0C0C0602u);   // Y0.b2 Y1.b2
-        const uint32_t Q23 = __builtin_amdgcn_perm(Y3, Y2, 0x0C0C0602u);
-        *(uint32_t *)(seg + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x05040100u) ^ 0x80808080u;
-        *(uint32_t *)(seg + 32 + 4 * j) = __builtin_amdgcn_perm(P23, P01, 0x07060302u) ^ 0x80808080u;
-        *(uint32_t *)(seg + 64 + 4 * j) = __builtin_amdgcn_perm(Q23, Q01, 0x05040100u);
+        uint32_t w0[4], w1[4], w2[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t P01 = __builtin_amdgcn_perm(Y[i][1], Y[i][0], 0x05010400u);
+            const uint32_t P23 = __builtin_amdgcn_perm(Y[i][3], Y[i][2], 0x05010400u);
+            const uint32_t Q01 = __builtin_amdgcn_perm(Y[i][1], Y[i][0], 0x0C0C0602u);
+            const uint32_t Q23 = __builtin_amdgcn_perm(Y[i][3], Y[i][2], 0x0C0C0602u);
+            w0[i] = __builtin_amdgcn_perm(P23, P01, 0x05040100u) ^ 0x80808080u;
+            w1[i] = __builtin_amdgcn_perm(P23, P01, 0x07060302u) ^ 0x80808080u;
+            w2[i] = __builtin_amdgcn_perm(Q23, Q01, 0x05040100u);
+        }
+        *(uint4 *)(seg + 16u * h) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+        *(uint4 *)(seg + 32u + 16u * h) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        *(uint4 *)(seg + 64u + 16u * h) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
     } else {
-        // elements 4j, 4j+2 -> even positions 2j, 2j+1; 4j+1, 4j+3 -> odd positions 16+2j, 17+2j
-        const uint32_t E = __builtin_amdgcn_perm(Y2, Y0, 0x05010400u);     // Y0.b0 Y2.b0 Y0.b1 Y2.b1
-        const uint32_t O = __builtin_amdgcn_perm(Y3, Y1, 0x05010400u);
-        const uint32_t E2 = __builtin_amdgcn_perm(Y2, Y0, 0x0C0C0602u);    // Y0.b2 Y2.b2
-        const uint32_t O2 = __builtin_amdgcn_perm(Y3, Y1, 0x0C0C0602u);
-        *(uint16_t *)(seg + 2 * j) = (uint16_t)(E ^ 0x8080u);
-        *(uint16_t *)(seg + 32 + 2 * j) = (uint16_t)((E >> 16) ^ 0x8080u);
-        *(uint16_t *)(seg + 64 + 2 * j) = (uint16_t)E2;
-        *(uint16_t *)(seg + 16 + 2 * j) = (uint16_t)(O ^ 0x8080u);
-        *(uint16_t *)(seg + 48 + 2 * j) = (uint16_t)((O >> 16) ^ 0x8080u);
-        *(uint16_t *)(seg + 80 + 2 * j) = (uint16_t)O2;
+        // float4 i holds elements 4i..4i+3 of the half: its even ones go to
+        // even positions 8h + 2i, +1, its odd ones to 16 + 8h + 2i, +1
+        uint32_t E[4], O[4], E2[4], O2[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            E[i] = __builtin_amdgcn_perm(Y[i][2], Y[i][0], 0x05010400u);
+            O[i] = __builtin_amdgcn_perm(Y[i][3], Y[i][1], 0x05010400u);
+            E2[i] = __builtin_amdgcn_perm(Y[i][2], Y[i][0], 0x0C0C0602u);
+            O2[i] = __builtin_amdgcn_perm(Y[i][3], Y[i][1], 0x0C0C0602u);
+        }
+        auto lo2 = [](uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); };
+        auto hi2 = [](uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); };
+        *(uint2 *)(seg + 8u * h) = make_uint2(lo2(E[0], E[1]) ^ 0x80808080u, lo2(E[2], E[3]) ^ 0x80808080u);
+        *(uint2 *)(seg + 16u + 8u * h) = make_uint2(lo2(O[0], O[1]) ^ 0x80808080u, lo2(O[2], O[3]) ^ 0x80808080u);
+        *(uint2 *)(seg + 32u + 8u * h) = make_uint2(hi2(E[0], E[1]) ^ 0x80808080u, hi2(E[2], E[3]) ^ 0x80808080u);
+        *(uint2 *)(seg + 48u + 8u * h) = make_uint2(hi2(O[0], O[1]) ^ 0x80808080u, hi2(O[2], O[3]) ^ 0x80808080u);
+        *(uint2 *)(seg + 64u + 8u * h) = make_uint2(lo2(E2[0], E2[1]), lo2(E2[2], E2[3]));
+        *(uint2 *)(seg + 80u + 8u * h) = make_uint2(lo2(O2[0], O2[1]), lo2(O2[2], O2[3]));
     }
-    if (j == 0) *(float4 *)(lds + meta + 16u * g) = make_float4(ik, s, h, sy);
+    if (h == 0) *(float4 *)(lds + meta + 16u * g) = make_float4(ik, s, o, sy);
 }
 
 // sum q*Y from the three plane dot products (see above)
@@ -1050,28 +1074,38 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     const uint32_t team = bid * tpw + tw;
     const uint32_t g = G1 ? 1u : a.g;
 
-    // 1. x loads, then (once x is in) the first D batches of weight loads
+    // 1. x loads, then (once x is in) the first D batches of weight loads.
+    // x is read in pieces: 16 elements (four float4) when the workgroup
+    // converts it to planes (stage_planes16), one float4 otherwise; thread
+    // tid takes pieces tid, tid + blockDim, ...
+    constexpr uint32_t PW = CV ? 4u : 1u;
+    static_assert(XS % PW == 0, "whole pieces in registers");
+    constexpr int XR = XS / (int)PW;
     const uint32_t n16 = I::PLANES && !CV ? image_bytes(true, a.cols) / 16u : a.cols / 4u;
+    const uint32_t npc = n16 / PW;              // pieces (cols % 32 == 0 for the planes)
     const uint4 *src = (const uint4 *)a.x;
     const uint32_t meta = planes_bytes(a.cols);
     // The weight loads are unconditional (clamped addresses): the compiler's
     // wait counting stays exact only when no such load sits on a conditional
-    // path.  The x loads are the exception: only the ceil(n16 / blockDim)
+    // path.  The x loads are the exception: only the ceil(npc / blockDim)
     // pieces the shape needs are issued (a uniform branch; each surplus load
     // costs address-unit time, and with a 3584-wide x and three input vectors
-    // 18 of 24 would be surplus), and the wait below, visible to the
-    // compiler as a wait for every load, closes them before any weight load.
+    // most would be surplus), and the wait below, visible to the compiler as
+    // a wait for every load, closes them before any weight load.
     uint4 xv[XS];
     uint4 bvv[TWO ? XS : 1], wvv[NORM ? XS : 1];
     const uint4 *srcb = (const uint4 *)a.xb, *srcw = (const uint4 *)a.nw;
-    const uint32_t nxs = (n16 + blockDim.x - 1u) / blockDim.x;
+    const uint32_t nxs = (npc + blockDim.x - 1u) / blockDim.x;
 #pragma unroll
-    for (int k = 0; k < XS; k++) {
-        if ((uint32_t)k < nxs) {
-            const uint32_t j = tid + k * blockDim.x, jc = j < n16 ? j : n16 - 1u;
-            xv[k] = src[jc];
-            if constexpr (TWO) bvv[k] = srcb[jc];
-            if constexpr (NORM) wvv[k] = srcw[jc];
+    for (int r = 0; r < XR; r++) {
+        if ((uint32_t)r < nxs) {
+            const uint32_t c = tid + r * blockDim.x, cc = c < npc ? c : npc - 1u;
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) {
+                xv[r * PW + i] = src[cc * PW + i];
+                if constexpr (TWO) bvv[r * PW + i] = srcb[cc * PW + i];
+                if constexpr (NORM) wvv[r * PW + i] = srcw[cc * PW + i];
+            }
         }
     }
     // x first: issued behind the weight stream of the workgroups that started
@@ -1085,9 +1119,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
-    auto put = [&](uint4 v, uint32_t j) {
-        if constexpr (CV) stage_planes1<I::EVEN_ODD>(__builtin_bit_cast(float4, v), j, lds, meta);
-        else l4[I::PLANES ? j : j + (j >> 4)] = v;
+    auto put = [&](const uint4 (&u)[PW], uint32_t c) {
+        if constexpr (CV) stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
+        else l4[I::PLANES ? c : c + (c >> 4)] = u[0];
     };
     // kProNorm: 1 / rms, applied to every segment's 1/k and sums after the
     // barrier that publishes the planes (see below)
@@ -1114,43 +1148,83 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
             return __builtin_bit_cast(uint4, make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w));
         };
         float ss = 0.f;
+        auto piece = [&](const uint4 (&xa)[PW], const uint4 (&xb)[PW], const uint4 (&w)[PW], uint32_t c) {
+            uint4 u[PW];
 #pragma unroll
-        for (int k = 0; k < XS; k++) {
-            const uint32_t j = tid + k * blockDim.x;
-            if (j < n16) {
-                const float4 x = addv(xv[k], bvv[k]);
-                if (w0) store16(a.sum_out + 4 * j, x);
+            for (uint32_t i = 0; i < PW; i++) {
+                const float4 x = addv(xa[i], xb[i]);
+                if (w0) store16(a.sum_out + 4 * (c * PW + i), x);
                 ss = sq(ss, x);
-                put(mulw(x, wvv[k]), j);
+                u[i] = mulw(x, w[i]);
+            }
+            put(u, c);
+        };
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const uint32_t c = tid + r * blockDim.x;
+            if (c < npc) {
+                uint4 pa[PW], pb[PW], pw[PW];
+#pragma unroll
+                for (uint32_t i = 0; i < PW; i++) {
+                    pa[i] = xv[r * PW + i]; pb[i] = bvv[r * PW + i]; pw[i] = wvv[r * PW + i];
+                }
+                piece(pa, pb, pw, c);
             }
         }
-        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) {
-            const float4 x = addv(src[j], srcb[j]);
-            if (w0) store16(a.sum_out + 4 * j, x);
-            ss = sq(ss, x);
-            put(mulw(x, srcw[j]), j);
+        for (uint32_t c = tid + XR * blockDim.x; c < npc; c += blockDim.x) {
+            uint4 pa[PW], pb[PW], pw[PW];
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) {
+                pa[i] = src[c * PW + i]; pb[i] = srcb[c * PW + i]; pw[i] = srcw[c * PW + i];
+            }
+            piece(pa, pb, pw, c);
         }
         ss = group_sum<64>(ss);
         if ((tid & 63u) == 63u) nred[tid >> 6] = ss;
     } else if constexpr (PRO == kProSilu) {
-        auto sm = [](uint4 gq, uint4 uq) {
-            const float4 g = __builtin_bit_cast(float4, gq), u = __builtin_bit_cast(float4, uq);
-            return __builtin_bit_cast(uint4, make_float4(silu1(g.x) * u.x, silu1(g.y) * u.y,
-                                                         silu1(g.z) * u.z, silu1(g.w) * u.w));
+        auto piece = [&](const uint4 (&gq)[PW], const uint4 (&uq)[PW], uint32_t c) {
+            uint4 u[PW];
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) {
+                const float4 gv = __builtin_bit_cast(float4, gq[i]), uv = __builtin_bit_cast(float4, uq[i]);
+                u[i] = __builtin_bit_cast(uint4, make_float4(silu1(gv.x) * uv.x, silu1(gv.y) * uv.y,
+                                                             silu1(gv.z) * uv.z, silu1(gv.w) * uv.w));
+            }
+            put(u, c);
         };
 #pragma unroll
-        for (int k = 0; k < XS; k++) {
-            const uint32_t j = tid + k * blockDim.x;
-            if (j < n16) put(sm(xv[k], bvv[k]), j);
+        for (int r = 0; r < XR; r++) {
+            const uint32_t c = tid + r * blockDim.x;
+            if (c < npc) {
+                uint4 pg[PW], pu[PW];
+#pragma unroll
+                for (uint32_t i = 0; i < PW; i++) { pg[i] = xv[r * PW + i]; pu[i] = bvv[r * PW + i]; }
+                piece(pg, pu, c);
+            }
         }
-        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(sm(src[j], srcb[j]), j);
+        for (uint32_t c = tid + XR * blockDim.x; c < npc; c += blockDim.x) {
+            uint4 pg[PW], pu[PW];
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) { pg[i] = src[c * PW + i]; pu[i] = srcb[c * PW + i]; }
+            piece(pg, pu, c);
+        }
     } else {
 #pragma unroll
-        for (int k = 0; k < XS; k++) {
-            const uint32_t j = tid + k * blockDim.x;
-            if (j < n16) put(xv[k], j);
+        for (int r = 0; r < XR; r++) {
+            const uint32_t c = tid + r * blockDim.x;
+            if (c < npc) {
+                uint4 u[PW];
+#pragma unroll
+                for (uint32_t i = 0; i < PW; i++) u[i] = xv[r * PW + i];
+                put(u, c);
+            }
         }
-        for (uint32_t j = tid + XS * blockDim.x; j < n16; j += blockDim.x) put(src[j], j);
+        for (uint32_t c = tid + XR * blockDim.x; c < npc; c += blockDim.x) {
+            uint4 u[PW];
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) u[i] = src[c * PW + i];
+            put(u, c);
+        }
     }
     lds_barrier();
     if constexpr (NORM) {
