@@ -112,10 +112,11 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
         delete m;
         return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
     }
-    // Owned Q4_K / Q6_K matrices also get the repacked layout the stream
-    // kernels read with contiguous loads (a permutation of the same bytes;
-    // d keeps the GGUF layout for the dequant and generic kernels).  Bytes
-    // wrapped from caller memory keep the GGUF-layout kernels.
+    // Owned Q4_K / Q5_K / Q6_K matrices also get the repacked layout the
+    // stream kernels read with contiguous loads (the same bytes -- for Q5_K
+    // the same bits -- rearranged; d keeps the GGUF layout for the dequant
+    // and generic kernels).  Bytes wrapped from caller memory keep the
+    // GGUF-layout kernels.
     if (owned && qg::repack_eligible(type, m->plan, rows)) {
         uint8_t *r = nullptr;
         hipError_t e = hipMalloc((void **)&r, nbytes + qg::kTailPad);

@@ -623,6 +623,43 @@ template <> struct Item<T_Q5_K> {
         out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
         out[1] = __builtin_fmaf(d * ub(SC, 1), fix3(b0, b1, b2) * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
     }
+    // The repacked row group (repack_k): the nb = ni/4 block headers, piece k
+    // (16 bytes) of item it's 32 quant bytes at nb*16 + (k*ni + it)*16, and the
+    // item's two qh bits per element as 8 bytes at nb*16 + 32ni + 8it -- word
+    // w, byte b, bits 2t'+0/1 = bits j, j+1 of qh[16w + 4t' + b] -- so that
+    // quant word t = 4w + t' takes its fifth bits with constant shifts.
+    // r[4..5] hold those 8 bytes; r[6..11] are unused.
+    __device__ static void load_rp(const uint8_t *grp, uint32_t it, uint32_t ni, uint32_t (&r)[NRAW])
+    {
+        const uint4 h = *(const uint4 *)(grp + (it >> 2) * 16u);
+        const uint8_t *q = grp + (ni >> 2) * 16u + it * 16u;
+        const uint4 q0 = *(const uint4 *)q, q1 = *(const uint4 *)(q + ni * 16u);
+        const uint2 hb = *(const uint2 *)(grp + (ni >> 2) * 16u + 32u * ni + 8u * it);
+        r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
+        r[4] = hb.x; r[5] = hb.y;
+#pragma unroll
+        for (int k = 6; k < 12; k++) r[k] = 0u;
+        r[12] = q0.x; r[13] = q0.y; r[14] = q0.z; r[15] = q0.w;
+        r[16] = q1.x; r[17] = q1.y; r[18] = q1.z; r[19] = q1.w;
+    }
+    __device__ static void compute_rp(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t it,
+                                      float (&out)[S])
+    {
+        const float d = h2f(r[0]), dmin = h2f(r[0] >> 16);
+        uint32_t SC, MN;
+        k4pair(it & 3u, r[1], r[2], r[3], SC, MN);
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint32_t w = r[12 + t], hb = r[4 + (t >> 2)] >> (2 * (t & 3));
+            const uint32_t qa = andm(w, 0x0F0F0F0Fu) | ((hb & 0x01010101u) << 4);
+            const uint32_t qb = andm(w >> 4, 0x0F0F0F0Fu) | (((hb >> 1) & 0x01010101u) << 4);
+            a0 = sdot4(qa, x.p[0][0][t], a0); a1 = sdot4(qa, x.p[0][1][t], a1); a2 = sdot4(qa, x.p[0][2][t], a2);
+            b0 = sdot4(qb, x.p[1][0][t], b0); b1 = sdot4(qb, x.p[1][1][t], b1); b2 = sdot4(qb, x.p[1][2][t], b2);
+        }
+        out[0] = __builtin_fmaf(d * ub(SC, 0), fix3(a0, a1, a2) * x.ik[0], -(dmin * ub(MN, 0)) * x.sx[0]);
+        out[1] = __builtin_fmaf(d * ub(SC, 1), fix3(b0, b1, b2) * x.ik[1], -(dmin * ub(MN, 1)) * x.sx[1]);
+    }
 };
 
 // Q6_K (quant.rs:265-292): item = (block, half n, i = l/16): 4 slots of 16,
@@ -1439,7 +1476,7 @@ template <uint32_t T, bool G1, bool RP = false> static const void *stream_fn_glu
 
 // Types the upload repacks (repack_k): their items take 5 load instructions or
 // more in the GGUF layout.
-template <uint32_t T> constexpr bool repackable() { return T == T_Q4_K || T == T_Q6_K; }
+template <uint32_t T> constexpr bool repackable() { return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K; }
 
 static int max_lds_bytes()
 {
@@ -1558,7 +1595,7 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool r
     case T_Q5_0: plan_stream<T_Q5_0>(rows, cols, n_cu, false, p); break;
     case T_Q8_0: plan_stream<T_Q8_0>(rows, cols, n_cu, false, p); break;
     case T_Q4_K: plan_stream<T_Q4_K>(rows, cols, n_cu, rp, p); break;
-    case T_Q5_K: plan_stream<T_Q5_K>(rows, cols, n_cu, false, p); break;
+    case T_Q5_K: plan_stream<T_Q5_K>(rows, cols, n_cu, rp, p); break;
     case T_Q6_K: plan_stream<T_Q6_K>(rows, cols, n_cu, rp, p); break;
     default: return -1;
     }
@@ -1567,14 +1604,19 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool r
 
 bool repack_eligible(uint32_t type, const Plan &p, size_t rows)
 {
-    return (type == T_Q4_K || type == T_Q6_K) && p.kind == 1 && p.g > 0 && rows % p.g == 0;
+    return (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K) && p.kind == 1 && p.g > 0 && rows % p.g == 0;
 }
 
 // The repacked layout of a whole number of row groups, group by group (the
-// same bytes, permuted so that a wave's loads of one piece are contiguous):
+// same bytes -- for Q5_K the same bits -- rearranged so that a wave's loads
+// of one piece are contiguous):
 //   Q4_K (ni = 2 nb items of 128 weights): the nb 16-byte block headers, then
 //        piece k (bytes 16k..16k+15 of the item's 64 quant bytes) of item it
 //        at nb*16 + (k*ni + it)*16;
+//   Q5_K (ni = 4 nb items of 64 weights, j = 2 (it & 3)): the nb block
+//        headers, piece k of the item's 32 quant bytes at nb*16 + (k*ni + it)*16,
+//        then 8 bytes per item at nb*16 + 32ni + 8it: bits 8b + 2t' and
+//        8b + 2t' + 1 of word w are bits j and j + 1 of qh[16w + 4t' + b];
 //   Q6_K (ni = 4 nb items of 64 weights; item it = block it/4, half
 //        n = (it/2)&1, i = it&1): ql[64n+16i..+16] at it*16,
 //        ql[64n+32+16i..+16] at (ni+it)*16, qh[32n+16i..+16] at (2ni+it)*16,
@@ -1596,6 +1638,19 @@ __global__ void __launch_bounds__(256) repack_k(const uint8_t *__restrict__ src,
             for (int j = 0; j < 16; j++) dg[(it >> 1) * 16u + j] = b[j];
         for (uint32_t k = 0; k < 4; k++)
             for (int j = 0; j < 16; j++) dg[(ni >> 1) * 16u + (k * ni + it) * 16u + j] = b[16u + (it & 1u) * 64u + 16u * k + j];
+    } else if constexpr (T == T_Q5_K) {
+        const uint8_t *b = sg + (it >> 2) * 176u;
+        const uint32_t H = (ni >> 2) * 16u, j = (it & 3u) * 2u;
+        if ((it & 3u) == 0)
+            for (int k = 0; k < 16; k++) dg[(it >> 2) * 16u + k] = b[k];
+        for (uint32_t k = 0; k < 32; k++) dg[H + ((k >> 4) * ni + it) * 16u + (k & 15u)] = b[48u + (it & 3u) * 32u + k];
+        uint32_t W[2] = {0u, 0u};
+        for (uint32_t m = 0; m < 32; m++) {       // qh byte m = 16w + 4t' + b
+            const uint32_t w = m >> 4, tp = (m >> 2) & 3u, bb = m & 3u, v = b[16u + m];
+            W[w] |= ((v >> j) & 1u) << (8u * bb + 2u * tp);
+            W[w] |= ((v >> (j + 1u)) & 1u) << (8u * bb + 2u * tp + 1u);
+        }
+        for (uint32_t k = 0; k < 8; k++) dg[H + 32u * ni + 8u * it + k] = (uint8_t)(W[k >> 2] >> (8u * (k & 3u)));
     } else {
         const uint8_t *b = sg + (it >> 2) * 210u;
         const uint32_t n = (it >> 1) & 1u, i = it & 1u;
@@ -1621,6 +1676,9 @@ int launch_repack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst
     if (blocks > 0x7FFFFFFFull) return -1;
     if (type == T_Q4_K)
         hipLaunchKernelGGL(repack_k<T_Q4_K>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
+                           n_items, p.ni, (uint32_t)p.group_bytes);
+    else if (type == T_Q5_K)
+        hipLaunchKernelGGL(repack_k<T_Q5_K>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
                            n_items, p.ni, (uint32_t)p.group_bytes);
     else if (type == T_Q6_K)
         hipLaunchKernelGGL(repack_k<T_Q6_K>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
