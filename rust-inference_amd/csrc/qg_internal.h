@@ -17,7 +17,7 @@ struct qg_model;
 struct qg_mat {
     qg_ctx *ctx;
     uint8_t *d;        // device bytes in the GGUF layout (nbytes data + kTailPad zeros)
-    uint8_t *d_rp;     // the matrix in the repacked layout (owned Q4_K/Q5_K/Q6_K), or NULL
+    uint8_t *d_rp;     // the matrix in the repacked layout (owned Q8_0/Q4_K/Q5_K/Q6_K), or NULL
     size_t nbytes;     // bytes the kernels may treat as data
     uint32_t type;
     size_t rows, cols;

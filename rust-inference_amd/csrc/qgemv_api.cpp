@@ -112,7 +112,7 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
         delete m;
         return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
     }
-    // Owned Q4_K / Q5_K / Q6_K matrices also get the repacked layout the
+    // Owned Q8_0 / Q4_K / Q5_K / Q6_K matrices also get the repacked layout the
     // stream kernels read with contiguous loads (the same bytes -- for Q5_K
     // the same bits -- rearranged; d keeps the GGUF layout for the dequant
     // and generic kernels).  Bytes wrapped from caller memory keep the

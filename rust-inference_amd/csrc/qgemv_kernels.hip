@@ -795,6 +795,32 @@ template <> struct Item<T_Q8_0> {
             out[s] = dd[s] * (fix3(a0, a1, a2) * x.ik[s]);
         }
     }
+    // The repacked row group (repack_k): piece k (16 bytes) of the item's 64
+    // codes at (k*ni + it)*16, then the item's two d halves at 64ni + 4it.
+    __device__ static void load_rp(const uint8_t *grp, uint32_t it, uint32_t ni, uint32_t (&r)[NRAW])
+    {
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint4 v = *(const uint4 *)(grp + (k * ni + it) * 16u);
+            r[4 * k] = v.x; r[4 * k + 1] = v.y; r[4 * k + 2] = v.z; r[4 * k + 3] = v.w;
+        }
+        r[16] = *(const uint32_t *)(grp + 64u * ni + 4u * it);
+    }
+    __device__ static void compute_rp(const uint32_t (&r)[NRAW], const XP<S, SEG> &x, uint32_t,
+                                      float (&out)[S])
+    {
+        const float dd[2] = {h2f(r[16]), h2f(r[16] >> 16)};
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            int a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t q = r[8 * s + t];
+                a0 = sdot4(q, x.p[s][0][t], a0); a1 = sdot4(q, x.p[s][1][t], a1); a2 = sdot4(q, x.p[s][2][t], a2);
+            }
+            out[s] = dd[s] * (fix3(a0, a1, a2) * x.ik[s]);
+        }
+    }
 };
 
 // Q4_0 (quant.rs:114-121): two blocks (36 bytes).  Interleaved nibble order:
@@ -1476,7 +1502,7 @@ template <uint32_t T, bool G1, bool RP = false> static const void *stream_fn_glu
 
 // Types the upload repacks (repack_k): their items take 5 load instructions or
 // more in the GGUF layout.
-template <uint32_t T> constexpr bool repackable() { return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K; }
+template <uint32_t T> constexpr bool repackable() { return T == T_Q8_0 || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K; }
 
 static int max_lds_bytes()
 {
@@ -1593,7 +1619,7 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool r
     case T_F16: plan_stream<T_F16>(rows, cols, n_cu, false, p); break;
     case T_Q4_0: plan_stream<T_Q4_0>(rows, cols, n_cu, false, p); break;
     case T_Q5_0: plan_stream<T_Q5_0>(rows, cols, n_cu, false, p); break;
-    case T_Q8_0: plan_stream<T_Q8_0>(rows, cols, n_cu, false, p); break;
+    case T_Q8_0: plan_stream<T_Q8_0>(rows, cols, n_cu, rp, p); break;
     case T_Q4_K: plan_stream<T_Q4_K>(rows, cols, n_cu, rp, p); break;
     case T_Q5_K: plan_stream<T_Q5_K>(rows, cols, n_cu, rp, p); break;
     case T_Q6_K: plan_stream<T_Q6_K>(rows, cols, n_cu, rp, p); break;
@@ -1604,7 +1630,8 @@ int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool r
 
 bool repack_eligible(uint32_t type, const Plan &p, size_t rows)
 {
-    return (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K) && p.kind == 1 && p.g > 0 && rows % p.g == 0;
+    return (type == T_Q8_0 || type == T_Q4_K || type == T_Q5_K || type == T_Q6_K) && p.kind == 1 && p.g > 0 &&
+           rows % p.g == 0;
 }
 
 // The repacked layout of a whole number of row groups, group by group (the
@@ -1613,6 +1640,8 @@ bool repack_eligible(uint32_t type, const Plan &p, size_t rows)
 //   Q4_K (ni = 2 nb items of 128 weights): the nb 16-byte block headers, then
 //        piece k (bytes 16k..16k+15 of the item's 64 quant bytes) of item it
 //        at nb*16 + (k*ni + it)*16;
+//   Q8_0 (item = 2 blocks, 64 codes): piece k (codes 16k..16k+15) of item it
+//        at (k*ni + it)*16, then the two d halves of every item at 64ni + 4it;
 //   Q5_K (ni = 4 nb items of 64 weights, j = 2 (it & 3)): the nb block
 //        headers, piece k of the item's 32 quant bytes at nb*16 + (k*ni + it)*16,
 //        then 8 bytes per item at nb*16 + 32ni + 8it: bits 8b + 2t' and
@@ -1632,7 +1661,14 @@ __global__ void __launch_bounds__(256) repack_k(const uint8_t *__restrict__ src,
     const uint32_t it = (uint32_t)(idx - gidx * ni);
     const uint8_t *sg = src + gidx * group_bytes;
     uint8_t *dg = dst + gidx * group_bytes;
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q8_0) {
+        const uint8_t *b = sg + it * 68u;          // blocks 2it, 2it + 1: d, then 32 codes each
+        for (uint32_t k = 0; k < 64; k++) dg[((k >> 4) * ni + it) * 16u + (k & 15u)] = b[k < 32 ? 2u + k : 4u + k];
+        dg[64u * ni + 4u * it] = b[0];
+        dg[64u * ni + 4u * it + 1u] = b[1];
+        dg[64u * ni + 4u * it + 2u] = b[34];
+        dg[64u * ni + 4u * it + 3u] = b[35];
+    } else if constexpr (T == T_Q4_K) {
         const uint8_t *b = sg + (it >> 1) * 144u;
         if ((it & 1u) == 0)
             for (int j = 0; j < 16; j++) dg[(it >> 1) * 16u + j] = b[j];
@@ -1674,7 +1710,10 @@ int launch_repack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst
     if (n_items == 0) return 0;
     const uint64_t blocks = (n_items + 255) / 256;
     if (blocks > 0x7FFFFFFFull) return -1;
-    if (type == T_Q4_K)
+    if (type == T_Q8_0)
+        hipLaunchKernelGGL(repack_k<T_Q8_0>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
+                           n_items, p.ni, (uint32_t)p.group_bytes);
+    else if (type == T_Q4_K)
         hipLaunchKernelGGL(repack_k<T_Q4_K>, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, src, dst,
                            n_items, p.ni, (uint32_t)p.group_bytes);
     else if (type == T_Q5_K)

@@ -70,7 +70,7 @@ WRAP_SHAPES = [(896, 896), (128, 896), (4096, 14336), (37, 18944), (1200, 256), 
 @pytest.mark.parametrize("shape", WRAP_SHAPES, ids=[f"{r}x{c}" for r, c in WRAP_SHAPES])
 def test_wrapped_bytes_match_upload(ctx, oracle, synth, dtype, shape):
     """qg_wrap_device keeps the GGUF layout (its kernels read the file's
-    blocks), qg_upload of Q4_K/Q5_K/Q6_K also keeps a repacked copy for the
+    blocks), qg_upload of Q8_0/Q4_K/Q5_K/Q6_K also keeps a repacked copy for the
     stream kernels: both give the same y, bit for bit, and the oracle's within
     GEMV_TOL; the plain and the RMSNorm-prologue kernels of both layouts."""
     import torch
