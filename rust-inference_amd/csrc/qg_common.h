@@ -61,6 +61,9 @@ struct Plan {
     const void *fn_silu;   // the same kernel with the silu(g) * u input
     const void *fn_norm_glu;  // RMSNorm input, [gate; up] rows paired into silu(g) * u
     bool rp;               // the kernels read the repacked layout (launch_repack)
+    // plain mat-vec through the LDS ring kernel (gemv_ring_q4k) where it applies:
+    const void *fn_ring;   // nullptr otherwise
+    uint32_t ring_grid, ring_per, ring_lds;
 };
 
 }  // namespace qg
@@ -68,8 +71,8 @@ struct Plan {
 // Launchers implemented in qgemv_kernels.hip (C++ linkage, library-internal).
 struct ihipStream_t;
 namespace qg {
-// rp: plan the kernels of the repacked layout where the type has one (Q4_K,
-// Q6_K with whole row groups; Plan::rp tells whether it applied).
+// rp: plan the kernels of the repacked layout where the type has one (Q8_0,
+// Q4_K, Q5_K, Q6_K with whole row groups; Plan::rp tells whether it applied).
 int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool rp = false);
 // Whether make_plan(..., rp = true) would give a repacked-layout plan.
 bool repack_eligible(uint32_t type, const Plan &p, size_t rows);

@@ -1468,6 +1468,162 @@ __global__ void __launch_bounds__(LB) gemv_stream_pair(StreamArgs a1, StreamArgs
         stream_body<T2, TS2, 1, kDepth, G1B, true, kStage, LB, kDepth, kProNorm, false, RPB>(a2, blockIdx.x - grid1);
 }
 
+// ----------------------------------------------- LDS ring (Q4_K, wide rows)
+//
+// Plain mat-vec of a repacked Q4_K matrix whose rows are one row group of
+// 8448..14336 columns (66..112 items: teams of two waves).  Eight compute
+// waves (four teams) and two loader waves per workgroup.  The loaders copy
+// the four rows of each stage -- four consecutive row groups, contiguous in
+// memory -- straight into an LDS ring of kRingSlots slots with
+// global_load_lds_dwordx4, so the weight stream starts at kernel entry and
+// no compute wave ever waits behind a weight load: the compute waves load and
+// convert x at once, then read each item's 80 bytes from the ring.  One
+// workgroup barrier per stage publishes it; the loader refills the slot the
+// compute waves left before that barrier.  Loader l owns 16 KB of each slot
+// (rows 2l and 2l + 1, then padding): every one of its kRingInst copy
+// instructions is issued, for clamped sources too, so its wait counts are
+// exact, and what a clamped lane copies lands in the padding.  Same item
+// arithmetic and the same reduction order (per-wave sums, then wave 0 + wave
+// 1) as gemv_stream, so y is bit-identical.
+constexpr uint32_t kRingSlots = 3, kRingInst = 16, kRingLoader = kRingInst * 1024u;
+constexpr uint32_t kRingSlotBytes = 2u * kRingLoader;
+
+// s_waitcnt immediate for vmcnt(n), expcnt and lgkmcnt unconstrained (gfx9:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr uint32_t waitcnt_vm(uint32_t n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
+
+// 16 bytes per lane from gp into LDS at lds_base + 16 * lane (global_load_lds_dwordx4;
+// lds_base is wave-uniform, an LDS byte address)
+__device__ __forceinline__ void lds_dma16(const void *gp, uint32_t lds_base)
+{
+    __builtin_amdgcn_global_load_lds(gp, (__attribute__((address_space(3))) void *)(uintptr_t)lds_base, 16, 0, 0);
+}
+
+__global__ void __launch_bounds__(640) gemv_ring_q4k(StreamArgs a)
+{
+    using I = Item<T_Q4_K>;
+    constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
+    extern __shared__ float4 xl4[];
+    uint8_t *lds = (uint8_t *)xl4;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t gb = a.group_bytes, ring = a.red_off;
+    float *redf = (float *)(lds + ring + kRingSlots * kRingSlotBytes);   // 2 x 8 per-wave sums
+    if (wave >= 8u) {
+        // loader l: rows of teams 2l and 2l + 1 of every stage
+        const uint32_t l = wave - 8u;
+        auto issue = [&](uint32_t i) {
+            const uint32_t g0 = blockIdx.x * 4u + 2u * l + i * a.n_teams;   // its first row group
+            const uint32_t dst = lds0 + ring + (i % kRingSlots) * kRingSlotBytes + l * kRingLoader;
+#pragma unroll
+            for (uint32_t k = 0; k < kRingInst; k++) {
+                const uint32_t p = k * 64u + lane;                           // 16-byte piece of the two rows
+                const uint32_t r = p >= gb / 16u ? 1u : 0u;
+                const uint32_t grp = g0 + r, pc = p - r * (gb / 16u);
+                const bool ok = grp < a.n_groups && pc < gb / 16u;
+                lds_dma16(a.w + (ok ? grp * gb + pc * 16u : 0u), dst + k * 1024u);
+            }
+        };
+#pragma unroll
+        for (uint32_t i = 0; i < kRingSlots - 1u; i++)
+            if (i < a.per_team) issue(i);
+        lds_barrier();                                                      // x staged
+        for (uint32_t i = 0; i < a.per_team; i++) {
+            // stage i landed: at most the next stage's copies still in flight
+            if (a.per_team - 1u - i >= kRingSlots - 2u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kRingInst));
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            lds_barrier();                                                  // stage i published
+            if (i + kRingSlots - 1u < a.per_team) issue(i + kRingSlots - 1u);
+        }
+        lds_barrier();
+        return;
+    }
+    const uint32_t tw = tid >> 7, lt = tid & 127u, wt = wave & 1u;
+    const bool active = lt < a.ni;
+    const uint32_t it = active ? lt : 0u;
+    const uint32_t team = blockIdx.x * 4u + tw;
+    // x: 16-element pieces, converted by the 512 compute threads
+    const uint32_t npc = a.cols / 16u;
+    const uint4 *src = (const uint4 *)a.x;
+    const uint32_t meta = planes_bytes(a.cols);
+    constexpr int XR = kStage / 4;
+    uint4 xv[kStage];
+    const uint32_t nxs = (npc + 511u) / 512u;
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        if ((uint32_t)r < nxs) {
+            const uint32_t c = tid + r * 512u, cc = c < npc ? c : npc - 1u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[4 * r + i] = src[4 * cc + i];
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const uint32_t c = tid + r * 512u;
+        if (c < npc) {
+            uint4 u[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) u[i] = xv[4 * r + i];
+            stage_planes16<false>(u, c, lds, meta);
+        }
+    }
+    for (uint32_t c = tid + XR * 512u; c < npc; c += 512u) {
+        uint4 u[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) u[i] = src[4 * c + i];
+        stage_planes16<false>(u, c, lds, meta);
+    }
+    lds_barrier();
+    XP<S, SEG> xs;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint32_t gs = I::seg_elem(it, s) / 32u;
+        const uint8_t *sp = lds + plane_off(gs);
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const uint4 q = active ? *(const uint4 *)(sp + 32 * p) : make_uint4(0, 0, 0, 0);
+            const uint4 q2 = active ? *(const uint4 *)(sp + 32 * p + 16) : make_uint4(0, 0, 0, 0);
+            xs.p[s][p][0] = q.x; xs.p[s][p][1] = q.y; xs.p[s][p][2] = q.z; xs.p[s][p][3] = q.w;
+            xs.p[s][p][4] = q2.x; xs.p[s][p][5] = q2.y; xs.p[s][p][6] = q2.z; xs.p[s][p][7] = q2.w;
+        }
+        const float4 m = active ? *(const float4 *)(lds + meta + 16u * gs) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xs.ik[s] = m.x;
+        xs.sx[s] = m.y + m.z;
+        xs.sy[s] = m.w;
+    }
+    auto flush = [&](uint32_t i) {                          // after a barrier: y of stage i
+        if (wt == 0 && lane == 0) {
+            const uint32_t grp = team + i * a.n_teams;
+            const float v = redf[(i & 1u) * 8u + 2u * tw] + redf[(i & 1u) * 8u + 2u * tw + 1u];
+            if (grp < a.n_groups) store_y(a.y + grp, v);
+        }
+    };
+    const uint32_t nb16 = (a.ni >> 1) * 16u;
+    for (uint32_t i = 0; i < a.per_team; i++) {
+        lds_barrier();
+        if (i > 0) flush(i - 1);
+        const uint8_t *row = lds + ring + (i % kRingSlots) * kRingSlotBytes + (tw >> 1) * kRingLoader + (tw & 1u) * gb;
+        uint32_t raw[NR];
+        const uint4 h = *(const uint4 *)(row + (it >> 1) * 16u);
+        const uint8_t *q = row + nb16 + it * 16u;
+        const uint4 q0 = *(const uint4 *)q, q1 = *(const uint4 *)(q + a.ni * 16u);
+        const uint4 q2 = *(const uint4 *)(q + 2u * a.ni * 16u), q3 = *(const uint4 *)(q + 3u * a.ni * 16u);
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
+        raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
+        raw[12] = q2.x; raw[13] = q2.y; raw[14] = q2.z; raw[15] = q2.w;
+        raw[16] = q3.x; raw[17] = q3.y; raw[18] = q3.z; raw[19] = q3.w;
+        float t = I::compute_sum(raw, xs, it);
+        t = active ? t : 0.f;
+        t = group_sum<64>(t);
+        if (lane == 63u) redf[(i & 1u) * 8u + wave] = t;
+    }
+    lds_barrier();
+    if (a.per_team > 0) flush(a.per_team - 1);
+}
+
 // ------------------------------------------------------------ planning
 
 static uint32_t gcd_u(uint64_t a, uint64_t b)
@@ -1608,6 +1764,20 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     p->red_off = img;
     p->lds = lds;
     p->kind = 1;
+    // the LDS ring kernel for repacked Q4_K rows of 8448..14336 columns
+    p->fn_ring = nullptr;
+    if constexpr (T == T_Q4_K) {
+        const uint32_t ring_lds = img + kRingSlots * kRingSlotBytes + 64u;
+        if (rp && g == 1 && tsub == 0 && wpt == 2 && 2u * gbytes <= kRingLoader &&
+            ring_lds <= (uint32_t)max_lds_bytes()) {
+            const uint64_t wgs = (n_groups + 3) / 4;
+            const uint32_t rg = (uint32_t)(wgs < ncu ? wgs : ncu);
+            p->fn_ring = (const void *)gemv_ring_q4k;
+            p->ring_grid = rg;
+            p->ring_per = (uint32_t)((n_groups + 4ull * rg - 1) / (4ull * rg));
+            p->ring_lds = ring_lds;
+        }
+    }
 }
 
 int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool rp)
@@ -1747,6 +1917,11 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
     if (p.kind != 1 || !p.fn) return launch_gemv_generic(type, w, rows, cols, x, y, stream);
     StreamArgs a = stream_args(p, w, nbytes, rows, cols, x, y);
     void *args[] = {&a};
+    if (p.fn_ring) {
+        a.n_teams = 4u * p.ring_grid;
+        a.per_team = p.ring_per;
+        return hipLaunchKernel(p.fn_ring, dim3(p.ring_grid), dim3(640), args, p.ring_lds, st) == hipSuccess ? 0 : -2;
+    }
     return hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) == hipSuccess ? 0 : -2;
 }
 
