@@ -324,6 +324,7 @@ def main():
     raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
     x = synth.gen_x(cols, synth.config_seed(4))
     mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
+    kernel = {1: "qg::gemv_stream", 2: "qg::gemv_ring_q4k"}.get(mats[0].kernel_kind, "qg::gemv_generic")
     dx = torch.from_numpy(x).cuda()
     dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
@@ -394,7 +395,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                      "kernel_us_mean": round(kern_ms * 1e3, 3),
-                     "kernel": "qg::gemv_stream (rust-inference_amd/csrc/qgemv_kernels.hip)"},
+                     "kernel": kernel + " (rust-inference_amd/csrc/qgemv_kernels.hip)"},
         "cpu_baseline": cpu,
         "decode": decode,
     }

@@ -69,8 +69,10 @@ int qg_wrap_device(qg_ctx *ctx, const void *d_raw, size_t nbytes, uint32_t ggml_
 int qg_mat_free(qg_ctx *ctx, qg_mat *mat);
 int qg_mat_info(const qg_mat *mat, uint32_t *ggml_type, size_t *rows, size_t *cols,
                 size_t *nbytes);
-/* Kernel choice fixed at upload: 1 = stream kernel (fast path), 0 = generic
- * per-element kernel (cols % 32 != 0 and other shapes the planner rejects). */
+/* Kernel choice fixed at upload: 1 = stream kernel (fast path), 2 = the
+ * stream kernel family with the LDS-ring kernel for the plain mat-vec
+ * (repacked Q4_K rows of 8448..14336 columns), 0 = generic per-element kernel
+ * (cols % 32 != 0 and other shapes the planner rejects). */
 int qg_mat_kernel_kind(const qg_mat *mat);
 
 /* Device-resident mat-vec: y[r] = sum_c W[r,c] * x[c] (src/quant.rs:178-206).

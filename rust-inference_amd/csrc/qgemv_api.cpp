@@ -415,7 +415,11 @@ int qg_mat_info(const qg_mat *mat, uint32_t *type, size_t *rows, size_t *cols, s
     return QG_OK;
 }
 
-int qg_mat_kernel_kind(const qg_mat *mat) { return mat ? mat->plan.kind : -1; }
+int qg_mat_kernel_kind(const qg_mat *mat)
+{
+    if (!mat) return -1;
+    return mat->plan.kind == 1 && mat->plan.fn_ring ? 2 : mat->plan.kind;
+}
 
 int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, void *stream)
 {

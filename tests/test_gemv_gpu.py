@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 TYPES = [0, 1, 2, 6, 8, 12, 13, 14]
 NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 6: "Q5_0", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}
 KAT = json.loads((pathlib.Path(__file__).parent / "golden" / "kat_blocks.json").read_text())
-FAST = (1,)            # stream kernel (kind 0 is the per-element fallback)
+FAST = (1, 2)          # stream kernel, or with the LDS ring kernel (kind 0 is the per-element fallback)
 
 
 def gpu_gemv(ctx, raw, dtype, rows, cols, x):
@@ -63,10 +63,11 @@ def test_gemv_parity(ctx, oracle, synth, dtype, shape):
     assert err <= GEMV_TOL
 
 
-# (37, 14336), (1030, 8448): Q4_K through the LDS ring kernel (uploaded) against
-# the stream kernel (wrapped), with partial stages and the narrowest ring row
+# (37, 14336), (1030, 8448), (9000, 8448): Q4_K through the LDS ring kernel
+# (uploaded) against the stream kernel (wrapped), with partial stages, the
+# narrowest ring row and nine stages per team
 WRAP_SHAPES = [(896, 896), (128, 896), (4096, 14336), (37, 18944), (1200, 256), (21, 8320), (64, 288),
-               (37, 14336), (1030, 8448)]
+               (37, 14336), (1030, 8448), (9000, 8448)]
 
 
 @pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
@@ -172,7 +173,7 @@ def test_interleaved_launches_are_bit_identical(ctx, oracle, synth):
         mats.append(ctx.upload(raw, t, rows, cols))
         xs.append(synth.gen_x(cols, 40 + i))
         refs.append(oracle.mat_vec_mul(raw, t, rows, cols, xs[-1]))
-    assert all(m.kernel_kind == 1 for m in mats)
+    assert [m.kernel_kind for m in mats] == [2, 1, 1]       # the Q4_K rows take the LDS ring kernel
     first = [None] * len(cases)
     for rep in range(4):
         for i, m in enumerate(mats):
