@@ -324,7 +324,7 @@ def main():
     raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
     x = synth.gen_x(cols, synth.config_seed(4))
     mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
-    kernel = {1: "qg::gemv_stream", 2: "qg::gemv_ring_q4k"}.get(mats[0].kernel_kind, "qg::gemv_generic")
+    kernel = {1: "qg::gemv_stream", 2: "qg::gemv_ring"}.get(mats[0].kernel_kind, "qg::gemv_generic")
     dx = torch.from_numpy(x).cuda()
     dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()

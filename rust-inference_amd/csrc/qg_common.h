@@ -61,9 +61,9 @@ struct Plan {
     const void *fn_silu;   // the same kernel with the silu(g) * u input
     const void *fn_norm_glu;  // RMSNorm input, [gate; up] rows paired into silu(g) * u
     bool rp;               // the kernels read the repacked layout (launch_repack)
-    // plain mat-vec through the LDS ring kernel (gemv_ring_q4k) where it applies:
+    // plain mat-vec through the LDS ring kernel (gemv_ring) where it applies:
     const void *fn_ring;   // nullptr otherwise
-    uint32_t ring_grid, ring_per, ring_lds;
+    uint32_t ring_grid, ring_block, ring_per, ring_lds, ring_slot2;
 };
 
 }  // namespace qg

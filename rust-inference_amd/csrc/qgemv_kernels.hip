@@ -1001,6 +1001,7 @@ struct StreamArgs {
     uint32_t wpt;                  // waves per team (TSUB == 0)
     uint32_t chunk;                // batches per partial-sum flush (TSUB == 0)
     uint32_t red_off;              // LDS byte offset of the partial-sum slots
+    uint32_t ring_slot2;           // gemv_ring: LDS byte offset of the third ring slot
     // fused RMSNorm of the input (NORM kernels): x = rmsnorm(x + xb) * nw
     const float *xb;               // second addend (the residual branch), cols floats
     const float *nw;               // norm weights, cols floats
@@ -1080,6 +1081,37 @@ __device__ __forceinline__ void item_compute(const uint32_t (&r)[I::NRAW], const
 {
     if constexpr (RP && HasRp<I>::value) I::compute_rp(r, x, it, acc);
     else I::compute(r, x, it, acc);
+}
+
+// This lane's x slice for its item -- the S segments the item meets, as
+// fixed-point digits and records -- from the planes staged in LDS; srow[s]:
+// the row (within the row group) of slot s (0 with one row per group, G1,
+// where no division is needed).  Inactive lanes get zeros.
+template <class I, bool G1>
+__device__ __forceinline__ void plane_slice(const uint8_t *lds, uint32_t meta, uint32_t it, bool active,
+                                            uint32_t cols, XP<I::S, I::SEG> &xs, uint32_t (&srow)[I::S])
+{
+    constexpr int S = I::S, SEG = I::SEG;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint32_t e = I::seg_elem(it, s);
+        srow[s] = G1 ? 0u : e / cols;
+        const uint32_t c = G1 ? e : e - srow[s] * cols;
+        const uint32_t gs = c / 32u, h = (c / 16u) & 1u;
+        const uint8_t *sp = lds + plane_off(gs) + (SEG == 16 ? 16u * h : 0u);
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+#pragma unroll
+            for (int v = 0; v < SEG / 16; v++) {
+                const uint4 q = active ? *(const uint4 *)(sp + 32 * p + 16 * v) : make_uint4(0, 0, 0, 0);
+                xs.p[s][p][4 * v] = q.x; xs.p[s][p][4 * v + 1] = q.y;
+                xs.p[s][p][4 * v + 2] = q.z; xs.p[s][p][4 * v + 3] = q.w;
+            }
+        const float4 m = active ? *(const float4 *)(lds + meta + 16u * gs) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xs.ik[s] = m.x;
+        xs.sx[s] = SEG == 32 ? m.y + m.z : (h ? m.z : m.y);
+        xs.sy[s] = m.w;
+    }
 }
 
 // CONV: a.x is x itself (f32) and the workgroup converts it to the
@@ -1300,33 +1332,23 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     using XT = typename std::conditional<I::PLANES, XP<S, SEG>, XF<S, SEG>>::type;
     XT xs;
     uint32_t srow[S];
+    if constexpr (I::PLANES) {
+        plane_slice<I, G1>(lds, meta, it, active, a.cols, xs, srow);
+        if constexpr (NORM) {
+            // the digits are those of x * rms; x = (digits / k) / rms
 #pragma unroll
-    for (int s = 0; s < S; s++) {
-        const uint32_t e = I::seg_elem(it, s);
-        srow[s] = e / a.cols;
-        const uint32_t c = e - srow[s] * a.cols;
-        if constexpr (I::PLANES) {
-            const uint32_t gs = c / 32u, h = (c / 16u) & 1u;
-            const uint8_t *sp = lds + plane_off(gs) + (SEG == 16 ? 16u * h : 0u);
-#pragma unroll
-            for (int p = 0; p < 3; p++)
-#pragma unroll
-                for (int v = 0; v < SEG / 16; v++) {
-                    const uint4 q = active ? *(const uint4 *)(sp + 32 * p + 16 * v) : make_uint4(0, 0, 0, 0);
-                    xs.p[s][p][4 * v] = q.x; xs.p[s][p][4 * v + 1] = q.y;
-                    xs.p[s][p][4 * v + 2] = q.z; xs.p[s][p][4 * v + 3] = q.w;
-                }
-            const float4 m = active ? *(const float4 *)(lds + meta + 16u * gs) : make_float4(0.f, 0.f, 0.f, 0.f);
-            xs.ik[s] = m.x;
-            xs.sx[s] = SEG == 32 ? m.y + m.z : (h ? m.z : m.y);
-            xs.sy[s] = m.w;
-            if constexpr (NORM) {
-                // the digits are those of x * rms; x = (digits / k) / rms
+            for (int s = 0; s < S; s++) {
                 xs.ik[s] *= nscale;
                 xs.sx[s] *= nscale;
             }
-        } else {
-            const uint32_t j = c / 4;
+        }
+    } else {
+        // F16 / F32: x in f32, float4 i at xl4[i + i/16]
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const uint32_t e = I::seg_elem(it, s);
+            srow[s] = G1 ? 0u : e / a.cols;
+            const uint32_t j = (G1 ? e : e - srow[s] * a.cols) / 4;
             const float4 *xp = xl4 + j + (j >> 4);
 #pragma unroll
             for (int v = 0; v < SEG / 4; v++) {
@@ -1468,25 +1490,28 @@ __global__ void __launch_bounds__(LB) gemv_stream_pair(StreamArgs a1, StreamArgs
         stream_body<T2, TS2, 1, kDepth, G1B, true, kStage, LB, kDepth, kProNorm, false, RPB>(a2, blockIdx.x - grid1);
 }
 
-// ----------------------------------------------- LDS ring (Q4_K, wide rows)
+// ---------------------------------------------------- LDS ring (wide rows)
 //
-// Plain mat-vec of a repacked Q4_K matrix whose rows are one row group of
-// 8448..14336 columns (66..112 items: teams of two waves).  Eight compute
-// waves (four teams) and two loader waves per workgroup.  The loaders copy
-// the four rows of each stage -- four consecutive row groups, contiguous in
-// memory -- straight into an LDS ring of kRingSlots slots with
-// global_load_lds_dwordx4, so the weight stream starts at kernel entry and
-// no compute wave ever waits behind a weight load: the compute waves load and
-// convert x at once, then read each item's 80 bytes from the ring.  One
-// workgroup barrier per stage publishes it; the loader refills the slot the
-// compute waves left before that barrier.  Loader l owns 16 KB of each slot
-// (rows 2l and 2l + 1, then padding): every one of its kRingInst copy
-// instructions is issued, for clamped sources too, so its wait counts are
-// exact, and what a clamped lane copies lands in the padding.  Same item
-// arithmetic and the same reduction order (per-wave sums, then wave 0 + wave
-// 1) as gemv_stream, so y is bit-identical.
-constexpr uint32_t kRingSlots = 3, kRingInst = 16, kRingLoader = kRingInst * 1024u;
-constexpr uint32_t kRingSlotBytes = 2u * kRingLoader;
+// Plain mat-vec of a repacked matrix with one row per row group and teams of
+// WPT waves (rows of 65..320 items): TPW teams of compute waves and two
+// loader waves per workgroup.  The loaders copy the TPW rows of each stage --
+// TPW consecutive row groups, contiguous in memory -- straight into an LDS
+// ring of kRingSlots slots with global_load_lds_dwordx4, so the weight stream
+// starts at kernel entry and no compute wave ever waits behind a weight load:
+// the compute waves load and convert x at once, then read each item from the
+// ring.  One workgroup barrier per stage publishes it; after it the loaders
+// refill the slot the compute waves finished.  The first two stages go to
+// slots 0 and 1 at entry; slot 2 is first written after the compute waves
+// have copied their x slices, so it may overlay the x planes
+// (StreamArgs::ring_slot2).  Loader l owns LINST KB of each slot (its TPW/2
+// rows, each ceil(group_bytes / 16) 16-byte pieces -- the last piece reads
+// into the next row group or the tail padding -- then padding): every one of
+// its LINST copy instructions is issued,
+// for clamped sources too, so its wait counts are exact, and what a clamped
+// lane copies lands in the padding.  The same item arithmetic and reduction
+// order (per-wave sums added wave 0 first) as gemv_stream, so y is
+// bit-identical.
+constexpr uint32_t kRingSlots = 3;
 
 // s_waitcnt immediate for vmcnt(n), expcnt and lgkmcnt unconstrained (gfx9:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -1499,126 +1524,122 @@ __device__ __forceinline__ void lds_dma16(const void *gp, uint32_t lds_base)
     __builtin_amdgcn_global_load_lds(gp, (__attribute__((address_space(3))) void *)(uintptr_t)lds_base, 16, 0, 0);
 }
 
-__global__ void __launch_bounds__(640) gemv_ring_q4k(StreamArgs a)
+template <uint32_t T, int WPT, int TPW, int LINST>
+__global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
 {
-    using I = Item<T_Q4_K>;
+    static_assert(TPW % 2 == 0, "two loaders, TPW / 2 rows each");
+    using I = Item<T>;
     constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
+    constexpr uint32_t NW = WPT * TPW, NT = 64u * NW;           // compute waves, threads
+    constexpr uint32_t REGION = LINST * 1024u, SLOT = 2u * REGION;
     extern __shared__ float4 xl4[];
     uint8_t *lds = (uint8_t *)xl4;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t gb = a.group_bytes, ring = a.red_off;
-    float *redf = (float *)(lds + ring + kRingSlots * kRingSlotBytes);   // 2 x 8 per-wave sums
-    if (wave >= 8u) {
-        // loader l: rows of teams 2l and 2l + 1 of every stage
-        const uint32_t l = wave - 8u;
+    auto slot_off = [&](uint32_t i) { const uint32_t k = i % kRingSlots; return k < 2u ? ring + k * SLOT : a.ring_slot2; };
+    float *redf = (float *)(lds + ring + 2u * SLOT);            // 2 x NW per-wave sums
+    if (wave >= NW) {
+        // loader l: the rows of teams l*TPW/2 .. (l+1)*TPW/2 - 1 of every stage
+        const uint32_t l = wave - NW, np = (gb + 15u) / 16u;
         auto issue = [&](uint32_t i) {
-            const uint32_t g0 = blockIdx.x * 4u + 2u * l + i * a.n_teams;   // its first row group
-            const uint32_t dst = lds0 + ring + (i % kRingSlots) * kRingSlotBytes + l * kRingLoader;
+            const uint32_t g0 = blockIdx.x * TPW + l * (TPW / 2) + i * a.n_teams;
+            const uint32_t dst = lds0 + slot_off(i) + l * REGION;
 #pragma unroll
-            for (uint32_t k = 0; k < kRingInst; k++) {
-                const uint32_t p = k * 64u + lane;                           // 16-byte piece of the two rows
-                const uint32_t r = p >= gb / 16u ? 1u : 0u;
-                const uint32_t grp = g0 + r, pc = p - r * (gb / 16u);
-                const bool ok = grp < a.n_groups && pc < gb / 16u;
-                lds_dma16(a.w + (ok ? grp * gb + pc * 16u : 0u), dst + k * 1024u);
+            for (uint32_t k = 0; k < (uint32_t)LINST; k++) {
+                // 16-byte piece p of its rows: row r, piece pc; pieces past its
+                // rows and rows past the matrix read clamped (valid) bytes into
+                // the padding or into rows no lane stores
+                const uint32_t p = k * 64u + lane;
+                static_assert(TPW <= 4, "at most two rows per loader");
+                const uint32_t r = (TPW / 2 == 2 && p >= np) ? 1u : 0u;
+                const uint32_t pc = min(p - r * np, np - 1u), grp = min(g0 + r, a.n_groups - 1u);
+                lds_dma16(a.w + grp * gb + pc * 16u, dst + k * 1024u);
             }
         };
 #pragma unroll
         for (uint32_t i = 0; i < kRingSlots - 1u; i++)
             if (i < a.per_team) issue(i);
-        lds_barrier();                                                      // x staged
+        lds_barrier();                                                  // x staged
         for (uint32_t i = 0; i < a.per_team; i++) {
             // stage i landed: at most the next stage's copies still in flight
-            if (a.per_team - 1u - i >= kRingSlots - 2u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kRingInst));
+            if (a.per_team - 1u - i >= kRingSlots - 2u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(LINST));
             else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-            lds_barrier();                                                  // stage i published
+            lds_barrier();                                              // stage i published
             if (i + kRingSlots - 1u < a.per_team) issue(i + kRingSlots - 1u);
         }
         lds_barrier();
         return;
     }
-    const uint32_t tw = tid >> 7, lt = tid & 127u, wt = wave & 1u;
+    const uint32_t tw = tid / (64u * WPT), lt = tid % (64u * WPT), wt = wave % WPT;
     const bool active = lt < a.ni;
     const uint32_t it = active ? lt : 0u;
-    const uint32_t team = blockIdx.x * 4u + tw;
-    // x: 16-element pieces, converted by the 512 compute threads
+    const uint32_t team = blockIdx.x * TPW + tw;
+    // x: 16-element pieces, converted by the compute threads
     const uint32_t npc = a.cols / 16u;
     const uint4 *src = (const uint4 *)a.x;
     const uint32_t meta = planes_bytes(a.cols);
     constexpr int XR = kStage / 4;
     uint4 xv[kStage];
-    const uint32_t nxs = (npc + 511u) / 512u;
+    const uint32_t nxs = (npc + NT - 1u) / NT;
 #pragma unroll
     for (int r = 0; r < XR; r++) {
         if ((uint32_t)r < nxs) {
-            const uint32_t c = tid + r * 512u, cc = c < npc ? c : npc - 1u;
+            const uint32_t c = tid + r * NT, cc = c < npc ? c : npc - 1u;
 #pragma unroll
             for (int i = 0; i < 4; i++) xv[4 * r + i] = src[4 * cc + i];
         }
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 #pragma unroll
     for (int r = 0; r < XR; r++) {
-        const uint32_t c = tid + r * 512u;
+        const uint32_t c = tid + r * NT;
         if (c < npc) {
             uint4 u[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) u[i] = xv[4 * r + i];
-            stage_planes16<false>(u, c, lds, meta);
+            stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
         }
     }
-    for (uint32_t c = tid + XR * 512u; c < npc; c += 512u) {
+    for (uint32_t c = tid + XR * NT; c < npc; c += NT) {
         uint4 u[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) u[i] = src[4 * c + i];
-        stage_planes16<false>(u, c, lds, meta);
+        stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
     }
     lds_barrier();
     XP<S, SEG> xs;
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-        const uint32_t gs = I::seg_elem(it, s) / 32u;
-        const uint8_t *sp = lds + plane_off(gs);
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const uint4 q = active ? *(const uint4 *)(sp + 32 * p) : make_uint4(0, 0, 0, 0);
-            const uint4 q2 = active ? *(const uint4 *)(sp + 32 * p + 16) : make_uint4(0, 0, 0, 0);
-            xs.p[s][p][0] = q.x; xs.p[s][p][1] = q.y; xs.p[s][p][2] = q.z; xs.p[s][p][3] = q.w;
-            xs.p[s][p][4] = q2.x; xs.p[s][p][5] = q2.y; xs.p[s][p][6] = q2.z; xs.p[s][p][7] = q2.w;
-        }
-        const float4 m = active ? *(const float4 *)(lds + meta + 16u * gs) : make_float4(0.f, 0.f, 0.f, 0.f);
-        xs.ik[s] = m.x;
-        xs.sx[s] = m.y + m.z;
-        xs.sy[s] = m.w;
-    }
+    uint32_t srow[S];
+    plane_slice<I, true>(lds, meta, it, active, a.cols, xs, srow);
     auto flush = [&](uint32_t i) {                          // after a barrier: y of stage i
         if (wt == 0 && lane == 0) {
             const uint32_t grp = team + i * a.n_teams;
-            const float v = redf[(i & 1u) * 8u + 2u * tw] + redf[(i & 1u) * 8u + 2u * tw + 1u];
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < WPT; w++) v += redf[(i & 1u) * NW + tw * WPT + w];
             if (grp < a.n_groups) store_y(a.y + grp, v);
         }
     };
-    const uint32_t nb16 = (a.ni >> 1) * 16u;
     for (uint32_t i = 0; i < a.per_team; i++) {
         lds_barrier();
         if (i > 0) flush(i - 1);
-        const uint8_t *row = lds + ring + (i % kRingSlots) * kRingSlotBytes + (tw >> 1) * kRingLoader + (tw & 1u) * gb;
+        const uint8_t *row = lds + slot_off(i) + (tw / (TPW / 2)) * REGION + (tw % (TPW / 2)) * ((gb + 15u) & ~15u);
         uint32_t raw[NR];
-        const uint4 h = *(const uint4 *)(row + (it >> 1) * 16u);
-        const uint8_t *q = row + nb16 + it * 16u;
-        const uint4 q0 = *(const uint4 *)q, q1 = *(const uint4 *)(q + a.ni * 16u);
-        const uint4 q2 = *(const uint4 *)(q + 2u * a.ni * 16u), q3 = *(const uint4 *)(q + 3u * a.ni * 16u);
-        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
-        raw[4] = q0.x; raw[5] = q0.y; raw[6] = q0.z; raw[7] = q0.w;
-        raw[8] = q1.x; raw[9] = q1.y; raw[10] = q1.z; raw[11] = q1.w;
-        raw[12] = q2.x; raw[13] = q2.y; raw[14] = q2.z; raw[15] = q2.w;
-        raw[16] = q3.x; raw[17] = q3.y; raw[18] = q3.z; raw[19] = q3.w;
-        float t = I::compute_sum(raw, xs, it);
+        I::load_rp(row, it, a.ni, raw);
+        float t;
+        if constexpr (HasSum<I>::value) {
+            t = I::compute_sum(raw, xs, it);
+        } else {
+            float acc[S];
+            item_compute<I, true>(raw, xs, it, acc);
+            t = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < S; s2++) t += acc[s2];
+        }
         t = active ? t : 0.f;
         t = group_sum<64>(t);
-        if (lane == 63u) redf[(i & 1u) * 8u + wave] = t;
+        if (lane == 63u) redf[(i & 1u) * NW + wave] = t;
     }
     lds_barrier();
     if (a.per_team > 0) flush(a.per_team - 1);
@@ -1764,18 +1785,36 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     p->red_off = img;
     p->lds = lds;
     p->kind = 1;
-    // the LDS ring kernel for repacked Q4_K rows of 8448..14336 columns
+    // the LDS ring kernel for the plain mat-vec of repacked rows with
+    // several-wave teams, where a loader's rows fit its region and the LDS
+    // holds the x planes, two slots (the third overlays the x planes when they
+    // are large enough) and the per-wave sums
     p->fn_ring = nullptr;
-    if constexpr (T == T_Q4_K) {
-        const uint32_t ring_lds = img + kRingSlots * kRingSlotBytes + 64u;
-        if (rp && g == 1 && tsub == 0 && wpt == 2 && 2u * gbytes <= kRingLoader &&
-            ring_lds <= (uint32_t)max_lds_bytes()) {
-            const uint64_t wgs = (n_groups + 3) / 4;
-            const uint32_t rg = (uint32_t)(wgs < ncu ? wgs : ncu);
-            p->fn_ring = (const void *)gemv_ring_q4k;
-            p->ring_grid = rg;
-            p->ring_per = (uint32_t)((n_groups + 4ull * rg - 1) / (4ull * rg));
-            p->ring_lds = ring_lds;
+    if constexpr (T == T_Q4_K || T == T_Q6_K) {
+        const uint32_t rsz = (uint32_t)((gbytes + 15u) & ~15ull);     // a row in whole 16-byte pieces
+        const void *rf = nullptr;
+        uint32_t rt = 0, linst = 0;
+        if (T == T_Q4_K && wpt == 2 && 2u * rsz <= 16384u) {
+            rf = (const void *)gemv_ring<T_Q4_K, 2, 4, 16>; rt = 4; linst = 16;
+        } else if (T == T_Q6_K && wpt == 5 && rsz <= 16384u) {
+            rf = (const void *)gemv_ring<T_Q6_K, 5, 2, 16>; rt = 2; linst = 16;
+        } else if (T == T_Q6_K && wpt == 4 && rsz <= 12288u) {
+            rf = (const void *)gemv_ring<T_Q6_K, 4, 2, 12>; rt = 2; linst = 12;
+        }
+        if (rf && rp && g == 1 && tsub == 0) {
+            const uint32_t slot = 2u * linst * 1024u, red_bytes = 128u;
+            const bool xs = slot <= img;
+            const uint32_t ring_lds = img + 2u * slot + red_bytes + (xs ? 0u : slot);
+            if (ring_lds <= (uint32_t)max_lds_bytes()) {
+                const uint64_t wgs = (n_groups + rt - 1) / rt;
+                const uint32_t rg = (uint32_t)(wgs < ncu ? wgs : ncu);
+                p->fn_ring = rf;
+                p->ring_grid = rg;
+                p->ring_block = 64u * (wpt * rt + 2u);
+                p->ring_per = (uint32_t)((n_groups + (uint64_t)rt * rg - 1) / ((uint64_t)rt * rg));
+                p->ring_lds = ring_lds;
+                p->ring_slot2 = xs ? 0u : img + 2u * slot + red_bytes;
+            }
         }
     }
 }
@@ -1918,9 +1957,11 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
     StreamArgs a = stream_args(p, w, nbytes, rows, cols, x, y);
     void *args[] = {&a};
     if (p.fn_ring) {
-        a.n_teams = 4u * p.ring_grid;
+        a.n_teams = (p.ring_block / 64u - 2u) / p.wpt * p.ring_grid;
         a.per_team = p.ring_per;
-        return hipLaunchKernel(p.fn_ring, dim3(p.ring_grid), dim3(640), args, p.ring_lds, st) == hipSuccess ? 0 : -2;
+        a.ring_slot2 = p.ring_slot2;
+        return hipLaunchKernel(p.fn_ring, dim3(p.ring_grid), dim3(p.ring_block), args, p.ring_lds, st) == hipSuccess
+                   ? 0 : -2;
     }
     return hipLaunchKernel(p.fn, dim3(p.grid), dim3(p.block), args, p.lds, st) == hipSuccess ? 0 : -2;
 }
