@@ -71,8 +71,9 @@ int qg_mat_info(const qg_mat *mat, uint32_t *ggml_type, size_t *rows, size_t *co
                 size_t *nbytes);
 /* Kernel choice fixed at upload: 1 = stream kernel (fast path), 2 = the
  * stream kernel family with the LDS-ring kernel for the plain mat-vec
- * (repacked Q4_K / Q6_K rows with several-wave teams: Q4_K 8448..14336
- * columns, Q6_K 12288..19968), 0 = generic per-element kernel
+ * (repacked Q8_0 / Q4_K / Q5_K / Q6_K rows with several-wave teams that fit
+ * its ring, e.g. the 14336- and 18944-wide down projections), 0 = generic
+ * per-element kernel
  * (cols % 32 != 0 and other shapes the planner rejects). */
 int qg_mat_kernel_kind(const qg_mat *mat);
 

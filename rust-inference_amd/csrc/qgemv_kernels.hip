@@ -1790,16 +1790,24 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     // holds the x planes, two slots (the third overlays the x planes when they
     // are large enough) and the per-wave sums
     p->fn_ring = nullptr;
-    if constexpr (T == T_Q4_K || T == T_Q6_K) {
+    if constexpr (repackable<T>()) {
         const uint32_t rsz = (uint32_t)((gbytes + 15u) & ~15ull);     // a row in whole 16-byte pieces
         const void *rf = nullptr;
         uint32_t rt = 0, linst = 0;
-        if (T == T_Q4_K && wpt == 2 && 2u * rsz <= 16384u) {
-            rf = (const void *)gemv_ring<T_Q4_K, 2, 4, 16>; rt = 4; linst = 16;
-        } else if (T == T_Q6_K && wpt == 5 && rsz <= 16384u) {
-            rf = (const void *)gemv_ring<T_Q6_K, 5, 2, 16>; rt = 2; linst = 16;
-        } else if (T == T_Q6_K && wpt == 4 && rsz <= 12288u) {
-            rf = (const void *)gemv_ring<T_Q6_K, 4, 2, 12>; rt = 2; linst = 12;
+        // (waves per team, teams per workgroup, KB per loader): two rows per
+        // loader for two-wave teams, one row otherwise
+        auto pick = [&](const void *f, uint32_t teams, uint32_t kb) {
+            if (!rf && (teams / 2u) * rsz <= kb * 1024u) { rf = f; rt = teams; linst = kb; }
+        };
+        if constexpr (T == T_Q4_K) {
+            if (wpt == 2) pick((const void *)gemv_ring<T, 2, 4, 16>, 4, 16);
+            if (wpt == 3) pick((const void *)gemv_ring<T, 3, 2, 12>, 2, 12);
+        } else if constexpr (T == T_Q5_K || T == T_Q6_K) {
+            if (wpt == 5) pick((const void *)gemv_ring<T, 5, 2, 16>, 2, 16);
+            if (wpt == 4) pick((const void *)gemv_ring<T, 4, 2, 12>, 2, 12);
+        } else if constexpr (T == T_Q8_0) {
+            if (wpt == 5) pick((const void *)gemv_ring<T, 5, 2, 20>, 2, 20);
+            if (wpt == 4) pick((const void *)gemv_ring<T, 4, 2, 16>, 2, 16);
         }
         if (rf && rp && g == 1 && tsub == 0) {
             const uint32_t slot = 2u * linst * 1024u, red_bytes = 128u;
