@@ -1527,7 +1527,7 @@ __device__ __forceinline__ void lds_dma16(const void *gp, uint32_t lds_base)
 template <uint32_t T, int WPT, int TPW, int LINST>
 __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
 {
-    static_assert(TPW % 2 == 0, "two loaders, TPW / 2 rows each");
+    static_assert(TPW % 2 == 0 && TPW <= 4, "two loaders, one or two rows each");
     using I = Item<T>;
     constexpr int S = I::S, SEG = I::SEG, NR = I::NRAW;
     constexpr uint32_t NW = WPT * TPW, NT = 64u * NW;           // compute waves, threads
@@ -1552,7 +1552,6 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
                 // rows and rows past the matrix read clamped (valid) bytes into
                 // the padding or into rows no lane stores
                 const uint32_t p = k * 64u + lane;
-                static_assert(TPW <= 4, "at most two rows per loader");
                 const uint32_t r = (TPW / 2 == 2 && p >= np) ? 1u : 0u;
                 const uint32_t pc = min(p - r * np, np - 1u), grp = min(g0 + r, a.n_groups - 1u);
                 lds_dma16(a.w + grp * gb + pc * 16u, dst + k * 1024u);
