@@ -63,11 +63,12 @@ def test_gemv_parity(ctx, oracle, synth, dtype, shape):
     assert err <= GEMV_TOL
 
 
-# (37, 14336), (1030, 8448), (9000, 8448): Q4_K through the LDS ring kernel
-# (uploaded) against the stream kernel (wrapped), with partial stages, the
-# narrowest ring row and nine stages per team
+# (37, 14336), (1030, 8448), (9000, 8448), (3584, 18944): the LDS ring kernel
+# (uploaded; Q4_K, and at 18944 columns Q5_K, Q6_K, Q8_0 too) against the
+# stream kernel (wrapped), with partial stages, the narrowest ring row, nine
+# stages per team and the 7B down projection
 WRAP_SHAPES = [(896, 896), (128, 896), (4096, 14336), (37, 18944), (1200, 256), (21, 8320), (64, 288),
-               (37, 14336), (1030, 8448), (9000, 8448)]
+               (37, 14336), (1030, 8448), (9000, 8448), (3584, 18944)]
 
 
 @pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
