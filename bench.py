@@ -17,6 +17,19 @@ roofline     algorithmic bytes / average launch duration of the GEMV kernel:
              WRITE_SIZE (profiles/traffic.json, written by --pmc-summary), or null
 cpu_baseline the oracle's restatement of the reference's --cpu loop
              (src/quant.rs:188-205) on one host core, same matrix
+ceiling      the streaming-read ceiling at the same byte count: the library's
+             plain full-grid read (qg_probe_stream_read) and torch.sum over
+             the same number of rotating copies, also at 76 MB and 447 MB
+             (the 7B [gate;up] and lm_head sizes); roofline.ceiling_us is the
+             faster read at the headline size
+sweep        BASELINE.json configs[1]: the per-type GEMVs at the Qwen2-0.5B
+             shapes and the Q6_K 151936 x 896 lm_head
+decode, decode_configs
+             configs[3] (Qwen2-7B Q4_K_M, 64 + 256) and configs[2] / [4]
+             (Qwen2-0.5B Q4_K_M 32 + 128; Llama-3-8B Q4_K_M / Q5_K / Q8_0,
+             64 + 512): greedy decode tok/s with the HBM roofline fraction
+--timeline   instead of all that: the s_memrealtime stamps of the LDS-ring
+             GEMV (libqgemv_timeline.so) -- where a launch spends its time
 
 Algorithmic bytes per GEMV: ceil(rows*cols/256)*144 + 4*cols + 4*rows.
 Only rank 0 of one GPU is supported (--gpus > 1 exits with a message).
@@ -157,18 +170,22 @@ def cpu_baseline(oracle, raw, dtype, rows, cols, x, seconds, nbytes):
                              "path": "src/gpu_backend.rs:543-567 (dequantize + mat_vec_mul_transposed)"}}
 
 
-def decode_run(rinf, synth, ctx, args):
-    """greedy decode of a random-init model of
-    `args.decode` in the `args.decode_mix` GGUF mix, all GEMVs on this GPU.
-    Prompt tokens are processed one by one as the reference does
-    (src/model.rs:357-363), then `decode_tokens` greedy steps with the
-    reference's repetition penalty 1.1 over the last 64 tokens."""
+def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new=None, cfg_index=3):
+    """BASELINE.json configs[3] (by default): greedy decode of a random-init
+    model of `arch` in the `mix` GGUF mix, all GEMVs on this GPU.  The prompt
+    is processed as the reference does it, one token at a time
+    (src/model.rs:357-363), then `n_new` greedy steps with the reference's
+    repetition penalty 1.1 over the last 64 tokens."""
     import numpy as np
-    cfg = synth.ARCH[args.decode]
-    seed = synth.config_seed(3)
+    arch = arch or args.decode
+    mix = mix or args.decode_mix
+    n_prompt = args.decode_prompt if n_prompt is None else n_prompt
+    n_new = args.decode_tokens if n_new is None else n_new
+    cfg = synth.ARCH[arch]
+    seed = synth.config_seed(cfg_index)
     t0 = time.perf_counter()
-    t = synth.gen_model(cfg, args.decode_mix, seed)
-    max_seq = args.decode_prompt + args.decode_tokens + 1
+    t = synth.gen_model(cfg, mix, seed)
+    max_seq = n_prompt + n_new + 1
     dev = rinf.DeviceModel(ctx, cfg["embed_dim"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
                            cfg["hidden_dim"], cfg["vocab_size"], max_seq, cfg["rope_base"],
                            cfg["norm_eps"])
@@ -189,30 +206,187 @@ def decode_run(rinf, synth, ctx, args):
     for (name, layer), v in t["vecs"].items():
         dev.set_vector(vslots[name], layer, v)
     setup_s = time.perf_counter() - t0
-    prompt = np.random.default_rng(seed).integers(0, cfg["vocab_size"], args.decode_prompt)
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab_size"], n_prompt)
     dev.generate(prompt[:4], 4)                           # warm-up (kernels, clocks)
-    toks, pre_s, dec_s = dev.generate(prompt, args.decode_tokens)
+    toks, pre_s, dec_s = dev.generate(prompt, n_new)
     dev.close()
     if shared is not None:
         shared.free()
-    tok_s = args.decode_tokens / dec_s
-    wbytes = synth.model_bytes(cfg, args.decode_mix)
+    tok_s = n_new / dec_s
+    wbytes = synth.model_bytes(cfg, mix)
     E = cfg["embed_dim"]
     kv_dim = cfg["n_kv_heads"] * (E // cfg["n_heads"])
-    mean_pos = args.decode_prompt + (args.decode_tokens + 1) / 2
+    mean_pos = n_prompt + (n_new + 1) / 2
     kv_bytes = 2 * cfg["n_layers"] * mean_pos * kv_dim * 4
     per_tok = wbytes + kv_bytes
-    log(f"decode {args.decode} {args.decode_mix}: {tok_s:.1f} tok/s ({dec_s * 1e3 / args.decode_tokens:.3f} "
-        f"ms/token), {per_tok / 1e9:.3f} GB/token -> {per_tok * tok_s / 1e9:.1f} GB/s; prefill "
-        f"{args.decode_prompt / pre_s:.1f} tok/s; set-up {setup_s:.1f} s")
-    return {"model": f"{args.decode} ({args.decode_mix}, random init, synthetic)",
-            "prompt_tokens": args.decode_prompt, "decode_tokens": args.decode_tokens,
-            "tok_s": round(tok_s, 2), "ms_per_token": round(dec_s * 1e3 / args.decode_tokens, 4),
-            "prefill_tok_s": round(args.decode_prompt / pre_s, 2),
+    log(f"decode {arch} {mix}: {tok_s:.1f} tok/s ({dec_s * 1e3 / n_new:.3f} ms/token), "
+        f"{per_tok / 1e9:.3f} GB/token -> {per_tok * tok_s / 1e9:.1f} GB/s; prefill "
+        f"{n_prompt / pre_s:.1f} tok/s; set-up {setup_s:.1f} s")
+    return {"model": f"{arch} ({mix}, random init, synthetic)",
+            "prompt_tokens": n_prompt, "decode_tokens": n_new,
+            "tok_s": round(tok_s, 2), "ms_per_token": round(dec_s * 1e3 / n_new, 4),
+            "prefill_tok_s": round(n_prompt / pre_s, 2),
             "bytes_per_token": int(per_tok), "weight_bytes_per_token": int(wbytes),
             "achieved_GBs": round(per_tok * tok_s / 1e9, 2),
             "frac_of_8TBs": round(per_tok * tok_s / 8e12, 4),
             "first_tokens": [int(v) for v in toks[:8]]}
+
+
+def _event_loop(torch, st, fn, n, warmup):
+    """Wall ms of n back-to-back calls fn(i) on stream st, HIP events on st."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(n):
+        fn(i)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
+def ceiling_run(ctx, torch, sizes, rotate_min=1 << 30):
+    """Streaming-read ceiling at each byte count: the library's plain read
+    (qg_probe_stream_read, one 16-byte load per thread of a full grid) and
+    torch.sum of a float32 view, each over enough rotating copies (>= 1 GiB)
+    that every pass misses the 256 MB Infinity Cache."""
+    out = {}
+    st = torch.cuda.ExternalStream(ctx.stream)
+    for name, nbytes in sizes:
+        nb16 = nbytes // 16 * 16
+        ncopy = max(3, -(-rotate_min // nb16))
+        bufs = [torch.empty(nb16 // 4, dtype=torch.float32, device="cuda").uniform_() for _ in range(ncopy)]
+        dout = torch.zeros(4, dtype=torch.int32, device="cuda")
+        n = 60 if nbytes > 2e8 else 300
+        probe_ms = _event_loop(torch, st, lambda i: ctx.probe_stream_read(bufs[i % ncopy], nb16, dout, ctx.stream),
+                               n, 20)
+        cur = torch.cuda.current_stream()
+        torch_ms = _event_loop(torch, cur, lambda i: torch.sum(bufs[i % ncopy]), n, 20)
+        del bufs
+        torch.cuda.empty_cache()
+        p_us, t_us = probe_ms * 1e3 / n, torch_ms * 1e3 / n
+        out[name] = {"bytes": nb16, "rotating_copies": ncopy,
+                     "probe_read_us": round(p_us, 3), "probe_read_GBs": round(nb16 / p_us / 1e3, 1),
+                     "torch_sum_us": round(t_us, 3), "torch_sum_GBs": round(nb16 / t_us / 1e3, 1),
+                     "ceiling_us": round(min(p_us, t_us), 3),
+                     "ceiling_frac_of_8TBs": round(nb16 / min(p_us, t_us) / 1e3 / PEAK_GBS, 4)}
+        log(f"ceiling {name}: plain read {p_us:.2f} us ({nb16 / p_us / 1e3:.0f} GB/s), torch.sum "
+            f"{t_us:.2f} us ({nb16 / t_us / 1e3:.0f} GB/s)")
+    return out
+
+
+# BASELINE.json configs[1]: per-type GEMVs at Qwen2-0.5B shapes, plus the Q6_K lm_head
+SWEEP_TYPES = ("Q8_0", "Q4_0", "Q5_0", "Q5_K", "Q6_K", "F16")
+SWEEP_SHAPES = ((896, 896), (128, 896), (896, 4864))
+
+
+def sweep_run(rinf, synth, ctx, torch, rotate_mb=256, max_copies=256, steps=200):
+    """Per-type GEMV time at the configs[1] shapes: back-to-back launches
+    over rotating copies (>= rotate_mb MiB, at most max_copies copies: the
+    small shapes stay within the caches, where launch latency bounds them)."""
+    import numpy as np
+    entries = []
+    st = torch.cuda.ExternalStream(ctx.stream)
+    cases = [(t, r, c) for t in SWEEP_TYPES for r, c in SWEEP_SHAPES] + [("Q6_K", 151936, 896)]
+    for tname, rows, cols in cases:
+        dtype = rinf.TYPE_IDS[tname]
+        nb = rinf.nbytes_for(dtype, rows, cols)
+        ncopy = int(min(max_copies, max(2, -(-rotate_mb * 2**20 // nb))))
+        raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(1))
+        x = synth.gen_x(cols, synth.config_seed(1))
+        mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
+        n = steps if nb < 1e8 else 60
+        ms = _event_loop(torch, st, lambda i: mats[i % ncopy].matvec_dev(dx, dy, ctx.stream), n, 20)
+        us = ms * 1e3 / n
+        B = alg_bytes(rinf, dtype, rows, cols)
+        kind = {0: "generic", 1: "stream", 2: "ring"}.get(mats[0].kernel_kind, "?")
+        entries.append({"type": tname, "rows": rows, "cols": cols, "us": round(us, 3),
+                        "GBs": round(B / us / 1e3, 1), "frac_of_8TBs": round(B / us / 1e3 / PEAK_GBS, 4),
+                        "alg_bytes": B, "rotating_bytes": ncopy * nb, "kernel": kind})
+        log(f"sweep {tname} {rows}x{cols}: {us:.2f} us, {B / us / 1e3:.0f} GB/s ({kind}, {ncopy} copies)")
+        if not np.all(np.isfinite(dy.cpu().numpy())):
+            raise SystemExit(f"sweep {tname} {rows}x{cols}: non-finite output")
+        for m in mats:
+            m.free()
+        del dx, dy
+    return entries
+
+
+def timeline_run(rinf, synth, args):
+    """s_memrealtime stamps of the LDS-ring GEMV from libqgemv_timeline.so:
+    per event, the median over workgroups of (stamp - first entry stamp), for
+    the last of 20 back-to-back launches over rotating copies, over `reps`
+    repetitions (the median of the per-repetition medians)."""
+    import ctypes
+    import numpy as np
+    import torch
+    lib = rinf.use_library(ROOT / "rust-inference_amd" / "libqgemv_timeline.so")
+    lib.qg_timeline_read.restype = ctypes.c_int
+    lib.qg_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]
+    lib.qg_timeline_clear.restype = ctypes.c_int
+    dtype = rinf.TYPE_IDS[args.type]
+    rows, cols = args.rows, args.cols
+    nb = rinf.nbytes_for(dtype, rows, cols)
+    ncopy = max(2, -(-args.rotate_mb * 2**20 // nb))
+    ctx = rinf.GpuContext(0)
+    raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
+    x = synth.gen_x(cols, synth.config_seed(4))
+    mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
+    if mats[0].kernel_kind != 2:
+        raise SystemExit(f"{args.type} {rows}x{cols} does not run the LDS-ring kernel (kind {mats[0].kernel_kind})")
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    n_ev, n_wg = 64, 2048
+    buf = np.zeros(n_ev * n_wg, np.uint64)
+    khz = ctypes.c_int(0)
+    names = {0: "compute: entry", 1: "compute: x arrived", 2: "compute: x converted", 3: "compute: planes published",
+             30: "compute: last stage done", 31: "compute: y written (end)",
+             32: "loader: entry", 33: "loader: first stages issued", 34: "loader: planes published",
+             63: "loader: end"}
+    for i in range(13):
+        names[4 + 2 * i] = f"compute: stage {i} reached"
+        names[5 + 2 * i] = f"compute: stage {i} published"
+    for i in range(28):
+        names[35 + i] = f"loader: stage {i} landed"
+    per_rep = []
+    for rep in range(args.timeline_reps):
+        for i in range(20):
+            mats[(rep * 20 + i) % ncopy].matvec_dev(dx, dy, ctx.stream)
+        ctx.synchronize()
+        if lib.qg_timeline_read(buf.ctypes.data, buf.size, ctypes.byref(khz)):
+            raise SystemExit("qg_timeline_read failed")
+        t = buf.reshape(n_wg, n_ev).astype(np.int64)
+        wg = [w for w in range(n_wg) if t[w, 0] and t[w, 32]]
+        t = t[wg]
+        t0 = min(t[:, 0].min(), t[:, 32].min())
+        us = (t - t0) / (khz.value / 1e3)
+        med = {}
+        for e in names:
+            col = us[:, e][t[:, e] != 0]
+            if col.size:
+                med[e] = (float(np.median(col)), float(np.percentile(col, 10)), float(np.percentile(col, 90)))
+        med["end_max"] = (float(us[:, 31].max()),) * 3
+        per_rep.append(med)
+    table = []
+    for e in sorted(k for k in per_rep[0] if isinstance(k, int)):
+        vals = [r[e] for r in per_rep if e in r]
+        table.append({"event": names[e], "median_us": round(float(np.median([v[0] for v in vals])), 3),
+                      "p10_us": round(float(np.median([v[1] for v in vals])), 3),
+                      "p90_us": round(float(np.median([v[2] for v in vals])), 3)})
+    end_max = float(np.median([r["end_max"][0] for r in per_rep]))
+    for m in mats:
+        m.free()
+    ctx.close()
+    res = {"workload": f"{args.type.lower()}_gemv_{rows}x{cols}", "kernel": "qg::gemv_ring (timeline build)",
+           "workgroups": len(wg), "clock_khz": khz.value, "reps": args.timeline_reps,
+           "last_workgroup_end_us": round(end_max, 3), "events": table}
+    for r in table:
+        log(f"{r['event']:34s} {r['median_us']:8.3f} us  (p10 {r['p10_us']:.3f}, p90 {r['p90_us']:.3f})")
+    log(f"last workgroup ends at {end_max:.3f} us after the first entry")
+    print(json.dumps(res), flush=True)
 
 
 def _pmc_rows(d):
@@ -290,6 +464,13 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of this script (FETCH_SIZE, then "
                          "WRITE_SIZE, each with --copy-probe-mb) into profiles/traffic.json")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the streaming-read ceiling leg")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the configs[1] per-type sweep")
+    ap.add_argument("--no-decode-configs", action="store_true",
+                    help="skip the configs[2] / configs[4] decode runs")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the s_memrealtime timeline of the LDS-ring GEMV (libqgemv_timeline.so)")
+    ap.add_argument("--timeline-reps", type=int, default=9)
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args)
@@ -308,6 +489,9 @@ def main():
     import __graft_entry__ as ge
     rinf = ge.load_package()
     synth = importlib.import_module(ge.PKG_NAME + ".synth")
+    if args.timeline:
+        timeline_run(rinf, synth, args)
+        return
     dtype = rinf.TYPE_IDS[args.type]
     rows, cols = args.rows, args.cols
     nb = rinf.nbytes_for(dtype, rows, cols)
@@ -332,8 +516,10 @@ def main():
     wall_ms = min(eager_ms, graph_ms)
     ms_step = wall_ms / args.steps
     value = B / (ms_step * 1e-3) / 1e9
-    # average launch duration: the faster of the eager and graph-replay
-    # back-to-back loops (a profiler's callbacks inflate the eager one)
+    # average launch duration: HIP events on the launch stream around the
+    # back-to-back loops, the faster of eager and graph replay (a profiler's
+    # callbacks inflate the eager one); it includes the gaps between kernels,
+    # so it is an upper bound on rocprofv3's per-kernel average
     kern_ms = wall_ms / args.steps
     achieved = B / (kern_ms * 1e-3) / 1e9
     log(f"eager {eager_ms / args.steps * 1e3:.2f} us/step, graph {graph_ms / args.steps * 1e3:.2f} us/step")
@@ -376,15 +562,31 @@ def main():
         cpu = cpu_baseline(oracle, raw, dtype, rows, cols, x, args.cpu_seconds, B)
         log(f"cpu_baseline: {cpu['value']} GB/s ({cpu['us_per_gemv']} us/GEMV)")
 
+    ceiling = None
+    if not args.no_ceiling:
+        ceiling = ceiling_run(ctx, torch, [(workload, nb), ("qwen2_7b_gate_up_76MB", 76382208),
+                                           ("qwen2_7b_lm_head_447MB", 447166464)])
+
     decode = None
     if args.decode != "none":
         decode = decode_run(rinf, synth, ctx, args)
+
+    sweep = None if args.no_sweep else sweep_run(rinf, synth, ctx, torch)
+    decode_configs = None
+    if not args.no_decode_configs and args.decode != "none":
+        decode_configs = {
+            "configs[2] qwen2-0.5b q4_k_m 32+128": decode_run(rinf, synth, ctx, args, "qwen2-0.5b", "q4_k_m", 32, 128, 2),
+            "configs[4] llama3-8b q4_k_m 64+512": decode_run(rinf, synth, ctx, args, "llama3-8b", "q4_k_m", 64, 512, 4),
+            "configs[4] llama3-8b q5_k 64+512": decode_run(rinf, synth, ctx, args, "llama3-8b", "q5_k", 64, 512, 4),
+            "configs[4] llama3-8b q8_0 64+512": decode_run(rinf, synth, ctx, args, "llama3-8b", "q8_0", 64, 512, 4),
+        }
 
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "compute": "int8 dot4 of weight codes with 24-bit fixed-point x digits, f32 scales and accumulation",
+        "compute": "int8 dot4 of weight codes with x as 22-bit fixed point per 32-element segment "
+                   "(three signed-byte digit planes), exact int32 sums, f32 scales and accumulation",
         "data": "synthetic (seeded GGUF blocks: f16 scales U[1e-3,2e-2], uniform code bytes; x ~ N(0,1))",
         "config": {"workload": workload, "type": args.type, "rows": rows, "cols": cols,
                    "bytes_per_launch": B, "rotating_copies": ncopy,
@@ -394,11 +596,19 @@ def main():
                    "frac_of_8TBs_wall": round(value / PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                     "kernel_us_mean": round(kern_ms * 1e3, 3),
+                     "event_us_per_launch": round(kern_ms * 1e3, 3),
                      "kernel": kernel + " (rust-inference_amd/csrc/qgemv_kernels.hip)"},
         "cpu_baseline": cpu,
         "decode": decode,
+        "ceiling": ceiling,
+        "sweep": sweep,
+        "decode_configs": decode_configs,
     }
+    if ceiling:
+        c = ceiling[workload]
+        out["roofline"]["ceiling_us"] = c["ceiling_us"]
+        out["roofline"]["ceiling_frac"] = c["ceiling_frac_of_8TBs"]
+        out["roofline"]["frac_of_ceiling"] = round(c["ceiling_us"] / (kern_ms * 1e3), 4)
     for m in mats:
         m.free()
     ctx.close()

@@ -66,6 +66,10 @@ int qg_upload(qg_ctx *ctx, const void *raw, size_t nbytes, uint32_t ggml_type,
  * alive for the handle's lifetime. */
 int qg_wrap_device(qg_ctx *ctx, const void *d_raw, size_t nbytes, uint32_t ggml_type,
                    size_t rows, size_t cols, qg_mat **out);
+/* Frees a matrix.  QG_ERR_INVALID_ARG for a handle this context does not
+ * hold (already freed, or another context's) and for a matrix a decode-step
+ * model still uses through qg_model_share_matrix (destroy the model, or put
+ * another matrix into its slot, first). */
 int qg_mat_free(qg_ctx *ctx, qg_mat *mat);
 int qg_mat_info(const qg_mat *mat, uint32_t *ggml_type, size_t *rows, size_t *cols,
                 size_t *nbytes);
@@ -135,11 +139,27 @@ int qg_matvec_silu_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_g, const f
 int qg_matvec_host(qg_ctx *ctx, const qg_mat *mat, const float *x, float *y);
 
 /* Exact drop-in for GpuContext::mat_vec_mul(weight_data, dtype, x, out, rows,
- * cols) (src/gpu_backend.rs:429-437): device copies are keyed by
- * (weight_data, nbytes, dtype, rows, cols), uploaded on first sight and
- * reused afterwards (weights are immutable after Model::load). */
+ * cols) (src/gpu_backend.rs:429-437), which uploads the current bytes on
+ * every call (gpu_backend.rs:478-482).  Here device copies are keyed by
+ * (weight_data, nbytes, dtype, rows, cols) and reused while a fingerprint of
+ * the host bytes (64 bytes at 16 evenly spaced offsets, first and last
+ * included) still matches the one taken at upload; on a mismatch the current
+ * bytes are uploaded again.  A caller that edits weights in place where the
+ * fingerprint does not look calls qg_gpu_invalidate first.  On an error
+ * `out` is left untouched. */
 int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint32_t dtype,
                        const float *x, float *out, size_t rows, size_t cols);
+/* No counterpart in the reference (it keeps no device copies): drops every
+ * device copy qg_gpu_mat_vec_mul keeps for host address `weight_data`. */
+int qg_gpu_invalidate(qg_ctx *ctx, const void *weight_data);
+
+/* Test hook, no counterpart in the reference: of the allocations this
+ * context makes next (device matrices, repacked and stacked copies, pinned
+ * and device staging), the first `skip` go through and the `n` after them
+ * report QG_ERR_OUT_OF_MEMORY without calling HIP, so that tests can drive
+ * the status-code path a caller maps to its CPU fallback
+ * (gpu_backend.rs:444-447) without a device fault.  n = 0 switches it off. */
+int qg_test_fail_allocations(qg_ctx *ctx, int skip, int n);
 
 /* quant::dequantize (src/quant.rs:356-372) on device: rows*cols f32 values,
  * bit-exact with the CPU path.  The reference's Vec for Q4_K/Q5_K is padded
@@ -153,6 +173,12 @@ int qg_dequant_host(qg_ctx *ctx, const qg_mat *mat, float *out);
  * fresh vec! does). */
 int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_out,
                           void *stream);
+
+/* Measurement only, no counterpart in the reference: reads nbytes of device
+ * memory once (16-byte aligned, a multiple of 16 bytes) with the plainest
+ * full-grid coalesced read, writing at most d_out[0].  Its duration is the
+ * streaming ceiling the GEMV's HBM rate is compared with at the same size. */
+int qg_probe_stream_read(qg_ctx *ctx, const void *d_buf, size_t nbytes, uint32_t *d_out, void *stream);
 
 /* Waits for all work on the context's stream. */
 int qg_synchronize(qg_ctx *ctx);

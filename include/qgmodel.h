@@ -60,7 +60,9 @@ int qg_model_destroy(qg_model *m);
 int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void *raw,
                         size_t nbytes, uint32_t ggml_type, size_t rows, size_t cols);
 /* Uses an already uploaded matrix (e.g. a tied lm_head = token_embd,
- * src/model.rs:221-226) without copying; the model does not free it. */
+ * src/model.rs:221-226) without copying; the model does not free it, and
+ * qg_mat_free refuses it while any model slot still uses it (the slot is
+ * released when the model is destroyed or the slot gets another matrix). */
 int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_mat *mat);
 int qg_model_set_vector(qg_model *m, uint32_t which, uint32_t layer, const float *v, size_t n);
 

@@ -78,6 +78,9 @@ _SIGS = {
     "qg_matvec_silu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, _P]),
     "qg_matvec_norm_glu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
+    "qg_gpu_invalidate": (ctypes.c_int, [_P, _P]),
+    "qg_probe_stream_read": (ctypes.c_int, [_P, _P, _SZ, _P, _P]),
+    "qg_test_fail_allocations": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
     "qg_gpu_mat_vec_mul": (ctypes.c_int, [_P, _P, _SZ, _U32, _P, _P, _SZ, _SZ]),
     "qg_dequant_dev": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -146,6 +149,15 @@ def header_symbols(paths=HEADERS) -> list[str]:
         text = re.sub(r"/\*.*?\*/", "", pathlib.Path(path).read_text(), flags=re.S)
         out.update(re.findall(r"\b(qg_[a-z0-9_]+)\s*\(", text))
     return sorted(out)
+
+
+def use_library(path: pathlib.Path | str):
+    """Make `path` (a build of the same library, e.g. libqgemv_timeline.so)
+    the library every context of this process binds; call before the first
+    GpuContext."""
+    global _lib
+    _lib = load_library(path)
+    return _lib
 
 
 def load_library(path: pathlib.Path | str = LIB_PATH):
@@ -259,6 +271,21 @@ class GpuContext:
         rc = self.lib.qg_gpu_mat_vec_mul(self.h, _ptr(weight_data), weight_data.nbytes, dtype,
                                          _ptr(x), _ptr(out), rows, cols)
         self.check(rc, "qg_gpu_mat_vec_mul")
+
+    def probe_stream_read(self, d_buf, nbytes: int, d_out, stream=None):
+        """One plain coalesced read of nbytes of a device tensor (qg_probe_stream_read)."""
+        rc = self.lib.qg_probe_stream_read(self.h, _ptr(d_buf), int(nbytes), _ptr(d_out),
+                                           ctypes.c_void_p(stream) if stream else None)
+        self.check(rc, "qg_probe_stream_read")
+
+    def invalidate(self, weight_data):
+        """Drop the device copies mat_vec_mul keeps for this host buffer (qg_gpu_invalidate)."""
+        self.check(self.lib.qg_gpu_invalidate(self.h, _ptr(weight_data)), "qg_gpu_invalidate")
+
+    def fail_allocations(self, n: int, skip: int = 0):
+        """Test hook: after `skip` more allocations, the next n allocations of
+        this context report out-of-memory (qg_test_fail_allocations)."""
+        self.check(self.lib.qg_test_fail_allocations(self.h, int(skip), int(n)), "qg_test_fail_allocations")
 
 
 class DeviceMatrix:

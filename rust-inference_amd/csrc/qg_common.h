@@ -117,6 +117,7 @@ int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t c
 int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
                               float *out, ihipStream_t *stream);
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
+int launch_stream_read(const void *buf, size_t nbytes, uint32_t *out, ihipStream_t *stream);
 // out = silu(g) * u elementwise
 int launch_silu_mul(const float *g, const float *u, float *out, size_t n, ihipStream_t *stream);
 // out = rmsnorm(a (+ b)) * w in one workgroup; sum_out (may be NULL) = a + b.

@@ -174,19 +174,33 @@ bool read_value(Cursor &c, uint32_t type, bool top, Value *v, std::string *err)
 // GgufDataType::from_u32 (gguf.rs:62-78): ids 0-3, 6-14
 bool known_type(uint32_t t) { return t <= 3 || (t >= 6 && t <= 14); }
 
-// bytes Model::load reads for a tensor (model.rs:166-180); 0 = skipped type
-uint64_t load_bytes(uint32_t type, uint64_t n)
+// Element count of a tensor (the product of its dims); false when the
+// product does not fit in 64 bits (a crafted header), which no tensor of a
+// real file reaches.
+bool n_elements(const Tensor &t, uint64_t *n)
 {
-    const uint64_t bs = qg::block_elems(type), bb = qg::block_bytes(type);
-    if (bb == 0) return 0;
-    return (n + bs - 1) / bs * bb;
+    uint64_t p = 1;
+    for (uint64_t d : t.dims) {
+        if (d != 0 && p > UINT64_MAX / d) return false;
+        p *= d;
+    }
+    *n = p;
+    return true;
 }
 
-uint64_t n_elements(const Tensor &t)
+// Bytes Model::load reads for a tensor (model.rs:166-180): *nb = 0 for a
+// type the loader skips.  False when the tensor's element or byte count
+// overflows 64 bits.
+bool load_bytes(const Tensor &t, uint64_t *nb)
 {
-    uint64_t n = 1;
-    for (uint64_t d : t.dims) n *= d;
-    return n;
+    uint64_t n;
+    if (!n_elements(t, &n)) return false;
+    const uint64_t bs = qg::block_elems(t.type), bb = qg::block_bytes(t.type);
+    if (bb == 0) { *nb = 0; return true; }
+    const uint64_t blocks = n / bs + (n % bs != 0);
+    if (blocks > UINT64_MAX / bb) return false;
+    *nb = blocks * bb;
+    return true;
 }
 
 int gfail(qg_gguf *g, int st, const std::string &what)
@@ -297,7 +311,16 @@ int qg_gguf_open(const char *path, qg_gguf **out)
         }
         g->map = (const uint8_t *)m;
     }
-    const int rc = parse(g);
+    int rc;
+    try {
+        rc = parse(g);
+    } catch (const std::bad_alloc &) {      // host memory for the metadata / descriptors
+        g->err = "host allocation failed while parsing";
+        rc = QG_ERR_OUT_OF_MEMORY;
+    } catch (...) {
+        g->err = "unexpected error while parsing";
+        rc = QG_ERR_INVALID_ARG;
+    }
     if (rc) {
         g_open_error = g->err;
         unmap(g);
@@ -411,15 +434,18 @@ int qg_gguf_tensor_info(const qg_gguf *g, size_t index, const char **name, uint3
     if (dims)
         for (int d = 0; d < 4; d++) dims[d] = d < (int)t.dims.size() ? t.dims[d] : 1;
     if (offset) *offset = t.offset;
-    if (nbytes) *nbytes = (size_t)load_bytes(t.type, n_elements(t));
-    return QG_OK;
+    uint64_t nb = 0;
+    const bool ok = load_bytes(t, &nb);
+    if (nbytes) *nbytes = ok ? (size_t)nb : 0;
+    return ok ? QG_OK : QG_ERR_SHAPE;
 }
 
 int qg_gguf_tensor_data(const qg_gguf *g, size_t index, const void **data, size_t *nbytes)
 {
     if (!g || index >= g->tensors.size() || !data) return QG_ERR_INVALID_ARG;
     const Tensor &t = g->tensors[index];
-    const uint64_t nb = load_bytes(t.type, n_elements(t));
+    uint64_t nb = 0;
+    if (!load_bytes(t, &nb)) return QG_ERR_SHAPE;             // dims overflow 64 bits
     if (nb == 0) return QG_ERR_UNSUPPORTED_TYPE;              // model.rs:176-179 skips it
     const uint64_t start = g->data_offset + t.offset;
     if (start < g->data_offset || start > g->size || nb > g->size - start) return QG_ERR_SHORT_DATA;
@@ -538,8 +564,12 @@ struct Loader {
         if (rc == QG_ERR_UNSUPPORTED_TYPE) return required ? missing(name + " (type skipped by the loader)") : QG_OK;
         if (rc) { why = "cannot read " + name; return rc; }
         const uint64_t n = t->dims.empty() ? 0 : t->dims[0];
+        // every vector slot holds embed_dim, q_dim or kv_dim floats (u32
+        // sizes): a longer ne0 cannot match the config, so it is refused
+        // before anything is allocated for it
+        if (n > 0xFFFFFFFFull) { why = name + ": length does not match the config"; return QG_ERR_SHAPE; }
         std::vector<float> v((size_t)n, 0.0f);
-        if (t->type == 0 && n * 4 <= nb) std::memcpy(v.data(), data, (size_t)n * 4);
+        if (t->type == 0 && n <= nb / 4) std::memcpy(v.data(), data, (size_t)n * 4);
         rc = qg_model_set_vector(m, slot, layer, v.data(), v.size());
         if (rc) why = name + ": " + qg_last_error(ctx);
         return rc;
@@ -548,23 +578,31 @@ struct Loader {
 
 }  // namespace
 
-extern "C" int qg_model_load_gguf(qg_ctx *ctx, const char *path, uint32_t max_seq_len, qg_model **out)
-{
-    if (!ctx || !path || !out) return QG_ERR_INVALID_ARG;
-    *out = nullptr;
+namespace {
+
+// Owners that release the mapping and a half-loaded model on every way out
+// of load_gguf, exceptions included.
+struct GgufGuard {
     qg_gguf *g = nullptr;
-    int rc = qg_gguf_open(path, &g);
+    ~GgufGuard() { if (g) qg_gguf_close(g); }
+};
+struct ModelGuard {
+    qg_model *m = nullptr;
+    ~ModelGuard() { if (m) qg_model_destroy(m); }
+};
+
+int load_gguf(qg_ctx *ctx, const char *path, uint32_t max_seq_len, qg_model **out)
+{
+    GgufGuard gg;
+    int rc = qg_gguf_open(path, &gg.g);
     if (rc) return qg_fail(ctx, rc, (std::string("GGUF: ") + qg_gguf_open_error()).c_str());
+    qg_gguf *g = gg.g;
     qg_model_config cfg;
-    if ((rc = qg_gguf_model_config(g, max_seq_len, &cfg))) {
-        qg_gguf_close(g);
-        return qg_fail(ctx, rc, "GGUF: model config out of range");
-    }
+    if ((rc = qg_gguf_model_config(g, max_seq_len, &cfg))) return qg_fail(ctx, rc, "GGUF: model config out of range");
     Loader L{ctx, g};
-    if ((rc = qg_model_create(ctx, &cfg, &L.m))) {
-        qg_gguf_close(g);
-        return rc;
-    }
+    ModelGuard mg;
+    if ((rc = qg_model_create(ctx, &cfg, &mg.m))) return rc;
+    L.m = mg.m;
     const std::string b = "blk.";
     auto blk = [&](uint32_t l, const char *s) { return b + std::to_string(l) + "." + s; };
     const size_t E = cfg.embed_dim, H = cfg.hidden_dim, V = cfg.vocab_size;
@@ -593,12 +631,27 @@ extern "C" int qg_model_load_gguf(qg_ctx *ctx, const char *path, uint32_t max_se
             (rc = L.mat(blk(l, "ffn_down.weight"), QG_M_DOWN, l, E, H)))
             break;
     }
-    qg_gguf_close(g);
     if (rc) {
         const std::string why = L.why.empty() ? std::string(qg_last_error(ctx)) : L.why;
-        qg_model_destroy(L.m);
         return qg_fail(ctx, rc, ("GGUF: " + why).c_str());
     }
-    *out = L.m;
+    *out = mg.m;
+    mg.m = nullptr;
     return QG_OK;
+}
+
+}  // namespace
+
+// Model::load (model.rs:136-329) from a GGUF file; no exception leaves the C ABI.
+extern "C" int qg_model_load_gguf(qg_ctx *ctx, const char *path, uint32_t max_seq_len, qg_model **out)
+{
+    if (!ctx || !path || !out) return QG_ERR_INVALID_ARG;
+    *out = nullptr;
+    try {
+        return load_gguf(ctx, path, max_seq_len, out);
+    } catch (const std::bad_alloc &) {
+        return qg_fail(ctx, QG_ERR_OUT_OF_MEMORY, "GGUF: host allocation failed");
+    } catch (...) {
+        return qg_fail(ctx, QG_ERR_INVALID_ARG, "GGUF: unexpected error while loading");
+    }
 }

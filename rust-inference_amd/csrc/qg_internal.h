@@ -8,6 +8,7 @@
 #include <set>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "qg_common.h"
 #include "qgemv.h"
@@ -22,6 +23,7 @@ struct qg_mat {
     uint32_t type;
     size_t rows, cols;
     bool owned;
+    int shares = 0;    // decode-step models using this matrix without owning it
     qg::Plan plan;     // plan.rp: the stream kernels read d_rp
 };
 
@@ -44,8 +46,34 @@ struct qg_ctx {
     size_t d_glu_cap = 0;
     std::set<qg_mat *> mats;
     std::set<qg_model *> models;            // decode-step engines on this context
-    std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, qg_mat *> keyed;
+    // qg_gpu_mat_vec_mul's device copies, keyed by (host address, bytes, type,
+    // rows, cols), each with a fingerprint of the host bytes it was made from
+    struct Keyed {
+        qg_mat *mat;
+        std::vector<uint8_t> fp;
+    };
+    std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, Keyed> keyed;
+    int fail_skip = 0, fail_allocs = 0;     // test hook: allocations to let through, then to fail
 };
+
+// Test hook (qg_test_fail_allocations): true when this allocation is to be
+// reported as failed without calling HIP.
+inline bool qg_alloc_injected(qg_ctx *ctx)
+{
+    if (!ctx || ctx->fail_allocs <= 0) return false;
+    if (ctx->fail_skip > 0) {
+        ctx->fail_skip--;
+        return false;
+    }
+    ctx->fail_allocs--;
+    return true;
+}
+
+// check_mat of the C ABI: ctx valid and mat one of its live matrices.
+int qg_check_mat(qg_ctx *ctx, const qg_mat *mat);
+
+// The model-owned or shared matrix `mat` is no longer used by a model slot.
+int qg_mat_release(qg_ctx *ctx, qg_mat *mat, bool owned);
 
 struct qg_model;
 // Frees every decode-step engine of the context (qg_model.hip); qg_destroy

@@ -566,7 +566,10 @@ struct qg_model {
     uint32_t att_grp = 0, att_nsplit = 0;   // split attention (head_dim 64, 128, 256)
     size_t att_lds = 0;                     // LDS of the one-workgroup-per-head kernel
     qg_mat *tok = nullptr, *lm = nullptr;
-    bool tok_owned = false, lm_owned = false;
+    // a slot holds a matrix the model owns (set_matrix), one it shares
+    // (share_matrix: counted in qg_mat::shares), or -- lm only -- an alias of
+    // tok (a tied output, neither owned nor shared)
+    bool tok_owned = false, lm_owned = false, tok_shared = false, lm_shared = false;
     std::vector<qg_mat *> w[kSlots];
     std::vector<bool> owned[kSlots];
     float *final_norm = nullptr;
@@ -668,6 +671,9 @@ int prepare(qg_model *m)
     return QG_OK;
 }
 
+// lm is an alias of tok (a tied output): it holds no reference of its own
+bool lm_alias(const qg_model *m) { return m->lm && m->lm == m->tok && !m->lm_owned && !m->lm_shared; }
+
 void free_model(qg_model *m)
 {
     m->ctx->models.erase(m);
@@ -675,9 +681,10 @@ void free_model(qg_model *m)
     drop_fused(m);
     for (int s = 0; s < kSlots; s++)
         for (size_t l = 0; l < m->w[s].size(); l++)
-            if (m->w[s][l] && m->owned[s][l]) qg_mat_free(m->ctx, m->w[s][l]);
-    if (m->tok && m->tok_owned) qg_mat_free(m->ctx, m->tok);
-    if (m->lm && m->lm_owned && m->lm != m->tok) qg_mat_free(m->ctx, m->lm);
+            qg_mat_release(m->ctx, m->w[s][l], m->owned[s][l]);
+    const bool alias = lm_alias(m);
+    qg_mat_release(m->ctx, m->tok, m->tok_owned);
+    if (!alias) qg_mat_release(m->ctx, m->lm, m->lm_owned);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->h_recent) (void)hipHostFree(m->h_recent);
     if (m->h_token) (void)hipHostFree(m->h_token);
@@ -698,6 +705,38 @@ void slot_shape(const qg_model *m, uint32_t which, size_t *rows, size_t *cols)
     case QG_M_DOWN: *rows = E; *cols = H; break;
     default: *rows = *cols = 0;
     }
+}
+
+// Puts `mat` into slot (which, layer), owned by the model or shared (counted
+// in mat->shares), releasing what the slot held.  A tied lm_head that aliases
+// the token_embd being replaced takes over that matrix, as the reference's
+// lm_head is a clone made at load time (model.rs:224-226).
+void put_slot(qg_model *m, uint32_t which, uint32_t layer, qg_mat *mat, bool shared)
+{
+    if (shared) mat->shares++;
+    if (which == QG_M_TOKEN_EMBD || which == QG_M_LM_HEAD) {
+        if (which == QG_M_TOKEN_EMBD && lm_alias(m) && m->tok != mat) {
+            m->lm_owned = m->tok_owned;
+            m->lm_shared = m->tok_shared;
+            m->tok = nullptr;
+            m->tok_owned = m->tok_shared = false;
+        }
+        const bool lm = which == QG_M_LM_HEAD;
+        qg_mat *&dst = lm ? m->lm : m->tok;
+        bool &own = lm ? m->lm_owned : m->tok_owned, &shr = lm ? m->lm_shared : m->tok_shared;
+        if (dst && !(lm && lm_alias(m))) {
+            if (shr) { if (dst->shares > 0) dst->shares--; }
+            else if (own) qg_mat_free(m->ctx, dst);
+        }
+        dst = mat;
+        own = !shared;
+        shr = shared;
+        return;
+    }
+    const int s = (int)which - QG_M_WQ;
+    qg_mat_release(m->ctx, m->w[s][layer], m->owned[s][layer]);
+    m->w[s][layer] = mat;
+    m->owned[s][layer] = !shared;
 }
 
 int gemv(qg_model *m, const qg_mat *a, const float *x, float *y)
@@ -1036,26 +1075,7 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
     drop_fused(m);
-    if (which == QG_M_TOKEN_EMBD && m->tok && m->lm == m->tok) {
-        // a tied lm_head keeps the old token_embd copy
-        m->lm_owned = m->tok_owned;
-        m->tok = nullptr;
-        m->tok_owned = false;
-    }
-    qg_mat **dst;
-    bool *own;
-    if (which == QG_M_TOKEN_EMBD) { dst = &m->tok; own = &m->tok_owned; }
-    else if (which == QG_M_LM_HEAD) { dst = &m->lm; own = &m->lm_owned; }
-    else {
-        const int s = (int)which - QG_M_WQ;
-        if (m->w[s][layer] && m->owned[s][layer]) qg_mat_free(m->ctx, m->w[s][layer]);
-        m->w[s][layer] = mat;
-        m->owned[s][layer] = true;
-        return QG_OK;
-    }
-    if (*dst && *own && !(which == QG_M_LM_HEAD && *dst == m->tok)) qg_mat_free(m->ctx, *dst);
-    *dst = mat;
-    *own = true;
+    put_slot(m, which, layer, mat, false);
     return QG_OK;
 }
 
@@ -1072,24 +1092,7 @@ int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
     drop_fused(m);
-    qg_mat *mm = const_cast<qg_mat *>(mat);
-    if (which == QG_M_TOKEN_EMBD && m->tok && m->lm == m->tok && m->tok != mm) {
-        m->lm_owned = m->tok_owned;                        // a tied lm_head keeps the old copy
-        m->tok = nullptr;
-        m->tok_owned = false;
-    }
-    if (which == QG_M_TOKEN_EMBD) {
-        if (m->tok && m->tok_owned) qg_mat_free(m->ctx, m->tok);
-        m->tok = mm; m->tok_owned = false;
-    } else if (which == QG_M_LM_HEAD) {
-        if (m->lm && m->lm_owned && m->lm != m->tok) qg_mat_free(m->ctx, m->lm);
-        m->lm = mm; m->lm_owned = false;
-    } else {
-        const int s = (int)which - QG_M_WQ;
-        if (m->w[s][layer] && m->owned[s][layer]) qg_mat_free(m->ctx, m->w[s][layer]);
-        m->w[s][layer] = mm;
-        m->owned[s][layer] = false;
-    }
+    put_slot(m, which, layer, const_cast<qg_mat *>(mat), true);
     return QG_OK;
 }
 
@@ -1228,9 +1231,9 @@ int qg_model_tie_lm_head(qg_model *m)
     if (!m || !m->tok) return QG_ERR_INVALID_ARG;
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
-    if (m->lm && m->lm_owned && m->lm != m->tok) qg_mat_free(m->ctx, m->lm);
+    if (!lm_alias(m)) qg_mat_release(m->ctx, m->lm, m->lm_owned);
     m->lm = m->tok;
-    m->lm_owned = false;
+    m->lm_owned = m->lm_shared = false;
     return QG_OK;
 }
 

@@ -74,6 +74,7 @@ hipStream_t pick(qg_ctx *ctx, void *stream)
 int grow_pinned(qg_ctx *ctx, float **p, size_t *cap, size_t n)
 {
     if (*cap >= n) return QG_OK;
+    if (qg_alloc_injected(ctx)) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipHostMalloc (injected failure)");
     if (*p) (void)hipHostFree(*p);
     *p = nullptr;
     *cap = 0;
@@ -86,6 +87,7 @@ int grow_pinned(qg_ctx *ctx, float **p, size_t *cap, size_t n)
 int grow_device(qg_ctx *ctx, float **p, size_t *cap, size_t n)
 {
     if (*cap >= n) return QG_OK;
+    if (qg_alloc_injected(ctx)) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc staging (injected failure)");
     if (*p) (void)hipFree(*p);
     *p = nullptr;
     *cap = 0;
@@ -119,7 +121,7 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
     // GGUF-layout kernels.
     if (owned && qg::repack_eligible(type, m->plan, rows)) {
         uint8_t *r = nullptr;
-        hipError_t e = hipMalloc((void **)&r, nbytes + qg::kTailPad);
+        hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&r, nbytes + qg::kTailPad);
         if (e != hipSuccess) {
             delete m;
             return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc repacked matrix", e);
@@ -148,7 +150,7 @@ void drop_mat(qg_ctx *ctx, qg_mat *m)
     if (m->d_rp) (void)hipFree(m->d_rp);
     ctx->mats.erase(m);
     for (auto it = ctx->keyed.begin(); it != ctx->keyed.end();) {
-        if (it->second == m)
+        if (it->second.mat == m)
             it = ctx->keyed.erase(it);
         else
             ++it;
@@ -156,14 +158,43 @@ void drop_mat(qg_ctx *ctx, qg_mat *m)
     delete m;
 }
 
+// A handle is valid while its context lists it: the set is consulted before
+// the handle is read, so a freed or foreign handle is an error, not a read of
+// freed memory.
 int check_mat(qg_ctx *ctx, const qg_mat *mat)
 {
     if (!ctx) return QG_ERR_INVALID_ARG;
-    if (!mat || mat->ctx != ctx) return fail(ctx, QG_ERR_INVALID_ARG, "matrix not of this context");
+    if (!mat || !ctx->mats.count(const_cast<qg_mat *>(mat)))
+        return fail(ctx, QG_ERR_INVALID_ARG, "matrix not of this context (or already freed)");
     return QG_OK;
 }
 
+// Fingerprint of a host weight buffer for qg_gpu_mat_vec_mul's cache: 64
+// bytes at each of 16 evenly spaced offsets (the first and the last 64 bytes
+// among them), or the whole buffer when it is shorter than 1 KiB.
+std::vector<uint8_t> fingerprint(const uint8_t *p, size_t n)
+{
+    constexpr size_t kWin = 64, kN = 16;
+    if (n <= kWin * kN) return std::vector<uint8_t>(p, p + n);
+    std::vector<uint8_t> fp(kWin * kN);
+    for (size_t i = 0; i < kN; i++) {
+        const size_t off = (n - kWin) / (kN - 1) * i + (i == kN - 1 ? (n - kWin) % (kN - 1) : 0);
+        memcpy(fp.data() + i * kWin, p + off, kWin);
+    }
+    return fp;
+}
+
 }  // namespace
+
+int qg_check_mat(qg_ctx *ctx, const qg_mat *mat) { return check_mat(ctx, mat); }
+
+int qg_mat_release(qg_ctx *ctx, qg_mat *mat, bool owned)
+{
+    if (!mat) return QG_OK;
+    if (owned) return qg_mat_free(ctx, mat);
+    if (mat->shares > 0) mat->shares--;
+    return QG_OK;
+}
 
 int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float *xb, const float *nw,
                    float eps, float *sum_out, float *y, float *scratch, hipStream_t st)
@@ -276,7 +307,7 @@ int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out)
     }
     QG_HIP(ctx, hipSetDevice(ctx->device));
     uint8_t *d = nullptr;
-    hipError_t e = hipMalloc((void **)&d, total + qg::kTailPad);
+    hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&d, total + qg::kTailPad);
     if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc", e);
     size_t off = 0;
     for (int i = 0; i < n && e == hipSuccess; i++) {
@@ -369,7 +400,7 @@ int qg_upload(qg_ctx *ctx, const void *raw, size_t nbytes, uint32_t type, size_t
     if (need > 0 && !raw) return fail(ctx, QG_ERR_INVALID_ARG, "raw == NULL");
     QG_HIP(ctx, hipSetDevice(ctx->device));
     uint8_t *d = nullptr;
-    hipError_t e = hipMalloc((void **)&d, need + qg::kTailPad);
+    hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&d, need + qg::kTailPad);
     if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc matrix", e);
     e = hipMemcpy(d, raw, need, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemset(d + need, 0, qg::kTailPad);
@@ -399,6 +430,8 @@ int qg_mat_free(qg_ctx *ctx, qg_mat *mat)
 {
     int rc = check_mat(ctx, mat);
     if (rc) return rc;
+    if (mat->shares > 0)
+        return fail(ctx, QG_ERR_INVALID_ARG, "matrix is in use by a decode-step model (qg_model_share_matrix)");
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     drop_mat(ctx, mat);
@@ -543,16 +576,49 @@ int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint
 {
     if (!ctx) return QG_ERR_INVALID_ARG;
     auto key = std::make_tuple((uintptr_t)weight_data, nbytes, dtype, rows, cols);
+    size_t need = 0;
+    int rc = required_bytes(dtype, rows, cols, &need);
+    if (rc != QG_OK) return fail(ctx, rc, "unsupported type or shape");
+    if (nbytes < need) return fail(ctx, QG_ERR_SHORT_DATA, "raw data shorter than the matrix needs");
+    if (need > 0 && !weight_data) return fail(ctx, QG_ERR_INVALID_ARG, "weight_data == NULL");
+    std::vector<uint8_t> fp = fingerprint((const uint8_t *)weight_data, need);
     qg_mat *m = nullptr;
     auto it = ctx->keyed.find(key);
-    if (it != ctx->keyed.end()) {
-        m = it->second;
+    if (it != ctx->keyed.end() && it->second.fp == fp) {
+        m = it->second.mat;
     } else {
-        int rc = qg_upload(ctx, weight_data, nbytes, dtype, rows, cols, &m);
-        if (rc) return rc;
-        ctx->keyed[key] = m;
+        // first sight, or the bytes at this address changed since the copy
+        // was made (weights edited in place, or a freed buffer's address
+        // reused): upload the current bytes
+        if (it != ctx->keyed.end()) {
+            QG_HIP(ctx, hipSetDevice(ctx->device));
+            (void)hipStreamSynchronize(ctx->stream);
+            drop_mat(ctx, it->second.mat);
+        }
+        if ((rc = qg_upload(ctx, weight_data, nbytes, dtype, rows, cols, &m))) return rc;
+        ctx->keyed[key] = qg_ctx::Keyed{m, std::move(fp)};
     }
     return qg_matvec_host(ctx, m, x, out);
+}
+
+int qg_gpu_invalidate(qg_ctx *ctx, const void *weight_data)
+{
+    if (!ctx) return QG_ERR_INVALID_ARG;
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    (void)hipStreamSynchronize(ctx->stream);
+    std::vector<qg_mat *> gone;
+    for (auto &kv : ctx->keyed)
+        if (std::get<0>(kv.first) == (uintptr_t)weight_data) gone.push_back(kv.second.mat);
+    for (qg_mat *m : gone) drop_mat(ctx, m);
+    return QG_OK;
+}
+
+int qg_test_fail_allocations(qg_ctx *ctx, int skip, int n)
+{
+    if (!ctx || skip < 0 || n < 0) return QG_ERR_INVALID_ARG;
+    ctx->fail_skip = skip;
+    ctx->fail_allocs = n;
+    return QG_OK;
 }
 
 int qg_dequant_dev(qg_ctx *ctx, const qg_mat *mat, float *d_out, void *stream)
@@ -599,6 +665,17 @@ int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_o
     if (qg::launch_dequantize_row(mat->type, mat->d, mat->rows, mat->cols, row, d_out,
                                   (ihipStream_t *)pick(ctx, stream)))
         return fail(ctx, QG_ERR_HIP, "dequantize_row launch", hipGetLastError());
+    return QG_OK;
+}
+
+int qg_probe_stream_read(qg_ctx *ctx, const void *d_buf, size_t nbytes, uint32_t *d_out, void *stream)
+{
+    if (!ctx) return QG_ERR_INVALID_ARG;
+    if ((nbytes && !d_buf) || !d_out || ((uintptr_t)d_buf & 15u) || nbytes % 16u)
+        return fail(ctx, QG_ERR_INVALID_ARG, "buffer NULL, not 16-byte aligned or not whole 16-byte pieces");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    if (qg::launch_stream_read(d_buf, nbytes, d_out, (ihipStream_t *)pick(ctx, stream)))
+        return fail(ctx, QG_ERR_HIP, "stream read launch", hipGetLastError());
     return QG_OK;
 }
 

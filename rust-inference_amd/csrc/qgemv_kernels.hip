@@ -1031,6 +1031,41 @@ __device__ __forceinline__ void store_y(float *p, float v)
     asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
 
+// ------------------------------------------------------------ timeline
+//
+// Only in the build with -DQG_TIMELINE (libqgemv_timeline.so, `make
+// timeline`): the LDS-ring kernel takes s_memrealtime stamps at fixed points.
+// A stamp goes into lane `ev` of a VGPR (a select, no memory operation and no
+// register indexing), and each stamping wave writes its lanes once, after its
+// last load, wait and barrier, so the kernel's memory traffic and waits are
+// those of the plain build.  Per workgroup, 64 stamps: compute wave 0 in
+// 0..31, the first loader wave in 32..63 (0 = never stamped).
+#ifdef QG_TIMELINE
+constexpr uint32_t kTlEv = 64, kTlWG = 2048;
+__device__ uint64_t qg_tl_buf[kTlWG * kTlEv];
+struct Timeline {
+    uint64_t v = 0;
+    __device__ __forceinline__ void stamp(uint32_t ev)
+    {
+        const uint64_t now = __builtin_amdgcn_s_memrealtime();
+        v = (threadIdx.x & 63u) == ev ? now : v;
+    }
+    // lanes 0..31 of this wave to stamps base .. base + 31 of this workgroup
+    __device__ __forceinline__ void write(uint32_t base)
+    {
+        const uint32_t l = threadIdx.x & 63u;
+        if (l < 32u && blockIdx.x < kTlWG) qg_tl_buf[blockIdx.x * kTlEv + base + l] = v;
+    }
+};
+#define QG_TL_DECL Timeline tl_
+#define QG_TL(ev) tl_.stamp(ev)
+#define QG_TL_WRITE(base) tl_.write(base)
+#else
+#define QG_TL_DECL
+#define QG_TL(ev) ((void)0)
+#define QG_TL_WRITE(base) ((void)0)
+#endif
+
 // Workgroup barrier that waits for this wave's LDS traffic only: global loads
 // issued before it stay in flight.
 __device__ __forceinline__ void lds_barrier()
@@ -1540,6 +1575,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
     const uint32_t gb = a.group_bytes, ring = a.red_off;
     auto slot_off = [&](uint32_t i) { const uint32_t k = i % kRingSlots; return k < 2u ? ring + k * SLOT : a.ring_slot2; };
     float *redf = (float *)(lds + ring + 2u * SLOT);            // 2 x NW per-wave sums
+    QG_TL_DECL;
     if (wave >= NW) {
         // loader l: the rows of teams l*TPW/2 .. (l+1)*TPW/2 - 1 of every stage
         const uint32_t l = wave - NW, np = (gb + 15u) / 16u;
@@ -1557,20 +1593,27 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
                 lds_dma16(a.w + grp * gb + pc * 16u, dst + k * 1024u);
             }
         };
+        QG_TL(0);
 #pragma unroll
         for (uint32_t i = 0; i < kRingSlots - 1u; i++)
             if (i < a.per_team) issue(i);
+        QG_TL(1);
         lds_barrier();                                                  // x staged
+        QG_TL(2);
         for (uint32_t i = 0; i < a.per_team; i++) {
             // stage i landed: at most the next stage's copies still in flight
             if (a.per_team - 1u - i >= kRingSlots - 2u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(LINST));
             else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            QG_TL(3u + min(i, 27u));
             lds_barrier();                                              // stage i published
             if (i + kRingSlots - 1u < a.per_team) issue(i + kRingSlots - 1u);
         }
         lds_barrier();
+        QG_TL(31);
+        if (wave == NW) QG_TL_WRITE(32);
         return;
     }
+    QG_TL(0);
     const uint32_t tw = tid / (64u * WPT), lt = tid % (64u * WPT), wt = wave % WPT;
     const bool active = lt < a.ni;
     const uint32_t it = active ? lt : 0u;
@@ -1591,6 +1634,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         }
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    QG_TL(1);
 #pragma unroll
     for (int r = 0; r < XR; r++) {
         const uint32_t c = tid + r * NT;
@@ -1607,7 +1651,9 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         for (int i = 0; i < 4; i++) u[i] = src[4 * c + i];
         stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
     }
+    QG_TL(2);
     lds_barrier();
+    QG_TL(3);
     XP<S, SEG> xs;
     uint32_t srow[S];
     plane_slice<I, true>(lds, meta, it, active, a.cols, xs, srow);
@@ -1621,7 +1667,9 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         }
     };
     for (uint32_t i = 0; i < a.per_team; i++) {
+        QG_TL(4u + 2u * min(i, 12u));
         lds_barrier();
+        QG_TL(5u + 2u * min(i, 12u));
         if (i > 0) flush(i - 1);
         const uint8_t *row = lds + slot_off(i) + (tw / (TPW / 2)) * REGION + (tw % (TPW / 2)) * ((gb + 15u) & ~15u);
         uint32_t raw[NR];
@@ -1640,8 +1688,11 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         t = group_sum<64>(t);
         if (lane == 63u) redf[(i & 1u) * NW + wave] = t;
     }
+    QG_TL(30);
     lds_barrier();
     if (a.per_team > 0) flush(a.per_team - 1);
+    QG_TL(31);
+    if (wave == 0) QG_TL_WRITE(0);
 }
 
 // ------------------------------------------------------------ planning
@@ -2207,6 +2258,31 @@ int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size
     return launch_dequantize_row_any(type, w, rows, cols, 0, d_row, out, stream);
 }
 
+// The streaming-read ceiling: every 16-byte piece of the buffer read once by
+// one thread of a full grid of 1024-thread workgroups (the fastest plain read
+// of 33-447 MB measured on MI355X among grid-wide, persistent, banded and
+// chunked forms with 1-4 loads per thread); an XOR of everything goes to
+// out[0] only if it matches a constant, so the loads cannot be dropped.
+__global__ void __launch_bounds__(1024) stream_read_k(const uint4 *__restrict__ p, uint64_t n16,
+                                                      uint32_t *__restrict__ out)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint4 v = i < n16 ? p[i] : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t acc = v.x ^ v.y ^ v.z ^ v.w;
+    if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
+int launch_stream_read(const void *buf, size_t nbytes, uint32_t *out, ihipStream_t *stream)
+{
+    const uint64_t n16 = nbytes / 16u;
+    if (n16 == 0) return 0;
+    const uint64_t grid = (n16 + 1023u) / 1024u;
+    if (grid > 0x7FFFFFFFull) return -1;
+    hipLaunchKernelGGL(stream_read_k, dim3((uint32_t)grid), dim3(1024), 0, (hipStream_t)stream,
+                       (const uint4 *)buf, n16, out);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream)
 {
     if (n == 0) return 0;
@@ -2233,3 +2309,32 @@ int launch_rmsnorm(const float *a, const float *b, float *sum_out, const float *
 }
 
 }  // namespace qg
+
+#ifdef QG_TIMELINE
+#include "qgemv.h"
+
+// The stamps of the last instrumented launch (libqgemv_timeline.so only):
+// n values, 64 per workgroup, and the stamp clock in kHz.
+extern "C" int qg_timeline_read(uint64_t *out, size_t n, int *clock_khz)
+{
+    const size_t cap = (size_t)qg::kTlWG * qg::kTlEv;
+    if (!out) return QG_ERR_INVALID_ARG;
+    if (n > cap) n = cap;
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(qg::qg_tl_buf), n * sizeof(uint64_t), 0, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return QG_ERR_HIP;
+    int dev = 0;
+    if (clock_khz && (hipGetDevice(&dev) != hipSuccess ||
+                      hipDeviceGetAttribute(clock_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess))
+        return QG_ERR_HIP;
+    return QG_OK;
+}
+
+extern "C" int qg_timeline_clear(void)
+{
+    static uint64_t zero[qg::kTlWG * qg::kTlEv];
+    return hipMemcpyToSymbol(HIP_SYMBOL(qg::qg_tl_buf), zero, sizeof zero, 0, hipMemcpyHostToDevice) == hipSuccess
+               ? QG_OK
+               : QG_ERR_HIP;
+}
+#endif

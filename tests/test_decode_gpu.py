@@ -223,15 +223,20 @@ def test_generate_matches_stepwise(rinf, synth, oracle, ctx):
     dev.close()
 
 
-def test_qwen2_05b_shape_config3(rinf, synth, oracle, ctx):
-    """Qwen2-0.5B architecture, Q4_K_M, tied lm_head,
-    token_embd Q4_K at cols = 896 (rows straddle superblocks: the
-    dequantize_row placement of quant.rs:152-174 is in the loop)."""
+def test_qwen2_05b_config3_as_stated(rinf, synth, oracle, ctx):
+    """BASELINE.json configs[2] exactly: Qwen2-0.5B architecture, Q4_K_M, tied
+    lm_head, token_embd Q4_K at cols = 896 (rows straddle superblocks: the
+    dequantize_row placement of quant.rs:152-174 is in the loop), a 32-token
+    random-id prompt then 128 greedy steps, the logits of every one of the
+    160 steps against the oracle's CPU forward pass and every greedy token
+    against the reference's sampler."""
     cfg = synth.ARCH["qwen2-0.5b"]
-    dev, ref, shared = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", synth.config_seed(2), 48)
-    prompt = np.random.default_rng(synth.config_seed(2)).integers(0, cfg["vocab_size"], 8)
-    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 8)
-    print(f"qwen2-0.5b: max logits err {max(errs):.2e}, tokens {out}", flush=True)
+    dev, ref, shared = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", synth.config_seed(2), 161)
+    prompt = np.random.default_rng(synth.config_seed(2)).integers(0, cfg["vocab_size"], 32)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 128)
+    print(f"qwen2-0.5b 32+128: max logits err {max(errs):.2e}, median {np.median(errs):.2e}, "
+          f"last {errs[-1]:.2e}, tokens {out[:16]}...", flush=True)
+    assert len(errs) == 160
     assert max(errs) <= DEEP_TOL
     dev.close()
     shared.free()
@@ -242,13 +247,16 @@ def test_qwen2_05b_shape_config3(rinf, synth, oracle, ctx):
 def test_full_size_models(rinf, synth, oracle, ctx, arch, mix, cidx):
     """BASELINE.json configs[3] and [4] at full size: the 28-layer Qwen2-7B
     model of the bench (Q4_K_M, same seed) and the 32-layer Llama-3-8B in the
-    Q4_K_M, Q5_K and Q8_0 mixes; 4 prompt tokens then 4 greedy steps, logits
-    and tokens against the oracle's CPU forward pass."""
+    Q4_K_M, Q5_K and Q8_0 mixes; 16 prompt tokens then 16 greedy steps
+    (32 positions: several attention ranges per head), logits and tokens
+    against the oracle's CPU forward pass."""
     cfg = synth.ARCH[arch]
-    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, mix, synth.config_seed(cidx), 16)
-    prompt = np.random.default_rng(synth.config_seed(cidx)).integers(0, cfg["vocab_size"], 4)
-    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 4)
-    print(f"{arch} {mix}: max logits err {max(errs):.2e}, tokens {out}", flush=True)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, mix, synth.config_seed(cidx), 40)
+    prompt = np.random.default_rng(synth.config_seed(cidx)).integers(0, cfg["vocab_size"], 16)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 16)
+    print(f"{arch} {mix} 16+16: max logits err {max(errs):.2e}, median {np.median(errs):.2e}, "
+          f"tokens {out}", flush=True)
+    assert len(errs) == 32
     assert max(errs) <= DEEP_TOL
     dev.close()
 

@@ -193,3 +193,25 @@ def test_tensor_past_end_of_file(rinf, gw, tmp_path):
     with pytest.raises(rinf.GgufError) as e:
         g.tensor_bytes("w")
     assert e.value.status == 3                                            # QG_ERR_SHORT_DATA
+
+
+def test_overflowing_dims_are_an_error(rinf, tmp_path):
+    """Tensor dims whose element or byte count does not fit in 64 bits (a
+    crafted header) give QG_ERR_SHAPE, never a wrapped small byte count that
+    would pass the bounds check."""
+    h = b"GGUF" + struct.pack("<IQQ", 3, 3, 0)
+    h += s("a") + struct.pack("<IQQIQ", 2, 1 << 32, 1 << 32, 0, 0)      # 2^64 elements: wraps to 0
+    h += s("b") + struct.pack("<IQIQ", 1, 1 << 62, 0, 0)                 # 2^62 f32: 2^64 bytes
+    h += s("c") + struct.pack("<IQQIQ", 2, (1 << 40) + 1, 1 << 24, 1, 0)  # wraps to 2^24 f16
+    pad = (-len(h)) % 32
+    p = tmp_path / "overflow.gguf"
+    p.write_bytes(h + b"\0" * pad + b"\0" * 4096)
+    g = rinf.GgufFile(p)
+    for name in ("a", "b", "c"):
+        with pytest.raises(rinf.GgufError) as e:
+            g.tensor_bytes(name)
+        assert e.value.status == 7                                        # QG_ERR_SHAPE
+    with pytest.raises(rinf.GgufError) as e:
+        g.tensors()                                                       # tensor_info reports it too
+    assert e.value.status == 7
+    g.close()

@@ -94,3 +94,22 @@ def test_missing_tensor_is_an_error(rinf, synth, ctx, gw, tmp_path):
         rinf.DeviceModel.load_gguf(ctx, p)
     assert e.value.status == 7
     assert "blk.0.ffn_up.weight" in str(e.value)
+
+
+def test_wrapped_dims_return_a_status(rinf, synth, ctx, gw, tmp_path):
+    """A norm whose dims multiply past 2^64 -- wrapping to a 32 MiB byte count
+    that lies inside the file -- is refused with QG_ERR_SHAPE: no attempt to
+    build a vector of ne0 = 2^40 + 1 floats, no exception out of the C ABI."""
+    cfg = dict(SMALL, n_layers=1)
+    tensors, _ = gw.model_tensors(synth, cfg, "q8_0", 45)
+    bad = []
+    for n, dims, ty, raw in tensors:
+        if n == "blk.0.ffn_norm.weight":
+            n, dims, ty, raw = n, [(1 << 40) + 1, 1 << 24], 1, np.zeros(1 << 24, np.float16)
+        bad.append((n, dims, ty, raw))
+    p = tmp_path / "wrapped.gguf"
+    gw.write_gguf(p, gw.model_metadata(cfg, context_length=16), bad)
+    with pytest.raises(rinf.QgemvError) as e:
+        rinf.DeviceModel.load_gguf(ctx, p)
+    assert e.value.status == 7
+    assert "ffn_norm" in str(e.value)
