@@ -60,12 +60,67 @@ def config_seed(index: int) -> int:
     return 0x5EED0000 + index
 
 
+def _f16(v) -> np.ndarray:
+    return np.asarray(v, np.float32).astype(np.float16).view(np.uint8)
+
+
+def _pack_k_scales(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """The 12-byte 6-bit scale/min pack of Q4_K/Q5_K (the inverse of
+    get_scale_min_k4, quant.rs:606-615) for (nb, 8) arrays of 0..63."""
+    q = np.zeros((sc.shape[0], 12), np.uint8)
+    q[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    q[:, 4:8] = (mn[:, 0:4] & 63) | ((mn[:, 4:8] >> 4) << 6)
+    q[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+    return q
+
+
+def gen_weights(dtype: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """Raw bytes of a random-init weight matrix: dequantized values centred on
+    zero with standard deviation about 1/sqrt(cols), so that every mat-vec of
+    a normalised input stays O(1) through any number of layers (the uniform
+    bytes of gen_blocks have a positive mean of about 2 per weight: a model
+    built from them grows activations to 1e7..1e10 and one-hot attention, where
+    the reference's own f32 path is 4e-3 away from exact).  Codes stay uniform
+    over their bit range; the scale fields carry the magnitude and the centring:
+      Q4_K/Q5_K: sub-block scales sc in 1..15, mins m = sc, dmin = f16(c * d)
+                 with c the codes' mean (7.5 / 15.5), so each sub-block is
+                 d * sc * (q - c);
+      Q6_K: int8 sub-block scales in -8..7; Q8_0/Q4_0/Q5_0: as in the format;
+      every block's d (and dmin with it) gets a random sign;
+      F16/F32: N(0, 1/cols)."""
+    bs, bb, _ = LAYOUT[dtype]
+    nb = n_blocks(dtype, rows, cols)
+    rng = np.random.default_rng(seed)
+    sigma = 1.0 / np.sqrt(max(cols, 1))
+    if dtype in (0, 1):
+        w = rng.standard_normal(nb, dtype=np.float32) * np.float32(sigma)
+        return (w if dtype == 0 else w.astype(np.float16)).view(np.uint8)
+    raw = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    # a random sign per block cancels the -d/2 mean of the unsigned codes
+    jitter = rng.uniform(0.75, 1.25, size=nb) * rng.choice([-1.0, 1.0], size=nb)
+    if dtype in (12, 13):                       # Q4_K, Q5_K
+        c, code_sd = (7.5, 4.61) if dtype == 12 else (15.5, 9.23)
+        sc = rng.integers(1, 16, size=(nb, 8), dtype=np.uint8)
+        d = sigma / (8.8 * code_sd) * jitter
+        raw[:, 0:2] = _f16(d).reshape(nb, 2)
+        raw[:, 2:4] = _f16(c * np.asarray(d, np.float16).astype(np.float64)).reshape(nb, 2)
+        raw[:, 4:16] = _pack_k_scales(sc, sc)
+    elif dtype == 14:                           # Q6_K: w = d * sc * (q - 32)
+        raw[:, 192:208] = rng.integers(-8, 8, size=(nb, 16)).astype(np.int8).view(np.uint8)
+        raw[:, 208:210] = _f16(sigma / (4.6 * 18.5) * jitter).reshape(nb, 2)
+    else:                                       # Q8_0 d*q, Q4_0 d*(q-8), Q5_0 d*(q-16)
+        code_sd = {8: 73.9, 2: 4.61, 6: 9.23}[dtype]
+        raw[:, 0:2] = _f16(sigma / code_sd * jitter).reshape(nb, 2)
+    return raw.reshape(-1)
+
+
 # ------------------------------------------------------------ whole models
 #
 # BASELINE.json configs 3-5: random-init models of a named architecture in a
 # GGUF quantization mix.  Q4_K_M: attn_v and ffn_down Q6_K, every other
-# matrix Q4_K; the lm_head is Q6_K unless it is tied to token_embd.  RMSNorm
-# weights are f32 1 + N(0, 0.02); q/k/v biases f32 N(0, 0.02).
+# matrix Q4_K; the lm_head is Q6_K unless it is tied to token_embd.  Weight
+# matrices come from gen_weights (centred, ~1/sqrt(cols)); RMSNorm weights
+# are f32 1 + N(0, 0.02); q/k/v biases f32 N(0, 0.02).
 
 ARCH = {
     # embed, layers, heads, kv heads, ffn, vocab, rope base, tied lm_head
@@ -113,7 +168,7 @@ def gen_model(cfg: dict, mix: str = "q4_k_m", seed: int = 0):
         dtype = m.get(slot, m["base"])
         for layer in layers:
             s = int(rng.integers(0, 2**31))
-            mats[(slot, layer)] = (gen_blocks(dtype, rows, cols, s), dtype, rows, cols)
+            mats[(slot, layer)] = (gen_weights(dtype, rows, cols, s), dtype, rows, cols)
     E = cfg["embed_dim"]
     hd = E // cfg["n_heads"]
     kv_dim = cfg["n_kv_heads"] * hd

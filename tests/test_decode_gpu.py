@@ -4,15 +4,13 @@ src/transformer.rs:63-98) and of the greedy sampler with repetition penalty
 (src/sampler.rs:72-83, 109-127; src/math.rs:328-339).
 
 Per step, the device logits must agree with the oracle's within normwise
-max|Δ| / max|logits_ref| <= LOGIT_TOL (2 layers) or DEEP_TOL (24 layers), and
-the greedily sampled token ids must be identical.  Both bounds are looser
-than the single-GEMV bound (1e-4) because every step chains ~7 mat-vecs per
-layer plus attention and RMSNorm, whose block reductions add in a different
-order than the reference's sequential loops, and the random-init models
-amplify such differences with depth: their residual stream grows by one to
-two orders of magnitude per layer and their attention scores are large
-enough that the softmax is nearly one-hot, so ulp-level differences in the
-scores move the weights of the other positions.
+max|Δ| / max|logits_ref| <= LOGIT_TOL (2 layers) or DEEP_TOL (full-depth
+models, long contexts), and the greedily sampled token ids must be
+identical.  The models are synth.gen_model's random-init weights (centred,
+~1/sqrt(cols)), whose activations stay O(1) at any depth; the device and the
+oracle then differ only by reduction order and the GEMV's exact integer
+accumulation (measured: at most 9.4e-6 over every test here, Qwen2-0.5B at
+32 + 128 steps 6.0e-6).
 """
 from __future__ import annotations
 
@@ -24,7 +22,7 @@ from conftest import normwise_err
 pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-4
-DEEP_TOL = 1e-3
+DEEP_TOL = 1e-4
 
 SMALL = dict(embed_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=512, vocab_size=600,
              rope_base=1e6, norm_eps=1e-6, tied=False, bias=True)
@@ -141,9 +139,8 @@ def test_long_sequence(rinf, synth, oracle, ctx):
 def test_long_ranges(rinf, synth, oracle, ctx, embed):
     """~600 cached positions over 64 ranges of 10: a wave runs two chunks of
     positions, and the appended slot sits in a later chunk of its range.  At
-    this length a few steps' softmax is nearly one-hot (ulp-level score
-    differences reach 1e-4 in the logits), so the maximum is held to
-    DEEP_TOL and the typical step to 1e-5."""
+    this length the maximum is held to DEEP_TOL and the typical step to
+    1e-5."""
     cfg = dict(SMALL, n_layers=1, embed_dim=embed, hidden_dim=2 * embed)
     dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q8_0", 23, 640)
     prompt = np.random.default_rng(10).integers(0, cfg["vocab_size"], 590)
