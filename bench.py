@@ -61,7 +61,9 @@ def alg_bytes(rinf, dtype, rows, cols):
 
 
 def time_gemv(ctx, torch, mats, dx, dy, steps, warmup):
-    """Three timings of `steps` launches that rotate over `mats`:
+    """Four timings of `steps` launches that rotate over `mats`:
+    c_loop -- wall ms of back-to-back qg_matvec_dev calls issued from C
+              (qg_matvec_dev_repeat), as a compiled caller issues them,
     eager  -- wall ms of back-to-back launches from Python (host-bound if the
               launch call is slower than the kernel),
     graph  -- wall ms of the same launches captured once in a HIP graph
@@ -103,6 +105,18 @@ def time_gemv(ctx, torch, mats, dx, dy, steps, warmup):
     torch.cuda.synchronize()
     graph = g0.elapsed_time(g1) * steps / (reps * n)
 
+    ctx.matvec_repeat(mats, dx, dy, warmup, ctx.stream)
+    torch.cuda.synchronize()
+    c0, c1 = ev(), ev()
+    c0.record(st)
+    h0 = time.perf_counter()
+    ctx.matvec_repeat(mats, dx, dy, steps, ctx.stream)
+    h1 = time.perf_counter()
+    c1.record(st)
+    torch.cuda.synchronize()
+    c_loop = c0.elapsed_time(c1)
+    log(f"C loop: host enqueue {(h1 - h0) * 1e6 / steps:.2f} us per launch")
+
     evs = [(ev(), ev()) for _ in range(steps)]
     for i, (a, b) in enumerate(evs):
         a.record(st)
@@ -111,7 +125,7 @@ def time_gemv(ctx, torch, mats, dx, dy, steps, warmup):
     torch.cuda.synchronize()
     per = [a.elapsed_time(b) for a, b in evs]
     del g
-    return eager, graph, per
+    return c_loop, eager, graph, per
 
 
 def _cpu_model() -> str:
@@ -302,7 +316,7 @@ def sweep_run(rinf, synth, ctx, torch, rotate_mb=256, max_copies=256, steps=200)
         ms = _event_loop(torch, st, lambda i: mats[i % ncopy].matvec_dev(dx, dy, ctx.stream), n, 20)
         us = ms * 1e3 / n
         B = alg_bytes(rinf, dtype, rows, cols)
-        kind = {0: "generic", 1: "stream", 2: "ring"}.get(mats[0].kernel_kind, "?")
+        kind = {0: "generic", 1: "stream", 2: "ring", 3: "wave"}.get(mats[0].kernel_kind, "?")
         entries.append({"type": tname, "rows": rows, "cols": cols, "us": round(us, 3),
                         "GBs": round(B / us / 1e3, 1), "frac_of_8TBs": round(B / us / 1e3 / PEAK_GBS, 4),
                         "alg_bytes": B, "rotating_bytes": ncopy * nb, "kernel": kind})
@@ -508,21 +522,23 @@ def main():
     raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
     x = synth.gen_x(cols, synth.config_seed(4))
     mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
-    kernel = {1: "qg::gemv_stream", 2: "qg::gemv_ring"}.get(mats[0].kernel_kind, "qg::gemv_generic")
+    kernel = {1: "qg::gemv_stream", 2: "qg::gemv_ring", 3: "qg::gemv_wave"}.get(mats[0].kernel_kind, "qg::gemv_generic")
     dx = torch.from_numpy(x).cuda()
     dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
-    eager_ms, graph_ms, per = time_gemv(ctx, torch, mats, dx, dy, args.steps, args.warmup)
-    wall_ms = min(eager_ms, graph_ms)
+    c_ms, eager_ms, graph_ms, per = time_gemv(ctx, torch, mats, dx, dy, args.steps, args.warmup)
+    wall_ms = min(c_ms, eager_ms, graph_ms)
     ms_step = wall_ms / args.steps
     value = B / (ms_step * 1e-3) / 1e9
     # average launch duration: HIP events on the launch stream around the
-    # back-to-back loops, the faster of eager and graph replay (a profiler's
-    # callbacks inflate the eager one); it includes the gaps between kernels,
-    # so it is an upper bound on rocprofv3's per-kernel average
+    # back-to-back loops, the fastest of the C loop, Python eager and graph
+    # replay (a profiler's callbacks inflate the eager ones); it includes the
+    # gaps between kernels, so it is an upper bound on rocprofv3's per-kernel
+    # average
     kern_ms = wall_ms / args.steps
     achieved = B / (kern_ms * 1e-3) / 1e9
-    log(f"eager {eager_ms / args.steps * 1e3:.2f} us/step, graph {graph_ms / args.steps * 1e3:.2f} us/step")
+    log(f"C loop {c_ms / args.steps * 1e3:.2f} us/step, Python eager {eager_ms / args.steps * 1e3:.2f} us/step, "
+        f"graph {graph_ms / args.steps * 1e3:.2f} us/step")
     log(f"wall {wall_ms:.3f} ms / {args.steps} launches = {ms_step * 1e3:.2f} us/step -> "
         f"{value:.1f} GB/s; kernel {kern_ms * 1e3:.2f} us -> {achieved:.1f} GB/s "
         f"({achieved / PEAK_GBS:.1%} of 8 TB/s); isolated launches with event pairs: median "
@@ -590,7 +606,8 @@ def main():
         "data": "synthetic (seeded GGUF blocks: f16 scales U[1e-3,2e-2], uniform code bytes; x ~ N(0,1))",
         "config": {"workload": workload, "type": args.type, "rows": rows, "cols": cols,
                    "bytes_per_launch": B, "rotating_copies": ncopy,
-                   "launch": "hip_graph" if graph_ms <= eager_ms else "eager",
+                   "launch": {c_ms: "c_loop", eager_ms: "eager", graph_ms: "hip_graph"}[wall_ms],
+                   "us_per_step_c_loop": round(c_ms / args.steps * 1e3, 3),
                    "us_per_step_eager": round(eager_ms / args.steps * 1e3, 3),
                    "us_per_step_graph": round(graph_ms / args.steps * 1e3, 3),
                    "frac_of_8TBs_wall": round(value / PEAK_GBS, 4)},

@@ -76,8 +76,10 @@ int qg_mat_info(const qg_mat *mat, uint32_t *ggml_type, size_t *rows, size_t *co
 /* Kernel choice fixed at upload: 1 = stream kernel (fast path), 2 = the
  * stream kernel family with the LDS-ring kernel for the plain mat-vec
  * (repacked Q8_0 / Q4_K / Q5_K / Q6_K rows with several-wave teams that fit
- * its ring, e.g. the 14336- and 18944-wide down projections), 0 = generic
- * per-element kernel
+ * its ring, e.g. the 14336- and 18944-wide down projections), 3 = the stream
+ * kernel family with the wave-private column kernel for the plain mat-vec
+ * (repacked Q4_K rows of 12288 or 14336 columns, at least 16 rows per compute
+ * unit), 0 = generic per-element kernel
  * (cols % 32 != 0 and other shapes the planner rejects). */
 int qg_mat_kernel_kind(const qg_mat *mat);
 
@@ -179,6 +181,14 @@ int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_o
  * full-grid coalesced read, writing at most d_out[0].  Its duration is the
  * streaming ceiling the GEMV's HBM rate is compared with at the same size. */
 int qg_probe_stream_read(qg_ctx *ctx, const void *d_buf, size_t nbytes, uint32_t *d_out, void *stream);
+
+/* Measurement only, no counterpart in the reference: n_launches calls of
+ * qg_matvec_dev(ctx, mats[i % n_mats], d_x, d_y, stream), i = 0, 1, ..., issued
+ * back to back from compiled code, as a Rust caller issues its mat-vecs
+ * (a Python loop over the same calls is bound by its own per-call cost when a
+ * launch takes less time than the interpreter).  Stops at the first error. */
+int qg_matvec_dev_repeat(qg_ctx *ctx, const qg_mat *const *mats, size_t n_mats, const float *d_x, float *d_y,
+                         size_t n_launches, void *stream);
 
 /* Waits for all work on the context's stream. */
 int qg_synchronize(qg_ctx *ctx);

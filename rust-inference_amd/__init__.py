@@ -80,6 +80,7 @@ _SIGS = {
     "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
     "qg_gpu_invalidate": (ctypes.c_int, [_P, _P]),
     "qg_probe_stream_read": (ctypes.c_int, [_P, _P, _SZ, _P, _P]),
+    "qg_matvec_dev_repeat": (ctypes.c_int, [_P, _P, _SZ, _P, _P, _SZ, _P]),
     "qg_test_fail_allocations": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
     "qg_gpu_mat_vec_mul": (ctypes.c_int, [_P, _P, _SZ, _U32, _P, _P, _SZ, _SZ]),
@@ -277,6 +278,14 @@ class GpuContext:
         rc = self.lib.qg_probe_stream_read(self.h, _ptr(d_buf), int(nbytes), _ptr(d_out),
                                            ctypes.c_void_p(stream) if stream else None)
         self.check(rc, "qg_probe_stream_read")
+
+    def matvec_repeat(self, mats, d_x, d_y, n_launches: int, stream=None):
+        """n_launches qg_matvec_dev calls cycling over mats, issued from C
+        (qg_matvec_dev_repeat)."""
+        arr = (ctypes.c_void_p * len(mats))(*[m.h for m in mats])
+        rc = self.lib.qg_matvec_dev_repeat(self.h, arr, len(mats), _ptr(d_x), _ptr(d_y), int(n_launches),
+                                           ctypes.c_void_p(stream) if stream else None)
+        self.check(rc, "qg_matvec_dev_repeat")
 
     def invalidate(self, weight_data):
         """Drop the device copies mat_vec_mul keeps for this host buffer (qg_gpu_invalidate)."""

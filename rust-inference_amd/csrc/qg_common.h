@@ -40,7 +40,7 @@ constexpr size_t kTailPad = 512;
 
 // How a matrix is mat-vec'd; fixed at upload time.
 struct Plan {
-    int kind;              // 0 = generic per-element kernel, 1 = stream kernel
+    int kind;              // 0 = generic per-element kernel, 1 = stream kernel family
     uint32_t g;            // rows per row group
     uint32_t n_groups;     // ceil(rows / g)
     uint32_t ni;           // items (64- or 32-element units) per row group
@@ -64,6 +64,10 @@ struct Plan {
     // plain mat-vec through the LDS ring kernel (gemv_ring) where it applies:
     const void *fn_ring;   // nullptr otherwise
     uint32_t ring_grid, ring_block, ring_per, ring_lds, ring_slot2;
+    // plain mat-vec through the wave-private column kernel (gemv_wave, repacked
+    // Q4_K rows of 96 or 112 items) where it applies; it takes precedence
+    const void *fn_wave;   // nullptr otherwise
+    uint32_t wave_grid;
 };
 
 }  // namespace qg

@@ -451,6 +451,7 @@ int qg_mat_info(const qg_mat *mat, uint32_t *type, size_t *rows, size_t *cols, s
 int qg_mat_kernel_kind(const qg_mat *mat)
 {
     if (!mat) return -1;
+    if (mat->plan.kind == 1 && mat->plan.fn_wave) return 3;
     return mat->plan.kind == 1 && mat->plan.fn_ring ? 2 : mat->plan.kind;
 }
 
@@ -676,6 +677,17 @@ int qg_probe_stream_read(qg_ctx *ctx, const void *d_buf, size_t nbytes, uint32_t
     QG_HIP(ctx, hipSetDevice(ctx->device));
     if (qg::launch_stream_read(d_buf, nbytes, d_out, (ihipStream_t *)pick(ctx, stream)))
         return fail(ctx, QG_ERR_HIP, "stream read launch", hipGetLastError());
+    return QG_OK;
+}
+
+int qg_matvec_dev_repeat(qg_ctx *ctx, const qg_mat *const *mats, size_t n_mats, const float *d_x, float *d_y,
+                         size_t n_launches, void *stream)
+{
+    if (!ctx || (n_launches && (!mats || n_mats == 0))) return QG_ERR_INVALID_ARG;
+    for (size_t i = 0; i < n_launches; i++) {
+        const int rc = qg_matvec_dev(ctx, mats[i % n_mats], d_x, d_y, stream);
+        if (rc) return rc;
+    }
     return QG_OK;
 }
 

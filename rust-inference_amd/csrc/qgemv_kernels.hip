@@ -1695,6 +1695,207 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
     if (wave == 0) QG_TL_WRITE(0);
 }
 
+// ------------------------------------------- wave-private column streaming
+//
+// Plain mat-vec of repacked Q4_K rows of 12 or 14 items per eighth of a row
+// (cols 12288 / 14336): a workgroup of eight waves owns 16 consecutive rows,
+// and wave w owns column chunk w (CJ items, CJ * 128 columns) of all 16.
+// Every wave moves its own bytes into its own LDS region with
+// global_load_lds_dwordx4 and waits on its own vmcnt only -- no workgroup
+// barrier until the final sum -- in steps of 4 rows, one step in flight
+// (the next step is requested the moment a step lands; more bytes in flight
+// per CU measured slower):
+//   * x: the wave's 4*CJ segments of 32 elements, one 128-byte line per
+//     lane, copied with a rotation (slot p of line L holds piece (p - L) mod 8)
+//     so that the lane's own 8 reads of its line are free of bank conflicts;
+//     lane (jj, r) = 4*jj + r converts segment r of item jj in registers
+//     (stage_seg32, the same arithmetic as stage_planes16) and the four lanes
+//     of a quad exchange their segments with DPP quad broadcasts, so each lane
+//     holds the x slice of item jj (the 108 registers of XP<4, 32>);
+//   * weights: the wave's part of a row is the item's block headers and its
+//     four 16-byte pieces per item, 72 * CJ bytes gathered from the repacked
+//     row by one copy instruction (lane l fetches piece l; the per-lane offset
+//     within a row is computed once); row i of the workgroup lands in slot i
+//     of the region (slot stride 1088 == 64 mod 256 bytes: the 16 lanes of a
+//     read pass see 16 different bank groups);
+//   * lane (jj, r) computes item jj of row 4s + r with Item<T_Q4_K>::compute_sum
+//     (per item exactly the gemv_stream arithmetic), the 14 items of a row in
+//     a wave are summed with two DPP row shifts, and the 8 waves' sums of a
+//     row are added in fixed order after the one workgroup barrier.
+// The copies are issued from inline asm: the compiler does not see them, so
+// it adds no vmcnt(0) before this wave's later LDS reads (with the builtin it
+// waits for every outstanding copy before each read).  The waits are exact
+// immediates.  x lands in the slots of rows 8..15, which are requested only
+// after the x reads (lgkmcnt(0)).
+constexpr uint32_t kWaveRows = 16;          // rows per workgroup (4 steps of 4)
+constexpr uint32_t kWaveSlot = 1088;        // LDS bytes per row slot
+constexpr uint32_t kWaveLds = 8u * kWaveRows * kWaveSlot + kWaveRows * 32u * 4u;
+
+// 16 bytes per lane from gp into LDS at lds_addr + 16 * lane (wave-uniform
+// lds_addr), invisible to the compiler's wait bookkeeping; M0 needs one wait
+// state before the copy reads it
+__device__ __forceinline__ void lds_dma16_asm(const void *gp, uint32_t lds_addr)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds_addr)
+                 : "memory", "m0");
+}
+template <uint32_t N> __device__ __forceinline__ void wait_vm_n()
+{
+    static_assert(N < 64, "vmcnt holds 63");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One 32-element segment converted in one lane, with the arithmetic and the
+// summation trees of stage_planes16 for its two halves: P = the three digit
+// planes (8 dwords each), ik = 1/k, sx = sum x, sy = sum Y.
+__device__ __forceinline__ void stage_seg32(const float4 (&v)[8], uint32_t (&P)[3][8], float &ik, float &sx, float &sy)
+{
+    uint32_t mb = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) mb = max(mb, __float_as_uint(absmax4(v[i])));
+    const float m = __uint_as_float(mb);
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) t[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float s0 = (t[0] + t[1]) + (t[2] + t[3]), s1 = (t[4] + t[5]) + (t[6] + t[7]);
+    const bool bad = !__builtin_isfinite(s0 + s1);
+    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.2676506e30f) : 0.f;
+    ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
+    const int off = 0x8080 - kMagicBits;
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t Y0 = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].x, k, kMagic)) + off);
+        const uint32_t Y1 = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].y, k, kMagic)) + off);
+        const uint32_t Y2 = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].z, k, kMagic)) + off);
+        const uint32_t Y3 = (uint32_t)(__float_as_int(__builtin_fmaf(v[i].w, k, kMagic)) + off);
+        f[i] = (float)((int)((Y0 + Y1) + (Y2 + Y3)) - 4 * 0x8080);
+        const uint32_t P01 = __builtin_amdgcn_perm(Y1, Y0, 0x05010400u);
+        const uint32_t P23 = __builtin_amdgcn_perm(Y3, Y2, 0x05010400u);
+        const uint32_t Q01 = __builtin_amdgcn_perm(Y1, Y0, 0x0C0C0602u);
+        const uint32_t Q23 = __builtin_amdgcn_perm(Y3, Y2, 0x0C0C0602u);
+        P[0][i] = __builtin_amdgcn_perm(P23, P01, 0x05040100u) ^ 0x80808080u;
+        P[1][i] = __builtin_amdgcn_perm(P23, P01, 0x07060302u) ^ 0x80808080u;
+        P[2][i] = __builtin_amdgcn_perm(Q23, Q01, 0x05040100u);
+    }
+    sx = s0 + s1;
+    sy = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+}
+
+// lane i of every quad receives lane S of its quad
+template <int S> __device__ __forceinline__ uint32_t quad_bcast(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, S | (S << 2) | (S << 4) | (S << 6), 0xF, 0xF, false);
+}
+template <int S> __device__ __forceinline__ float quad_bcastf(float v)
+{
+    return __uint_as_float(quad_bcast<S>(__float_as_uint(v)));
+}
+
+template <uint32_t CJ>
+__global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
+{
+    using I = Item<T_Q4_K>;
+    constexpr uint32_t NSTEP = kWaveRows / 4u, SLOT = kWaveSlot, REG = kWaveRows * SLOT;
+    constexpr uint32_t NPC = 72u * CJ / 16u;                 // 16-byte pieces of a wave's row part
+    constexpr uint32_t XINST = CJ / 2u;                      // x: 4 CJ lines of 128 bytes, 8 per copy
+    constexpr uint32_t XROW = kWaveRows - 8u;                // x lands in slots XROW..
+    static_assert(CJ % 2 == 0 && NPC <= 64 && 4 * CJ <= 64 && XINST * 1024u <= 8u * SLOT, "shape");
+    extern __shared__ float4 xl4[];
+    uint8_t *lds = (uint8_t *)xl4;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t row0 = blockIdx.x * kWaveRows;
+    uint8_t *reg = lds + w * REG;
+    const uint32_t reg0 = lds0 + w * REG;
+    float *red = (float *)(lds + 8u * REG);                  // [kWaveRows][8 waves x 4 DPP rows]
+    // x lines L = 8k + lane/8 (item L/4, segment L%4 of the wave's chunk)
+    const float *xw = a.x + w * CJ * 128u;
+#pragma unroll
+    for (uint32_t k = 0; k < XINST; k++) {
+        const uint32_t L = 8u * k + (lane >> 3), p = lane & 7u;
+        lds_dma16_asm(xw + 32u * L + 4u * ((p - L) & 7u), reg0 + XROW * SLOT + 1024u * k);
+    }
+    // this lane's piece of a row part: the CJ/2 headers, then pieces k = 0..3
+    // of the CJ items (repacked row: headers, then piece k of item it at
+    // 16 * (ni/2) + (k * ni + it) * 16)
+    uint32_t loff;
+    {
+        const uint32_t l = lane < NPC ? lane : NPC - 1u;
+        const uint32_t m = l - CJ / 2u, k = m / CJ, t = m - k * CJ;
+        loff = l < CJ / 2u ? (w * (CJ / 2u) + l) * 16u : (a.ni / 2u) * 16u + (k * a.ni + w * CJ + t) * 16u;
+    }
+    auto issue = [&](uint32_t i) {
+        const uint32_t gr = min(row0 + i, a.rows - 1u);
+        lds_dma16_asm(a.w + (size_t)gr * a.group_bytes + loff, reg0 + i * SLOT);
+    };
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; i++) issue(i);
+    wait_vm_n<4u>();                                         // x landed
+    const uint32_t jj = lane >> 2, r = lane & 3u;
+    const bool active = jj < CJ && w * CJ + jj < a.ni;
+    const uint32_t it = jj < CJ ? jj : 0u;
+    XP<4, 32> xs;
+    {
+        float4 v[8];
+        const uint8_t *xl = reg + XROW * SLOT + 128u * (lane < 4u * CJ ? lane : 0u);
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) v[k] = *(const float4 *)(xl + 16u * ((k + lane) & 7u));
+        uint32_t P[3][8];
+        float ik, sx, sy;
+        stage_seg32(v, P, ik, sx, sy);
+#pragma unroll
+        for (int c = 0; c < 3; c++)
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                xs.p[0][c][q] = quad_bcast<0>(P[c][q]);
+                xs.p[1][c][q] = quad_bcast<1>(P[c][q]);
+                xs.p[2][c][q] = quad_bcast<2>(P[c][q]);
+                xs.p[3][c][q] = quad_bcast<3>(P[c][q]);
+            }
+        xs.ik[0] = quad_bcastf<0>(ik); xs.ik[1] = quad_bcastf<1>(ik);
+        xs.ik[2] = quad_bcastf<2>(ik); xs.ik[3] = quad_bcastf<3>(ik);
+        xs.sx[0] = quad_bcastf<0>(sx); xs.sx[1] = quad_bcastf<1>(sx);
+        xs.sx[2] = quad_bcastf<2>(sx); xs.sx[3] = quad_bcastf<3>(sx);
+        xs.sy[0] = quad_bcastf<0>(sy); xs.sy[1] = quad_bcastf<1>(sy);
+        xs.sy[2] = quad_bcastf<2>(sy); xs.sy[3] = quad_bcastf<3>(sy);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // x read before rows 8.. overwrite it
+    }
+#pragma unroll 1
+    for (uint32_t s = 0; s < NSTEP; s++) {
+        wait_vm_n<0u>();                                     // step s landed
+        if (s + 1u < NSTEP) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) issue(4u * (s + 1u) + i);
+        }
+        const uint8_t *grp = reg + (4u * s + r) * SLOT;
+        uint32_t raw[I::NRAW];
+        {
+            const uint4 h = *(const uint4 *)(grp + (it >> 1) * 16u);
+            raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+            const uint8_t *q = grp + (CJ / 2u) * 16u + it * 16u;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint4 v = *(const uint4 *)(q + k * CJ * 16u);
+                raw[4 + 4 * k] = v.x; raw[5 + 4 * k] = v.y; raw[6 + 4 * k] = v.z; raw[7 + 4 * k] = v.w;
+            }
+        }
+        float t = I::compute_sum(raw, xs, it);
+        t = active ? t : 0.f;
+        t += dpp<0x114>(t);                                  // row_shr:4
+        t += dpp<0x118>(t);                                  // row_shr:8: lanes 12..15 hold rows r = 0..3
+        if ((lane & 15u) >= 12u) red[(4u * s + r) * 32u + w * 4u + (lane >> 4)] = t;
+    }
+    lds_barrier();
+    if (w == 0 && lane < kWaveRows && row0 + lane < a.rows) {
+        float v = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 32u; i++) v += red[lane * 32u + i];
+        store_y(a.y + row0 + lane, v);
+    }
+}
+
 // ------------------------------------------------------------ planning
 
 static uint32_t gcd_u(uint64_t a, uint64_t b)
@@ -1875,6 +2076,17 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
             }
         }
     }
+    // the wave-private column kernel for repacked Q4_K rows of 8 * CJ items,
+    // CJ = 12 or 14, when its 16-row workgroups cover every CU at least once
+    p->fn_wave = nullptr;
+    if constexpr (T == T_Q4_K) {
+        const uint64_t wg = (rows + kWaveRows - 1) / kWaveRows;
+        if (rp && g == 1 && wg >= ncu && kWaveLds <= (uint32_t)max_lds_bytes() && wg <= 0x7FFFFFFFull) {
+            if (ni == 8u * 14u) p->fn_wave = (const void *)gemv_wave<14>;
+            if (ni == 8u * 12u) p->fn_wave = (const void *)gemv_wave<12>;
+            p->wave_grid = (uint32_t)wg;
+        }
+    }
 }
 
 int make_plan(uint32_t type, size_t rows, size_t cols, int n_cu, Plan *p, bool rp)
@@ -2014,6 +2226,8 @@ int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, s
     if (p.kind != 1 || !p.fn) return launch_gemv_generic(type, w, rows, cols, x, y, stream);
     StreamArgs a = stream_args(p, w, nbytes, rows, cols, x, y);
     void *args[] = {&a};
+    if (p.fn_wave)
+        return hipLaunchKernel(p.fn_wave, dim3(p.wave_grid), dim3(512), args, kWaveLds, st) == hipSuccess ? 0 : -2;
     if (p.fn_ring) {
         a.n_teams = (p.ring_block / 64u - 2u) / p.wpt * p.ring_grid;
         a.per_team = p.ring_per;
