@@ -117,6 +117,19 @@ int qg_matvec_norm_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_xa, const 
 int qg_matvec_norm_glu_dev(qg_ctx *ctx, const qg_mat *gu, const float *d_xa, const float *d_xb,
                            const float *d_nw, float eps, float *d_sum_out, float *d_h, void *stream);
 
+/* No counterpart in the reference: qg_matvec_norm_glu_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and
+ * results; it calls no hipMalloc/hipFree.  Where its path needs scratch (the
+ * normalised x and the [gate; up] outputs of the unfused path), it uses a
+ * static 1 MiB device array that each GPU holds for the life of the process:
+ * QG_ERR_SHAPE when round_up(cols, 64) + rows > 262144 floats.  All calls on
+ * one GPU share that array and it keeps the last call's contents, so calls
+ * that overlap on one GPU (other streams, other contexts, other host
+ * threads) race; nothing in it needs to start at zero. */
+int qg_matvec_norm_glu_dev_noalloc(qg_ctx *ctx, const qg_mat *gu, const float *d_xa, const float *d_xb,
+                                   const float *d_nw, float eps, float *d_sum_out, float *d_h, void *stream);
+
 /* One matrix whose rows are those of parts[0], parts[1], ... in order (the
  * same GGML type and cols; every part but the last a whole number of blocks),
  * as model.rs keeps wq/wk/wv and ffn_gate/ffn_up as separate

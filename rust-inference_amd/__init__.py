@@ -77,6 +77,7 @@ _SIGS = {
     "qg_matvec_norm_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_matvec_silu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, _P]),
     "qg_matvec_norm_glu_dev": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
+    "qg_matvec_norm_glu_dev_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
     "qg_gpu_invalidate": (ctypes.c_int, [_P, _P]),
     "qg_probe_stream_read": (ctypes.c_int, [_P, _P, _SZ, _P, _P]),
@@ -338,6 +339,16 @@ class DeviceMatrix:
                                                  _ptr(d_sum_out) if d_sum_out is not None else None,
                                                  _ptr(d_h), ctypes.c_void_p(stream) if stream else None)
         self.ctx.check(rc, "qg_matvec_norm_glu_dev")
+
+    def matvec_norm_glu_dev_noalloc(self, d_xa, d_xb, d_nw, eps, d_h, d_sum_out=None, stream=None):
+        """matvec_norm_glu_dev through qg_matvec_norm_glu_dev_noalloc (no device
+        allocation; the per-GPU static scratch array)."""
+        rc = self.ctx.lib.qg_matvec_norm_glu_dev_noalloc(self.ctx.h, self.h, _ptr(d_xa),
+                                                         _ptr(d_xb) if d_xb is not None else None, _ptr(d_nw),
+                                                         float(eps),
+                                                         _ptr(d_sum_out) if d_sum_out is not None else None,
+                                                         _ptr(d_h), ctypes.c_void_p(stream) if stream else None)
+        self.ctx.check(rc, "qg_matvec_norm_glu_dev_noalloc")
 
     def matvec_silu_dev(self, d_g, d_u, d_y, stream=None):
         """y = W · (silu(g) * u); torch device tensors (float32)."""

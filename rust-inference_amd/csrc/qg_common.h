@@ -121,6 +121,11 @@ int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t c
 int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
                               float *out, ihipStream_t *stream);
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
+// Floats of the per-GPU static scratch array (1 MiB) of the no-allocation
+// entry point, and its device address on `device` (made current); -2 if
+// the runtime cannot resolve it.
+constexpr size_t kNoAllocScratchFloats = 262144;
+int scratch_address(int device, float **ptr);
 int launch_stream_read(const void *buf, size_t nbytes, uint32_t *out, ihipStream_t *stream);
 // out = silu(g) * u elementwise
 int launch_silu_mul(const float *g, const float *u, float *out, size_t n, ihipStream_t *stream);

@@ -44,6 +44,9 @@ struct qg_ctx {
     size_t d_norm_cap = 0;
     float *d_glu = nullptr;                 // gate and up outputs of qg_matvec_norm_glu_dev's unfused path
     size_t d_glu_cap = 0;
+    // device address of this GPU's static scratch array (qg_matvec_norm_glu_dev_noalloc),
+    // resolved once in qg_init; NULL if the runtime could not resolve it
+    float *d_static_scratch = nullptr;
     std::set<qg_mat *> mats;
     std::set<qg_model *> models;            // decode-step engines on this context
     // qg_gpu_mat_vec_mul's device copies, keyed by (host address, bytes, type,

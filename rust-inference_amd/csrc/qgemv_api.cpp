@@ -361,6 +361,13 @@ int qg_init(int device, qg_ctx **out)
         return QG_ERR_HIP;
     }
     ctx->n_cu = prop.multiProcessorCount;
+    // the static scratch array's address on this device (each GPU holds its
+    // own copy at its own address); a failure only disables the no-allocation
+    // entry point
+    if (qg::scratch_address(device, &ctx->d_static_scratch) != 0) {
+        ctx->d_static_scratch = nullptr;
+        (void)hipGetLastError();
+    }
     // default-priority stream (hipStreamCreateWithFlags keeps the default priority)
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
@@ -530,6 +537,32 @@ int qg_mat_stack(qg_ctx *ctx, qg_mat *const *parts, int n_parts, qg_mat **out)
         if (rc) return rc;
     }
     return qg_stack_mats(ctx, parts, n_parts, out);
+}
+
+int qg_matvec_norm_glu_dev_noalloc(qg_ctx *ctx, const qg_mat *gu, const float *d_xa, const float *d_xb,
+                                   const float *d_nw, float eps, float *d_sum_out, float *d_h, void *stream)
+{
+    int rc = check_mat(ctx, gu);
+    if (rc) return rc;
+    if (gu->rows % 2 != 0) return fail(ctx, QG_ERR_SHAPE, "[gate; up] matrix with an odd row count");
+    if (gu->rows == 0 && !d_sum_out) return QG_OK;
+    const size_t n = gu->cols;
+    if (!d_h || (n > 0 && (!d_xa || !d_nw))) return fail(ctx, QG_ERR_INVALID_ARG, "xa, nw or h is NULL");
+    auto a4 = [](const void *p) { return ((uintptr_t)p & 3u) == 0; };
+    if (!a4(d_xa) || !a4(d_xb) || !a4(d_nw) || !a4(d_sum_out) || !a4(d_h))
+        return fail(ctx, QG_ERR_INVALID_ARG, "vectors not 4-byte aligned");
+    auto overlap = [n](const float *p, const float *q) { return p && q && p < q + n && q < p + n; };
+    if (overlap(d_sum_out, d_xa) || overlap(d_sum_out, d_xb))
+        return fail(ctx, QG_ERR_INVALID_ARG, "sum_out overlaps xa or xb");
+    // the normalised x (cols floats, rounded up to 64 so the [gate; up]
+    // outputs start 256-byte aligned), then the [gate; up] outputs (rows floats)
+    const size_t xn = (n + 63) / 64 * 64;
+    if (xn + gu->rows > qg::kNoAllocScratchFloats)
+        return fail(ctx, QG_ERR_SHAPE, "cols + rows exceed the no-allocation scratch (262144 floats, 1 MiB)");
+    if (!ctx->d_static_scratch) return fail(ctx, QG_ERR_HIP, "static scratch address not resolved at qg_init");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    float *s = ctx->d_static_scratch;
+    return qg_norm_glu_matvec(ctx, gu, d_xa, d_xb, d_nw, eps, d_sum_out, d_h, s + xn, s, pick(ctx, stream));
 }
 
 int qg_matvec_silu_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_g, const float *d_u, float *d_y,

@@ -1896,6 +1896,25 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
     }
 }
 
+// ------------------------------------------------ no-allocation scratch
+//
+// The device scratch of qg_matvec_norm_glu_dev_noalloc: the normalised x and
+// the [gate; up] outputs of its unfused path, kNoAllocScratchFloats floats
+// per GPU for the life of the process.  Host code never passes this array's
+// name to a kernel (on the host it is only a stand-in for the symbol): it
+// passes the device address that scratch_address returns.
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+int scratch_address(int device, float **ptr)
+{
+    *ptr = nullptr;
+    if (hipSetDevice(device) != hipSuccess) return -2;
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -2;
+    *ptr = (float *)p;
+    return 0;
+}
+
 // ------------------------------------------------------------ planning
 
 static uint32_t gcd_u(uint64_t a, uint64_t b)
