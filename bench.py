@@ -187,9 +187,11 @@ def cpu_baseline(oracle, raw, dtype, rows, cols, x, seconds, nbytes):
 def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new=None, cfg_index=3):
     """BASELINE.json configs[3] (by default): greedy decode of a random-init
     model of `arch` in the `mix` GGUF mix, all GEMVs on this GPU.  The prompt
-    is processed as the reference does it, one token at a time
-    (src/model.rs:357-363), then `n_new` greedy steps with the reference's
-    repetition penalty 1.1 over the last 64 tokens."""
+    goes through the batched prefill (chunks of up to 64 tokens per layer,
+    MFMA GEMMs; qg_model_prefill) where the mix has it, then `n_new` greedy
+    steps with the reference's repetition penalty 1.1 over the last 64
+    tokens; the prompt is then timed again one token at a time, as the
+    reference feeds it (src/model.rs:361-365)."""
     import numpy as np
     arch = arch or args.decode
     mix = mix or args.decode_mix
@@ -223,6 +225,8 @@ def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new
     prompt = np.random.default_rng(seed).integers(0, cfg["vocab_size"], n_prompt)
     dev.generate(prompt[:4], 4)                           # warm-up (kernels, clocks)
     toks, pre_s, dec_s = dev.generate(prompt, n_new)
+    dev.use_batched_prefill(False)
+    _, pre_tt_s, _ = dev.generate(prompt, 1)
     dev.close()
     if shared is not None:
         shared.free()
@@ -235,11 +239,12 @@ def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new
     per_tok = wbytes + kv_bytes
     log(f"decode {arch} {mix}: {tok_s:.1f} tok/s ({dec_s * 1e3 / n_new:.3f} ms/token), "
         f"{per_tok / 1e9:.3f} GB/token -> {per_tok * tok_s / 1e9:.1f} GB/s; prefill "
-        f"{n_prompt / pre_s:.1f} tok/s; set-up {setup_s:.1f} s")
+        f"{n_prompt / pre_s:.1f} tok/s (token by token {n_prompt / pre_tt_s:.1f}); set-up {setup_s:.1f} s")
     return {"model": f"{arch} ({mix}, random init, synthetic)",
             "prompt_tokens": n_prompt, "decode_tokens": n_new,
             "tok_s": round(tok_s, 2), "ms_per_token": round(dec_s * 1e3 / n_new, 4),
             "prefill_tok_s": round(n_prompt / pre_s, 2),
+            "prefill_token_by_token_tok_s": round(n_prompt / pre_tt_s, 2),
             "bytes_per_token": int(per_tok), "weight_bytes_per_token": int(wbytes),
             "achieved_GBs": round(per_tok * tok_s / 1e9, 2),
             "frac_of_8TBs": round(per_tok * tok_s / 8e12, 4),

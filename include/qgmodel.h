@@ -83,6 +83,22 @@ int qg_model_seq_len(const qg_model *m, size_t *len);
  * the caches are full (kv_cache.rs:54-59 panics there) or token >= vocab. */
 int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits);
 
+/* The prompt loop of Model::generate (src/model.rs:361-365): n forward passes
+ * of tokens[0..n) at positions seq, seq + 1, ... (seq = the positions already
+ * cached), leaving the caches and the device logits as those n calls of
+ * qg_model_forward would -- the logits are the last token's.  Chunks of up to
+ * 64 tokens go through each layer together, every projection one int8 MFMA
+ * GEMM over the tokens' fixed-point x (batched prefill), when every layer
+ * matrix is Q4_K, Q5_K, Q6_K or Q8_0 with cols % 32 == 0; otherwise, or after
+ * qg_model_use_batched_prefill(m, 0), one forward pass per token.  `logits`,
+ * if not NULL, receives vocab_size floats (host memory).  QG_ERR_SHAPE when
+ * the tokens would not fit the caches or a token >= vocab. */
+int qg_model_prefill(qg_model *m, const uint32_t *tokens, size_t n, float *logits);
+/* No counterpart in the reference: batched prefill in qg_model_prefill and
+ * qg_model_generate where it applies (enable != 0, the default), or one
+ * forward pass per prompt token (enable == 0). */
+int qg_model_use_batched_prefill(qg_model *m, int enable);
+
 /* Greedy Sampler::sample on the device logits of the last forward:
  * repetition penalty over `recent` (the last `window` entries, applied in
  * order, sampler.rs:109-127) then argmax (math.rs:328-339).  Modifies the
@@ -91,7 +107,7 @@ int qg_model_sample_greedy(qg_model *m, const uint32_t *recent, size_t n_recent,
                            size_t window, uint32_t *token);
 
 /* Model::generate's loop (src/model.rs:357-440) without the tokenizer and
- * without stop tokens: forward over the prompt, then n_new times sample
+ * without stop tokens: the prompt as in qg_model_prefill, then n_new times sample
  * (over the last 64 tokens, as model.rs:370-374 passes them) + forward.
  * out_tokens receives the n_new sampled tokens.  *prefill_s / *decode_s (if
  * not NULL) receive the wall seconds of the two phases. */

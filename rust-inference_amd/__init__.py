@@ -123,6 +123,8 @@ _SIGS = {
     "qg_model_reset": (ctypes.c_int, [_P]),
     "qg_model_seq_len": (ctypes.c_int, [_P, ctypes.POINTER(_SZ)]),
     "qg_model_forward": (ctypes.c_int, [_P, _U32, _U32, _P]),
+    "qg_model_prefill": (ctypes.c_int, [_P, _P, _SZ, _P]),
+    "qg_model_use_batched_prefill": (ctypes.c_int, [_P, ctypes.c_int]),
     "qg_model_sample_greedy": (ctypes.c_int, [_P, _P, _SZ, ctypes.c_float, _SZ, ctypes.POINTER(_U32)]),
     "qg_model_generate": (ctypes.c_int, [_P, _P, _SZ, _SZ, ctypes.c_float, _SZ, _P,
                                          ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
@@ -562,6 +564,18 @@ class DeviceModel:
         n = _SZ()
         self.ctx.check(self.ctx.lib.qg_model_seq_len(self.h, ctypes.byref(n)), "qg_model_seq_len")
         return n.value
+
+    def prefill(self, tokens, logits=None):
+        """qg_model_prefill: the prompt loop at the cached positions; logits
+        (numpy f32 [vocab], optional) receives the last token's."""
+        import numpy as np
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        self.ctx.check(self.ctx.lib.qg_model_prefill(self.h, _ptr(t) if len(t) else None, len(t), _ptr(logits)),
+                       "qg_model_prefill")
+
+    def use_batched_prefill(self, enable: bool):
+        self.ctx.check(self.ctx.lib.qg_model_use_batched_prefill(self.h, int(bool(enable))),
+                       "qg_model_use_batched_prefill")
 
     def forward(self, token: int, pos: int, logits=None):
         """logits: numpy float32[vocab] receiving the step's logits, or None."""

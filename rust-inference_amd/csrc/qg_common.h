@@ -121,6 +121,48 @@ int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t c
 int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
                               float *out, ihipStream_t *stream);
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
+// Batched prefill (qg_prefill.hip): tokens per chunk, supported matrix types,
+// and the launchers of its kernels (0 = launched, -1 = shape not supported,
+// -2 = launch failure).  x of every token as three bf16 pieces xp[c][t][i]
+// (c = 0..2, piece stride ntok * n) and records rec[(4 g + f) * 64 + t] per
+// 32-element segment g (f = 0: sum x, 1: sum x[0..16), 2: sum x[16..32)).
+// GEMM outputs are K-split: slice s of a result lives sstride floats after
+// slice 0, and its consumer sums the slices.
+constexpr uint32_t kPfMaxTokens = 64;
+bool prefill_type_supported(uint32_t type);
+// one matrix of a grouped prefill GEMM: y[t * ldy + r] (+ s * sstride)
+struct PfMat {
+    uint32_t type;
+    const uint8_t *w;
+    size_t rows;
+    float *y;
+};
+uint32_t pf_tiles(size_t rows);
+// slices of the K split of a GEMM over `tiles` row tiles and nseg sub-blocks
+uint32_t pf_split(uint32_t tiles, uint32_t nseg);
+// 1..3 matrices (16-byte aligned) of `cols` columns over the same x, K split
+// into `slices` slices (1 .. cols / 32; pf_split of the group's row tiles)
+// that every matrix writes, empty or not; one launch per run of one type
+int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *xp, const float *rec, uint32_t ntok,
+                   uint32_t ldy, uint32_t slices, size_t sstride, ihipStream_t *stream);
+// x = sum of the na slices of a (nb of b); mode 0: x = a; 1: x =
+// rmsnorm(a + b) * nw (b may be NULL; sum_out, if not NULL, receives a + b
+// and must not alias a or b); 2: x = silu(a) * b.  Rows of lda floats.
+int launch_pf_planes(const float *a, uint32_t na, const float *b, uint32_t nb, size_t sstride, float *sum_out,
+                     const float *nw, float eps, size_t n, size_t lda, int mode, uint16_t *xp, float *rec,
+                     uint32_t ntok, ihipStream_t *stream);
+// out[i] = sum of the ns slices of x[i], i < n
+int launch_pf_sum(const float *x, uint32_t ns, size_t sstride, size_t n, float *out, ihipStream_t *stream);
+int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *bq, const float *bk,
+                       const float *bv, float *kc, float *vc, const float *cos_t, const float *sin_t, uint32_t q_dim,
+                       uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0, uint32_t ntok,
+                       ihipStream_t *stream);
+int launch_pf_attention(const float *qkv, uint32_t ldq, const float *kc, const float *vc, float *out, uint32_t n_heads,
+                        uint32_t hd, uint32_t kv_dim, uint32_t n_rep, float scale, uint32_t slot0, uint32_t ntok,
+                        size_t lds, ihipStream_t *stream);
+// rows d_rows[0..n) of a matrix, dequantized into out + i * ldo
+int launch_dequantize_rows_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_rows,
+                               uint32_t n, float *out, size_t ldo, ihipStream_t *stream);
 // Floats of the per-GPU static scratch array (1 MiB) of the no-allocation
 // entry point, and its device address on `device` (made current); -2 if
 // the runtime cannot resolve it.

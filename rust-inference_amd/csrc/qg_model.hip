@@ -597,6 +597,20 @@ struct qg_model {
     qgm::Step *h_steps = nullptr;                       // pinned ring
     uint32_t ring = 0;
     bool use_graphs = true;
+    // batched prefill (qg_prefill.hip): per chunk of up to kPfMaxTokens tokens,
+    // the residual stream (two buffers, read one / write the other), q|k|v,
+    // attention output, wo output, [gate|up] and down outputs of every token
+    // (the GEMM outputs with room for their K-split slices: pf_s* slices of
+    // kPfMaxTokens rows each), the last token's summed down output, the x
+    // planes / records of the GEMMs and the prompt's token ids; allocated on
+    // first use
+    bool pf_batched = true;
+    float *pf_h[2] = {nullptr, nullptr}, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_ao2 = nullptr,
+          *pf_g = nullptr, *pf_fo = nullptr, *pf_last = nullptr;
+    uint16_t *pf_xp = nullptr;
+    float *pf_rec = nullptr;
+    uint32_t *pf_tok = nullptr;
+    uint32_t pf_s_qkv = 1, pf_s_o = 1, pf_s_gu = 1, pf_s_down = 1;
     hipGraphExec_t g_fwd = nullptr;       // forward pass
     hipGraphExec_t g_dec = nullptr;       // sample + advance + forward (generate)
     float g_dec_penalty = 0.f;
@@ -947,6 +961,154 @@ int put_step(qg_model *m, uint32_t token, uint32_t pos, uint32_t slot)
     return QG_OK;
 }
 
+// ---------------------------------------------------------- batched prefill
+
+// Every layer matrix on the MFMA path: supported type, cols % 32 == 0; and
+// the prefill attention's scores fit its LDS.
+bool pf_supported(const qg_model *m)
+{
+    if (!m->pf_batched) return false;
+    if ((m->hd + (size_t)m->cfg.max_seq_len) * sizeof(float) > 65536) return false;
+    for (int s = 0; s < kSlots; s++)
+        for (const qg_mat *p : m->w[s])
+            if (!p || !qg::prefill_type_supported(p->type) || p->cols % 32 != 0) return false;
+    return true;
+}
+
+int pf_alloc(qg_model *m)
+{
+    if (m->pf_h[0]) return QG_OK;
+    const size_t T = qg::kPfMaxTokens, E = m->cfg.embed_dim, H = m->cfg.hidden_dim;
+    const size_t ldq = m->q_dim + 2 * (size_t)m->kv_dim;
+    size_t kmax = E > H ? E : H;
+    if (m->q_dim > kmax) kmax = m->q_dim;
+    // the K splits of the four GEMM groups (the same shapes in every layer)
+    m->pf_s_qkv = qg::pf_split(qg::pf_tiles(m->q_dim) + 2 * qg::pf_tiles(m->kv_dim), (uint32_t)(E / 32));
+    m->pf_s_o = qg::pf_split(qg::pf_tiles(E), (uint32_t)(m->q_dim / 32));
+    m->pf_s_gu = qg::pf_split(2 * qg::pf_tiles(H), (uint32_t)(E / 32));
+    m->pf_s_down = qg::pf_split(qg::pf_tiles(E), (uint32_t)(H / 32));
+    int rc;
+    if ((rc = dalloc(m, &m->pf_h[0], T * E)) || (rc = dalloc(m, &m->pf_h[1], T * E)) ||
+        (rc = dalloc(m, &m->pf_qkv, m->pf_s_qkv * T * ldq)) || (rc = dalloc(m, &m->pf_ao, T * m->q_dim)) ||
+        (rc = dalloc(m, &m->pf_ao2, m->pf_s_o * T * E)) || (rc = dalloc(m, &m->pf_g, m->pf_s_gu * T * 2 * H)) ||
+        (rc = dalloc(m, &m->pf_fo, m->pf_s_down * T * E)) || (rc = dalloc(m, &m->pf_last, E)) ||
+        (rc = dalloc(m, &m->pf_xp, 3 * T * kmax)) || (rc = dalloc(m, &m->pf_rec, T * (kmax / 32) * 4)) ||
+        (rc = dalloc(m, &m->pf_tok, (size_t)m->cfg.max_seq_len)))
+        return rc;
+    return QG_OK;
+}
+
+// y[t][0..rows) (row stride ldy, slices of T * ldy floats) = mat . x_t for the
+// chunk's tokens and 1..3 matrices over the same x, given as the bf16 pieces
+// of the last pf_planes call over `cols` elements
+int pf_gemm(qg_model *m, const qg::PfMat *mats, int n, size_t cols, uint32_t ntok, uint32_t ldy, uint32_t slices)
+{
+    const int r = qg::launch_pf_gemm(mats, n, cols, m->pf_xp, m->pf_rec, ntok, ldy, slices,
+                                     (size_t)qg::kPfMaxTokens * ldy, (ihipStream_t *)m->ctx->stream);
+    return r ? mfail(m, QG_ERR_HIP, "prefill GEMM launch", hipGetLastError()) : QG_OK;
+}
+
+qg::PfMat pf_mat(const qg_mat *mat, float *y) { return qg::PfMat{mat->type, mat->d, mat->rows, y}; }
+
+// bf16 pieces of x = f(a, b) for the chunk's tokens; a and b of na / nb slices
+// kPfMaxTokens * lda floats apart
+int pf_planes(qg_model *m, const float *a, uint32_t na, const float *b, uint32_t nb, float *sum_out, const float *nw,
+              size_t n, size_t lda, int mode, uint32_t ntok)
+{
+    const int r = qg::launch_pf_planes(a, na, b, nb, (size_t)qg::kPfMaxTokens * lda, sum_out, nw, m->cfg.norm_eps, n,
+                                       lda, mode, m->pf_xp, m->pf_rec, ntok, (ihipStream_t *)m->ctx->stream);
+    return r ? mfail(m, QG_ERR_HIP, "prefill planes launch", hipGetLastError()) : QG_OK;
+}
+
+// Transformer::forward (transformer.rs:63-98) for tokens d_tok[0..ntok) (on
+// device) at positions / cache slots s0 .. s0 + ntok - 1, every layer's
+// projections as GEMMs over the chunk; leaves the last token's logits in
+// m->logits.
+int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
+{
+    const qg_model_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    ihipStream_t *sti = (ihipStream_t *)st;
+    const uint32_t E = c.embed_dim, H = c.hidden_dim, ldq = m->q_dim + 2 * m->kv_dim;
+    const size_t T = qg::kPfMaxTokens;
+    int rc;
+    // embedding rows into zeroed rows (transformer.rs:74-75, quant.rs:152-174)
+    float *h = m->pf_h[0], *h2 = m->pf_h[1];
+    if (qg::launch_fill(h, (size_t)ntok * E, 0.0f, sti) ||
+        qg::launch_dequantize_rows_dev(m->tok->type, m->tok->d, m->tok->rows, m->tok->cols, d_tok, ntok, h, E, sti))
+        return mfail(m, QG_ERR_HIP, "embedding", hipGetLastError());
+    const size_t kv_layer = (size_t)c.max_seq_len * m->kv_dim;
+    const float scale = 1.0f / sqrtf((float)m->hd);                      // attention.rs:99
+    const size_t att_lds = ((size_t)m->hd + c.max_seq_len) * sizeof(float);
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        // the residual stream entering the layer: the embeddings, or h + fo of
+        // the previous layer (written to the other buffer), then attn_norm
+        if (l) {
+            if ((rc = pf_planes(m, h, 1, m->pf_fo, m->pf_s_down, h2, m->vec[QG_V_ATTN_NORM][l], E, E, 1, ntok)))
+                return rc;
+            std::swap(h, h2);
+        } else if ((rc = pf_planes(m, h, 1, nullptr, 0, nullptr, m->vec[QG_V_ATTN_NORM][l], E, E, 1, ntok))) {
+            return rc;
+        }
+        const qg::PfMat qkv[3] = {pf_mat(m->w[QG_M_WQ - 2][l], m->pf_qkv),
+                                  pf_mat(m->w[QG_M_WK - 2][l], m->pf_qkv + m->q_dim),
+                                  pf_mat(m->w[QG_M_WV - 2][l], m->pf_qkv + m->q_dim + m->kv_dim)};
+        if ((rc = pf_gemm(m, qkv, 3, E, ntok, ldq, m->pf_s_qkv))) return rc;
+        float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
+        if (qg::launch_pf_qkv_post(m->pf_qkv, ldq, m->pf_s_qkv, T * ldq, m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l],
+                                   m->vec[QG_V_BV][l], kc, vc, m->cos_t, m->sin_t, m->q_dim, m->kv_dim, m->hd, s0, s0,
+                                   ntok, sti) ||
+            qg::launch_pf_attention(m->pf_qkv, ldq, kc, vc, m->pf_ao, c.n_heads, m->hd, m->kv_dim, m->n_rep, scale, s0,
+                                    ntok, att_lds, sti))
+            return mfail(m, QG_ERR_HIP, "prefill attention", hipGetLastError());
+        const qg::PfMat wo = pf_mat(m->w[QG_M_WO - 2][l], m->pf_ao2);
+        if ((rc = pf_planes(m, m->pf_ao, 1, nullptr, 0, nullptr, nullptr, m->q_dim, m->q_dim, 0, ntok)) ||
+            (rc = pf_gemm(m, &wo, 1, m->q_dim, ntok, E, m->pf_s_o)))
+            return rc;
+        // h = h + attention output; MLP input = ffn_norm(h) (transformer.rs:31-46)
+        if ((rc = pf_planes(m, h, 1, m->pf_ao2, m->pf_s_o, h2, m->vec[QG_V_FFN_NORM][l], E, E, 1, ntok))) return rc;
+        std::swap(h, h2);
+        const qg::PfMat gu[2] = {pf_mat(m->w[QG_M_GATE - 2][l], m->pf_g), pf_mat(m->w[QG_M_UP - 2][l], m->pf_g + H)};
+        if ((rc = pf_gemm(m, gu, 2, E, ntok, 2 * H, m->pf_s_gu))) return rc;
+        // down(silu(gate) * up) (mlp.rs:36-45)
+        const qg::PfMat down = pf_mat(m->w[QG_M_DOWN - 2][l], m->pf_fo);
+        if ((rc = pf_planes(m, m->pf_g, m->pf_s_gu, m->pf_g + H, m->pf_s_gu, nullptr, nullptr, H, 2 * (size_t)H, 2,
+                            ntok)) ||
+            (rc = pf_gemm(m, &down, 1, H, ntok, E, m->pf_s_down)))
+            return rc;
+    }
+    // the last token's final norm of h + fo inside the lm_head GEMV (transformer.rs:87-97)
+    const size_t last = (size_t)(ntok - 1) * E;
+    if (qg::launch_pf_sum(m->pf_fo + last, m->pf_s_down, T * E, E, m->pf_last, sti))
+        return mfail(m, QG_ERR_HIP, "prefill sum", hipGetLastError());
+    return gemv_norm(m, m->lm, h + last, m->pf_last, m->final_norm, nullptr, m->logits);
+}
+
+// n tokens at cache slots / positions m->seq ..; leaves the last logits on
+// device and advances m->seq
+int prefill(qg_model *m, const uint32_t *tok, size_t n)
+{
+    int rc;
+    if (n == 0) return QG_OK;
+    if (pf_supported(m)) {
+        if ((rc = prepare(m)) || (rc = pf_alloc(m))) return rc;
+        // the token ids to device once (n <= max_seq_len - seq, checked by the caller)
+        QGM_HIP(m, hipMemcpyAsync(m->pf_tok, tok, n * sizeof(uint32_t), hipMemcpyHostToDevice, m->ctx->stream));
+        QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
+        for (size_t i = 0; i < n; i += qg::kPfMaxTokens) {
+            const uint32_t nt = (uint32_t)(n - i < qg::kPfMaxTokens ? n - i : qg::kPfMaxTokens);
+            if ((rc = pf_chunk(m, m->pf_tok + i, nt, (uint32_t)(m->seq + i)))) return rc;
+        }
+        m->seq += n;
+        return QG_OK;
+    }
+    for (size_t i = 0; i < n; i++) {
+        if ((rc = put_step(m, tok[i], (uint32_t)m->seq, (uint32_t)m->seq)) || (rc = run_forward(m))) return rc;
+        m->seq += 1;
+    }
+    return QG_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1157,6 +1319,33 @@ int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits)
     return QG_OK;
 }
 
+int qg_model_prefill(qg_model *m, const uint32_t *tokens, size_t n, float *logits)
+{
+    if (!m || (n && !tokens)) return QG_ERR_INVALID_ARG;
+    if (!complete(m)) return mfail(m, QG_ERR_INVALID_ARG, "model matrices / final norm not all set");
+    const qg_model_config &c = m->cfg;
+    if (n > c.max_seq_len || m->seq + n > c.max_seq_len)
+        return mfail(m, QG_ERR_SHAPE, "KV cache full (max_seq_len)");   // kv_cache.rs:54-59
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= c.vocab_size) return mfail(m, QG_ERR_SHAPE, "token id >= vocab_size");
+    QGM_HIP(m, hipSetDevice(m->ctx->device));
+    int rc;
+    if ((rc = prefill(m, tokens, n))) return rc;
+    if (logits && n) {
+        QGM_HIP(m, hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float), hipMemcpyDeviceToHost,
+                                  m->ctx->stream));
+        QGM_HIP(m, hipStreamSynchronize(m->ctx->stream));
+    }
+    return QG_OK;
+}
+
+int qg_model_use_batched_prefill(qg_model *m, int enable)
+{
+    if (!m) return QG_ERR_INVALID_ARG;
+    m->pf_batched = enable != 0;
+    return QG_OK;
+}
+
 int qg_model_sample_greedy(qg_model *m, const uint32_t *recent, size_t n_recent, float penalty, size_t window,
                            uint32_t *token)
 {
@@ -1202,12 +1391,19 @@ int qg_model_generate(qg_model *m, const uint32_t *prompt, size_t n_prompt, size
     const uint32_t win = window > qgm::kRecentMax ? qgm::kRecentMax : (uint32_t)window;
     int rc;
     auto t0 = clk::now();
-    if ((rc = put_step(m, prompt[0], 0, 0))) return rc;
-    for (size_t p = 0; p < n_prompt; p++) {
-        if ((rc = run_forward(m))) return rc;
-        if (p + 1 < n_prompt) {
-            hipLaunchKernelGGL(qgm::advance_k, dim3(1), dim3(64), 0, st, m->d_step, m->d_hist);
-            if ((rc = launched(m, "advance"))) return rc;
+    if (pf_supported(m)) {
+        // batched prefill, then the Step record the token-by-token loop ends with
+        if ((rc = prefill(m, prompt, n_prompt)) ||
+            (rc = put_step(m, prompt[n_prompt - 1], (uint32_t)(n_prompt - 1), (uint32_t)(n_prompt - 1))))
+            return rc;
+    } else {
+        if ((rc = put_step(m, prompt[0], 0, 0))) return rc;
+        for (size_t p = 0; p < n_prompt; p++) {
+            if ((rc = run_forward(m))) return rc;
+            if (p + 1 < n_prompt) {
+                hipLaunchKernelGGL(qgm::advance_k, dim3(1), dim3(64), 0, st, m->d_step, m->d_hist);
+                if ((rc = launched(m, "advance"))) return rc;
+            }
         }
     }
     QGM_HIP(m, hipStreamSynchronize(st));

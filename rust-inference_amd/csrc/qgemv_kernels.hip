@@ -174,17 +174,19 @@ __global__ void __launch_bounds__(256) dequant_k(const uint8_t *__restrict__ w, 
 }
 
 // quant.rs:152-174: writes only the positions the reference writes.  The
-// row is `row`, or *d_row when d_row is not NULL (a row index that lives in
-// device memory, e.g. the token id of a decode step); rows past the end write
+// row is `row`, or d_row[blockIdx.y] when d_row is not NULL (row indices
+// that live in device memory, e.g. the token ids of a decode step or a
+// prefill chunk), written to out + blockIdx.y * ldo; rows past the end write
 // nothing.
 template <uint32_t T>
 __global__ void __launch_bounds__(256) deq_row_k(const uint8_t *__restrict__ w, uint64_t rows,
                                                  uint64_t cols, uint64_t row_arg,
                                                  const uint32_t *__restrict__ d_row,
-                                                 float *__restrict__ out)
+                                                 float *__restrict__ out, uint64_t ldo)
 {
     constexpr uint64_t BS = block_elems(T), BB = block_bytes(T);
-    const uint64_t row = d_row ? (uint64_t)*d_row : row_arg;
+    const uint64_t row = d_row ? (uint64_t)d_row[blockIdx.y] : row_arg;
+    out += blockIdx.y * ldo;
     if (row >= rows) return;
     const uint64_t nbpr = (cols + BS - 1) / BS;
     const uint64_t start_block = row * cols / BS, col_off = row * cols % BS;
@@ -2452,29 +2454,30 @@ int launch_dequant(uint32_t type, const uint8_t *w, size_t n, float *out, ihipSt
 
 template <uint32_t T>
 static int launch_deq_row_t(const uint8_t *w, size_t rows, size_t cols, size_t row, const uint32_t *d_row,
-                            float *out, hipStream_t st)
+                            uint32_t nrows, float *out, size_t ldo, hipStream_t st)
 {
     const uint64_t bs = block_elems(T);
     const uint64_t n = (cols + bs - 1) / bs * bs;
-    hipLaunchKernelGGL((deq_row_k<T>), dim3(grid_for(n)), dim3(256), 0, st, w, (uint64_t)rows,
-                       (uint64_t)cols, (uint64_t)row, d_row, out);
+    hipLaunchKernelGGL((deq_row_k<T>), dim3(grid_for(n), nrows), dim3(256), 0, st, w, (uint64_t)rows,
+                       (uint64_t)cols, (uint64_t)row, d_row, out, (uint64_t)ldo);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 static int launch_dequantize_row_any(uint32_t type, const uint8_t *w, size_t rows, size_t cols, size_t row,
-                              const uint32_t *d_row, float *out, ihipStream_t *stream)
+                              const uint32_t *d_row, uint32_t nrows, float *out, size_t ldo, ihipStream_t *stream)
 {
     hipStream_t st = (hipStream_t)stream;
-    if (cols == 0) return 0;
+    if (cols == 0 || nrows == 0) return 0;
+    if (nrows > 65535u) return -1;
     switch (type) {
-    case T_F32: return launch_deq_row_t<T_F32>(w, rows, cols, row, d_row, out, st);
-    case T_F16: return launch_deq_row_t<T_F16>(w, rows, cols, row, d_row, out, st);
-    case T_Q4_0: return launch_deq_row_t<T_Q4_0>(w, rows, cols, row, d_row, out, st);
-    case T_Q5_0: return launch_deq_row_t<T_Q5_0>(w, rows, cols, row, d_row, out, st);
-    case T_Q8_0: return launch_deq_row_t<T_Q8_0>(w, rows, cols, row, d_row, out, st);
-    case T_Q4_K: return launch_deq_row_t<T_Q4_K>(w, rows, cols, row, d_row, out, st);
-    case T_Q5_K: return launch_deq_row_t<T_Q5_K>(w, rows, cols, row, d_row, out, st);
-    case T_Q6_K: return launch_deq_row_t<T_Q6_K>(w, rows, cols, row, d_row, out, st);
+    case T_F32: return launch_deq_row_t<T_F32>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_F16: return launch_deq_row_t<T_F16>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_Q4_0: return launch_deq_row_t<T_Q4_0>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_Q5_0: return launch_deq_row_t<T_Q5_0>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_Q8_0: return launch_deq_row_t<T_Q8_0>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_Q4_K: return launch_deq_row_t<T_Q4_K>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_Q5_K: return launch_deq_row_t<T_Q5_K>(w, rows, cols, row, d_row, nrows, out, ldo, st);
+    case T_Q6_K: return launch_deq_row_t<T_Q6_K>(w, rows, cols, row, d_row, nrows, out, ldo, st);
     default: return -1;
     }
 }
@@ -2482,13 +2485,19 @@ static int launch_dequantize_row_any(uint32_t type, const uint8_t *w, size_t row
 int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t cols, size_t row,
                           float *out, ihipStream_t *stream)
 {
-    return launch_dequantize_row_any(type, w, rows, cols, row, nullptr, out, stream);
+    return launch_dequantize_row_any(type, w, rows, cols, row, nullptr, 1, out, 0, stream);
 }
 
 int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_row,
                               float *out, ihipStream_t *stream)
 {
-    return launch_dequantize_row_any(type, w, rows, cols, 0, d_row, out, stream);
+    return launch_dequantize_row_any(type, w, rows, cols, 0, d_row, 1, out, 0, stream);
+}
+
+int launch_dequantize_rows_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_rows,
+                               uint32_t n, float *out, size_t ldo, ihipStream_t *stream)
+{
+    return launch_dequantize_row_any(type, w, rows, cols, 0, d_rows, n, out, ldo, stream);
 }
 
 // The streaming-read ceiling: every 16-byte piece of the buffer read once by

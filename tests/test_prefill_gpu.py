@@ -1,0 +1,148 @@
+"""GPU parity of the batched prefill (qg_model_prefill, include/qgmodel.h):
+the prompt's tokens through each layer together, every projection an int8
+MFMA GEMM over the tokens' fixed-point x.  Checked against the oracle's
+token-by-token forward pass (oracle/qref_model.c, transformer.rs:63-98 as
+model.rs:361-365 calls it): the last prompt token's logits, then greedy
+decode steps on the caches the prefill wrote (every cached position's K/V
+enters those steps), within DEEP_TOL, identical tokens.  Also: chunks of 64
+tokens, a prefill that continues a cache, the token-by-token fallback for a
+mix without an MFMA path (F16), and generate with the batched prefill."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import normwise_err
+from test_decode_gpu import DEEP_TOL, SMALL, build
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_compare(dev, ref, oracle, cfg, ids, ref_l, n_new, pos):
+    """n_new greedy steps on both sides after a prompt: logits errors, tokens."""
+    V = cfg["vocab_size"]
+    logits = np.zeros(V, np.float32)
+    errs, out = [], []
+    for _ in range(n_new):
+        recent = ids[-64:]
+        rl = ref_l.copy()
+        oracle.repetition_penalty(rl, recent, 1.1, 64)
+        t_ref = oracle.argmax(rl)
+        t_dev = dev.sample_greedy(recent, 1.1, 64)
+        assert t_dev == t_ref
+        out.append(t_ref)
+        dev.forward(t_ref, pos, logits)
+        ref_l = ref.forward(t_ref, pos)
+        errs.append(normwise_err(logits, ref_l))
+        ids.append(t_ref)
+        pos += 1
+    return errs, out
+
+
+def prefill_and_compare(rinf, synth, oracle, ctx, cfg, mix, seed, n_prompt, n_new, max_seq, split=None):
+    dev, ref, shared = build(rinf, synth, oracle, ctx, cfg, mix, seed, max_seq)
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab_size"], n_prompt)
+    logits = np.zeros(cfg["vocab_size"], np.float32)
+    parts = [prompt] if split is None else [prompt[:split], prompt[split:]]
+    for p in parts:
+        dev.prefill(p, logits)
+    ref_l = None
+    for pos, tok in enumerate(prompt):
+        ref_l = ref.forward(int(tok), pos)
+    assert dev.seq_len == n_prompt
+    e0 = normwise_err(logits, ref_l)
+    errs, out = decode_compare(dev, ref, oracle, cfg, [int(t) for t in prompt], ref_l, n_new, n_prompt)
+    dev.close()
+    if shared is not None:
+        shared.free()
+    return e0, errs, out
+
+
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k", "q8_0", "q5_k_m"])
+def test_small_model_prefill(rinf, synth, oracle, ctx, mix):
+    e0, errs, out = prefill_and_compare(rinf, synth, oracle, ctx, SMALL, mix, 41, 20, 10, 64)
+    print(f"{mix}: prefill logits err {e0:.2e}, decode max {max(errs):.2e}, tokens {out}", flush=True)
+    assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL
+
+
+def test_prefill_chunks_and_continuation(rinf, synth, oracle, ctx):
+    """150 prompt tokens (chunks of 64, 64, 22), fed as 37 + 113 (the second
+    call continues the caches at position 37)."""
+    cfg = dict(SMALL, n_layers=2)
+    e0, errs, out = prefill_and_compare(rinf, synth, oracle, ctx, cfg, "q4_k_m", 43, 150, 6, 200, split=37)
+    print(f"chunks: prefill logits err {e0:.2e}, decode max {max(errs):.2e}", flush=True)
+    assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL
+
+
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m"])
+def test_qwen2_7b_layer_shape_prefill(rinf, synth, oracle, ctx, mix):
+    """One layer of the Qwen2-7B shape (head_dim 128, 7 query heads per kv
+    head, 3584 columns), 40-token prompt."""
+    cfg = dict(SMALL, n_layers=1, embed_dim=3584, n_heads=28, n_kv_heads=4, hidden_dim=1024)
+    e0, errs, out = prefill_and_compare(rinf, synth, oracle, ctx, cfg, mix, 47, 40, 6, 64)
+    print(f"7b layer {mix}: prefill logits err {e0:.2e}, decode max {max(errs):.2e}", flush=True)
+    assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL
+
+
+def test_qwen2_05b_prefill_then_decode(rinf, synth, oracle, ctx):
+    """BASELINE.json configs[2]'s model (24 layers, tied Q4_K embedding at
+    cols = 896, two-row groups) with its 32-token prompt through the batched
+    prefill, then 32 greedy steps."""
+    cfg = synth.ARCH["qwen2-0.5b"]
+    e0, errs, out = prefill_and_compare(rinf, synth, oracle, ctx, cfg, "q4_k_m", synth.config_seed(2), 32, 32, 80)
+    print(f"qwen2-0.5b: prefill logits err {e0:.2e}, decode max {max(errs):.2e}, tokens {out[:8]}", flush=True)
+    assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL
+
+
+def test_prefill_fallback_matches_forward(rinf, synth, oracle, ctx):
+    """F16 matrices have no MFMA path: qg_model_prefill runs one forward pass
+    per token, bit-identical to qg_model_forward calls; the batched path can
+    be switched off for a supported mix with the same result as forward."""
+    for mix, batched in (("f16", True), ("q4_k_m", False)):
+        dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, mix, 53, 40)
+        dev.use_batched_prefill(batched)
+        prompt = np.random.default_rng(53).integers(0, SMALL["vocab_size"], 9)
+        a = np.zeros(SMALL["vocab_size"], np.float32)
+        dev.prefill(prompt, a)
+        dev.reset()
+        b = np.zeros_like(a)
+        for pos, tok in enumerate(prompt):
+            dev.forward(int(tok), pos, b)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        dev.close()
+
+
+def test_generate_with_batched_prefill(rinf, synth, oracle, ctx):
+    """qg_model_generate's tokens with the batched prefill equal those of the
+    token-by-token prompt loop and of the oracle."""
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, "q4_k_m", 59, 64)
+    prompt = np.random.default_rng(59).integers(0, SMALL["vocab_size"], 24)
+    toks_b, _, _ = dev.generate(prompt, 12)
+    dev.use_batched_prefill(False)
+    toks_t, _, _ = dev.generate(prompt, 12)
+    ref_l = None
+    for pos, tok in enumerate(prompt):
+        ref_l = ref.forward(int(tok), pos)
+    ids = [int(t) for t in prompt]
+    want = []
+    for _ in range(12):
+        rl = ref_l.copy()
+        oracle.repetition_penalty(rl, ids[-64:], 1.1, 64)
+        t = oracle.argmax(rl)
+        want.append(t)
+        ref_l = ref.forward(t, len(ids))
+        ids.append(t)
+    assert list(toks_b) == list(toks_t) == want
+    dev.close()
+
+
+def test_prefill_errors(rinf, synth, oracle, ctx):
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, "q4_k_m", 61, 16)
+    with pytest.raises(rinf.QgemvError) as e:
+        dev.prefill(np.arange(17) % SMALL["vocab_size"])          # more than max_seq_len
+    assert e.value.status == 7
+    with pytest.raises(rinf.QgemvError) as e:
+        dev.prefill([1, SMALL["vocab_size"]])                      # token >= vocab
+    assert e.value.status == 7
+    assert dev.seq_len == 0
+    dev.close()
