@@ -57,107 +57,143 @@ __device__ __forceinline__ uint32_t abyte(uint32_t b, uint32_t a, uint32_t s)
     return __builtin_amdgcn_alignbyte(b, a, s);
 }
 
-// quant.rs:606-615: scale and min of sub-block j from the 12-byte pack held
-// in the dwords q0, q1, q2
-__device__ __forceinline__ void k4sm(uint32_t j, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t &sc, uint32_t &m)
+// quant.rs:606-615: scale and min of sub-block j (0..7) from the 12-byte pack
+// held in the dwords q0, q1, q2, without branches on j (a lane-varying value
+// when rows straddle blocks)
+__device__ __forceinline__ void k4sm(uint32_t j, uint32_t q0, uint32_t q1, uint32_t q2, float &sc, float &m)
 {
-    const uint64_t lo = (uint64_t)q0 | ((uint64_t)q1 << 32);        // bytes 0..7
-    const uint32_t bj = (uint32_t)(lo >> (8 * (j & 7u))) & 0xFFu;       // q[j] (j < 8)
-    if (j < 4u) {
-        sc = bj & 63u;
-        m = (uint32_t)(lo >> (8 * (j + 4u))) & 63u;                   // q[j + 4]
-    } else {
-        const uint32_t b8 = (q2 >> (8 * (j - 4u))) & 0xFFu;            // q[j + 4]
-        const uint32_t bm4 = (uint32_t)(lo >> (8 * (j - 4u))) & 0xFFu; // q[j - 4]
-        sc = (b8 & 0xFu) | ((bm4 >> 6) << 4);
-        m = (b8 >> 4) | ((bj >> 6) << 4);
-    }
+    const uint32_t s = 8u * (j & 3u);
+    const uint32_t A = (q0 >> s) & 0xFFu, B = (q1 >> s) & 0xFFu, C = (q2 >> s) & 0xFFu;   // q[j%4], q[j%4+4], q[j%4+8]
+    const bool lo = j < 4u;
+    sc = (float)(lo ? (A & 63u) : ((C & 0xFu) | ((A >> 6) << 4)));
+    m = (float)(lo ? (B & 63u) : ((C >> 4) | ((B >> 6) << 4)));
 }
 
-// Per-type access to one 32-element sub-block (flat index f: elements
-// 32f .. 32f + 31 of the matrix, i.e. of one row since cols % 32 == 0), in
-// two steps so that the loads can be issued a chunk ahead:
-//   load(w, f, kq): the raw dwords the lane needs;
-//   decode(raw, f, kq, c, mul, add): c = the 8 codes 8 kq .. 8 kq + 7 as
-//     bytes, and the sub-block's contribution is sum over sets h of
-//     mul_h * (sum q x) + add_h * (sum x over the set);
+// bf16 of 1 + q / 2^b for the four b-bit codes in the bytes of c (q < 2^b,
+// b <= 7): the exponent of 1 and q as the top b bits of the 7-bit mantissa,
+// exact.  Two dwords of two bf16 each.
+template <int B>
+__device__ __forceinline__ void biased_bf16(uint32_t c, uint32_t &r0, uint32_t &r1)
+{
+    const uint32_t t = (c << (7 - B)) | 0x80808080u;                   // low byte of each bf16
+    r0 = __builtin_amdgcn_perm(0x3F3F3F3Fu, t, 0x04010400u);           // [t0, 3F, t1, 3F]
+    r1 = __builtin_amdgcn_perm(0x3F3F3F3Fu, t, 0x04030402u);           // [t2, 3F, t3, 3F]
+}
+
+// 8 signed byte codes as bf16 (exact: f32 conversion, top half)
+__device__ __forceinline__ uint4 signed_bf16(uint32_t c0, uint32_t c1)
+{
+    uint32_t r[4];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t c = h ? c1 : c0;
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) f[i] = (float)(int8_t)((c >> (8 * i)) & 0xFFu);
+        r[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+        r[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u);
+    }
+    return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+// B operands of the K-quant codes: the MFMA over 32 x with B = 1 + q / 2^b
+// gives D' = sum x + (sum q x) / 2^b, so sum q x = 2^b (D' - sum x) and a
+// sub-block's mul * (sum q x) + add * (sum x) = mul' D' + add' (sum x) with
+// mul' = 2^b mul, add' = add - mul'.  (Masked codes -- the other half of a
+// Q6_K sub-block -- are B = 0.)
+template <int B>
+__device__ __forceinline__ uint4 kquant_b(uint32_t c0, uint32_t c1, bool keep)
+{
+    uint4 r;
+    biased_bf16<B>(c0, r.x, r.y);
+    biased_bf16<B>(c1, r.z, r.w);
+    return keep ? r : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Per-type access to one 32-element sub-block (sub-block j of the block at
+// blk; rows hold whole sub-blocks since cols % 32 == 0), in two steps so that
+// the loads can be issued a chunk ahead:
+//   load(blk, j, kq): the raw dwords the lane needs (every byte read lies in
+//     the matrix or its tail pad);
+//   decode(raw, j, kq, b, mul, add): b[h] = the B operand (codes 8 kq ..
+//     8 kq + 7 as bf16) of set h, and the sub-block's contribution is sum
+//     over sets of mul_h * D_h + add_h * (sum x over the set), D_h the MFMA
+//     result;
 //   NSET = 1 when one scale covers all 32 codes, 2 for Q6_K's 16-code
-//   sub-blocks (h = 0 codes 0..15, h = 1 codes 16..31); SIGNED: the codes
-//   are int8 (else unsigned, below 128).
+//   sub-blocks (h = 0 codes 0..15, h = 1 codes 16..31); SUMS: add is used.
 template <uint32_t T> struct PfW;
 
 // Q4_K (quant.rs:210-228): 8 sub-blocks per 144-byte block; sub-block j is
-// the low (j even) or high (j odd) nibbles of qs[32 (j/2) .. +32).
+// the low (j even) or high (j odd) nibbles of qs[32 (j/2) .. +32); the value
+// is d * sc * q - dmin * m.
 template <> struct PfW<T_Q4_K> {
     static constexpr int NSET = 1;
-    static constexpr bool SIGNED = false;
+    static constexpr bool SUMS = true;
     struct Raw {
         uint4 head;
         uint2 v;
     };
-    __device__ static Raw load(const uint8_t *w, uint64_t f, uint32_t kq)
+    static constexpr uint32_t BB = 144;
+    __device__ static Raw load(const uint8_t *b, uint32_t j, uint32_t kq)
     {
-        const uint8_t *b = w + (f >> 3) * 144u;
-        const uint32_t j = (uint32_t)(f & 7u);
         return Raw{*(const uint4 *)b, *(const uint2 *)(b + 16u + 32u * (j >> 1) + 8u * kq)};
     }
-    __device__ static void decode(const Raw &r, uint64_t f, uint32_t, uint32_t (&c)[2], float (&mul)[2],
+    __device__ static void decode(const Raw &r, uint32_t j, uint32_t, uint4 (&bq)[2], float (&mul)[2],
                                   float (&add)[2])
     {
-        const uint32_t j = (uint32_t)(f & 7u), sh = (j & 1u) * 4u;
-        c[0] = (r.v.x >> sh) & 0x0F0F0F0Fu;
-        c[1] = (r.v.y >> sh) & 0x0F0F0F0Fu;
-        uint32_t sc, m;
+        const uint32_t sh = (j & 1u) * 4u;
+        bq[0] = kquant_b<4>((r.v.x >> sh) & 0x0F0F0F0Fu, (r.v.y >> sh) & 0x0F0F0F0Fu, true);
+        float sc, m;
         k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
-        mul[0] = h2f(r.head.x) * (float)sc;
-        add[0] = -(h2f(r.head.x >> 16) * (float)m);
+        mul[0] = 16.0f * (h2f(r.head.x) * sc);
+        add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
     }
 };
 
 // Q5_K (quant.rs:231-262): as Q4_K with a fifth bit, bit j of qh[l].
 template <> struct PfW<T_Q5_K> {
     static constexpr int NSET = 1;
-    static constexpr bool SIGNED = false;
+    static constexpr bool SUMS = true;
     struct Raw {
         uint4 head;
         uint2 v, h;
     };
-    __device__ static Raw load(const uint8_t *w, uint64_t f, uint32_t kq)
+    static constexpr uint32_t BB = 176;
+    __device__ static Raw load(const uint8_t *b, uint32_t j, uint32_t kq)
     {
-        const uint8_t *b = w + (f >> 3) * 176u;
-        const uint32_t j = (uint32_t)(f & 7u);
         return Raw{*(const uint4 *)b, *(const uint2 *)(b + 48u + 32u * (j >> 1) + 8u * kq),
                    *(const uint2 *)(b + 16u + 8u * kq)};
     }
-    __device__ static void decode(const Raw &r, uint64_t f, uint32_t, uint32_t (&c)[2], float (&mul)[2],
+    __device__ static void decode(const Raw &r, uint32_t j, uint32_t, uint4 (&bq)[2], float (&mul)[2],
                                   float (&add)[2])
     {
-        const uint32_t j = (uint32_t)(f & 7u), sh = (j & 1u) * 4u;
-        c[0] = ((r.v.x >> sh) & 0x0F0F0F0Fu) | (((r.h.x >> j) & 0x01010101u) << 4);
-        c[1] = ((r.v.y >> sh) & 0x0F0F0F0Fu) | (((r.h.y >> j) & 0x01010101u) << 4);
-        uint32_t sc, m;
+        const uint32_t sh = (j & 1u) * 4u;
+        const uint32_t c0 = ((r.v.x >> sh) & 0x0F0F0F0Fu) | (((r.h.x >> j) & 0x01010101u) << 4);
+        const uint32_t c1 = ((r.v.y >> sh) & 0x0F0F0F0Fu) | (((r.h.y >> j) & 0x01010101u) << 4);
+        bq[0] = kquant_b<5>(c0, c1, true);
+        float sc, m;
         k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
-        mul[0] = h2f(r.head.x) * (float)sc;
-        add[0] = -(h2f(r.head.x >> 16) * (float)m);
+        mul[0] = 32.0f * (h2f(r.head.x) * sc);
+        add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
     }
 };
 
 // Q6_K (quant.rs:265-292): 210-byte blocks (2-byte aligned), halves n of 128
 // elements; within a half, sub-block k4 (32 elements, l = 0..31) takes the
 // low (k4 < 2) or high nibbles of ql[64 n + 32 (k4 & 1) + l], bits 2 k4 of
-// qh[32 n + l], and scale sc[8 n + l/16 + 2 k4]; the code is q - 32 (the -32
-// goes to add).  Reads stay inside the block but for the dword holding d,
-// which can end 2 bytes past the last block (inside the buffer's tail pad).
+// qh[32 n + l], and scale sc[8 n + l/16 + 2 k4]; the value is
+// d * sc * (q - 32).  Reads stay inside the block but for the dword holding
+// d, which can end 2 bytes past the last block (inside the buffer's tail pad).
 template <> struct PfW<T_Q6_K> {
     static constexpr int NSET = 2;
-    static constexpr bool SIGNED = false;
+    static constexpr bool SUMS = true;
     struct Raw {
-        uint32_t ql[3], qh[3], s, d;
+        uint32_t ql[3], qh[3], s, d, sb;
     };
-    __device__ static Raw load(const uint8_t *w, uint64_t f, uint32_t kq)
+    static constexpr uint32_t BB = 210;
+    __device__ static Raw load(const uint8_t *b, uint32_t j, uint32_t kq)
     {
-        const uint8_t *b = w + (f >> 3) * 210u;
-        const uint32_t j = (uint32_t)(f & 7u), n = j >> 2, k4 = j & 3u;
+        const uint32_t n = j >> 2, k4 = j & 3u;
         const uint32_t *pl = adown(b + 64u * n + 32u * (k4 & 1u) + 8u * kq);
         const uint32_t *ph = adown(b + 128u + 32u * n + 8u * kq);
         Raw r;
@@ -169,76 +205,72 @@ template <> struct PfW<T_Q6_K> {
         r.qh[2] = ph[2];
         r.s = *adown(b + 192u + 8u * n + 2u * k4);
         r.d = *adown(b + 208u);
+        r.sb = (uint32_t)((uintptr_t)b & 3u);
         return r;
     }
-    __device__ static void decode(const Raw &r, uint64_t f, uint32_t, uint32_t (&c)[2], float (&mul)[2],
+    __device__ static void decode(const Raw &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
                                   float (&add)[2])
     {
         // w is 4-byte aligned: the block starts at byte sb = 0 or 2 of a dword;
         // ql, qh and d at offsets 0 mod 4 from it, the scale pair at 2 k4
-        const uint32_t sb = (uint32_t)(((f >> 3) * 210u) & 3u);
-        const uint32_t j = (uint32_t)(f & 7u), k4 = j & 3u, ss = (sb + 2u * k4) & 3u;
+        const uint32_t sb = r.sb, k4 = j & 3u, ss = (sb + 2u * k4) & 3u;
         const uint32_t sl = (k4 >> 1) * 4u, shh = 2u * k4;
         const uint32_t L0 = abyte(r.ql[1], r.ql[0], sb), L1 = abyte(r.ql[2], r.ql[1], sb);
         const uint32_t H0 = abyte(r.qh[1], r.qh[0], sb), H1 = abyte(r.qh[2], r.qh[1], sb);
-        c[0] = ((L0 >> sl) & 0x0F0F0F0Fu) | (((H0 >> shh) & 0x03030303u) << 4);
-        c[1] = ((L1 >> sl) & 0x0F0F0F0Fu) | (((H1 >> shh) & 0x03030303u) << 4);
+        const uint32_t c0 = ((L0 >> sl) & 0x0F0F0F0Fu) | (((H0 >> shh) & 0x03030303u) << 4);
+        const uint32_t c1 = ((L1 >> sl) & 0x0F0F0F0Fu) | (((H1 >> shh) & 0x03030303u) << 4);
+        const bool lo = kq < 2u;                                      // codes 0..15 of the sub-block
+        bq[0] = kquant_b<6>(c0, c1, lo);
+        bq[1] = kquant_b<6>(c0, c1, !lo);
         const uint32_t s = r.s >> (8 * ss), dd = r.d >> (8 * sb);   // sc[8n + 2k4], sc[8n + 2k4 + 1]; d
         const float d = h2f(dd);
-        mul[0] = d * (float)(int8_t)(s & 0xFFu);
-        mul[1] = d * (float)(int8_t)((s >> 8) & 0xFFu);
-        add[0] = -32.0f * mul[0];
-        add[1] = -32.0f * mul[1];
+        const float m0 = d * (float)(int8_t)(s & 0xFFu), m1 = d * (float)(int8_t)((s >> 8) & 0xFFu);
+        mul[0] = 64.0f * m0;
+        mul[1] = 64.0f * m1;
+        add[0] = -32.0f * m0 - mul[0];
+        add[1] = -32.0f * m1 - mul[1];
     }
 };
 
 // Q8_0 (quant.rs:106-113): one 34-byte block (2-byte aligned) per sub-block,
-// int8 codes.
+// int8 codes as bf16 (exact), value d * q.
 template <> struct PfW<T_Q8_0> {
     static constexpr int NSET = 1;
-    static constexpr bool SIGNED = true;
+    static constexpr bool SUMS = false;
     struct Raw {
-        uint32_t q[3], d;
+        uint32_t q[3], d, sb;
     };
-    __device__ static Raw load(const uint8_t *w, uint64_t f, uint32_t kq)
+    static constexpr uint32_t BB = 34;
+    __device__ static Raw load(const uint8_t *b, uint32_t, uint32_t kq)
     {
-        const uint8_t *b = w + f * 34u;
         const uint32_t *pq = adown(b + 2u + 8u * kq);
-        return Raw{{pq[0], pq[1], pq[2]}, *adown(b)};
+        return Raw{{pq[0], pq[1], pq[2]}, *adown(b), (uint32_t)((uintptr_t)b & 3u)};
     }
-    __device__ static void decode(const Raw &r, uint64_t f, uint32_t, uint32_t (&c)[2], float (&mul)[2],
+    __device__ static void decode(const Raw &r, uint32_t, uint32_t, uint4 (&bq)[2], float (&mul)[2],
                                   float (&add)[2])
     {
         // w is 4-byte aligned: block b starts at byte 0 or 2 of a dword, its
         // codes (b + 2 + 8 kq) at byte 2 or 0 of q[0]
-        const uint32_t sb = (uint32_t)((f * 34u) & 3u), sq = (sb + 2u) & 3u;
-        c[0] = abyte(r.q[1], r.q[0], sq);
-        c[1] = abyte(r.q[2], r.q[1], sq);
+        const uint32_t sb = r.sb, sq = (sb + 2u) & 3u;
+        bq[0] = signed_bf16(abyte(r.q[1], r.q[0], sq), abyte(r.q[2], r.q[1], sq));
         mul[0] = h2f(r.d >> (8 * sb));
         add[0] = 0.0f;
     }
 };
 
-// 8 codes (bytes of c0, c1) as bf16: f32 conversion (exact), top half.
-template <bool SIGNED>
-__device__ __forceinline__ bf8 codes_bf16(uint32_t c0, uint32_t c1)
-{
-    uint32_t r[4];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const uint32_t c = h ? c1 : c0;
-        float f[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            f[i] = SIGNED ? (float)(int8_t)((c >> (8 * i)) & 0xFFu) : (float)((c >> (8 * i)) & 0xFFu);
-        r[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
-        r[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u);
-    }
-    return __builtin_bit_cast(bf8, make_uint4(r[0], r[1], r[2], r[3]));
-}
-
-constexpr uint32_t kPfKC = 2;                                // sub-blocks per staged chunk
-constexpr uint32_t kPfR = 2;                                 // 16-row tiles per wave
+#ifndef QG_PF_KC
+#define QG_PF_KC 2
+#endif
+#ifndef QG_PF_R
+#define QG_PF_R 2
+#endif
+#ifndef QG_PF_WAVES
+#define QG_PF_WAVES 4
+#endif
+constexpr uint32_t kPfKC = QG_PF_KC;                         // sub-blocks per staged chunk
+constexpr uint32_t kPfR = QG_PF_R;                           // 16-row tiles per wave
+constexpr uint32_t kPfWaves = QG_PF_WAVES;                   // waves per workgroup
+constexpr uint32_t kPfRows = 16u * kPfR * kPfWaves;          // rows per workgroup tile
 constexpr uint32_t kPfBufX = kPfKC * 3u * 64u * 64u;         // bytes of x pieces per buffer
 constexpr uint32_t kPfBuf = kPfBufX + kPfKC * 1024u;         // ... and of the sums
 constexpr uint32_t kPfLds = 2u * kPfBuf;                     // two buffers
@@ -255,19 +287,25 @@ __device__ __forceinline__ void pf_dma16(const void *gp, uint32_t lds_addr)
 // Issue the copies of chunk kc (nk sub-blocks) into the buffer at LDS byte
 // address b0: x block u = (kk * 3 + c) * 4 + g (sub-block kk, piece c,
 // tokens 16 g .. 16 g + 15; 1 KB, token t's 64 bytes as four 16-byte slots,
-// slot s stored at position s ^ ((t >> 2) & 3) so that the A-operand reads
-// of 16 tokens hit distinct banks), then per sub-block the 256 sums.  Tokens
+// slot s stored at position s ^ pf_swz(t) so that the A-operand reads of
+// 8 or 16 consecutive tokens at one slot hit distinct banks), then per
+// sub-block the 256 sums.  Tokens
 // past the chunk repeat the last one (their outputs are never stored).
+// slot position of token t's slots in its 64-byte LDS row: the 16-byte
+// reads of tokens t..t+7 (t % 8 == 0) at one slot cover 8 distinct 16-byte
+// bank groups mod 128 bytes, those of t..t+15 16 distinct groups mod 256
+__device__ __forceinline__ uint32_t pf_swz(uint32_t t) { return ((t >> 1) ^ (t >> 3)) & 3u; }
+
 __device__ __forceinline__ void pf_stage(const uint16_t *__restrict__ xp, const float *__restrict__ rec,
-                                         uint32_t ntok, uint32_t n, uint32_t ntt, uint32_t kc, uint32_t nk,
-                                         uint32_t b0, uint32_t wave, uint32_t lane)
+                                         uint32_t ntok, uint32_t n, uint32_t kc, uint32_t nk, uint32_t b0,
+                                         uint32_t wave, uint32_t lane)
 {
 #pragma unroll
-    for (uint32_t v = 0; v < kPfKC * 12u / 4u; v++) {
-        const uint32_t u = v * 4u + wave, kk = u / 12u, c = (u >> 2) % 3u, g = u & 3u;
-        if (kk < nk && g < ntt) {                                   // wave-uniform
+    for (uint32_t v = 0; v < (kPfKC * 12u + kPfWaves - 1u) / kPfWaves; v++) {
+        const uint32_t u = v * kPfWaves + wave, kk = u / 12u, c = (u >> 2) % 3u, g = u & 3u;
+        if (kk < nk) {                                               // wave-uniform (u past the chunk: kk >= kPfKC)
             const uint32_t t = min(16u * g + (lane >> 2), ntok - 1u);
-            const uint32_t s = (lane & 3u) ^ ((lane >> 4) & 3u);
+            const uint32_t s = (lane & 3u) ^ pf_swz(lane >> 2);
             pf_dma16(xp + ((size_t)c * ntok + t) * n + 32u * (kc + kk) + 8u * s, b0 + u * 1024u);
         }
     }
@@ -281,8 +319,10 @@ __device__ __forceinline__ void pf_stage(const uint16_t *__restrict__ xp, const 
 // f = 0: sum x, 1: sum x[0..16), 2: sum x[16..32).  Chunks of kPfKC
 // sub-blocks are copied into two LDS buffers in turn, the next chunk's copy
 // and weight loads in flight while this one is computed.  D[4 kq + i][c16]
-// of an MFMA is token 16 tt + 4 kq + i of row r0 + c16.
-template <uint32_t T, int R>
+// of an MFMA is token 16 tt + 4 kq + i of row r0 + c16.  AL: every row
+// starts a block (nseg % 8 == 0, or single-sub-block blocks), so the
+// sub-block index within the block is the same in every lane.
+template <uint32_t T, int R, bool AL>
 __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint32_t rows, uint32_t row0,
                                              uint32_t nseg, uint32_t k0, uint32_t k1,
                                              const uint16_t *__restrict__ xp, const float *__restrict__ rec,
@@ -291,88 +331,119 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
 {
     using P = PfW<T>;
     using Raw = typename P::Raw;
+    constexpr bool SB1 = T == T_Q8_0;                                 // one sub-block per block
     const uint32_t lane = threadIdx.x & 63u, kq = lane >> 4, c16 = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
-    const uint32_t ntt = (ntok + 15u) / 16u;
     const bool active = row0 < rows;                                  // wave-uniform
-    const uint32_t swz = kq ^ ((c16 >> 2) & 3u);                     // this lane's slot position
+    const uint32_t swz = kq ^ pf_swz(c16);                           // this lane's slot position
+    // per row tile: the flat index of the row's first sub-block, and (AL) its
+    // first block
     uint64_t fb[R];
+    const uint8_t *rb[R];
 #pragma unroll
-    for (int i = 0; i < R; i++) fb[i] = (uint64_t)min(row0 + 16u * i + c16, rows - 1u) * nseg;
-    float acc[R][4][4];
+    for (int i = 0; i < R; i++) {
+        fb[i] = (uint64_t)min(row0 + 16u * i + c16, rows - 1u) * nseg;
+        rb[i] = w + (SB1 ? fb[i] : fb[i] / 8u) * P::BB;
+    }
+    // sub-block k of row tile i: its index in its block, and the block
+    auto subj = [&](int i, uint32_t k) -> uint32_t {
+        if constexpr (SB1) return 0u;
+        else if constexpr (AL) return k & 7u;
+        else return ((uint32_t)fb[i] + k) & 7u;
+    };
+    auto block = [&](int i, uint32_t k) -> const uint8_t * {
+        if constexpr (SB1) return rb[i] + (size_t)k * P::BB;
+        else if constexpr (AL) return rb[i] + (size_t)(k >> 3) * P::BB;
+        else return w + ((fb[i] + k) >> 3) * P::BB;
+    };
+    // weights of sub-block k (clamped into the slice: the loads past its end
+    // are harmless repeats, unconditional so that none waits on a branch)
+    auto wload = [&](int i, uint32_t k) {
+        const uint32_t kc = min(k, k1 - 1u);
+        return P::load(block(i, kc), subj(i, kc), kq);
+    };
+    v4f acc[R][4];
 #pragma unroll
     for (int i = 0; i < R; i++)
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[i][tt][e] = 0.0f;
+        for (int tt = 0; tt < 4; tt++) acc[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
     Raw raw[kPfKC][R];
-    pf_stage(xp, rec, ntok, n, ntt, k0, min(kPfKC, k1 - k0), lds0, wave, lane);
+    pf_stage(xp, rec, ntok, n, k0, min(kPfKC, k1 - k0), lds0, wave, lane);
 #pragma unroll
     for (uint32_t kk = 0; kk < kPfKC; kk++)
 #pragma unroll
-        for (int i = 0; i < R; i++)
-            if (active && k0 + kk < k1) raw[kk][i] = P::load(w, fb[i] + k0 + kk, kq);
+        for (int i = 0; i < R; i++) raw[kk][i] = wload(i, k0 + kk);
     uint32_t buf = 0;
     for (uint32_t kc = k0; kc < k1; kc += kPfKC, buf ^= 1u) {
         const uint32_t nk = min(kPfKC, k1 - kc);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // this wave's copies of chunk kc landed
         __syncthreads();                                              // everyone's; the other buffer is free
         if (kc + kPfKC < k1)
-            pf_stage(xp, rec, ntok, n, ntt, kc + kPfKC, min(kPfKC, k1 - kc - kPfKC), lds0 + (buf ^ 1u) * kPfBuf,
-                     wave, lane);
+            pf_stage(xp, rec, ntok, n, kc + kPfKC, min(kPfKC, k1 - kc - kPfKC), lds0 + (buf ^ 1u) * kPfBuf, wave,
+                     lane);
         const uint8_t *xb = lds + buf * kPfBuf;
         const float *rs = (const float *)(xb + kPfBufX);
+        float addv[R][kPfKC][2];
+#pragma unroll
+        for (int i = 0; i < R; i++)
+#pragma unroll
+            for (uint32_t kk = 0; kk < kPfKC; kk++) addv[i][kk][0] = addv[i][kk][1] = 0.f;
 #pragma unroll
         for (uint32_t kk = 0; kk < kPfKC; kk++) {
             if (kk >= nk) break;
             // decode this sub-block's weights, then reuse their registers for
             // the next chunk's
-            bf8 bq[R][P::NSET];
-            float mul[R][2], add[R][2];
+            uint4 bq[R][2];
+            float mul[R][2];
 #pragma unroll
-            for (int i = 0; i < R; i++) {
-                uint32_t c[2];
-                P::decode(raw[kk][i], fb[i] + kc + kk, kq, c, mul[i], add[i]);
-                if constexpr (P::NSET == 2) {
-                    const bool lo = kq < 2u;                         // codes 0..15 of the sub-block
-                    bq[i][0] = codes_bf16<P::SIGNED>(lo ? c[0] : 0u, lo ? c[1] : 0u);
-                    bq[i][P::NSET - 1] = codes_bf16<P::SIGNED>(lo ? 0u : c[0], lo ? 0u : c[1]);
-                } else {
-                    bq[i][0] = codes_bf16<P::SIGNED>(c[0], c[1]);
-                }
-            }
+            for (int i = 0; i < R; i++) P::decode(raw[kk][i], subj(i, kc + kk), kq, bq[i], mul[i], addv[i][kk]);
 #pragma unroll
-            for (int i = 0; i < R; i++)
-                if (active && kc + kPfKC + kk < k1) raw[kk][i] = P::load(w, fb[i] + kc + kPfKC + kk, kq);
+            for (int i = 0; i < R; i++) raw[kk][i] = wload(i, kc + kPfKC + kk);
             if (!active) continue;
 #pragma unroll
             for (uint32_t tt = 0; tt < 4; tt++) {
-                if (tt >= ntt) break;                                // wave-uniform
                 const uint8_t *xa = xb + ((((kk * 3u) * 64u + 16u * tt + c16) * 4u + swz) << 4);
                 const bf8 a0 = *(const bf8 *)xa;
                 const bf8 a1 = *(const bf8 *)(xa + 64u * 64u);
                 const bf8 a2 = *(const bf8 *)(xa + 128u * 64u);
-                const float *sr = rs + kk * 256u + 16u * tt + 4u * kq;
 #pragma unroll
-                for (int h = 0; h < P::NSET; h++) {
-                    const float4 sx = *(const float4 *)(sr + (P::NSET == 1 ? 0u : 64u * (1u + h)));
-                    const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
+                for (int h = 0; h < P::NSET; h++)
 #pragma unroll
                     for (int i = 0; i < R; i++) {
+                        const bf8 b = __builtin_bit_cast(bf8, bq[i][h]);
                         const v4f z = {0.f, 0.f, 0.f, 0.f};
-                        v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[i][h], z, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[i][h], d, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bq[i][h], d, 0, 0, 0);
+                        v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, z, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b, d, 0, 0, 0);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            float s = acc[i][tt][e];
-                            if (!P::SIGNED) s = __builtin_fmaf(add[i][h], sxv[e], s);
-                            acc[i][tt][e] = __builtin_fmaf(mul[i][h], d[e], s);
-                        }
+                        for (int e = 0; e < 4; e++) acc[i][tt][e] = __builtin_fmaf(mul[i][h], d[e], acc[i][tt][e]);
                     }
-                }
+            }
+        }
+        if constexpr (P::SUMS) {
+            if (!active) continue;
+            // the chunk's add * (sum x) terms as one f32 MFMA (K = 4) per row
+            // tile and token tile: K slot kq is sub-block qk, set qh of the
+            // chunk (A: the sums of the tile's 16 tokens, B: the row's add)
+            const uint32_t qk = P::NSET == 1 ? kq : kq >> 1, qh = P::NSET == 1 ? 0u : kq & 1u;
+            const bool qv = qk < nk;
+            float bv[R];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                float s = 0.f;
+#pragma unroll
+                for (uint32_t kk = 0; kk < kPfKC; kk++)
+#pragma unroll
+                    for (uint32_t h = 0; h < (uint32_t)P::NSET; h++) s = (qk == kk && qh == h) ? addv[i][kk][h] : s;
+                bv[i] = qv ? s : 0.f;
+            }
+            const float *sa = rs + min(qk, kPfKC - 1u) * 256u + (P::NSET == 1 ? 0u : 64u * (1u + qh)) + c16;
+#pragma unroll
+            for (uint32_t tt = 0; tt < 4; tt++) {
+                const float av = qv ? sa[16u * tt] : 0.f;
+#pragma unroll
+                for (int i = 0; i < R; i++) acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[i], acc[i][tt], 0, 0, 0);
             }
         }
     }
@@ -383,7 +454,6 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
         if (r >= rows) continue;
 #pragma unroll
         for (uint32_t tt = 0; tt < 4; tt++) {
-            if (tt >= ntt) break;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t t = 16u * tt + 4u * kq + (uint32_t)e;
@@ -410,8 +480,8 @@ struct PfJobs {
 // sub-blocks; slice s of a job writes its partial products to
 // y + s * sstride (the consumer sums the slices in order s = 0, 1, ...).
 // 4 waves of 16 kPfR rows per workgroup.
-template <uint32_t T>
-__global__ void __launch_bounds__(256) pf_gemm_k(PfJobs jobs, uint32_t nseg, uint32_t sps,
+template <uint32_t T, bool AL>
+__global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t nseg, uint32_t sps,
                                                  const uint16_t *__restrict__ xp, const float *__restrict__ rec,
                                                  uint32_t ntok, uint32_t n, uint32_t ldy, uint64_t sstride)
 {
@@ -426,9 +496,9 @@ __global__ void __launch_bounds__(256) pf_gemm_k(PfJobs jobs, uint32_t nseg, uin
             J = jobs.j2;
         }
     }
-    const uint32_t row0 = tile * (64u * kPfR) + (threadIdx.x >> 6) * (16u * kPfR);
+    const uint32_t row0 = tile * kPfRows + (threadIdx.x >> 6) * (16u * kPfR);
     const uint32_t k0 = blockIdx.y * sps, k1 = min(nseg, k0 + sps);
-    pf_gemm_rows<T, kPfR>(J.w, J.rows, row0, nseg, k0, k1, xp, rec, ntok, n, (uint8_t *)pf_lds4,
+    pf_gemm_rows<T, kPfR, AL>(J.w, J.rows, row0, nseg, k0, k1, xp, rec, ntok, n, (uint8_t *)pf_lds4,
                           J.y + (size_t)blockIdx.y * sstride, ldy);
 }
 
@@ -711,7 +781,7 @@ uint32_t pf_split(uint32_t tiles, uint32_t nseg)
     return (nseg + sps - 1) / sps;
 }
 
-uint32_t pf_tiles(size_t rows) { return (uint32_t)((rows + 64 * qgp::kPfR - 1) / (64 * qgp::kPfR)); }
+uint32_t pf_tiles(size_t rows) { return (uint32_t)((rows + qgp::kPfRows - 1) / qgp::kPfRows); }
 
 template <uint32_t T>
 static void pf_gemm_launch(const qgp::PfJobs &jobs, uint32_t tiles, uint32_t nseg, uint32_t slices,
@@ -719,8 +789,18 @@ static void pf_gemm_launch(const qgp::PfJobs &jobs, uint32_t tiles, uint32_t nse
                            size_t sstride, hipStream_t st)
 {
     const uint32_t sps = (nseg + slices - 1) / slices;
-    hipLaunchKernelGGL(qgp::pf_gemm_k<T>, dim3(tiles, slices), dim3(256), qgp::kPfLds, st, jobs, nseg, sps, xp, rec,
-                       ntok, cols, ldy, (uint64_t)sstride);
+    // rows of whole blocks: the sub-block index within a block is the same in
+    // every row (Q8_0 blocks are single sub-blocks)
+    const dim3 grid(tiles, slices), block(64 * qgp::kPfWaves);
+    if constexpr (T == T_Q8_0)
+        hipLaunchKernelGGL((qgp::pf_gemm_k<T, true>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
+                           cols, ldy, (uint64_t)sstride);
+    else if (nseg % 8u == 0)
+        hipLaunchKernelGGL((qgp::pf_gemm_k<T, true>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
+                           cols, ldy, (uint64_t)sstride);
+    else
+        hipLaunchKernelGGL((qgp::pf_gemm_k<T, false>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
+                           cols, ldy, (uint64_t)sstride);
 }
 
 int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *xp, const float *rec, uint32_t ntok,
