@@ -87,8 +87,9 @@ int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits);
  * of tokens[0..n) at positions seq, seq + 1, ... (seq = the positions already
  * cached), leaving the caches and the device logits as those n calls of
  * qg_model_forward would -- the logits are the last token's.  Chunks of up to
- * 64 tokens go through each layer together, every projection one int8 MFMA
- * GEMM over the tokens' fixed-point x (batched prefill), when every layer
+ * 64 tokens go through each layer together, every projection one bf16 MFMA
+ * GEMM over the tokens' x split into three bf16 pieces (batched prefill,
+ * f32 accumulation), when every layer
  * matrix is Q4_K, Q5_K, Q6_K or Q8_0 with cols % 32 == 0; otherwise, or after
  * qg_model_use_batched_prefill(m, 0), one forward pass per token.  `logits`,
  * if not NULL, receives vocab_size floats (host memory).  QG_ERR_SHAPE when
@@ -98,6 +99,12 @@ int qg_model_prefill(qg_model *m, const uint32_t *tokens, size_t n, float *logit
  * qg_model_generate where it applies (enable != 0, the default), or one
  * forward pass per prompt token (enable == 0). */
 int qg_model_use_batched_prefill(qg_model *m, int enable);
+/* No counterpart in the reference (tuning and tests): the decode step's
+ * attention for head_dim 64, 128 and 256 -- path 0 (the default) by length:
+ * whole query heads in one launch up to 512 cached positions, split over
+ * position ranges and merged beyond; 1 always whole heads; 2 always split.
+ * Both compute attention.rs:93-121; they differ in summation order only. */
+int qg_model_set_attention_path(qg_model *m, int path);
 
 /* Greedy Sampler::sample on the device logits of the last forward:
  * repetition penalty over `recent` (the last `window` entries, applied in

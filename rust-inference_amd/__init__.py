@@ -125,6 +125,7 @@ _SIGS = {
     "qg_model_forward": (ctypes.c_int, [_P, _U32, _U32, _P]),
     "qg_model_prefill": (ctypes.c_int, [_P, _P, _SZ, _P]),
     "qg_model_use_batched_prefill": (ctypes.c_int, [_P, ctypes.c_int]),
+    "qg_model_set_attention_path": (ctypes.c_int, [_P, ctypes.c_int]),
     "qg_model_sample_greedy": (ctypes.c_int, [_P, _P, _SZ, ctypes.c_float, _SZ, ctypes.POINTER(_U32)]),
     "qg_model_generate": (ctypes.c_int, [_P, _P, _SZ, _SZ, ctypes.c_float, _SZ, _P,
                                          ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
@@ -576,6 +577,11 @@ class DeviceModel:
     def use_batched_prefill(self, enable: bool):
         self.ctx.check(self.ctx.lib.qg_model_use_batched_prefill(self.h, int(bool(enable))),
                        "qg_model_use_batched_prefill")
+
+    def set_attention_path(self, path: int):
+        """0: by length (whole heads up to 512 cached positions, else split),
+        1: always whole heads, 2: always split over position ranges."""
+        self.ctx.check(self.ctx.lib.qg_model_set_attention_path(self.h, int(path)), "qg_model_set_attention_path")
 
     def forward(self, token: int, pos: int, logits=None):
         """logits: numpy float32[vocab] receiving the step's logits, or None."""

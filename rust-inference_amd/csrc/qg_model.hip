@@ -392,6 +392,143 @@ __global__ void __launch_bounds__(256) attn_combine_k(const float *__restrict__ 
     }
 }
 
+// Short contexts: the whole attention of query head blockIdx.x in one
+// workgroup, with the projections' post-processing of attn_rope_split_k
+// (biases, RoPE of q and k, the cache append at `slot` by the first query
+// head of each kv head, this token's k and v from registers at `slot`).
+// kHeadWaves waves take positions wave + kHeadWaves p in chunks of 8 (4 for
+// head_dim 256: one chunk, or a few, per wave up to kShortSeq positions, all
+// its K and V rows loaded before any use) with a running (max, sum, output)
+// each, merged in LDS into the normalised output row (math.rs:104-118 over
+// all positions).  One launch, no partial sums: at a few hundred cached
+// positions the split kernel's second launch and its reads of the partials
+// cost more than the positions per wave here.
+constexpr uint32_t kHeadWaves = 16;
+// cached positions up to which the forward pass uses attn_rope_head_k
+constexpr uint32_t kShortSeq = 512;
+template <int E>
+__global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, float *__restrict__ out)
+{
+    constexpr uint32_t HD = 64 * E, NW = kHeadWaves, PW = E <= 2 ? 8u : 4u;   // positions per wave per chunk
+    __shared__ float sacc[NW][HD];
+    __shared__ float sml[NW][2];
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t h = blockIdx.x, kvo = (h / a.n_rep) * HD;
+    // unconditional loads; the projections are in flight while the step record arrives
+    float qv[E], kn[E], vn[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const uint32_t i = h * HD + lane + 64 * e;
+        qv[e] = a.q[i] + a.bq[i];
+        kn[e] = a.k[kvo + lane + 64 * e] + a.bk[kvo + lane + 64 * e];
+        vn[e] = a.v[kvo + lane + 64 * e] + a.bv[kvo + lane + 64 * e];
+    }
+    const uint32_t pos = a.st->pos, slot = a.st->slot, seq = slot + 1;
+    float kk[PW][E], vv[PW][E], nk[PW][E], nv[PW][E];
+    auto load = [&](uint32_t b, float (&ko)[PW][E], float (&vo)[PW][E]) {
+#pragma unroll
+        for (uint32_t p = 0; p < PW; p++) {
+            const uint32_t j = min(b + NW * p, slot);
+            const float *kr = a.kc + (size_t)j * a.kv_dim + kvo, *vr = a.vc + (size_t)j * a.kv_dim + kvo;
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                ko[p][e] = kr[lane + 64 * e];
+                vo[p][e] = vr[lane + 64 * e];
+            }
+        }
+    };
+    uint32_t base = wave;
+    load(base, kk, vv);
+    float cv[E], sv[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        cv[e] = a.cos_t[(size_t)pos * (HD / 2) + ((lane + 64 * e) >> 1)];
+        sv[e] = a.sin_t[(size_t)pos * (HD / 2) + ((lane + 64 * e) >> 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        qv[e] = rope1(qv[e], __shfl_xor(qv[e], 1, 64), lane + 64 * e, cv[e], sv[e]);
+        kn[e] = rope1(kn[e], __shfl_xor(kn[e], 1, 64), lane + 64 * e, cv[e], sv[e]);
+    }
+    if (h % a.n_rep == 0 && wave == 0) {
+        float *kr = a.kc + (size_t)slot * a.kv_dim + kvo, *vr = a.vc + (size_t)slot * a.kv_dim + kvo;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            kr[lane + 64 * e] = kn[e];
+            vr[lane + 64 * e] = vn[e];
+        }
+    }
+    float m = -INFINITY, l = 0.f, acc[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) acc[e] = 0.f;
+    for (; base < seq; base += NW * PW) {
+        const uint32_t np = min((seq - base + NW - 1) / NW, PW);   // this wave's positions in the chunk
+        if (base + NW * PW < seq) load(base + NW * PW, nk, nv);
+#pragma unroll
+        for (uint32_t p = 0; p < PW; p++)
+            if (base + NW * p == slot)
+#pragma unroll
+                for (int e = 0; e < E; e++) { kk[p][e] = kn[e]; vv[p][e] = vn[e]; }
+        float sc[PW], cm = -INFINITY;
+#pragma unroll
+        for (uint32_t p = 0; p < PW; p++) {
+            if (p >= np) break;
+            float t = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; e++) t += qv[e] * kk[p][e];
+            sc[p] = wave_sum(t) * a.scale;
+            cm = fmaxf(cm, sc[p]);
+        }
+        const float mn = fmaxf(m, cm);
+        const float al = m == -INFINITY ? 0.f : expf(m - mn);
+        float ls = 0.f, o[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) o[e] = 0.f;
+#pragma unroll
+        for (uint32_t p = 0; p < PW; p++) {
+            if (p >= np) break;
+            const float ex = expf(sc[p] - mn);
+            ls += ex;
+#pragma unroll
+            for (int e = 0; e < E; e++) o[e] += ex * vv[p][e];
+        }
+        l = l * al + ls;
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[e] = acc[e] * al + o[e];
+        m = mn;
+#pragma unroll
+        for (uint32_t p = 0; p < PW; p++)
+#pragma unroll
+            for (int e = 0; e < E; e++) { kk[p][e] = nk[p][e]; vv[p][e] = nv[p][e]; }
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) sacc[wave][lane + 64 * e] = acc[e];
+    if (lane == 0) { sml[wave][0] = m; sml[wave][1] = l; }
+    __syncthreads();
+    // merge the waves: weights exp(m_w - M) (0 for a wave without positions),
+    // derived once by the first kHeadWaves lanes, over their sum
+    __shared__ float swt[NW];
+    if (threadIdx.x < NW) {
+        const uint32_t w = threadIdx.x;
+        float mx = sml[0][0];
+#pragma unroll
+        for (uint32_t v = 1; v < NW; v++) mx = fmaxf(mx, sml[v][0]);
+        const float mw = sml[w][0];
+        const float f = mw == -INFINITY ? 0.f : expf(mw - mx);
+        float lsum = f * sml[w][1];
+#pragma unroll
+        for (uint32_t o = 1; o < NW; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
+        swt[w] = f / lsum;
+    }
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x) {
+        float sum = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < NW; w++) sum += swt[w] * sacc[w][d];
+        out[h * HD + d] = sum;
+    }
+}
+
 // One workgroup per query head for any even head_dim; LDS: hd floats of q,
 // max_seq_len floats of scores.
 __global__ void __launch_bounds__(256) attention_k(const float *__restrict__ q, const float *__restrict__ kc,
@@ -611,8 +748,13 @@ struct qg_model {
     float *pf_rec = nullptr;
     uint32_t *pf_tok = nullptr;
     uint32_t pf_s_qkv = 1, pf_s_o = 1, pf_s_gu = 1, pf_s_down = 1;
-    hipGraphExec_t g_fwd = nullptr;       // forward pass
-    hipGraphExec_t g_dec = nullptr;       // sample + advance + forward (generate)
+    // captured graphs, [1] with the short-context attention (attn_rope_head_k),
+    // [0] with the split attention; att_short selects what enqueue_forward
+    // launches
+    hipGraphExec_t g_fwd[2] = {nullptr, nullptr};   // forward pass
+    hipGraphExec_t g_dec[2] = {nullptr, nullptr};   // sample + advance + forward (generate)
+    bool att_short = false;
+    int att_path = 0;                     // qg_model_set_attention_path
     float g_dec_penalty = 0.f;
     uint32_t g_dec_window = 0;
     std::vector<void *> allocs;
@@ -645,9 +787,11 @@ template <class T> int dalloc(qg_model *m, T **p, size_t n)
 
 void drop_graphs(qg_model *m)
 {
-    if (m->g_fwd) (void)hipGraphExecDestroy(m->g_fwd);
-    if (m->g_dec) (void)hipGraphExecDestroy(m->g_dec);
-    m->g_fwd = m->g_dec = nullptr;
+    for (int i = 0; i < 2; i++) {
+        if (m->g_fwd[i]) (void)hipGraphExecDestroy(m->g_fwd[i]);
+        if (m->g_dec[i]) (void)hipGraphExecDestroy(m->g_dec[i]);
+        m->g_fwd[i] = m->g_dec[i] = nullptr;
+    }
 }
 
 void drop_fused(qg_model *m)
@@ -832,15 +976,26 @@ int enqueue_forward(qg_model *m)
             aa.part = m->att_part; aa.ml = m->att_ml; aa.st = m->d_step;
             aa.kv_dim = m->kv_dim; aa.n_rep = m->n_rep; aa.grp = m->att_grp; aa.nsplit = m->att_nsplit;
             aa.scale = scale;
-            const dim3 grid(c.n_heads / m->att_grp * m->att_nsplit);
-            if (m->hd == 64)
-                hipLaunchKernelGGL(qgm::attn_rope_split_k<1>, grid, dim3(256), 0, st, aa);
-            else if (m->hd == 128)
-                hipLaunchKernelGGL(qgm::attn_rope_split_k<2>, grid, dim3(256), 0, st, aa);
-            else
-                hipLaunchKernelGGL(qgm::attn_rope_split_k<4>, grid, dim3(256), 0, st, aa);
-            hipLaunchKernelGGL(qgm::attn_combine_k, dim3(c.n_heads), dim3(256), 0, st, m->att_part, m->att_ml,
-                               m->ao, m->d_step, m->hd, m->att_nsplit);
+            if (m->att_short) {
+                // one launch: whole heads, normalised output (short contexts)
+                const dim3 grid(c.n_heads), block(64 * qgm::kHeadWaves);
+                if (m->hd == 64)
+                    hipLaunchKernelGGL(qgm::attn_rope_head_k<1>, grid, block, 0, st, aa, m->ao);
+                else if (m->hd == 128)
+                    hipLaunchKernelGGL(qgm::attn_rope_head_k<2>, grid, block, 0, st, aa, m->ao);
+                else
+                    hipLaunchKernelGGL(qgm::attn_rope_head_k<4>, grid, block, 0, st, aa, m->ao);
+            } else {
+                const dim3 grid(c.n_heads / m->att_grp * m->att_nsplit);
+                if (m->hd == 64)
+                    hipLaunchKernelGGL(qgm::attn_rope_split_k<1>, grid, dim3(256), 0, st, aa);
+                else if (m->hd == 128)
+                    hipLaunchKernelGGL(qgm::attn_rope_split_k<2>, grid, dim3(256), 0, st, aa);
+                else
+                    hipLaunchKernelGGL(qgm::attn_rope_split_k<4>, grid, dim3(256), 0, st, aa);
+                hipLaunchKernelGGL(qgm::attn_combine_k, dim3(c.n_heads), dim3(256), 0, st, m->att_part, m->att_ml,
+                                   m->ao, m->d_step, m->hd, m->att_nsplit);
+            }
         } else {
             hipLaunchKernelGGL(qgm::qkv_post_k, dim3((pairs + 255) / 256), dim3(256), 0, st, m->q, m->k, m->v,
                                m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
@@ -922,29 +1077,45 @@ int capture(qg_model *m, int (*fn)(qg_model *), hipGraphExec_t *out)
     return QG_OK;
 }
 
-int run_forward(qg_model *m)
+// the attention path of the forward pass that writes cache slot `slot`:
+// whole heads in one launch up to kShortSeq cached positions, else split
+// over position ranges (att_path: 0 by length, 1 always whole heads, 2
+// always split)
+void pick_attention(qg_model *m, uint32_t slot)
+{
+    m->att_short = m->att_grp && (m->att_path == 1 || (m->att_path == 0 && slot + 1 <= qgm::kShortSeq));
+}
+
+int run_forward(qg_model *m, uint32_t slot)
 {
     int rc;
     if ((rc = prepare(m))) return rc;
+    pick_attention(m, slot);
     if (!m->use_graphs) return enqueue_forward(m);
-    if (!m->g_fwd && (rc = capture(m, enqueue_forward, &m->g_fwd))) return rc;
-    QGM_HIP(m, hipGraphLaunch(m->g_fwd, m->ctx->stream));
+    hipGraphExec_t &g = m->g_fwd[m->att_short ? 1 : 0];
+    if (!g && (rc = capture(m, enqueue_forward, &g))) return rc;
+    QGM_HIP(m, hipGraphLaunch(g, m->ctx->stream));
     return QG_OK;
 }
 
-int run_decode(qg_model *m, float penalty, uint32_t window)
+// slot: the cache slot of the forward pass after the sampled token
+int run_decode(qg_model *m, float penalty, uint32_t window, uint32_t slot)
 {
-    if (m->g_dec && (m->g_dec_penalty != penalty || m->g_dec_window != window)) {
-        (void)hipGraphExecDestroy(m->g_dec);
-        m->g_dec = nullptr;
-    }
+    if (m->g_dec_penalty != penalty || m->g_dec_window != window)
+        for (hipGraphExec_t &g : m->g_dec)
+            if (g) {
+                (void)hipGraphExecDestroy(g);
+                g = nullptr;
+            }
     m->g_dec_penalty = penalty;
     m->g_dec_window = window;
     int rc;
     if ((rc = prepare(m))) return rc;
+    pick_attention(m, slot);
     if (!m->use_graphs) return enqueue_decode(m);
-    if (!m->g_dec && (rc = capture(m, enqueue_decode, &m->g_dec))) return rc;
-    QGM_HIP(m, hipGraphLaunch(m->g_dec, m->ctx->stream));
+    hipGraphExec_t &g = m->g_dec[m->att_short ? 1 : 0];
+    if (!g && (rc = capture(m, enqueue_decode, &g))) return rc;
+    QGM_HIP(m, hipGraphLaunch(g, m->ctx->stream));
     return QG_OK;
 }
 
@@ -1103,7 +1274,8 @@ int prefill(qg_model *m, const uint32_t *tok, size_t n)
         return QG_OK;
     }
     for (size_t i = 0; i < n; i++) {
-        if ((rc = put_step(m, tok[i], (uint32_t)m->seq, (uint32_t)m->seq)) || (rc = run_forward(m))) return rc;
+        if ((rc = put_step(m, tok[i], (uint32_t)m->seq, (uint32_t)m->seq)) || (rc = run_forward(m, (uint32_t)m->seq)))
+            return rc;
         m->seq += 1;
     }
     return QG_OK;
@@ -1309,7 +1481,7 @@ int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits)
         return mfail(m, QG_ERR_SHAPE, "KV cache full (max_seq_len)");   // kv_cache.rs:54-59
     QGM_HIP(m, hipSetDevice(m->ctx->device));
     int rc;
-    if ((rc = put_step(m, token, pos, (uint32_t)m->seq)) || (rc = run_forward(m))) return rc;
+    if ((rc = put_step(m, token, pos, (uint32_t)m->seq)) || (rc = run_forward(m, (uint32_t)m->seq))) return rc;
     m->seq += 1;
     if (logits) {
         QGM_HIP(m, hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float),
@@ -1343,6 +1515,13 @@ int qg_model_use_batched_prefill(qg_model *m, int enable)
 {
     if (!m) return QG_ERR_INVALID_ARG;
     m->pf_batched = enable != 0;
+    return QG_OK;
+}
+
+int qg_model_set_attention_path(qg_model *m, int path)
+{
+    if (!m || path < 0 || path > 2) return QG_ERR_INVALID_ARG;
+    m->att_path = path;
     return QG_OK;
 }
 
@@ -1399,7 +1578,7 @@ int qg_model_generate(qg_model *m, const uint32_t *prompt, size_t n_prompt, size
     } else {
         if ((rc = put_step(m, prompt[0], 0, 0))) return rc;
         for (size_t p = 0; p < n_prompt; p++) {
-            if ((rc = run_forward(m))) return rc;
+            if ((rc = run_forward(m, (uint32_t)p))) return rc;
             if (p + 1 < n_prompt) {
                 hipLaunchKernelGGL(qgm::advance_k, dim3(1), dim3(64), 0, st, m->d_step, m->d_hist);
                 if ((rc = launched(m, "advance"))) return rc;
@@ -1409,7 +1588,7 @@ int qg_model_generate(qg_model *m, const uint32_t *prompt, size_t n_prompt, size
     QGM_HIP(m, hipStreamSynchronize(st));
     auto t1 = clk::now();
     for (size_t s = 0; s < n_new; s++)
-        if ((rc = run_decode(m, penalty, win))) return rc;
+        if ((rc = run_decode(m, penalty, win, (uint32_t)(n_prompt + s)))) return rc;
     QGM_HIP(m, hipStreamSynchronize(st));
     auto t2 = clk::now();
     m->seq = n_prompt + n_new;

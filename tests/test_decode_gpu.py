@@ -151,6 +151,41 @@ def test_long_ranges(rinf, synth, oracle, ctx, embed):
     dev.close()
 
 
+@pytest.mark.parametrize("path", [1, 2], ids=["whole-heads", "split"])
+@pytest.mark.parametrize("embed", [256, 512, 1024], ids=["hd64", "hd128", "hd256"])
+def test_attention_paths(rinf, synth, oracle, ctx, path, embed):
+    """Both attention kernels of the decode step (qg_model_set_attention_path:
+    whole query heads in one launch, or position ranges then a merge) against
+    the oracle at the same lengths, for head_dim 64, 128 and 256: 70 prompt
+    positions, then 10 greedy steps."""
+    cfg = dict(SMALL, n_layers=1, embed_dim=embed, hidden_dim=2 * embed)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q8_0", 29, 96)
+    dev.set_attention_path(path)
+    prompt = np.random.default_rng(14).integers(0, cfg["vocab_size"], 70)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 10)
+    print(f"path {path} hd {embed // 4}: max logits err {max(errs):.2e}", flush=True)
+    assert max(errs) <= LOGIT_TOL
+    dev.close()
+
+
+def test_attention_path_switch_in_generate(rinf, synth, oracle, ctx):
+    """A generation across the 512-position boundary (505 prompt tokens, 14
+    new): the decode graph changes from whole-head to split attention
+    mid-run.  The tokens equal those of the step-by-step run, which follows
+    the oracle within DEEP_TOL."""
+    cfg = dict(SMALL, n_layers=1)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", 31, 540)
+    prompt = np.random.default_rng(13).integers(0, cfg["vocab_size"], 505)
+    toks, _, _ = dev.generate(prompt, 14)
+    dev.reset()
+    ref.reset()
+    step, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 14)
+    print(f"switch: max logits err {max(errs):.2e}", flush=True)
+    assert list(toks) == step
+    assert max(errs) <= DEEP_TOL
+    dev.close()
+
+
 @pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m"])
 def test_qwen2_7b_layer_shape(rinf, synth, oracle, ctx, mix):
     """One layer of the Qwen2-7B shape: [Q;K] (Q4_K or Q5_K) and V (Q6_K) in
