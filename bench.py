@@ -227,6 +227,7 @@ def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new
     toks, pre_s, dec_s = dev.generate(prompt, n_new)
     dev.use_batched_prefill(False)
     _, pre_tt_s, _ = dev.generate(prompt, 1)
+    rb = dev.resident_bytes()
     dev.close()
     if shared is not None:
         shared.free()
@@ -239,7 +240,9 @@ def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new
     per_tok = wbytes + kv_bytes
     log(f"decode {arch} {mix}: {tok_s:.1f} tok/s ({dec_s * 1e3 / n_new:.3f} ms/token), "
         f"{per_tok / 1e9:.3f} GB/token -> {per_tok * tok_s / 1e9:.1f} GB/s; prefill "
-        f"{n_prompt / pre_s:.1f} tok/s (token by token {n_prompt / pre_tt_s:.1f}); set-up {setup_s:.1f} s")
+        f"{n_prompt / pre_s:.1f} tok/s (token by token {n_prompt / pre_tt_s:.1f}); set-up {setup_s:.1f} s; "
+        f"weights resident {rb['weights'] / 1e9:.3f} GB = {rb['weights'] / rb['file_bytes']:.4f} x the file's "
+        f"{rb['file_bytes'] / 1e9:.3f} GB, device total {rb['total'] / 1e9:.3f} GB")
     return {"model": f"{arch} ({mix}, random init, synthetic)",
             "prompt_tokens": n_prompt, "decode_tokens": n_new,
             "tok_s": round(tok_s, 2), "ms_per_token": round(dec_s * 1e3 / n_new, 4),
@@ -248,6 +251,9 @@ def decode_run(rinf, synth, ctx, args, arch=None, mix=None, n_prompt=None, n_new
             "bytes_per_token": int(per_tok), "weight_bytes_per_token": int(wbytes),
             "achieved_GBs": round(per_tok * tok_s / 1e9, 2),
             "frac_of_8TBs": round(per_tok * tok_s / 8e12, 4),
+            "resident_weight_bytes": rb["weights"], "file_weight_bytes": rb["file_bytes"],
+            "resident_over_file": round(rb["weights"] / rb["file_bytes"], 4),
+            "resident_total_bytes": rb["total"],
             "first_tokens": [int(v) for v in toks[:8]]}
 
 

@@ -105,6 +105,17 @@ int qg_model_use_batched_prefill(qg_model *m, int enable);
  * position ranges and merged beyond; 1 always whole heads; 2 always split.
  * Both compute attention.rs:93-121; they differ in summation order only. */
 int qg_model_set_attention_path(qg_model *m, int path);
+/* No counterpart in the reference (memory accounting): device bytes the
+ * model reads.  weights: every distinct matrix it uses (token_embd, lm_head,
+ * layer matrices, the stacked [Q;K;V] / [gate; up] matrices the decode step
+ * builds), each counted with the copies it holds (tail pads included);
+ * file_bytes: the quantized bytes of its slots (what a GGUF file holds for
+ * them); total: weights plus the norms, biases, KV caches, RoPE tables and
+ * activation buffers.  Uploaded Q8_0/Q4_K/Q5_K/Q6_K matrices are held once,
+ * in the repacked layout; layer parts the model owns are views into their
+ * stacked matrix; token_embd is held in the GGUF layout (and repacked too
+ * only when it is also the lm_head).  Any output may be NULL. */
+int qg_model_resident_bytes(qg_model *m, size_t *weights, size_t *file_bytes, size_t *total);
 
 /* Greedy Sampler::sample on the device logits of the last forward:
  * repetition penalty over `recent` (the last `window` entries, applied in

@@ -126,6 +126,7 @@ _SIGS = {
     "qg_model_prefill": (ctypes.c_int, [_P, _P, _SZ, _P]),
     "qg_model_use_batched_prefill": (ctypes.c_int, [_P, ctypes.c_int]),
     "qg_model_set_attention_path": (ctypes.c_int, [_P, ctypes.c_int]),
+    "qg_model_resident_bytes": (ctypes.c_int, [_P, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "qg_model_sample_greedy": (ctypes.c_int, [_P, _P, _SZ, ctypes.c_float, _SZ, ctypes.POINTER(_U32)]),
     "qg_model_generate": (ctypes.c_int, [_P, _P, _SZ, _SZ, ctypes.c_float, _SZ, _P,
                                          ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
@@ -577,6 +578,13 @@ class DeviceModel:
     def use_batched_prefill(self, enable: bool):
         self.ctx.check(self.ctx.lib.qg_model_use_batched_prefill(self.h, int(bool(enable))),
                        "qg_model_use_batched_prefill")
+
+    def resident_bytes(self) -> dict:
+        """Device bytes: {"weights", "file_bytes", "total"} (qg_model_resident_bytes)."""
+        w, f, t = _SZ(), _SZ(), _SZ()
+        self.ctx.check(self.ctx.lib.qg_model_resident_bytes(self.h, ctypes.byref(w), ctypes.byref(f), ctypes.byref(t)),
+                       "qg_model_resident_bytes")
+        return {"weights": w.value, "file_bytes": f.value, "total": t.value}
 
     def set_attention_path(self, path: int):
         """0: by length (whole heads up to 512 cached positions, else split),

@@ -83,6 +83,9 @@ bool repack_eligible(uint32_t type, const Plan &p, size_t rows);
 // dst = the repacked layout of src's n_groups row groups (same size); both
 // device pointers; asynchronous.
 int launch_repack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst, ihipStream_t *stream);
+// dst = the GGUF layout of the repacked src (the inverse of launch_repack;
+// p: the repacked plan, p.rp)
+int launch_unrepack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst, ihipStream_t *stream);
 int launch_gemv(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows,
                 size_t cols, const float *x, float *y, ihipStream_t *stream);
 // y = W · (rmsnorm(xa + xb) * nw) with the stream kernel (kind 1 plans only;
@@ -130,12 +133,17 @@ int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
 // slice 0, and its consumer sums the slices.
 constexpr uint32_t kPfMaxTokens = 64;
 bool prefill_type_supported(uint32_t type);
-// one matrix of a grouped prefill GEMM: y[t * ldy + r] (+ s * sstride)
+// one matrix of a grouped prefill GEMM: y[t * ldy + r] (+ s * sstride); w in
+// the GGUF layout, or (rp) in the repacked layout of launch_repack with g
+// rows, ni items and gb bytes per row group
 struct PfMat {
     uint32_t type;
     const uint8_t *w;
     size_t rows;
     float *y;
+    bool rp;
+    uint32_t g, ni;
+    size_t gb;
 };
 uint32_t pf_tiles(size_t rows);
 // slices of the K split of a GEMM over `tiles` row tiles and nseg sub-blocks

@@ -17,19 +17,29 @@ struct qg_model;
 
 struct qg_mat {
     qg_ctx *ctx;
-    uint8_t *d;        // device bytes in the GGUF layout (nbytes data + kTailPad zeros)
+    uint8_t *d;        // device bytes in the GGUF layout (nbytes data + kTailPad zeros), or NULL:
+                       // an owned repacked matrix keeps only d_rp (qg_mat_gguf rebuilds the
+                       // GGUF layout where a kernel needs it; qg_mat_keep_gguf keeps it)
     uint8_t *d_rp;     // the matrix in the repacked layout (owned Q8_0/Q4_K/Q5_K/Q6_K), or NULL
     size_t nbytes;     // bytes the kernels may treat as data
     uint32_t type;
     size_t rows, cols;
     bool owned;
+    bool rp_view = false;  // d_rp points into a stacked matrix's repacked copy (not owned)
     int shares = 0;    // decode-step models using this matrix without owning it
     qg::Plan plan;     // plan.rp: the stream kernels read d_rp
 };
 
 // The bytes the stream GEMV kernels read (the dequant and generic kernels
-// always read d).
+// read the GGUF layout: d, or qg_mat_gguf).
 inline const uint8_t *qg_gemv_bytes(const qg_mat *m) { return m->plan.rp ? m->d_rp : m->d; }
+
+// Device bytes of the matrix (both layouts it holds, tail pads included).
+inline size_t qg_mat_resident(const qg_mat *m)
+{
+    const size_t one = m->nbytes + qg::kTailPad;
+    return (m->owned && m->d ? one : 0) + (m->d_rp && !m->rp_view ? one : 0);
+}
 
 struct qg_ctx {
     int device = 0;
@@ -44,6 +54,8 @@ struct qg_ctx {
     size_t d_norm_cap = 0;
     float *d_glu = nullptr;                 // gate and up outputs of qg_matvec_norm_glu_dev's unfused path
     size_t d_glu_cap = 0;
+    float *d_xal = nullptr;                 // 16-byte aligned copy of an unaligned x (repacked-only matrices)
+    size_t d_xal_cap = 0;
     // device address of this GPU's static scratch array (qg_matvec_norm_glu_dev_noalloc),
     // resolved once in qg_init; NULL if the runtime could not resolve it
     float *d_static_scratch = nullptr;
@@ -74,6 +86,16 @@ inline bool qg_alloc_injected(qg_ctx *ctx)
 
 // check_mat of the C ABI: ctx valid and mat one of its live matrices.
 int qg_check_mat(qg_ctx *ctx, const qg_mat *mat);
+
+// The matrix in the GGUF layout: *out = mat->d (*temp = false), or a new
+// device allocation (nbytes + kTailPad, *temp = true, the caller frees it)
+// rebuilt from the repacked copy.  Synchronous.
+int qg_mat_gguf(qg_ctx *ctx, const qg_mat *mat, uint8_t **out, bool *temp);
+// Keep a GGUF-layout copy (rebuilt from the repacked copy if d is NULL).
+int qg_mat_keep_gguf(qg_ctx *ctx, qg_mat *mat);
+// Drop the repacked copy of a matrix that keeps its GGUF layout (the kernels
+// of the GGUF layout serve it from then on).
+int qg_mat_drop_repacked(qg_ctx *ctx, qg_mat *mat);
 
 // The model-owned or shared matrix `mat` is no longer used by a model slot.
 int qg_mat_release(qg_ctx *ctx, qg_mat *mat, bool owned);
@@ -115,6 +137,17 @@ int qg_norm_pair_matvec(qg_ctx *ctx, const qg_mat *m1, const qg_mat *m2, const f
 // type and cols; every part but the last a whole number of blocks): device
 // copies of the parts' blocks, one after the other.  Synchronous.
 int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out);
+
+// The same stacked matrix without a second copy of the parts: parts that
+// hold only a repacked copy (not a view), all with one row-group layout
+// (same g, ni, group_bytes; whole groups), are copied into one allocation
+// -- the repacked layout of stacked rows is the parts' repacked bytes one
+// after the other -- and become views into it (rp_view; their own copies
+// are freed).  QG_ERR_SHAPE (nothing changed) when the parts do not qualify.
+// Synchronous.
+int qg_stack_views(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out);
+// A view part gets its own repacked copy again (before its stack is freed).
+int qg_mat_unview(qg_ctx *ctx, qg_mat *mat);
 
 // lm_head = the model's token_embd device matrix (a tied output, model.rs:224-226).
 int qg_model_tie_lm_head(qg_model *m);

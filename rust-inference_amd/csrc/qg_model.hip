@@ -758,6 +758,7 @@ struct qg_model {
     float g_dec_penalty = 0.f;
     uint32_t g_dec_window = 0;
     std::vector<void *> allocs;
+    size_t alloc_bytes = 0;               // device bytes of allocs
 };
 
 namespace {
@@ -781,6 +782,7 @@ template <class T> int dalloc(qg_model *m, T **p, size_t n)
     e = hipMemset(d, 0, (n ? n : 1) * sizeof(T));
     if (e != hipSuccess) { (void)hipFree(d); return mfail(m, QG_ERR_HIP, "hipMemset", e); }
     m->allocs.push_back(d);
+    m->alloc_bytes += (n ? n : 1) * sizeof(T);
     *p = (T *)d;
     return QG_OK;
 }
@@ -794,12 +796,48 @@ void drop_graphs(qg_model *m)
     }
 }
 
-void drop_fused(qg_model *m)
+// Frees the stacked matrices.  Parts that are views into them (qg_stack_views)
+// first get their own copies back (restore), unless the model is being freed
+// with them.
+int drop_fused(qg_model *m, bool restore = true)
 {
-    for (qg_mat *&p : m->f_qkv) if (p) { qg_mat_free(m->ctx, p); p = nullptr; }
-    for (qg_mat *&p : m->f_gu) if (p) { qg_mat_free(m->ctx, p); p = nullptr; }
+    int rc = QG_OK;
+    for (size_t l = 0; l < m->f_qkv.size(); l++) {
+        if (m->f_qkv[l]) {
+            for (int i = 0; i < m->f_qkv_n[l] && restore; i++) {
+                const int r = qg_mat_unview(m->ctx, m->w[QG_M_WQ - 2 + i][l]);
+                rc = rc ? rc : r;
+            }
+            qg_mat_free(m->ctx, m->f_qkv[l]);
+            m->f_qkv[l] = nullptr;
+        }
+        if (m->f_gu[l]) {
+            for (int s : {QG_M_GATE - 2, QG_M_UP - 2})
+                if (restore) {
+                    const int r = qg_mat_unview(m->ctx, m->w[s][l]);
+                    rc = rc ? rc : r;
+                }
+            qg_mat_free(m->ctx, m->f_gu[l]);
+            m->f_gu[l] = nullptr;
+        }
+    }
     for (uint8_t &n : m->f_qkv_n) n = 0;
     m->fused_ready = false;
+    return rc;
+}
+
+// One stacked matrix of parts (owned[i]: the model owns part i): the parts
+// become views into it when the model owns them all and their layout allows
+// (no second copy), else a stacked copy beside them.
+int stack_parts(qg_model *m, qg_mat *const *parts, const bool *owned, int n, qg_mat **out)
+{
+    bool all = true;
+    for (int i = 0; i < n; i++) all = all && owned[i];
+    if (all) {
+        const int rc = qg_stack_views(m->ctx, parts, n, out);
+        if (rc != QG_ERR_SHAPE) return rc;
+    }
+    return qg_stack_mats(m->ctx, parts, n, out);
 }
 
 // parts stack into one matrix: same type and cols, all but the last a whole
@@ -815,15 +853,25 @@ bool stackable(qg_mat *const *p, int n)
 
 int prepare(qg_model *m)
 {
+    // the embedding rows are read in the GGUF layout (dequantize_row); a
+    // token_embd the model owns that is not also the lm_head needs no
+    // repacked copy
+    if (m->tok) {
+        int rc;
+        if ((rc = qg_mat_keep_gguf(m->ctx, m->tok))) return rc;
+        if (m->tok_owned && m->lm != m->tok && m->tok->d_rp && (rc = qg_mat_drop_repacked(m->ctx, m->tok))) return rc;
+    }
     if (m->fused_ready) return QG_OK;
     for (uint32_t l = 0; l < m->cfg.n_layers; l++) {
         qg_mat *qkv[3] = {m->w[QG_M_WQ - 2][l], m->w[QG_M_WK - 2][l], m->w[QG_M_WV - 2][l]};
         const int n = stackable(qkv, 3) ? 3 : stackable(qkv, 2) ? 2 : 0;
+        const bool oq[3] = {m->owned[QG_M_WQ - 2][l], m->owned[QG_M_WK - 2][l], m->owned[QG_M_WV - 2][l]};
         int rc;
-        if (n && (rc = qg_stack_mats(m->ctx, qkv, n, &m->f_qkv[l]))) return rc;
+        if (n && (rc = stack_parts(m, qkv, oq, n, &m->f_qkv[l]))) return rc;
         m->f_qkv_n[l] = (uint8_t)n;
         qg_mat *gu[2] = {m->w[QG_M_GATE - 2][l], m->w[QG_M_UP - 2][l]};
-        if (stackable(gu, 2) && (rc = qg_stack_mats(m->ctx, gu, 2, &m->f_gu[l]))) return rc;
+        const bool og[2] = {m->owned[QG_M_GATE - 2][l], m->owned[QG_M_UP - 2][l]};
+        if (stackable(gu, 2) && (rc = stack_parts(m, gu, og, 2, &m->f_gu[l]))) return rc;
     }
     m->fused_ready = true;
     return QG_OK;
@@ -836,7 +884,7 @@ void free_model(qg_model *m)
 {
     m->ctx->models.erase(m);
     drop_graphs(m);
-    drop_fused(m);
+    (void)drop_fused(m, false);
     for (int s = 0; s < kSlots; s++)
         for (size_t l = 0; l < m->w[s].size(); l++)
             qg_mat_release(m->ctx, m->w[s][l], m->owned[s][l]);
@@ -1179,7 +1227,13 @@ int pf_gemm(qg_model *m, const qg::PfMat *mats, int n, size_t cols, uint32_t nto
     return r ? mfail(m, QG_ERR_HIP, "prefill GEMM launch", hipGetLastError()) : QG_OK;
 }
 
-qg::PfMat pf_mat(const qg_mat *mat, float *y) { return qg::PfMat{mat->type, mat->d, mat->rows, y}; }
+// a layer matrix for the prefill GEMM: its GGUF-layout bytes, or its
+// repacked copy (an uploaded matrix keeps only that)
+qg::PfMat pf_mat(const qg_mat *mat, float *y)
+{
+    if (mat->d) return qg::PfMat{mat->type, mat->d, mat->rows, y, false, 0, 0, 0};
+    return qg::PfMat{mat->type, mat->d_rp, mat->rows, y, true, mat->plan.g, mat->plan.ni, (size_t)mat->plan.group_bytes};
+}
 
 // bf16 pieces of x = f(a, b) for the chunk's tokens; a and b of na / nb slices
 // kPfMaxTokens * lda floats apart
@@ -1408,7 +1462,10 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
     if (rc) return rc;
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
-    drop_fused(m);
+    if ((rc = drop_fused(m))) {
+        qg_mat_free(m->ctx, mat);
+        return rc;
+    }
     put_slot(m, which, layer, mat, false);
     return QG_OK;
 }
@@ -1425,7 +1482,8 @@ int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_
     if (per_layer && layer >= m->cfg.n_layers) return mfail(m, QG_ERR_INVALID_ARG, "layer");
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
-    drop_fused(m);
+    int rc;
+    if ((rc = drop_fused(m))) return rc;
     put_slot(m, which, layer, const_cast<qg_mat *>(mat), true);
     return QG_OK;
 }
@@ -1515,6 +1573,30 @@ int qg_model_use_batched_prefill(qg_model *m, int enable)
 {
     if (!m) return QG_ERR_INVALID_ARG;
     m->pf_batched = enable != 0;
+    return QG_OK;
+}
+
+int qg_model_resident_bytes(qg_model *m, size_t *weights, size_t *file_bytes, size_t *total)
+{
+    if (!m) return QG_ERR_INVALID_ARG;
+    int rc;
+    if (complete(m) && (rc = prepare(m))) return rc;
+    std::set<const qg_mat *> mats;
+    size_t w = 0, f = 0;
+    auto add = [&](const qg_mat *p, bool slot) {
+        if (!p) return;
+        if (slot) f += p->nbytes;
+        if (mats.insert(p).second) w += qg_mat_resident(p);
+    };
+    add(m->tok, true);
+    if (!lm_alias(m)) add(m->lm, true);
+    for (int s = 0; s < kSlots; s++)
+        for (const qg_mat *p : m->w[s]) add(p, true);
+    for (const qg_mat *p : m->f_qkv) add(p, false);
+    for (const qg_mat *p : m->f_gu) add(p, false);
+    if (weights) *weights = w;
+    if (file_bytes) *file_bytes = f;
+    if (total) *total = w + m->alloc_bytes;
     return QG_OK;
 }
 

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "qg_common.h"
 
@@ -148,6 +149,21 @@ template <> struct PfW<T_Q4_K> {
         mul[0] = 16.0f * (h2f(r.head.x) * sc);
         add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
     }
+    // the repacked row group G (the library's repack_k layout: the nb = ni/2
+    // block heads, then piece k' (16 bytes) of item it at 16 nb + (k' ni + it)
+    // 16; item it = the quant bytes 64 (it & 1) .. +64 of block it / 2): the
+    // same registers as load
+    using RawR = Raw;
+    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t j, uint32_t kq, uint32_t ni)
+    {
+        const uint32_t it = 2u * b + (j >> 2), kp = 2u * ((j >> 1) & 1u) + (kq >> 1);
+        return Raw{*(const uint4 *)(G + 16u * b), *(const uint2 *)(G + 8u * ni + (kp * ni + it) * 16u + 8u * (kq & 1u))};
+    }
+    __device__ static void decode_rp(const RawR &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
+                                     float (&add)[2])
+    {
+        decode(r, j, kq, bq, mul, add);
+    }
 };
 
 // Q5_K (quant.rs:231-262): as Q4_K with a fifth bit, bit j of qh[l].
@@ -170,6 +186,38 @@ template <> struct PfW<T_Q5_K> {
         const uint32_t sh = (j & 1u) * 4u;
         const uint32_t c0 = ((r.v.x >> sh) & 0x0F0F0F0Fu) | (((r.h.x >> j) & 0x01010101u) << 4);
         const uint32_t c1 = ((r.v.y >> sh) & 0x0F0F0F0Fu) | (((r.h.y >> j) & 0x01010101u) << 4);
+        bq[0] = kquant_b<5>(c0, c1, true);
+        float sc, m;
+        k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
+        mul[0] = 32.0f * (h2f(r.head.x) * sc);
+        add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
+    }
+    // the repacked row group G (repack_k: the nb = ni/4 block heads, piece k'
+    // of item it's 32 quant bytes at 16 nb + (k' ni + it) 16, then 8 bytes per
+    // item at 16 nb + 32 ni + 8 it: bits 8 bb + 2 t' + q of word w are bit
+    // 2 (it & 3) + q of qh[16 w + 4 t' + bb]; item it = block it / 4, sub-blocks
+    // 2 (it & 3) and 2 (it & 3) + 1)
+    struct RawR {
+        uint4 head;
+        uint2 v;
+        uint32_t w;
+    };
+    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t j, uint32_t kq, uint32_t ni)
+    {
+        const uint32_t it = 4u * b + (j >> 1), H = 4u * ni;             // 16 nb
+        return RawR{*(const uint4 *)(G + 16u * b),
+                    *(const uint2 *)(G + H + ((kq >> 1) * ni + it) * 16u + 8u * (kq & 1u)),
+                    *(const uint32_t *)(G + H + 32u * ni + 8u * it + 4u * (kq >> 1))};
+    }
+    __device__ static void decode_rp(const RawR &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
+                                     float (&add)[2])
+    {
+        // code 8 kq + e: qh byte 16 w + 4 t' + bb with w = kq / 2, t' =
+        // 2 (kq & 1) + e / 4, bb = e % 4, so its bit j sits at 8 (e % 4) + s
+        // (+ 2 for e >= 4), s = 4 (kq & 1) + (j & 1)
+        const uint32_t sh = (j & 1u) * 4u, s = 4u * (kq & 1u) + (j & 1u);
+        const uint32_t c0 = ((r.v.x >> sh) & 0x0F0F0F0Fu) | (((r.w >> s) & 0x01010101u) << 4);
+        const uint32_t c1 = ((r.v.y >> sh) & 0x0F0F0F0Fu) | (((r.w >> (s + 2u)) & 0x01010101u) << 4);
         bq[0] = kquant_b<5>(c0, c1, true);
         float sc, m;
         k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
@@ -230,6 +278,41 @@ template <> struct PfW<T_Q6_K> {
         add[0] = -32.0f * m0 - mul[0];
         add[1] = -32.0f * m1 - mul[1];
     }
+    // the repacked row group G (repack_k: item it = block it/4, half
+    // n = (it/2) & 1, i = it & 1 -- l in 16 i .. 16 i + 15 of the half;
+    // ql[64n+16i..+16] at 16 it, ql[64n+32+16i..+16] at 16 (ni + it),
+    // qh[32n+16i..+16] at 16 (2 ni + it), sc[8n+i+2k] at 48 ni + 4 it + k, d
+    // at 52 ni + 2 b)
+    struct RawR {
+        uint2 ql, qh, sc;
+        uint32_t d;
+    };
+    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t j, uint32_t kq, uint32_t ni)
+    {
+        const uint32_t n = j >> 2, k4 = j & 3u, it0 = 4u * b + 2u * n, it = it0 + (kq >> 1);
+        return RawR{*(const uint2 *)(G + ((k4 & 1u) * ni + it) * 16u + 8u * (kq & 1u)),
+                    *(const uint2 *)(G + (2u * ni + it) * 16u + 8u * (kq & 1u)),
+                    *(const uint2 *)(G + 48u * ni + 4u * it0),          // scales of items it0, it0 + 1
+                    (uint32_t)*(const uint16_t *)(G + 52u * ni + 2u * b)};
+    }
+    __device__ static void decode_rp(const RawR &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
+                                     float (&add)[2])
+    {
+        const uint32_t k4 = j & 3u, sl = (k4 >> 1) * 4u, shh = 2u * k4;
+        const uint32_t c0 = ((r.ql.x >> sl) & 0x0F0F0F0Fu) | (((r.qh.x >> shh) & 0x03030303u) << 4);
+        const uint32_t c1 = ((r.ql.y >> sl) & 0x0F0F0F0Fu) | (((r.qh.y >> shh) & 0x03030303u) << 4);
+        const bool lo = kq < 2u;                                      // codes 0..15 of the sub-block
+        bq[0] = kquant_b<6>(c0, c1, lo);
+        bq[1] = kquant_b<6>(c0, c1, !lo);
+        const float d = h2f(r.d);
+        // sc[8n + 2k4] (l < 16: item it0) and sc[8n + 2k4 + 1] (item it0 + 1)
+        const float m0 = d * (float)(int8_t)((r.sc.x >> (8u * k4)) & 0xFFu);
+        const float m1 = d * (float)(int8_t)((r.sc.y >> (8u * k4)) & 0xFFu);
+        mul[0] = 64.0f * m0;
+        mul[1] = 64.0f * m1;
+        add[0] = -32.0f * m0 - mul[0];
+        add[1] = -32.0f * m1 - mul[1];
+    }
 };
 
 // Q8_0 (quant.rs:106-113): one 34-byte block (2-byte aligned) per sub-block,
@@ -254,6 +337,26 @@ template <> struct PfW<T_Q8_0> {
         const uint32_t sb = r.sb, sq = (sb + 2u) & 3u;
         bq[0] = signed_bf16(abyte(r.q[1], r.q[0], sq), abyte(r.q[2], r.q[1], sq));
         mul[0] = h2f(r.d >> (8 * sb));
+        add[0] = 0.0f;
+    }
+    // the repacked row group G (repack_k: item it = blocks 2 it, 2 it + 1;
+    // piece k' (codes 16 k' .. +16) at (k' ni + it) 16, the two d halves at
+    // 64 ni + 4 it)
+    struct RawR {
+        uint2 q;
+        uint32_t d;
+    };
+    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t, uint32_t kq, uint32_t ni)
+    {
+        const uint32_t it = b >> 1, kp = 2u * (b & 1u) + (kq >> 1);
+        return RawR{*(const uint2 *)(G + (kp * ni + it) * 16u + 8u * (kq & 1u)),
+                    (uint32_t)*(const uint16_t *)(G + 64u * ni + 4u * it + 2u * (b & 1u))};
+    }
+    __device__ static void decode_rp(const RawR &r, uint32_t, uint32_t, uint4 (&bq)[2], float (&mul)[2],
+                                     float (&add)[2])
+    {
+        bq[0] = signed_bf16(r.q.x, r.q.y);
+        mul[0] = h2f(r.d);
         add[0] = 0.0f;
     }
 };
@@ -319,37 +422,47 @@ __device__ __forceinline__ void pf_stage(const uint16_t *__restrict__ xp, const 
 // f = 0: sum x, 1: sum x[0..16), 2: sum x[16..32).  Chunks of kPfKC
 // sub-blocks are copied into two LDS buffers in turn, the next chunk's copy
 // and weight loads in flight while this one is computed.  D[4 kq + i][c16]
-// of an MFMA is token 16 tt + 4 kq + i of row r0 + c16.  AL: every row
-// starts a block (nseg % 8 == 0, or single-sub-block blocks), so the
-// sub-block index within the block is the same in every lane.
-template <uint32_t T, int R, bool AL>
+// of an MFMA is token 16 tt + 4 kq + i of row r0 + c16.  LAY, the weight
+// layout: 0 GGUF, rows straddling blocks; 1 GGUF, every row starts a block
+// (nseg % 8 == 0, or single-sub-block blocks), so the sub-block index within
+// the block is the same in every lane; 2 repacked (repack_k), one row per
+// row group; 3 repacked, gg rows per group of gb bytes (ni items).
+template <uint32_t T, int R, int LAY>
 __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint32_t rows, uint32_t row0,
                                              uint32_t nseg, uint32_t k0, uint32_t k1,
                                              const uint16_t *__restrict__ xp, const float *__restrict__ rec,
                                              uint32_t ntok, uint32_t n, uint8_t *lds, float *__restrict__ y,
-                                             uint32_t ldy)
+                                             uint32_t ldy, uint32_t gg, uint64_t gb, uint32_t ni)
 {
     using P = PfW<T>;
-    using Raw = typename P::Raw;
+    constexpr bool RPL = LAY >= 2, AL = LAY != 0;
+    using Raw = std::conditional_t<RPL, typename P::RawR, typename P::Raw>;
     constexpr bool SB1 = T == T_Q8_0;                                 // one sub-block per block
     const uint32_t lane = threadIdx.x & 63u, kq = lane >> 4, c16 = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
     const bool active = row0 < rows;                                  // wave-uniform
     const uint32_t swz = kq ^ pf_swz(c16);                           // this lane's slot position
-    // per row tile: the flat index of the row's first sub-block, and (AL) its
-    // first block
+    // per row tile: GGUF, the flat index of the row's first sub-block and
+    // (AL) its first block; repacked, the row's sub-block offset in its row
+    // group and the group
     uint64_t fb[R];
     const uint8_t *rb[R];
 #pragma unroll
     for (int i = 0; i < R; i++) {
-        fb[i] = (uint64_t)min(row0 + 16u * i + c16, rows - 1u) * nseg;
-        rb[i] = w + (SB1 ? fb[i] : fb[i] / 8u) * P::BB;
+        const uint32_t r = min(row0 + 16u * i + c16, rows - 1u);
+        if constexpr (RPL) {
+            fb[i] = LAY == 2 ? 0u : (uint64_t)(r % gg) * nseg;
+            rb[i] = w + (size_t)(LAY == 2 ? r : r / gg) * gb;
+        } else {
+            fb[i] = (uint64_t)r * nseg;
+            rb[i] = w + (SB1 ? fb[i] : fb[i] / 8u) * P::BB;
+        }
     }
     // sub-block k of row tile i: its index in its block, and the block
     auto subj = [&](int i, uint32_t k) -> uint32_t {
         if constexpr (SB1) return 0u;
-        else if constexpr (AL) return k & 7u;
+        else if constexpr (AL && LAY != 3) return k & 7u;
         else return ((uint32_t)fb[i] + k) & 7u;
     };
     auto block = [&](int i, uint32_t k) -> const uint8_t * {
@@ -359,9 +472,14 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
     };
     // weights of sub-block k (clamped into the slice: the loads past its end
     // are harmless repeats, unconditional so that none waits on a branch)
-    auto wload = [&](int i, uint32_t k) {
+    auto wload = [&](int i, uint32_t k) -> Raw {
         const uint32_t kc = min(k, k1 - 1u);
-        return P::load(block(i, kc), subj(i, kc), kq);
+        if constexpr (RPL) {
+            const uint32_t f = (uint32_t)fb[i] + kc;                 // sub-block in the row group
+            return P::load_rp(rb[i], SB1 ? f : f >> 3, f & 7u, kq, ni);
+        } else {
+            return P::load(block(i, kc), subj(i, kc), kq);
+        }
     };
     v4f acc[R][4];
 #pragma unroll
@@ -397,7 +515,10 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             uint4 bq[R][2];
             float mul[R][2];
 #pragma unroll
-            for (int i = 0; i < R; i++) P::decode(raw[kk][i], subj(i, kc + kk), kq, bq[i], mul[i], addv[i][kk]);
+            for (int i = 0; i < R; i++) {
+                if constexpr (RPL) P::decode_rp(raw[kk][i], subj(i, kc + kk), kq, bq[i], mul[i], addv[i][kk]);
+                else P::decode(raw[kk][i], subj(i, kc + kk), kq, bq[i], mul[i], addv[i][kk]);
+            }
 #pragma unroll
             for (int i = 0; i < R; i++) raw[kk][i] = wload(i, kc + kPfKC + kk);
             if (!active) continue;
@@ -469,6 +590,8 @@ struct PfJob {
     const uint8_t *w;
     float *y;
     uint32_t type, rows, tiles;
+    uint32_t g, ni;        // repacked layout: rows per row group, items per group
+    uint64_t gb;           // ... and bytes per group
 };
 struct PfJobs {
     PfJob j0, j1, j2;
@@ -480,7 +603,7 @@ struct PfJobs {
 // sub-blocks; slice s of a job writes its partial products to
 // y + s * sstride (the consumer sums the slices in order s = 0, 1, ...).
 // 4 waves of 16 kPfR rows per workgroup.
-template <uint32_t T, bool AL>
+template <uint32_t T, int LAY>
 __global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t nseg, uint32_t sps,
                                                  const uint16_t *__restrict__ xp, const float *__restrict__ rec,
                                                  uint32_t ntok, uint32_t n, uint32_t ldy, uint64_t sstride)
@@ -498,8 +621,8 @@ __global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t
     }
     const uint32_t row0 = tile * kPfRows + (threadIdx.x >> 6) * (16u * kPfR);
     const uint32_t k0 = blockIdx.y * sps, k1 = min(nseg, k0 + sps);
-    pf_gemm_rows<T, kPfR, AL>(J.w, J.rows, row0, nseg, k0, k1, xp, rec, ntok, n, (uint8_t *)pf_lds4,
-                          J.y + (size_t)blockIdx.y * sstride, ldy);
+    pf_gemm_rows<T, kPfR, LAY>(J.w, J.rows, row0, nseg, k0, k1, xp, rec, ntok, n, (uint8_t *)pf_lds4,
+                               J.y + (size_t)blockIdx.y * sstride, ldy, J.g, J.gb, J.ni);
 }
 
 // ---------------------------------------------------------------- planes
@@ -784,23 +907,28 @@ uint32_t pf_split(uint32_t tiles, uint32_t nseg)
 uint32_t pf_tiles(size_t rows) { return (uint32_t)((rows + qgp::kPfRows - 1) / qgp::kPfRows); }
 
 template <uint32_t T>
-static void pf_gemm_launch(const qgp::PfJobs &jobs, uint32_t tiles, uint32_t nseg, uint32_t slices,
+static void pf_gemm_launch(const qgp::PfJobs &jobs, bool rp, uint32_t tiles, uint32_t nseg, uint32_t slices,
                            const uint16_t *xp, const float *rec, uint32_t ntok, uint32_t cols, uint32_t ldy,
                            size_t sstride, hipStream_t st)
 {
     const uint32_t sps = (nseg + slices - 1) / slices;
-    // rows of whole blocks: the sub-block index within a block is the same in
-    // every row (Q8_0 blocks are single sub-blocks)
     const dim3 grid(tiles, slices), block(64 * qgp::kPfWaves);
-    if constexpr (T == T_Q8_0)
-        hipLaunchKernelGGL((qgp::pf_gemm_k<T, true>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
-                           cols, ldy, (uint64_t)sstride);
-    else if (nseg % 8u == 0)
-        hipLaunchKernelGGL((qgp::pf_gemm_k<T, true>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
-                           cols, ldy, (uint64_t)sstride);
-    else
-        hipLaunchKernelGGL((qgp::pf_gemm_k<T, false>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
-                           cols, ldy, (uint64_t)sstride);
+    // the layout: repacked with one or several rows per group, or GGUF with
+    // rows of whole blocks (Q8_0 blocks are single sub-blocks) or straddling
+    if (rp) {
+        if (jobs.j0.g == 1)
+            hipLaunchKernelGGL((qgp::pf_gemm_k<T, 2>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
+                               cols, ldy, (uint64_t)sstride);
+        else
+            hipLaunchKernelGGL((qgp::pf_gemm_k<T, 3>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok,
+                               cols, ldy, (uint64_t)sstride);
+    } else if (T == T_Q8_0 || nseg % 8u == 0) {
+        hipLaunchKernelGGL((qgp::pf_gemm_k<T, 1>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok, cols,
+                           ldy, (uint64_t)sstride);
+    } else if constexpr (T != T_Q8_0) {
+        hipLaunchKernelGGL((qgp::pf_gemm_k<T, 0>), grid, block, qgp::kPfLds, st, jobs, nseg, sps, xp, rec, ntok, cols,
+                           ldy, (uint64_t)sstride);
+    }
 }
 
 int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *xp, const float *rec, uint32_t ntok,
@@ -811,28 +939,36 @@ int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *x
         return -1;
     const uint32_t nseg = (uint32_t)(cols / 32);
     if (slices < 1 || slices > nseg || slices > qgp::kPfMaxSlices) return -1;
-    for (int i = 0; i < n_mats; i++)
-        // 16-byte aligned weights (the K-quant block heads are read as one uint4)
-        if (!prefill_type_supported(mats[i].type) || mats[i].rows == 0 || mats[i].rows > 0xFFFFFFFFull ||
-            ((uintptr_t)mats[i].w & 15u) != 0)
+    for (int i = 0; i < n_mats; i++) {
+        const PfMat &m = mats[i];
+        // 16-byte aligned weights (the K-quant block heads are read as one
+        // uint4); a repacked matrix: whole row groups
+        if (!prefill_type_supported(m.type) || m.rows == 0 || m.rows > 0xFFFFFFFFull || ((uintptr_t)m.w & 15u) != 0)
             return -1;
-    // one launch per run of matrices of the same type
+        if (m.rp && (m.g == 0 || m.g > 8 || m.rows % m.g != 0 || m.ni == 0 || m.gb == 0)) return -1;
+    }
+    // one launch per run of matrices of the same type and layout
     for (int i = 0; i < n_mats;) {
         qgp::PfJob j[3] = {};
         uint32_t tiles = 0;
         int n = 0;
         const uint32_t type = mats[i].type;
-        for (; i < n_mats && mats[i].type == type; i++, n++) {
-            j[n] = qgp::PfJob{mats[i].w, mats[i].y, mats[i].type, (uint32_t)mats[i].rows, pf_tiles(mats[i].rows)};
+        const bool rp = mats[i].rp;
+        const uint32_t g = mats[i].g;
+        for (; i < n_mats && mats[i].type == type && mats[i].rp == rp && (!rp || mats[i].g == g); i++, n++) {
+            const PfMat &m = mats[i];
+            j[n] = qgp::PfJob{m.w, m.y, m.type, (uint32_t)m.rows, pf_tiles(m.rows), rp ? m.g : 1u, rp ? m.ni : 0u,
+                              rp ? (uint64_t)m.gb : 0u};
             tiles += j[n].tiles;
         }
         const qgp::PfJobs jobs{j[0], j[1], j[2], (uint32_t)n};
         hipStream_t st = (hipStream_t)stream;
+        const uint32_t c = (uint32_t)cols;
         switch (type) {
-        case T_Q4_K: pf_gemm_launch<T_Q4_K>(jobs, tiles, nseg, slices, xp, rec, ntok, (uint32_t)cols, ldy, sstride, st); break;
-        case T_Q5_K: pf_gemm_launch<T_Q5_K>(jobs, tiles, nseg, slices, xp, rec, ntok, (uint32_t)cols, ldy, sstride, st); break;
-        case T_Q6_K: pf_gemm_launch<T_Q6_K>(jobs, tiles, nseg, slices, xp, rec, ntok, (uint32_t)cols, ldy, sstride, st); break;
-        case T_Q8_0: pf_gemm_launch<T_Q8_0>(jobs, tiles, nseg, slices, xp, rec, ntok, (uint32_t)cols, ldy, sstride, st); break;
+        case T_Q4_K: pf_gemm_launch<T_Q4_K>(jobs, rp, tiles, nseg, slices, xp, rec, ntok, c, ldy, sstride, st); break;
+        case T_Q5_K: pf_gemm_launch<T_Q5_K>(jobs, rp, tiles, nseg, slices, xp, rec, ntok, c, ldy, sstride, st); break;
+        case T_Q6_K: pf_gemm_launch<T_Q6_K>(jobs, rp, tiles, nseg, slices, xp, rec, ntok, c, ldy, sstride, st); break;
+        case T_Q8_0: pf_gemm_launch<T_Q8_0>(jobs, rp, tiles, nseg, slices, xp, rec, ntok, c, ldy, sstride, st); break;
         default: return -1;
         }
         if (hipGetLastError() != hipSuccess) return -2;

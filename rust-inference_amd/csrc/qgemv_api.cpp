@@ -114,11 +114,11 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
         delete m;
         return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
     }
-    // Owned Q8_0 / Q4_K / Q5_K / Q6_K matrices also get the repacked layout the
-    // stream kernels read with contiguous loads (the same bytes -- for Q5_K
-    // the same bits -- rearranged; d keeps the GGUF layout for the dequant
-    // and generic kernels).  Bytes wrapped from caller memory keep the
-    // GGUF-layout kernels.
+    // Owned Q8_0 / Q4_K / Q5_K / Q6_K matrices are kept in the repacked layout
+    // the stream kernels read with contiguous loads (the same bytes -- for
+    // Q5_K the same bits -- rearranged), and only in it: d is freed, and the
+    // dequant kernels get the GGUF layout back from qg_mat_gguf.  Bytes
+    // wrapped from caller memory keep the GGUF-layout kernels.
     if (owned && qg::repack_eligible(type, m->plan, rows)) {
         uint8_t *r = nullptr;
         hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&r, nbytes + qg::kTailPad);
@@ -138,6 +138,10 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
         }
         m->d_rp = r;
         m->plan = rp_plan;
+        // one device copy: the kernels that need the GGUF layout rebuild it
+        // (qg_mat_gguf)
+        (void)hipFree(d);
+        m->d = nullptr;
     }
     ctx->mats.insert(m);
     *out = m;
@@ -147,7 +151,7 @@ int new_mat(qg_ctx *ctx, uint8_t *d, size_t nbytes, uint32_t type, size_t rows, 
 void drop_mat(qg_ctx *ctx, qg_mat *m)
 {
     if (m->owned && m->d) (void)hipFree(m->d);
-    if (m->d_rp) (void)hipFree(m->d_rp);
+    if (m->d_rp && !m->rp_view) (void)hipFree(m->d_rp);
     ctx->mats.erase(m);
     for (auto it = ctx->keyed.begin(); it != ctx->keyed.end();) {
         if (it->second.mat == m)
@@ -188,6 +192,133 @@ std::vector<uint8_t> fingerprint(const uint8_t *p, size_t n)
 
 int qg_check_mat(qg_ctx *ctx, const qg_mat *mat) { return check_mat(ctx, mat); }
 
+int qg_mat_gguf(qg_ctx *ctx, const qg_mat *mat, uint8_t **out, bool *temp)
+{
+    *out = nullptr;
+    *temp = false;
+    if (mat->d) {
+        *out = mat->d;
+        return QG_OK;
+    }
+    if (!mat->d_rp || !mat->plan.rp) return fail(ctx, QG_ERR_INVALID_ARG, "matrix holds no device copy");
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    uint8_t *d = nullptr;
+    hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&d, mat->nbytes + qg::kTailPad);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc GGUF-layout copy", e);
+    const int lr = qg::launch_unrepack(mat->type, mat->plan, mat->d_rp, d, (ihipStream_t *)ctx->stream);
+    if (lr == 0) e = hipMemsetAsync(d + mat->nbytes, 0, qg::kTailPad, ctx->stream);
+    if (lr == 0 && e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (lr != 0 || e != hipSuccess) {
+        (void)hipFree(d);
+        return fail(ctx, QG_ERR_HIP, "rebuilding the GGUF layout", e != hipSuccess ? e : hipGetLastError());
+    }
+    *out = d;
+    *temp = true;
+    return QG_OK;
+}
+
+int qg_mat_keep_gguf(qg_ctx *ctx, qg_mat *mat)
+{
+    if (mat->d) return QG_OK;
+    bool temp = false;
+    uint8_t *d = nullptr;
+    const int rc = qg_mat_gguf(ctx, mat, &d, &temp);
+    if (rc) return rc;
+    mat->d = d;                      // owned (the matrix was uploaded)
+    return QG_OK;
+}
+
+int qg_mat_drop_repacked(qg_ctx *ctx, qg_mat *mat)
+{
+    if (!mat->d_rp) return QG_OK;
+    if (!mat->d) return fail(ctx, QG_ERR_INVALID_ARG, "the repacked copy is the only one");
+    qg::Plan p;
+    if (qg::make_plan(mat->type, mat->rows, mat->cols, ctx->n_cu, &p) != 0)
+        return fail(ctx, QG_ERR_UNSUPPORTED_TYPE, "no kernel for type");
+    QG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (!mat->rp_view) (void)hipFree(mat->d_rp);
+    mat->d_rp = nullptr;
+    mat->rp_view = false;
+    mat->plan = p;
+    return QG_OK;
+}
+
+int qg_stack_views(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out)
+{
+    *out = nullptr;
+    if (!ctx || n < 1) return QG_ERR_INVALID_ARG;
+    const qg_mat *p0 = parts[0];
+    size_t rows = 0, total = 0;
+    for (int i = 0; i < n; i++) {
+        const qg_mat *p = parts[i];
+        if (p->type != p0->type || p->cols != p0->cols || !p->d_rp || p->rp_view || p->d || !p->plan.rp ||
+            p->plan.g != p0->plan.g || p->plan.ni != p0->plan.ni || p->plan.group_bytes != p0->plan.group_bytes ||
+            p->rows % p->plan.g != 0 || p->nbytes != (p->rows / p->plan.g) * p->plan.group_bytes)
+            return QG_ERR_SHAPE;
+        rows += p->rows;
+        total += p->nbytes;
+    }
+    qg::Plan plan;
+    if (qg::make_plan(p0->type, rows, p0->cols, ctx->n_cu, &plan, true) != 0 || !plan.rp || plan.g != p0->plan.g ||
+        plan.ni != p0->plan.ni || plan.group_bytes != p0->plan.group_bytes)
+        return QG_ERR_SHAPE;
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    uint8_t *r = nullptr;
+    hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&r, total + qg::kTailPad);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc stacked matrix", e);
+    size_t off = 0;
+    for (int i = 0; i < n && e == hipSuccess; i++) {
+        e = hipMemcpyAsync(r + off, parts[i]->d_rp, parts[i]->nbytes, hipMemcpyDeviceToDevice, ctx->stream);
+        off += parts[i]->nbytes;
+    }
+    if (e == hipSuccess) e = hipMemsetAsync(r + total, 0, qg::kTailPad, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    qg_mat *s = e == hipSuccess ? new (std::nothrow) qg_mat : nullptr;
+    if (!s) {
+        (void)hipFree(r);
+        return e != hipSuccess ? fail(ctx, QG_ERR_HIP, "stacking copies", e)
+                               : fail(ctx, QG_ERR_OUT_OF_MEMORY, "host allocation");
+    }
+    s->ctx = ctx;
+    s->d = nullptr;
+    s->d_rp = r;
+    s->nbytes = total;
+    s->type = p0->type;
+    s->rows = rows;
+    s->cols = p0->cols;
+    s->owned = true;
+    s->plan = plan;
+    ctx->mats.insert(s);
+    off = 0;
+    for (int i = 0; i < n; i++) {
+        (void)hipFree(parts[i]->d_rp);
+        parts[i]->d_rp = r + off;
+        parts[i]->rp_view = true;
+        off += parts[i]->nbytes;
+    }
+    *out = s;
+    return QG_OK;
+}
+
+int qg_mat_unview(qg_ctx *ctx, qg_mat *mat)
+{
+    if (!mat->rp_view) return QG_OK;
+    QG_HIP(ctx, hipSetDevice(ctx->device));
+    uint8_t *r = nullptr;
+    hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&r, mat->nbytes + qg::kTailPad);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc matrix copy", e);
+    e = hipMemcpyAsync(r, mat->d_rp, mat->nbytes, hipMemcpyDeviceToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(r + mat->nbytes, 0, qg::kTailPad, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(r);
+        return fail(ctx, QG_ERR_HIP, "copying a stacked part out", e);
+    }
+    mat->d_rp = r;
+    mat->rp_view = false;
+    return QG_OK;
+}
+
 int qg_mat_release(qg_ctx *ctx, qg_mat *mat, bool owned)
 {
     if (!mat) return QG_OK;
@@ -214,7 +345,7 @@ int qg_norm_matvec(qg_ctx *ctx, const qg_mat *mat, const float *xa, const float 
         // two kernels: RMSNorm into scratch, then the mat-vec
         lr = qg::launch_rmsnorm(xa, xb, sum_out, nw, scratch, cols, eps, sti);
         if (lr == 0) {
-            if (mat->plan.kind == 1 && a16(scratch))
+            if (mat->plan.kind == 1 && (a16(scratch) || !mat->d))
                 lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, cols, scratch, y, sti);
             else
                 lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, cols, scratch, y, sti);
@@ -242,7 +373,7 @@ int qg_silu_matvec(qg_ctx *ctx, const qg_mat *mat, const float *g, const float *
     if (lr == -1) {
         lr = qg::launch_silu_mul(g, u, scratch, cols, sti);
         if (lr == 0) {
-            if (mat->plan.kind == 1 && a16(scratch))
+            if (mat->plan.kind == 1 && (a16(scratch) || !mat->d))
                 lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, cols, scratch, y, sti);
             else
                 lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, cols, scratch, y, sti);
@@ -311,7 +442,12 @@ int qg_stack_mats(qg_ctx *ctx, qg_mat *const *parts, int n, qg_mat **out)
     if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc", e);
     size_t off = 0;
     for (int i = 0; i < n && e == hipSuccess; i++) {
-        e = hipMemcpyAsync(d + off, parts[i]->d, need[i], hipMemcpyDeviceToDevice, ctx->stream);
+        if (parts[i]->d) {
+            e = hipMemcpyAsync(d + off, parts[i]->d, need[i], hipMemcpyDeviceToDevice, ctx->stream);
+        } else if (qg::launch_unrepack(type, parts[i]->plan, parts[i]->d_rp, d + off, (ihipStream_t *)ctx->stream)) {
+            e = hipGetLastError();
+            if (e == hipSuccess) e = hipErrorLaunchFailure;
+        }
         off += need[i];
     }
     if (e == hipSuccess) e = hipMemsetAsync(d + total, 0, qg::kTailPad, ctx->stream);
@@ -390,6 +526,7 @@ int qg_destroy(qg_ctx *ctx)
     if (ctx->d_y) (void)hipFree(ctx->d_y);
     if (ctx->d_norm) (void)hipFree(ctx->d_norm);
     if (ctx->d_glu) (void)hipFree(ctx->d_glu);
+    if (ctx->d_xal) (void)hipFree(ctx->d_xal);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return QG_OK;
@@ -477,7 +614,13 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
     else if (mat->plan.kind == 1 && ((uintptr_t)d_x & 15u) == 0)
         lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, mat->cols, d_x,
                              d_y, (ihipStream_t *)st);
-    else
+    else if (!mat->d) {
+        // the repacked copy only: the stream kernel on an aligned copy of x
+        if ((rc = grow_device(ctx, &ctx->d_xal, &ctx->d_xal_cap, mat->cols))) return rc;
+        QG_HIP(ctx, hipMemcpyAsync(ctx->d_xal, d_x, mat->cols * sizeof(float), hipMemcpyDeviceToDevice, st));
+        lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, mat->cols, ctx->d_xal,
+                             d_y, (ihipStream_t *)st);
+    } else
         lr = qg::launch_gemv_generic(mat->type, mat->d, mat->rows, mat->cols, d_x, d_y,
                                      (ihipStream_t *)st);
     if (lr != 0) return fail(ctx, QG_ERR_HIP, "kernel launch", hipGetLastError());
@@ -663,8 +806,19 @@ int qg_dequant_dev(qg_ctx *ctx, const qg_mat *mat, float *d_out, void *stream)
     if (n == 0) return QG_OK;
     if (!d_out) return fail(ctx, QG_ERR_INVALID_ARG, "out is NULL");
     QG_HIP(ctx, hipSetDevice(ctx->device));
-    if (qg::launch_dequant(mat->type, mat->d, n, d_out, (ihipStream_t *)pick(ctx, stream)))
+    uint8_t *w = nullptr;
+    bool temp = false;
+    if ((rc = qg_mat_gguf(ctx, mat, &w, &temp))) return rc;
+    hipStream_t st = pick(ctx, stream);
+    if (qg::launch_dequant(mat->type, w, n, d_out, (ihipStream_t *)st)) {
+        if (temp) (void)hipFree(w);
         return fail(ctx, QG_ERR_HIP, "dequant launch", hipGetLastError());
+    }
+    if (temp) {                                          // the rebuilt copy lives until the kernel ends
+        const hipError_t e = hipStreamSynchronize(st);
+        (void)hipFree(w);
+        if (e != hipSuccess) return fail(ctx, QG_ERR_HIP, "dequant", e);
+    }
     return QG_OK;
 }
 
@@ -696,9 +850,29 @@ int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_o
     if (row >= mat->rows) return fail(ctx, QG_ERR_SHAPE, "row out of range");   // quant.rs:153
     if (!d_out) return fail(ctx, QG_ERR_INVALID_ARG, "out is NULL");
     QG_HIP(ctx, hipSetDevice(ctx->device));
-    if (qg::launch_dequantize_row(mat->type, mat->d, mat->rows, mat->cols, row, d_out,
-                                  (ihipStream_t *)pick(ctx, stream)))
-        return fail(ctx, QG_ERR_HIP, "dequantize_row launch", hipGetLastError());
+    hipStream_t st = pick(ctx, stream);
+    if (mat->d) {
+        if (qg::launch_dequantize_row(mat->type, mat->d, mat->rows, mat->cols, row, d_out, (ihipStream_t *)st))
+            return fail(ctx, QG_ERR_HIP, "dequantize_row launch", hipGetLastError());
+        return QG_OK;
+    }
+    // repacked only: the row's row group (whole blocks) in the GGUF layout,
+    // as a matrix of g rows
+    const qg::Plan &p = mat->plan;
+    const size_t grp = row / p.g;
+    uint8_t *t = nullptr;
+    hipError_t e = qg_alloc_injected(ctx) ? hipErrorOutOfMemory : hipMalloc((void **)&t, p.group_bytes + qg::kTailPad);
+    if (e != hipSuccess) return fail(ctx, QG_ERR_OUT_OF_MEMORY, "hipMalloc row group", e);
+    qg::Plan one = p;
+    one.n_groups = 1;
+    int lr = qg::launch_unrepack(mat->type, one, mat->d_rp + grp * p.group_bytes, t, (ihipStream_t *)st);
+    if (lr == 0) e = hipMemsetAsync(t + p.group_bytes, 0, qg::kTailPad, st);
+    if (lr == 0 && e == hipSuccess)
+        lr = qg::launch_dequantize_row(mat->type, t, p.g, mat->cols, row % p.g, d_out, (ihipStream_t *)st);
+    if (lr == 0 && e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(t);
+    if (lr != 0 || e != hipSuccess)
+        return fail(ctx, QG_ERR_HIP, "dequantize_row", e != hipSuccess ? e : hipGetLastError());
     return QG_OK;
 }
 

@@ -2227,6 +2227,88 @@ int launch_repack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+// The GGUF layout of repacked row groups (the inverse of repack_k, one thread
+// per item; for Q5_K the block's first item also rebuilds the 32 qh bytes
+// from the four items' bit words).
+template <uint32_t T>
+__global__ void __launch_bounds__(256) unrepack_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                  uint64_t n_items, uint32_t ni, uint32_t group_bytes)
+{
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_items) return;
+    const uint64_t gidx = idx / ni;
+    const uint32_t it = (uint32_t)(idx - gidx * ni);
+    const uint8_t *sg = src + gidx * group_bytes;          // repacked group
+    uint8_t *dg = dst + gidx * group_bytes;                // GGUF-layout group
+    if constexpr (T == T_Q8_0) {
+        uint8_t *b = dg + it * 68u;
+        for (uint32_t k = 0; k < 64; k++) b[k < 32 ? 2u + k : 4u + k] = sg[((k >> 4) * ni + it) * 16u + (k & 15u)];
+        b[0] = sg[64u * ni + 4u * it];
+        b[1] = sg[64u * ni + 4u * it + 1u];
+        b[34] = sg[64u * ni + 4u * it + 2u];
+        b[35] = sg[64u * ni + 4u * it + 3u];
+    } else if constexpr (T == T_Q4_K) {
+        uint8_t *b = dg + (it >> 1) * 144u;
+        if ((it & 1u) == 0)
+            for (int j = 0; j < 16; j++) b[j] = sg[(it >> 1) * 16u + j];
+        for (uint32_t k = 0; k < 4; k++)
+            for (int j = 0; j < 16; j++) b[16u + (it & 1u) * 64u + 16u * k + j] = sg[(ni >> 1) * 16u + (k * ni + it) * 16u + j];
+    } else if constexpr (T == T_Q5_K) {
+        uint8_t *b = dg + (it >> 2) * 176u;
+        const uint32_t H = (ni >> 2) * 16u;
+        for (uint32_t k = 0; k < 32; k++) b[48u + (it & 3u) * 32u + k] = sg[H + ((k >> 4) * ni + it) * 16u + (k & 15u)];
+        if ((it & 3u) == 0) {
+            for (int k = 0; k < 16; k++) b[k] = sg[(it >> 2) * 16u + k];
+            uint32_t W[4][2];
+            for (uint32_t q = 0; q < 4; q++)
+                for (uint32_t w = 0; w < 2; w++) {
+                    const uint8_t *pw = sg + H + 32u * ni + 8u * (it + q) + 4u * w;
+                    W[q][w] = (uint32_t)pw[0] | ((uint32_t)pw[1] << 8) | ((uint32_t)pw[2] << 16) | ((uint32_t)pw[3] << 24);
+                }
+            for (uint32_t m = 0; m < 32; m++) {          // qh byte m = 16w + 4t' + bb
+                const uint32_t w = m >> 4, tp = (m >> 2) & 3u, bb = m & 3u;
+                uint32_t v = 0;
+                for (uint32_t q = 0; q < 4; q++)        // item q of the block holds bits 2q, 2q + 1
+                    for (uint32_t h = 0; h < 2; h++) v |= ((W[q][w] >> (8u * bb + 2u * tp + h)) & 1u) << (2u * q + h);
+                b[16u + m] = (uint8_t)v;
+            }
+        }
+    } else {
+        uint8_t *b = dg + (it >> 2) * 210u;
+        const uint32_t n = (it >> 1) & 1u, i = it & 1u;
+        for (int j = 0; j < 16; j++) {
+            b[64u * n + 16u * i + j] = sg[it * 16u + j];
+            b[64u * n + 32u + 16u * i + j] = sg[(ni + it) * 16u + j];
+            b[128u + 32u * n + 16u * i + j] = sg[(2u * ni + it) * 16u + j];
+        }
+        for (uint32_t k = 0; k < 4; k++) b[192u + 8u * n + i + 2u * k] = sg[48u * ni + 4u * it + k];
+        if ((it & 3u) == 0) {
+            b[208] = sg[52u * ni + (it >> 2) * 2u];
+            b[209] = sg[52u * ni + (it >> 2) * 2u + 1u];
+        }
+    }
+}
+
+int launch_unrepack(uint32_t type, const Plan &p, const uint8_t *src, uint8_t *dst, ihipStream_t *stream)
+{
+    if (p.kind != 1 || p.ni == 0 || !p.rp) return -1;
+    const uint64_t n_items = (uint64_t)p.n_groups * p.ni;
+    if (n_items == 0) return 0;
+    const uint64_t blocks = (n_items + 255) / 256;
+    if (blocks > 0x7FFFFFFFull) return -1;
+    const dim3 grid((uint32_t)blocks), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    const uint32_t gb = (uint32_t)p.group_bytes;
+    switch (type) {
+    case T_Q8_0: hipLaunchKernelGGL(unrepack_k<T_Q8_0>, grid, block, 0, st, src, dst, n_items, p.ni, gb); break;
+    case T_Q4_K: hipLaunchKernelGGL(unrepack_k<T_Q4_K>, grid, block, 0, st, src, dst, n_items, p.ni, gb); break;
+    case T_Q5_K: hipLaunchKernelGGL(unrepack_k<T_Q5_K>, grid, block, 0, st, src, dst, n_items, p.ni, gb); break;
+    case T_Q6_K: hipLaunchKernelGGL(unrepack_k<T_Q6_K>, grid, block, 0, st, src, dst, n_items, p.ni, gb); break;
+    default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
 // ------------------------------------------------------------ launchers
 
 static StreamArgs stream_args(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
