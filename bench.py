@@ -433,7 +433,7 @@ def pmc_summary(args):
     res = {}
     for key, d in (("fetch", args.pmc_summary[0]), ("write", args.pmc_summary[1])):
         rows = _pmc_rows(d)
-        gemv = [v for k, v, _ in rows if "gemv_stream" in k or "gemv_ring" in k]
+        gemv = [v for k, v, _ in rows if "qg::gemv_" in k]
         copy = [v for k, v, _ in rows if "elementwise" in k.lower() and "mul" in k.lower()]
         if not gemv or not copy:
             raise SystemExit(f"{d}: no gemv or no copy-probe dispatches found")
