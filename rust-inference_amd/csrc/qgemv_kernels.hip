@@ -1123,12 +1123,16 @@ __device__ __forceinline__ void item_compute(const uint32_t (&r)[I::NRAW], const
 // This lane's x slice for its item -- the S segments the item meets, as
 // fixed-point digits and records -- from the planes staged in LDS; srow[s]:
 // the row (within the row group) of slot s (0 with one row per group, G1,
-// where no division is needed).  Inactive lanes get zeros.
+// where no division is needed).  Every read is unconditional, so the
+// compiler issues them together and waits once: an inactive lane reads the
+// slice of its clamped item (it = 0), and its callers discard what such a
+// lane computes.
 template <class I, bool G1>
 __device__ __forceinline__ void plane_slice(const uint8_t *lds, uint32_t meta, uint32_t it, bool active,
                                             uint32_t cols, XP<I::S, I::SEG> &xs, uint32_t (&srow)[I::S])
 {
     constexpr int S = I::S, SEG = I::SEG;
+    (void)active;
 #pragma unroll
     for (int s = 0; s < S; s++) {
         const uint32_t e = I::seg_elem(it, s);
@@ -1140,11 +1144,11 @@ __device__ __forceinline__ void plane_slice(const uint8_t *lds, uint32_t meta, u
         for (int p = 0; p < 3; p++)
 #pragma unroll
             for (int v = 0; v < SEG / 16; v++) {
-                const uint4 q = active ? *(const uint4 *)(sp + 32 * p + 16 * v) : make_uint4(0, 0, 0, 0);
+                const uint4 q = *(const uint4 *)(sp + 32 * p + 16 * v);
                 xs.p[s][p][4 * v] = q.x; xs.p[s][p][4 * v + 1] = q.y;
                 xs.p[s][p][4 * v + 2] = q.z; xs.p[s][p][4 * v + 3] = q.w;
             }
-        const float4 m = active ? *(const float4 *)(lds + meta + 16u * gs) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 m = *(const float4 *)(lds + meta + 16u * gs);
         xs.ik[s] = m.x;
         xs.sx[s] = SEG == 32 ? m.y + m.z : (h ? m.z : m.y);
         xs.sy[s] = m.w;
@@ -1243,8 +1247,12 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     // x first: issued behind the weight stream of the workgroups that started
     // earlier, x reaches the late ones after most of the matrix; waiting for
     // it here (the weights then overlap the conversion) is measurably faster.
+    // The RMSNorm prologue is the exception: its three input vectors take
+    // long enough to arrive that issuing the first batches behind them, with
+    // no wait, is faster (decode +0.9 %); the compiler's own wait before the
+    // conversion then covers x alone.
     // 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding).
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    if constexpr (!NORM) __builtin_amdgcn_s_waitcnt(0x0F70);
     uint32_t raw[D][R][NR];
 #pragma unroll
     for (int d = 0; d < D0; d++) issue<T, R, GLU, RP>(a, team, d, it, ib, active, raw[d]);
@@ -1360,8 +1368,15 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     }
     lds_barrier();
     if constexpr (NORM) {
+        // all the waves' sums read at once (one LDS wait), added in wave order;
+        // the slots past the last wave add 0 to a sum of squares
+        const uint32_t nwv = (blockDim.x + 63u) / 64u;
         float tot = 0.f;
-        for (uint32_t i = 0; i < (blockDim.x + 63u) / 64u; i++) tot += nred[i];
+#pragma unroll
+        for (uint32_t i = 0; i < (uint32_t)(LB / 64); i++) {
+            const float v = nred[i];
+            tot += i < nwv ? v : 0.f;
+        }
         const float rms = sqrtf(tot / (float)a.cols + a.eps);
         nscale = 1.0f / rms;
     }
