@@ -101,9 +101,13 @@ int qg_model_prefill(qg_model *m, const uint32_t *tokens, size_t n, float *logit
 int qg_model_use_batched_prefill(qg_model *m, int enable);
 /* No counterpart in the reference (tuning and tests): the decode step's
  * attention for head_dim 64, 128 and 256 -- path 0 (the default) by length:
- * whole query heads in one launch up to 512 cached positions, split over
- * position ranges and merged beyond; 1 always whole heads; 2 always split.
- * Both compute attention.rs:93-121; they differ in summation order only. */
+ * up to 512 cached positions each query head in two workgroups (even and odd
+ * positions) merged in the output projection's input where every wo matrix
+ * allows it (a fixed-point type with whole blocks per row), else in one
+ * workgroup; split over position ranges and merged beyond.  1 always one
+ * workgroup per head; 2 always split; 3 always two workgroups per head where
+ * allowed.  All compute attention.rs:93-121; they differ in summation order
+ * only. */
 int qg_model_set_attention_path(qg_model *m, int path);
 /* No counterpart in the reference (memory accounting): device bytes the
  * model reads.  weights: every distinct matrix it uses (token_embd, lm_head,

@@ -587,8 +587,10 @@ class DeviceModel:
         return {"weights": w.value, "file_bytes": f.value, "total": t.value}
 
     def set_attention_path(self, path: int):
-        """0: by length (whole heads up to 512 cached positions, else split),
-        1: always whole heads, 2: always split over position ranges."""
+        """0: by length (up to 512 cached positions two workgroups per head
+        merged in the wo GEMV where every wo allows it, else one; beyond,
+        split), 1: always one workgroup per head, 2: always split over
+        position ranges, 3: always two workgroups per head where allowed."""
         self.ctx.check(self.ctx.lib.qg_model_set_attention_path(self.h, int(path)), "qg_model_set_attention_path")
 
     def forward(self, token: int, pos: int, logits=None):

@@ -60,6 +60,7 @@ struct Plan {
     const void *fn_norm;   // the same kernel with the fused RMSNorm input
     const void *fn_silu;   // the same kernel with the silu(g) * u input
     const void *fn_norm_glu;  // RMSNorm input, [gate; up] rows paired into silu(g) * u
+    const void *fn_attn;   // the same kernel with the two-range attention merge input
     bool rp;               // the kernels read the repacked layout (launch_repack)
     // plain mat-vec through the LDS ring kernel (gemv_ring) where it applies:
     const void *fn_ring;   // nullptr otherwise
@@ -114,6 +115,16 @@ int launch_gemv_norm_pair(uint32_t t1, const Plan &p1, const uint8_t *w1, size_t
 // otherwise).  g, u: cols floats, 16-byte aligned.
 int launch_gemv_silu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
                      const float *g, const float *u, float *y, ihipStream_t *stream);
+// y = W · x with x the attention output of n_heads heads of hd elements,
+// merged from two position ranges: part[r * cols + i] is range r's
+// unnormalised output sum_j exp(s_j - m) v_j[i], ml[2 (r n_heads + h)] and
+// ml[2 (r n_heads + h) + 1] its (m, sum_j exp(s_j - m)) for head h, and
+// x[i] = sum_r w_r part_r[i] with w_r = exp(m_r - M) / sum_r' exp(m_r' - M) l_r'.
+// Stream kernel plans of the fixed-point types only (-1 otherwise); part
+// 16-byte aligned, cols = n_heads * hd, hd a multiple of 16.
+int launch_gemv_attn(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                     const float *part, const float *ml, uint32_t n_heads, uint32_t hd, float *y,
+                     ihipStream_t *stream);
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                         const float *x, float *y, ihipStream_t *stream);
 int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,

@@ -166,6 +166,9 @@ struct AttnArgs {
     const Step *st;
     uint32_t kv_dim, n_rep, grp, nsplit;
     float scale;
+    // attn_rope_head_k<E, 2>: floats between the ranges' outputs in part (q_dim)
+    // and between their (max, sum) rows in ml (2 n_heads)
+    uint32_t part_stride, ml_stride;
 };
 
 // Element d of a head after RoPE (rope.rs: the pair (2i, 2i+1) turned by
@@ -403,17 +406,26 @@ __global__ void __launch_bounds__(256) attn_combine_k(const float *__restrict__ 
 // all positions).  One launch, no partial sums: at a few hundred cached
 // positions the split kernel's second launch and its reads of the partials
 // cost more than the positions per wave here.
+//
+// NR = 2: two workgroups per head, workgroup (h, r) taking the positions
+// j = r (mod 2) -- twice the CUs, each reading half the K and V rows, which is
+// what bounds the kernel -- and writing its range's unnormalised output and
+// (max, sum of exponentials) instead, range-major: part[r * q_dim + h * hd + d],
+// ml[2 (r * n_heads + h) + {0, 1}].  The consumer (the wo GEMV's input
+// prologue, launch_gemv_attn) merges the two ranges.
 constexpr uint32_t kHeadWaves = 16;
 // cached positions up to which the forward pass uses attn_rope_head_k
 constexpr uint32_t kShortSeq = 512;
-template <int E>
+template <int E, int NR = 1>
 __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, float *__restrict__ out)
 {
+    static_assert(NR == 1 || NR == 2, "one or two position ranges");
     constexpr uint32_t HD = 64 * E, NW = kHeadWaves, PW = E <= 2 ? 8u : 4u;   // positions per wave per chunk
+    constexpr uint32_t ST = NR * NW;                 // position stride between a wave's positions
     __shared__ float sacc[NW][HD];
     __shared__ float sml[NW][2];
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t h = blockIdx.x, kvo = (h / a.n_rep) * HD;
+    const uint32_t h = blockIdx.x / NR, rg = blockIdx.x % NR, kvo = (h / a.n_rep) * HD;
     // unconditional loads; the projections are in flight while the step record arrives
     float qv[E], kn[E], vn[E];
 #pragma unroll
@@ -428,7 +440,7 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
     auto load = [&](uint32_t b, float (&ko)[PW][E], float (&vo)[PW][E]) {
 #pragma unroll
         for (uint32_t p = 0; p < PW; p++) {
-            const uint32_t j = min(b + NW * p, slot);
+            const uint32_t j = min(b + ST * p, slot);
             const float *kr = a.kc + (size_t)j * a.kv_dim + kvo, *vr = a.vc + (size_t)j * a.kv_dim + kvo;
 #pragma unroll
             for (int e = 0; e < E; e++) {
@@ -437,7 +449,7 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
             }
         }
     };
-    uint32_t base = wave;
+    uint32_t base = rg + NR * wave;
     load(base, kk, vv);
     float cv[E], sv[E];
 #pragma unroll
@@ -450,7 +462,7 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
         qv[e] = rope1(qv[e], __shfl_xor(qv[e], 1, 64), lane + 64 * e, cv[e], sv[e]);
         kn[e] = rope1(kn[e], __shfl_xor(kn[e], 1, 64), lane + 64 * e, cv[e], sv[e]);
     }
-    if (h % a.n_rep == 0 && wave == 0) {
+    if (h % a.n_rep == 0 && rg == 0 && wave == 0) {
         float *kr = a.kc + (size_t)slot * a.kv_dim + kvo, *vr = a.vc + (size_t)slot * a.kv_dim + kvo;
 #pragma unroll
         for (int e = 0; e < E; e++) {
@@ -461,12 +473,12 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
     float m = -INFINITY, l = 0.f, acc[E];
 #pragma unroll
     for (int e = 0; e < E; e++) acc[e] = 0.f;
-    for (; base < seq; base += NW * PW) {
-        const uint32_t np = min((seq - base + NW - 1) / NW, PW);   // this wave's positions in the chunk
-        if (base + NW * PW < seq) load(base + NW * PW, nk, nv);
+    for (; base < seq; base += ST * PW) {
+        const uint32_t np = min((seq - base + ST - 1) / ST, PW);   // this wave's positions in the chunk
+        if (base + ST * PW < seq) load(base + ST * PW, nk, nv);
 #pragma unroll
         for (uint32_t p = 0; p < PW; p++)
-            if (base + NW * p == slot)
+            if (base + ST * p == slot)
 #pragma unroll
                 for (int e = 0; e < E; e++) { kk[p][e] = kn[e]; vv[p][e] = vn[e]; }
         float sc[PW], cm = -INFINITY;
@@ -506,7 +518,8 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
     if (lane == 0) { sml[wave][0] = m; sml[wave][1] = l; }
     __syncthreads();
     // merge the waves: weights exp(m_w - M) (0 for a wave without positions),
-    // derived once by the first kHeadWaves lanes, over their sum
+    // derived once by the first kHeadWaves lanes, over their sum (NR = 2:
+    // unnormalised, the sum goes out with M)
     __shared__ float swt[NW];
     if (threadIdx.x < NW) {
         const uint32_t w = threadIdx.x;
@@ -518,14 +531,24 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
         float lsum = f * sml[w][1];
 #pragma unroll
         for (uint32_t o = 1; o < NW; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
-        swt[w] = f / lsum;
+        if constexpr (NR == 1) {
+            swt[w] = f / lsum;
+        } else {
+            swt[w] = f;
+            if (w == 0) {
+                const size_t o = (size_t)rg * (a.ml_stride / 2) + h;
+                a.ml[2 * o] = mx;
+                a.ml[2 * o + 1] = lsum;
+            }
+        }
     }
     __syncthreads();
+    float *dst = NR == 1 ? out + h * HD : a.part + (size_t)rg * a.part_stride + h * HD;
     for (uint32_t d = threadIdx.x; d < HD; d += blockDim.x) {
         float sum = 0.f;
 #pragma unroll
         for (uint32_t w = 0; w < NW; w++) sum += swt[w] * sacc[w][d];
-        out[h * HD + d] = sum;
+        dst[d] = sum;
     }
 }
 
@@ -748,12 +771,14 @@ struct qg_model {
     float *pf_rec = nullptr;
     uint32_t *pf_tok = nullptr;
     uint32_t pf_s_qkv = 1, pf_s_o = 1, pf_s_gu = 1, pf_s_down = 1;
-    // captured graphs, [1] with the short-context attention (attn_rope_head_k),
-    // [0] with the split attention; att_short selects what enqueue_forward
-    // launches
-    hipGraphExec_t g_fwd[2] = {nullptr, nullptr};   // forward pass
-    hipGraphExec_t g_dec[2] = {nullptr, nullptr};   // sample + advance + forward (generate)
-    bool att_short = false;
+    // captured graphs per attention mode: [0] the split attention
+    // (attn_rope_split_k + attn_combine_k), [1] whole heads in one workgroup
+    // each (attn_rope_head_k), [2] two position ranges per head merged in the
+    // wo GEMV's input (attn_rope_head_k<E, 2> + launch_gemv_attn); att_mode
+    // selects what enqueue_forward launches
+    hipGraphExec_t g_fwd[3] = {nullptr, nullptr, nullptr};   // forward pass
+    hipGraphExec_t g_dec[3] = {nullptr, nullptr, nullptr};   // sample + advance + forward (generate)
+    int att_mode = 0;
     int att_path = 0;                     // qg_model_set_attention_path
     float g_dec_penalty = 0.f;
     uint32_t g_dec_window = 0;
@@ -789,7 +814,7 @@ template <class T> int dalloc(qg_model *m, T **p, size_t n)
 
 void drop_graphs(qg_model *m)
 {
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 3; i++) {
         if (m->g_fwd[i]) (void)hipGraphExecDestroy(m->g_fwd[i]);
         if (m->g_dec[i]) (void)hipGraphExecDestroy(m->g_dec[i]);
         m->g_fwd[i] = m->g_dec[i] = nullptr;
@@ -1024,7 +1049,19 @@ int enqueue_forward(qg_model *m)
             aa.part = m->att_part; aa.ml = m->att_ml; aa.st = m->d_step;
             aa.kv_dim = m->kv_dim; aa.n_rep = m->n_rep; aa.grp = m->att_grp; aa.nsplit = m->att_nsplit;
             aa.scale = scale;
-            if (m->att_short) {
+            if (m->att_mode == 2) {
+                // two workgroups per head (even / odd positions); the wo GEMV
+                // below merges their outputs
+                aa.part_stride = m->q_dim;
+                aa.ml_stride = 2 * c.n_heads;
+                const dim3 grid(2 * c.n_heads), block(64 * qgm::kHeadWaves);
+                if (m->hd == 64)
+                    hipLaunchKernelGGL((qgm::attn_rope_head_k<1, 2>), grid, block, 0, st, aa, m->ao);
+                else if (m->hd == 128)
+                    hipLaunchKernelGGL((qgm::attn_rope_head_k<2, 2>), grid, block, 0, st, aa, m->ao);
+                else
+                    hipLaunchKernelGGL((qgm::attn_rope_head_k<4, 2>), grid, block, 0, st, aa, m->ao);
+            } else if (m->att_mode == 1) {
                 // one launch: whole heads, normalised output (short contexts)
                 const dim3 grid(c.n_heads), block(64 * qgm::kHeadWaves);
                 if (m->hd == 64)
@@ -1052,7 +1089,14 @@ int enqueue_forward(qg_model *m)
                                m->d_step, m->hd, m->kv_dim, m->n_rep, scale);
         }
         if ((rc = launched(m, "attention"))) return rc;
-        if ((rc = gemv(m, m->w[QG_M_WO - 2][l], m->ao, m->ao2))) return rc;
+        if (m->att_grp && m->att_mode == 2) {
+            const qg_mat *wo = m->w[QG_M_WO - 2][l];
+            if (qg::launch_gemv_attn(wo->plan, qg_gemv_bytes(wo), wo->nbytes, wo->rows, wo->cols, m->att_part,
+                                     m->att_ml, c.n_heads, m->hd, m->ao2, (ihipStream_t *)st) != 0)
+                return mfail(m, QG_ERR_HIP, "GEMV launch (attention merge)", hipGetLastError());
+        } else if ((rc = gemv(m, m->w[QG_M_WO - 2][l], m->ao, m->ao2))) {
+            return rc;
+        }
         // h1 = h0 + attention output (stored by the gate GEMV); MLP input = ffn_norm(h1)
         const float *fnorm = m->vec[QG_V_FFN_NORM][l];
         if (m->f_gu[l]) {
@@ -1125,13 +1169,30 @@ int capture(qg_model *m, int (*fn)(qg_model *), hipGraphExec_t *out)
     return QG_OK;
 }
 
-// the attention path of the forward pass that writes cache slot `slot`:
-// whole heads in one launch up to kShortSeq cached positions, else split
-// over position ranges (att_path: 0 by length, 1 always whole heads, 2
-// always split)
+// Whether every layer's wo can take the two-range attention output
+// (launch_gemv_attn: a stream-kernel plan of a fixed-point type with one row
+// per group) and the partial-output buffers hold two ranges.
+bool two_range_ok(const qg_model *m)
+{
+    if (!m->att_grp || m->att_nsplit < 2 || m->hd % 16 != 0) return false;
+    for (uint32_t l = 0; l < m->cfg.n_layers; l++) {
+        const qg_mat *wo = m->w[QG_M_WO - 2][l];
+        if (!wo || wo->plan.kind != 1 || !wo->plan.fn_attn) return false;
+    }
+    return true;
+}
+
+// the attention mode of the forward pass that writes cache slot `slot`: up to
+// kShortSeq cached positions whole heads, as two position ranges per head
+// where every wo takes them (mode 2) or in one workgroup per head (mode 1);
+// beyond, split over position ranges (mode 0).  att_path: 0 by length, 1
+// always one workgroup per head, 2 always split, 3 always two ranges where
+// the wo matrices allow it (else one workgroup per head).
 void pick_attention(qg_model *m, uint32_t slot)
 {
-    m->att_short = m->att_grp && (m->att_path == 1 || (m->att_path == 0 && slot + 1 <= qgm::kShortSeq));
+    const bool shrt = m->att_path == 1 || m->att_path == 3 || (m->att_path == 0 && slot + 1 <= qgm::kShortSeq);
+    if (!m->att_grp || !shrt) m->att_mode = 0;
+    else m->att_mode = m->att_path != 1 && two_range_ok(m) ? 2 : 1;
 }
 
 int run_forward(qg_model *m, uint32_t slot)
@@ -1140,7 +1201,7 @@ int run_forward(qg_model *m, uint32_t slot)
     if ((rc = prepare(m))) return rc;
     pick_attention(m, slot);
     if (!m->use_graphs) return enqueue_forward(m);
-    hipGraphExec_t &g = m->g_fwd[m->att_short ? 1 : 0];
+    hipGraphExec_t &g = m->g_fwd[m->att_mode];
     if (!g && (rc = capture(m, enqueue_forward, &g))) return rc;
     QGM_HIP(m, hipGraphLaunch(g, m->ctx->stream));
     return QG_OK;
@@ -1161,7 +1222,7 @@ int run_decode(qg_model *m, float penalty, uint32_t window, uint32_t slot)
     if ((rc = prepare(m))) return rc;
     pick_attention(m, slot);
     if (!m->use_graphs) return enqueue_decode(m);
-    hipGraphExec_t &g = m->g_dec[m->att_short ? 1 : 0];
+    hipGraphExec_t &g = m->g_dec[m->att_mode];
     if (!g && (rc = capture(m, enqueue_decode, &g))) return rc;
     QGM_HIP(m, hipGraphLaunch(g, m->ctx->stream));
     return QG_OK;
@@ -1602,7 +1663,7 @@ int qg_model_resident_bytes(qg_model *m, size_t *weights, size_t *file_bytes, si
 
 int qg_model_set_attention_path(qg_model *m, int path)
 {
-    if (!m || path < 0 || path > 2) return QG_ERR_INVALID_ARG;
+    if (!m || path < 0 || path > 3) return QG_ERR_INVALID_ARG;
     m->att_path = path;
     return QG_OK;
 }

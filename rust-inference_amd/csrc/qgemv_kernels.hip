@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(256) deq_row_k(const uint8_t *__restrict__ w, 
     }
 }
 
-constexpr int kProPlain = 0, kProNorm = 1, kProSilu = 2;
+constexpr int kProPlain = 0, kProNorm = 1, kProSilu = 2, kProAttn = 3;
 
 // silu(x) = x / (1 + exp(-x)), in the two branches of math.rs:137-146
 __device__ __forceinline__ float silu1(float x)
@@ -1012,6 +1012,11 @@ struct StreamArgs {
     // gate/up pairs (GLU kernels): the matrix is [gate; up] with glu_half row
     // groups each; y[r] = silu(gate_r . x) * (up_r . x), rows / 2 floats
     uint32_t glu_half;
+    // two-range attention merge (kProAttn): x = range 0's partial output, xb =
+    // range 1's, ml = their (m, l) per head, [range][att_nh][2]; heads of
+    // att_hd elements
+    const float *ml;
+    uint32_t att_nh, att_hd;
 };
 
 // 16 bytes of v to p as an inline-asm store (not counted by the compiler's
@@ -1182,6 +1187,12 @@ __device__ __forceinline__ void plane_slice(const uint8_t *lds, uint32_t meta, u
 //             also stores the residual sum.
 //   kProSilu: the input is silu(a.x) * a.xb, elementwise (mlp.rs:36-43 with
 //             math.rs:137-146).
+//   kProAttn: the input is the attention output (attention.rs:101-119)
+//             merged from two position ranges: a.x and a.xb hold each
+//             range's unnormalised output, a.ml its (max, sum of
+//             exponentials) per head, and x = w0 a.x + w1 a.xb with
+//             w_r = exp(m_r - M) / (exp(m_0 - M) l_0 + exp(m_1 - M) l_1),
+//             M = max(m_0, m_1).
 // GLU: y[r] = silu(gate_r . x) * (up_r . x) over the [gate; up] matrix
 // (mlp.rs:31-43): one team runs row group j of gate and row group j of up in
 // consecutive batches (teams of one wave or less).
@@ -1228,9 +1239,18 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     // costs address-unit time, and with a 3584-wide x and three input vectors
     // most would be surplus), and the wait below, visible to the compiler as
     // a wait for every load, closes them before any weight load.
+    constexpr bool ATT = PRO == kProAttn;
+    static_assert(!ATT || CV, "the attention merge converts x itself");
     uint4 xv[XS];
     uint4 bvv[TWO ? XS : 1], wvv[NORM ? XS : 1];
+    float4 mlv[ATT ? XR : 1];                    // kProAttn: (m0, l0, m1, l1) of the piece's head
     const uint4 *srcb = (const uint4 *)a.xb, *srcw = (const uint4 *)a.nw;
+    const float2 *ml2 = (const float2 *)a.ml;
+    auto ml_of = [&](uint32_t c) {               // piece c = elements 16c .. 16c + 15
+        const uint32_t h = 16u * c / a.att_hd;
+        const float2 r0 = ml2[h], r1 = ml2[a.att_nh + h];
+        return make_float4(r0.x, r0.y, r1.x, r1.y);
+    };
     const uint32_t nxs = (npc + blockDim.x - 1u) / blockDim.x;
 #pragma unroll
     for (int r = 0; r < XR; r++) {
@@ -1242,6 +1262,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
                 if constexpr (TWO) bvv[r * PW + i] = srcb[cc * PW + i];
                 if constexpr (NORM) wvv[r * PW + i] = srcw[cc * PW + i];
             }
+            if constexpr (ATT) mlv[r] = ml_of(cc);
         }
     }
     // x first: issued behind the weight stream of the workgroups that started
@@ -1347,6 +1368,39 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 #pragma unroll
             for (uint32_t i = 0; i < PW; i++) { pg[i] = src[c * PW + i]; pu[i] = srcb[c * PW + i]; }
             piece(pg, pu, c);
+        }
+    } else if constexpr (ATT) {
+        auto piece = [&](const uint4 (&p0)[PW], const uint4 (&p1)[PW], float4 mv, uint32_t c) {
+            // a range without positions has m = -inf, l = 0 and weight 0;
+            // range 0 always holds position 0
+            const float M = fmaxf(mv.x, mv.z);
+            const float e0 = expf(mv.x - M), e1 = expf(mv.z - M);
+            const float inv = 1.0f / (e0 * mv.y + e1 * mv.w);
+            const float w0 = e0 * inv, w1 = e1 * inv;
+            uint4 u[PW];
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) {
+                const float4 f0 = __builtin_bit_cast(float4, p0[i]), f1 = __builtin_bit_cast(float4, p1[i]);
+                u[i] = __builtin_bit_cast(uint4, make_float4(w0 * f0.x + w1 * f1.x, w0 * f0.y + w1 * f1.y,
+                                                             w0 * f0.z + w1 * f1.z, w0 * f0.w + w1 * f1.w));
+            }
+            put(u, c);
+        };
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const uint32_t c = tid + r * blockDim.x;
+            if (c < npc) {
+                uint4 q0[PW], q1[PW];
+#pragma unroll
+                for (uint32_t i = 0; i < PW; i++) { q0[i] = xv[r * PW + i]; q1[i] = bvv[r * PW + i]; }
+                piece(q0, q1, mlv[r], c);
+            }
+        }
+        for (uint32_t c = tid + XR * blockDim.x; c < npc; c += blockDim.x) {
+            uint4 q0[PW], q1[PW];
+#pragma unroll
+            for (uint32_t i = 0; i < PW; i++) { q0[i] = src[c * PW + i]; q1[i] = srcb[c * PW + i]; }
+            piece(q0, q1, ml_of(c), c);
         }
     } else {
 #pragma unroll
@@ -1998,7 +2052,8 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     else { wpt = (uint32_t)((ni + 63) / 64); tl = 64 * wpt; }
     // prologue variants for the quant types (F16/F32 x tiles leave no registers for them)
     constexpr int PN = I::PLANES ? kProNorm : kProPlain, PS = I::PLANES ? kProSilu : kProPlain;
-    const void *fn = nullptr, *fn_norm = nullptr, *fn_silu = nullptr, *fn_norm_glu = nullptr;
+    constexpr int PA = I::PLANES ? kProAttn : kProPlain;
+    const void *fn = nullptr, *fn_norm = nullptr, *fn_silu = nullptr, *fn_norm_glu = nullptr, *fn_attn = nullptr;
     rp = rp && repackable<T>() && rows % g == 0;
     if constexpr (repackable<T>()) {
         if (rp) {
@@ -2006,6 +2061,8 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
             fn_norm = g == 1 ? stream_fn_g<T, true, PN, true>(tsub) : stream_fn_g<T, false, PN, true>(tsub);
             fn_silu = g == 1 ? stream_fn_g<T, true, PS, true>(tsub) : stream_fn_g<T, false, PS, true>(tsub);
             fn_norm_glu = g == 1 ? stream_fn_glu<T, true, true>(tsub) : stream_fn_glu<T, false, true>(tsub);
+            // the attention merge input: one row per group only
+            fn_attn = g == 1 ? stream_fn_g<T, true, PA, true>(tsub) : nullptr;
         }
     }
     if (!rp) {
@@ -2015,6 +2072,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
             fn_norm = g == 1 ? stream_fn_g<T, true, PN>(tsub) : stream_fn_g<T, false, PN>(tsub);
             fn_silu = g == 1 ? stream_fn_g<T, true, PS>(tsub) : stream_fn_g<T, false, PS>(tsub);
             fn_norm_glu = g == 1 ? stream_fn_glu<T, true>(tsub) : stream_fn_glu<T, false>(tsub);
+            fn_attn = g == 1 ? stream_fn_g<T, true, PA>(tsub) : nullptr;
         }
     }
     if (!fn) return;
@@ -2054,6 +2112,7 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
     p->fn_norm = fn_norm;
     p->fn_silu = fn_silu;
     p->fn_norm_glu = fn_norm_glu;
+    p->fn_attn = fn_attn;
     p->rp = rp;
     p->g = (uint32_t)g;
     p->ni = (uint32_t)ni;
@@ -2364,6 +2423,23 @@ int launch_gemv_silu(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows
     a.xb = u;
     void *args[] = {&a};
     return hipLaunchKernel(p.fn_silu, dim3(p.grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
+                   hipSuccess ? 0 : -2;
+}
+
+int launch_gemv_attn(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                     const float *part, const float *ml, uint32_t n_heads, uint32_t hd, float *y,
+                     ihipStream_t *stream)
+{
+    if (p.kind != 1 || !p.fn_attn || hd == 0 || hd % 16 != 0 || (size_t)n_heads * hd != cols ||
+        ((uintptr_t)part & 15u) != 0)
+        return -1;
+    StreamArgs a = stream_args(p, w, nbytes, rows, cols, part, y);
+    a.xb = part + cols;
+    a.ml = ml;
+    a.att_nh = n_heads;
+    a.att_hd = hd;
+    void *args[] = {&a};
+    return hipLaunchKernel(p.fn_attn, dim3(p.grid), dim3(p.block), args, p.lds, (hipStream_t)stream) ==
                    hipSuccess ? 0 : -2;
 }
 

@@ -151,13 +151,14 @@ def test_long_ranges(rinf, synth, oracle, ctx, embed):
     dev.close()
 
 
-@pytest.mark.parametrize("path", [1, 2], ids=["whole-heads", "split"])
+@pytest.mark.parametrize("path", [1, 2, 3], ids=["whole-heads", "split", "two-range"])
 @pytest.mark.parametrize("embed", [256, 512, 1024], ids=["hd64", "hd128", "hd256"])
 def test_attention_paths(rinf, synth, oracle, ctx, path, embed):
-    """Both attention kernels of the decode step (qg_model_set_attention_path:
-    whole query heads in one launch, or position ranges then a merge) against
-    the oracle at the same lengths, for head_dim 64, 128 and 256: 70 prompt
-    positions, then 10 greedy steps."""
+    """The attention kernels of the decode step (qg_model_set_attention_path:
+    whole query heads in one launch; position ranges then a merge kernel; two
+    workgroups per head merged in the wo GEMV's input) against the oracle at
+    the same lengths, for head_dim 64, 128 and 256: 70 prompt positions, then
+    10 greedy steps."""
     cfg = dict(SMALL, n_layers=1, embed_dim=embed, hidden_dim=2 * embed)
     dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q8_0", 29, 96)
     dev.set_attention_path(path)
@@ -170,7 +171,7 @@ def test_attention_paths(rinf, synth, oracle, ctx, path, embed):
 
 def test_attention_path_switch_in_generate(rinf, synth, oracle, ctx):
     """A generation across the 512-position boundary (505 prompt tokens, 14
-    new): the decode graph changes from whole-head to split attention
+    new): the decode graph changes from two-range to split attention
     mid-run.  The tokens equal those of the step-by-step run, which follows
     the oracle within DEEP_TOL."""
     cfg = dict(SMALL, n_layers=1)
@@ -182,6 +183,22 @@ def test_attention_path_switch_in_generate(rinf, synth, oracle, ctx):
     step, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 14)
     print(f"switch: max logits err {max(errs):.2e}", flush=True)
     assert list(toks) == step
+    assert max(errs) <= DEEP_TOL
+    dev.close()
+
+
+@pytest.mark.parametrize("path", [1, 3], ids=["whole-heads", "two-range"])
+def test_attention_paths_qwen2_7b_heads(rinf, synth, oracle, ctx, path):
+    """28 query heads on 4 kv heads of dim 128 (wo Q4_K, 3584 columns): the
+    two-range attention, its merge in the wo GEMV's input and the one-launch
+    kernel against the oracle over 150 positions, including a position range
+    with no positions (the first token of the prompt)."""
+    cfg = dict(SMALL, n_layers=1, embed_dim=3584, n_heads=28, n_kv_heads=4, hidden_dim=1024)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", 33, 160)
+    dev.set_attention_path(path)
+    prompt = np.random.default_rng(15).integers(0, cfg["vocab_size"], 140)
+    out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 10)
+    print(f"7b heads path {path}: max logits err {max(errs):.2e}, median {np.median(errs):.2e}", flush=True)
     assert max(errs) <= DEEP_TOL
     dev.close()
 
