@@ -412,7 +412,9 @@ __global__ void __launch_bounds__(256) attn_combine_k(const float *__restrict__ 
 // what bounds the kernel -- and writing its range's unnormalised output and
 // (max, sum of exponentials) instead, range-major: part[r * q_dim + h * hd + d],
 // ml[2 (r * n_heads + h) + {0, 1}].  The consumer (the wo GEMV's input
-// prologue, launch_gemv_attn) merges the two ranges.
+// prologue, launch_gemv_attn) merges the two ranges.  Chunks of 4 positions
+// per wave there: a workgroup then loads the rows of about the positions it
+// has, 64 at a time, instead of 128 (decode +0.4 %).
 constexpr uint32_t kHeadWaves = 16;
 // cached positions up to which the forward pass uses attn_rope_head_k
 constexpr uint32_t kShortSeq = 512;
@@ -420,7 +422,8 @@ template <int E, int NR = 1>
 __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, float *__restrict__ out)
 {
     static_assert(NR == 1 || NR == 2, "one or two position ranges");
-    constexpr uint32_t HD = 64 * E, NW = kHeadWaves, PW = E <= 2 ? 8u : 4u;   // positions per wave per chunk
+    // positions per wave per chunk
+    constexpr uint32_t HD = 64 * E, NW = kHeadWaves, PW = E <= 2 && NR == 1 ? 8u : 4u;
     constexpr uint32_t ST = NR * NW;                 // position stride between a wave's positions
     __shared__ float sacc[NW][HD];
     __shared__ float sml[NW][2];
