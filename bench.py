@@ -29,7 +29,8 @@ decode, decode_configs
              (Qwen2-0.5B Q4_K_M 32 + 128; Llama-3-8B Q4_K_M / Q5_K / Q8_0,
              64 + 512): greedy decode tok/s with the HBM roofline fraction
 --timeline   instead of all that: the s_memrealtime stamps of the LDS-ring
-             GEMV (libqgemv_timeline.so) -- where a launch spends its time
+             GEMV (libqgemv_timeline.so) -- where a launch spends its time;
+             with --timeline-glu those of the stream kernel's [gate; up] form
 
 Algorithmic bytes per GEMV: ceil(rows*cols/256)*144 + 4*cols + 4*rows.
 Only rank 0 of one GPU is supported (--gpus > 1 exits with a message).
@@ -341,9 +342,11 @@ def sweep_run(rinf, synth, ctx, torch, rotate_mb=256, max_copies=256, steps=200)
 
 
 def timeline_run(rinf, synth, args):
-    """s_memrealtime stamps of the LDS-ring GEMV from libqgemv_timeline.so:
-    per event, the median over workgroups of (stamp - first entry stamp), for
-    the last of 20 back-to-back launches over rotating copies, over `reps`
+    """s_memrealtime stamps of one GEMV kernel from libqgemv_timeline.so: the
+    LDS-ring GEMV, or with --timeline-glu the stream kernel's [gate; up] form
+    (RMSNorm prologue, silu(gate) * up) on a matrix of 2 * hidden rows.  Per
+    event, the median over workgroups of (stamp - first entry stamp), for the
+    last of 20 back-to-back launches over rotating copies, over `reps`
     repetitions (the median of the per-repetition medians)."""
     import ctypes
     import numpy as np
@@ -352,6 +355,7 @@ def timeline_run(rinf, synth, args):
     lib.qg_timeline_read.restype = ctypes.c_int
     lib.qg_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]
     lib.qg_timeline_clear.restype = ctypes.c_int
+    glu = args.timeline_glu
     dtype = rinf.TYPE_IDS[args.type]
     rows, cols = args.rows, args.cols
     nb = rinf.nbytes_for(dtype, rows, cols)
@@ -360,40 +364,62 @@ def timeline_run(rinf, synth, args):
     raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
     x = synth.gen_x(cols, synth.config_seed(4))
     mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
-    if mats[0].kernel_kind != 2:
-        raise SystemExit(f"{args.type} {rows}x{cols} does not run the LDS-ring kernel (kind {mats[0].kernel_kind})")
+    want = 1 if glu else 2
+    if mats[0].kernel_kind != want or (glu and rows % 2):
+        raise SystemExit(f"{args.type} {rows}x{cols} does not run the {'stream' if glu else 'LDS-ring'} kernel "
+                         f"(kind {mats[0].kernel_kind})")
     dx = torch.from_numpy(x).cuda()
     dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    if glu:
+        dxb = torch.from_numpy(synth.gen_x(cols, synth.config_seed(5))).cuda()
+        dnw = torch.ones(cols, dtype=torch.float32, device="cuda")
+        launch = lambda m: m.matvec_norm_glu_dev(dx, dxb, dnw, 1e-6, dy, None, ctx.stream)
+        names = {0: "wave 0: entry", 1: "wave 0: x loads issued", 2: "wave 0: first weight batches issued",
+                 3: "wave 0: x staged as planes", 4: "wave 0: workgroup barrier passed",
+                 5: "wave 0: x slice in registers", 31: "wave 0: end"}
+        for i in range(25):
+            names[6 + i] = f"wave 0: batch {i} done"
+        first = list(range(48, 64))                       # every wave's entry
+    else:
+        launch = lambda m: m.matvec_dev(dx, dy, ctx.stream)
+        names = {0: "compute: entry", 1: "compute: x arrived", 2: "compute: x converted",
+                 3: "compute: planes published", 30: "compute: last stage done", 31: "compute: y written (end)",
+                 32: "loader: entry", 33: "loader: first stages issued", 34: "loader: planes published",
+                 63: "loader: end"}
+        for i in range(13):
+            names[4 + 2 * i] = f"compute: stage {i} reached"
+            names[5 + 2 * i] = f"compute: stage {i} published"
+        for i in range(28):
+            names[35 + i] = f"loader: stage {i} landed"
+        first = [32]
     n_ev, n_wg = 64, 2048
     buf = np.zeros(n_ev * n_wg, np.uint64)
     khz = ctypes.c_int(0)
-    names = {0: "compute: entry", 1: "compute: x arrived", 2: "compute: x converted", 3: "compute: planes published",
-             30: "compute: last stage done", 31: "compute: y written (end)",
-             32: "loader: entry", 33: "loader: first stages issued", 34: "loader: planes published",
-             63: "loader: end"}
-    for i in range(13):
-        names[4 + 2 * i] = f"compute: stage {i} reached"
-        names[5 + 2 * i] = f"compute: stage {i} published"
-    for i in range(28):
-        names[35 + i] = f"loader: stage {i} landed"
-    per_rep = []
+    per_rep, wave_end = [], []
     for rep in range(args.timeline_reps):
         for i in range(20):
-            mats[(rep * 20 + i) % ncopy].matvec_dev(dx, dy, ctx.stream)
+            launch(mats[(rep * 20 + i) % ncopy])
         ctx.synchronize()
         if lib.qg_timeline_read(buf.ctypes.data, buf.size, ctypes.byref(khz)):
             raise SystemExit("qg_timeline_read failed")
         t = buf.reshape(n_wg, n_ev).astype(np.int64)
-        wg = [w for w in range(n_wg) if t[w, 0] and t[w, 32]]
+        wg = [w for w in range(n_wg) if t[w, 0] and t[w, 31]]
         t = t[wg]
-        t0 = min(t[:, 0].min(), t[:, 32].min())
+        starts = t[:, [0] + first]
+        t0 = starts[starts != 0].min()
         us = (t - t0) / (khz.value / 1e3)
         med = {}
         for e in names:
             col = us[:, e][t[:, e] != 0]
             if col.size:
                 med[e] = (float(np.median(col)), float(np.percentile(col, 10)), float(np.percentile(col, 90)))
-        med["end_max"] = (float(us[:, 31].max()),) * 3
+        if glu:
+            ends = np.where(t[:, 32:48] != 0, us[:, 32:48], np.nan)
+            nw = int((~np.isnan(ends)).any(axis=0).sum())
+            wave_end.append([float(np.nanmedian(ends[:, w])) for w in range(nw)] + [float(np.nanmax(ends))])
+            med["end_max"] = (float(np.nanmax(ends)),) * 3
+        else:
+            med["end_max"] = (float(us[:, 31].max()),) * 3
         per_rep.append(med)
     table = []
     for e in sorted(k for k in per_rep[0] if isinstance(k, int)):
@@ -405,12 +431,19 @@ def timeline_run(rinf, synth, args):
     for m in mats:
         m.free()
     ctx.close()
-    res = {"workload": f"{args.type.lower()}_gemv_{rows}x{cols}", "kernel": "qg::gemv_ring (timeline build)",
+    kernel = "qg::gemv_stream, [gate; up] form (timeline build)" if glu else "qg::gemv_ring (timeline build)"
+    res = {"workload": f"{args.type.lower()}_gemv{'_glu' if glu else ''}_{rows}x{cols}", "kernel": kernel,
            "workgroups": len(wg), "clock_khz": khz.value, "reps": args.timeline_reps,
-           "last_workgroup_end_us": round(end_max, 3), "events": table}
+           "last_wave_end_us" if glu else "last_workgroup_end_us": round(end_max, 3), "events": table}
     for r in table:
-        log(f"{r['event']:34s} {r['median_us']:8.3f} us  (p10 {r['p10_us']:.3f}, p90 {r['p90_us']:.3f})")
-    log(f"last workgroup ends at {end_max:.3f} us after the first entry")
+        log(f"{r['event']:38s} {r['median_us']:8.3f} us  (p10 {r['p10_us']:.3f}, p90 {r['p90_us']:.3f})")
+    if glu:
+        we = np.median(np.array(wave_end), axis=0)
+        res["wave_end_median_us"] = [round(float(v), 3) for v in we[:-1]]
+        log("per wave index, median end over workgroups: " + " ".join(f"{v:.2f}" for v in we[:-1]) + " us")
+        log(f"last wave ends at {end_max:.3f} us after the first entry")
+    else:
+        log(f"last workgroup ends at {end_max:.3f} us after the first entry")
     print(json.dumps(res), flush=True)
 
 
@@ -496,6 +529,8 @@ def main():
     ap.add_argument("--timeline", action="store_true",
                     help="only the s_memrealtime timeline of the LDS-ring GEMV (libqgemv_timeline.so)")
     ap.add_argument("--timeline-reps", type=int, default=9)
+    ap.add_argument("--timeline-glu", action="store_true",
+                    help="with --timeline: the stream kernel's [gate; up] form instead of the LDS-ring kernel")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args)

@@ -1041,12 +1041,14 @@ __device__ __forceinline__ void store_y(float *p, float v)
 // ------------------------------------------------------------ timeline
 //
 // Only in the build with -DQG_TIMELINE (libqgemv_timeline.so, `make
-// timeline`): the LDS-ring kernel takes s_memrealtime stamps at fixed points.
-// A stamp goes into lane `ev` of a VGPR (a select, no memory operation and no
-// register indexing), and each stamping wave writes its lanes once, after its
-// last load, wait and barrier, so the kernel's memory traffic and waits are
-// those of the plain build.  Per workgroup, 64 stamps: compute wave 0 in
-// 0..31, the first loader wave in 32..63 (0 = never stamped).
+// timeline`): the LDS-ring kernel and the stream kernel take s_memrealtime
+// stamps at fixed points.  A stamp goes into lane `ev` of a VGPR (a select,
+// no memory operation and no register indexing), and each stamping wave
+// writes its lanes once, after its last load, wait and barrier, so the
+// kernel's memory traffic and waits are those of the plain build.  Per
+// workgroup, 64 stamps: compute wave 0 in 0..31 and, for the ring kernel,
+// the first loader wave in 32..63; the stream kernel puts every wave's end
+// in 32 + w and its entry in 48 + w instead (0 = never stamped).
 #ifdef QG_TIMELINE
 constexpr uint32_t kTlEv = 64, kTlWG = 2048;
 __device__ uint64_t qg_tl_buf[kTlWG * kTlEv];
@@ -1064,13 +1066,26 @@ struct Timeline {
         if (l < 32u && blockIdx.x < kTlWG) qg_tl_buf[blockIdx.x * kTlEv + base + l] = v;
     }
 };
+// this wave's entry and end stamps (lane 0, waves 0..15)
+__device__ __forceinline__ void tl_wave_marks(uint64_t entry)
+{
+    const uint32_t w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 0u && w < 16u && blockIdx.x < kTlWG) {
+        qg_tl_buf[blockIdx.x * kTlEv + 32u + w] = __builtin_amdgcn_s_memrealtime();
+        qg_tl_buf[blockIdx.x * kTlEv + 48u + w] = entry;
+    }
+}
 #define QG_TL_DECL Timeline tl_
 #define QG_TL(ev) tl_.stamp(ev)
 #define QG_TL_WRITE(base) tl_.write(base)
+#define QG_TL_WAVE_DECL const uint64_t tl_entry_ = __builtin_amdgcn_s_memrealtime()
+#define QG_TL_WAVE_END() tl_wave_marks(tl_entry_)
 #else
 #define QG_TL_DECL
 #define QG_TL(ev) ((void)0)
 #define QG_TL_WRITE(base) ((void)0)
+#define QG_TL_WAVE_DECL
+#define QG_TL_WAVE_END() ((void)0)
 #endif
 
 // Workgroup barrier that waits for this wave's LDS traffic only: global loads
@@ -1220,6 +1235,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     const uint32_t ib = I::item_byte(it);
     const uint32_t team = bid * tpw + tw;
     const uint32_t g = G1 ? 1u : a.g;
+    QG_TL_WAVE_DECL;
+    QG_TL_DECL;
+    QG_TL(0);
 
     // 1. x loads, then (once x is in) the first D batches of weight loads.
     // x is read in pieces: 16 elements (four float4) when the workgroup
@@ -1274,9 +1292,11 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
     // conversion then covers x alone.
     // 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding).
     if constexpr (!NORM) __builtin_amdgcn_s_waitcnt(0x0F70);
+    QG_TL(1);
     uint32_t raw[D][R][NR];
 #pragma unroll
     for (int d = 0; d < D0; d++) issue<T, R, GLU, RP>(a, team, d, it, ib, active, raw[d]);
+    QG_TL(2);
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
@@ -1420,7 +1440,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
             put(u, c);
         }
     }
+    QG_TL(3);
     lds_barrier();
+    QG_TL(4);
     if constexpr (NORM) {
         // all the waves' sums read at once (one LDS wait), added in wave order;
         // the slots past the last wave add 0 to a sum of squares
@@ -1465,6 +1487,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
         }
     }
 
+    QG_TL(5);
     // the rest of the ring, now that no conversion work waits behind it
 #pragma unroll
     for (int d = D0; d < D; d++) issue<T, R, GLU, RP>(a, team, d, it, ib, active, raw[d]);
@@ -1566,12 +1589,19 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 #pragma unroll
         for (int d = 0; d < D; d++) {
             process(raw[d], i + d);
+            QG_TL(6u + min(i + d, 24u));
             issue<T, R, GLU, RP>(a, team, i + d + D, it, ib, active, raw[d]);
         }
     }
 #pragma unroll
     for (int d = 0; d < D; d++)
-        if (i + d < a.per_team) process(raw[d], i + d);
+        if (i + d < a.per_team) {
+            process(raw[d], i + d);
+            QG_TL(6u + min(i + d, 24u));
+        }
+    QG_TL(31);
+    if ((tid >> 6) == 0u) QG_TL_WRITE(0);
+    QG_TL_WAVE_END();
 }
 
 template <uint32_t T, int TSUB, int R, int D, bool G1, bool CONV, int XS, int LB, int D0 = D,
