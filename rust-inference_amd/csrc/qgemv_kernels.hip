@@ -1631,8 +1631,10 @@ __global__ void __launch_bounds__(LB) gemv_stream_pair(StreamArgs a1, StreamArgs
 // Plain mat-vec of a repacked matrix with one row per row group and teams of
 // WPT waves (rows of 65..320 items): TPW teams of compute waves and two
 // loader waves per workgroup.  The loaders copy the TPW rows of each stage --
-// TPW consecutive row groups, contiguous in memory -- straight into an LDS
-// ring of kRingSlots slots with global_load_lds_dwordx4, so the weight stream
+// team t of workgroup b runs rows t G + b + i NT (G workgroups, NT teams), so
+// a stage's rows are G apart and every stage of the grid lies in one band of
+// NT rows (Qwen2-7B decode +0.4 % against TPW consecutive rows per workgroup)
+// -- straight into an LDS ring of kRingSlots slots with global_load_lds_dwordx4, so the weight stream
 // starts at kernel entry and no compute wave ever waits behind a weight load:
 // the compute waves load and convert x at once, then read each item from the
 // ring.  One workgroup barrier per stage publishes it; after it the loaders
@@ -1681,7 +1683,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         // loader l: the rows of teams l*TPW/2 .. (l+1)*TPW/2 - 1 of every stage
         const uint32_t l = wave - NW, np = (gb + 15u) / 16u;
         auto issue = [&](uint32_t i) {
-            const uint32_t g0 = blockIdx.x * TPW + l * (TPW / 2) + i * a.n_teams;
+            const uint32_t g0 = l * (TPW / 2) * gridDim.x + blockIdx.x + i * a.n_teams;
             const uint32_t dst = lds0 + slot_off(i) + l * REGION;
 #pragma unroll
             for (uint32_t k = 0; k < (uint32_t)LINST; k++) {
@@ -1690,7 +1692,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
                 // the padding or into rows no lane stores
                 const uint32_t p = k * 64u + lane;
                 const uint32_t r = (TPW / 2 == 2 && p >= np) ? 1u : 0u;
-                const uint32_t pc = min(p - r * np, np - 1u), grp = min(g0 + r, a.n_groups - 1u);
+                const uint32_t pc = min(p - r * np, np - 1u), grp = min(g0 + r * gridDim.x, a.n_groups - 1u);
                 lds_dma16(a.w + grp * gb + pc * 16u, dst + k * 1024u);
             }
         };
@@ -1718,7 +1720,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
     const uint32_t tw = tid / (64u * WPT), lt = tid % (64u * WPT), wt = wave % WPT;
     const bool active = lt < a.ni;
     const uint32_t it = active ? lt : 0u;
-    const uint32_t team = blockIdx.x * TPW + tw;
+    const uint32_t team = tw * gridDim.x + blockIdx.x;
     // x: 16-element pieces, converted by the compute threads
     const uint32_t npc = a.cols / 16u;
     const uint4 *src = (const uint4 *)a.x;
