@@ -145,7 +145,8 @@ def test_q4k_target_shapes(ctx, oracle, synth, shape):
 
 
 # The wave-private kernel: Q4_K rows of 12288 / 14336 columns with at least one
-# 16-row workgroup per CU; 4100 rows end in a workgroup of 4 rows, 8192 rows
+# 16-row workgroup per CU (workgroup b of G takes rows b + G i); 4100 rows leave
+# 12 of the 257 x 16 row slots past the end (clamped loads, no stores), 8192 rows
 # run two workgroups per CU.  Narrower or shorter matrices keep the ring /
 # stream kernels.
 WAVE_SHAPES = [((4096, 14336), 3), ((4096, 12288), 3), ((4100, 14336), 3), ((8192, 14336), 3),
