@@ -26,8 +26,9 @@
 //   SiLU * up        mlp.rs:31-43, silu as math.rs:137-146, in the epilogue
 //                    of the [gate; up] GEMV (gate and up rows paired), else
 //                    inside the down GEMV's prologue or a separate kernel
-//   sample_part_k    sampler.rs:109-127 then math.rs:328-339 over one range
-//   sample_final_k   of the logits per workgroup; then the first maximum
+//   sample_k         sampler.rs:109-127 then math.rs:328-339 over one range
+//                    of the logits per workgroup; the last workgroup to
+//                    finish takes the first maximum over the ranges
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -611,31 +612,63 @@ struct SampleArgs {
     float *pv;                   // per-workgroup maximum and its index
     uint32_t *pi;
     uint32_t *token;             // the sampled token
+    uint32_t *count;             // workgroups done (zero between launches)
 };
 
-// (value, index) of the first maximum over [lo, hi) after the repetition
-// penalty of the tokens in this range (applied in list order, each
-// occurrence again, as sampler.rs:109-127).  NaN never wins.
-__global__ void __launch_bounds__(256) sample_part_k(SampleArgs a)
+// (value, index) max with the smaller index on ties, over one wave
+__device__ __forceinline__ void argmax_wave(float &best, uint32_t &idx)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(idx, o, 64);
+        if (oi != 0xFFFFFFFFu && (idx == 0xFFFFFFFFu || ov > best || (ov == best && oi < idx))) {
+            best = ov; idx = oi;
+        }
+    }
+}
+
+// The sampler in one launch.  Workgroup b takes range b of the logits: the
+// repetition penalty of the recent tokens in its range (sampler.rs:109-127;
+// each occurrence applies it again, and since occurrences of different tokens
+// do not interact, lane r of wave 0 applies all k occurrences of token r when
+// r is its first occurrence, in list order as the sequential loop does), then
+// the range's first maximum (NaN never wins).  Each workgroup publishes its
+// (value, index) and counts itself in a device-scope counter; the last one to
+// arrive takes the first maximum over the ranges (math.rs:328-339: a NaN at
+// index 0 returns 0, as the reference's strict ">" scan does) and resets the
+// counter.  Ranges hold increasing indices and lane l of that wave scans
+// ranges l, l + 64, ... in order, so ties go to the smaller index.  In
+// generate the token is appended to the history and becomes the next step's
+// token.
+__global__ void __launch_bounds__(256) sample_k(SampleArgs a)
 {
     __shared__ float bv[4];
     __shared__ uint32_t bi[4];
+    __shared__ uint32_t last;
     const uint32_t per = (a.n + gridDim.x - 1) / gridDim.x;
     const uint32_t lo = blockIdx.x * per, hi = min(a.n, lo + per);
-    const uint32_t *rc = a.recent;
-    uint32_t nr = a.n_recent;
-    if (a.hist) {
-        const uint32_t cnt = a.st->slot + 1, w = min(min(a.window, kRecentMax), cnt);
-        rc = a.hist + (cnt - w);
-        nr = w;
-    }
-    if (threadIdx.x == 0 && a.penalty != 1.0f) {          // sampler.rs:76-78
-        for (uint32_t r = 0; r < nr; r++) {
-            const uint32_t t = rc[r];
-            if (t >= lo && t < hi) {
-                const float l = a.logits[t];
-                a.logits[t] = l > 0.0f ? l / a.penalty : l * a.penalty;
-            }
+    if (threadIdx.x < 64 && a.penalty != 1.0f) {                   // sampler.rs:76-78
+        const uint32_t *rc = a.recent;
+        uint32_t nr = a.n_recent;
+        if (a.hist) {
+            const uint32_t cnt = a.st->slot + 1, w = min(min(a.window, kRecentMax), cnt);
+            rc = a.hist + (cnt - w);
+            nr = w;
+        }
+        const uint32_t r = threadIdx.x;
+        const uint32_t t = r < nr ? rc[r] : 0xFFFFFFFFu;
+        uint32_t k = 0;
+        bool first = true;
+        for (uint32_t j = 0; j < nr; j++) {
+            const uint32_t u = __shfl(t, (int)j, 64);
+            k += u == t;
+            first = first && !(u == t && j < r);
+        }
+        if (r < nr && first && t >= lo && t < hi) {
+            float l = a.logits[t];
+            for (uint32_t i = 0; i < k; i++) l = l > 0.0f ? l / a.penalty : l * a.penalty;
+            a.logits[t] = l;
         }
     }
     __syncthreads();
@@ -645,15 +678,7 @@ __global__ void __launch_bounds__(256) sample_part_k(SampleArgs a)
         const float v = a.logits[i];
         if (v > best || (idx == 0xFFFFFFFFu && v == best)) { best = v; idx = i; }
     }
-    // (value, index) max with the smaller index on ties
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const uint32_t oi = __shfl_xor(idx, o, 64);
-        if (oi != 0xFFFFFFFFu && (idx == 0xFFFFFFFFu || ov > best || (ov == best && oi < idx))) {
-            best = ov; idx = oi;
-        }
-    }
+    argmax_wave(best, idx);
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = idx; }
     __syncthreads();
@@ -666,30 +691,22 @@ __global__ void __launch_bounds__(256) sample_part_k(SampleArgs a)
         }
         a.pv[blockIdx.x] = b;
         a.pi[blockIdx.x] = id;
+        __threadfence();                          // the pair (and penalised logits) before the count
+        last = atomicAdd(a.count, 1u) == gridDim.x - 1;
     }
-}
-
-// The first maximum over the ranges (math.rs:328-339: a NaN at index 0
-// returns 0, as the reference's strict ">" scan does).  In generate the token
-// is appended to the history and becomes the next step's token.  One wave:
-// lane l scans ranges l, l + 64, ... in order; ranges hold increasing indices,
-// so ties go to the smaller index.
-__global__ void __launch_bounds__(64) sample_final_k(SampleArgs a, uint32_t nparts)
-{
+    __syncthreads();
+    if (!last || threadIdx.x >= 64) return;
+    __threadfence();                              // every workgroup's pair is visible
     float b = -INFINITY;
     uint32_t id = 0xFFFFFFFFu;
-    for (uint32_t i = threadIdx.x; i < nparts; i += 64) {
+    for (uint32_t i = threadIdx.x; i < gridDim.x; i += 64) {
         const float v = a.pv[i];
         const uint32_t j = a.pi[i];
         if (j != 0xFFFFFFFFu && (id == 0xFFFFFFFFu || v > b)) { b = v; id = j; }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(b, o, 64);
-        const uint32_t oi = __shfl_xor(id, o, 64);
-        if (oi != 0xFFFFFFFFu && (id == 0xFFFFFFFFu || ov > b || (ov == b && oi < id))) { b = ov; id = oi; }
-    }
+    argmax_wave(b, id);
     if (threadIdx.x != 0) return;
+    atomicExch(a.count, 0u);                      // ready for the next launch
     const float l0 = a.logits[0];
     const uint32_t tok = (l0 != l0 || id == 0xFFFFFFFFu) ? 0u : id;
     *a.token = tok;
@@ -754,6 +771,7 @@ struct qg_model {
     bool fused_ready = false;
     float *s_pv = nullptr;
     uint32_t *s_pi = nullptr;
+    uint32_t *s_count = nullptr;     // sampler workgroups done; zero between launches
     uint32_t *d_recent = nullptr, *d_token = nullptr, *d_hist = nullptr;
     qgm::Step *d_step = nullptr;
     uint32_t *h_recent = nullptr, *h_token = nullptr;   // pinned
@@ -1005,6 +1023,14 @@ bool complete(const qg_model *m)
     return true;
 }
 
+// A row of a matrix whose rows are whole blocks starts on a block boundary,
+// so the reference's straddle placement (quant.rs:152-174) writes every
+// element of the row and leaves no gap to be zero.
+bool whole_rows(const qg_mat *t)
+{
+    return t->cols % qg::block_elems(t->type) == 0;
+}
+
 // Transformer::forward (transformer.rs:63-98) for the token, position and
 // slot in m->d_step; enqueues kernels only (also used under graph capture).
 int enqueue_forward(qg_model *m)
@@ -1014,8 +1040,9 @@ int enqueue_forward(qg_model *m)
     ihipStream_t *sti = (ihipStream_t *)st;
     const uint32_t E = c.embed_dim;
     int rc;
-    // embedding row into a zeroed buffer (transformer.rs:74-75, quant.rs:152-174)
-    if (qg::launch_fill(m->h0, E, 0.0f, sti) ||
+    // embedding row into a zeroed buffer (transformer.rs:74-75, quant.rs:152-174);
+    // with whole blocks per row every element is written, so no fill
+    if ((!whole_rows(m->tok) && qg::launch_fill(m->h0, E, 0.0f, sti)) ||
         qg::launch_dequantize_row_dev(m->tok->type, m->tok->d, m->tok->rows, m->tok->cols, &m->d_step->token,
                                       m->h0, sti))
         return mfail(m, QG_ERR_HIP, "embedding", hipGetLastError());
@@ -1135,14 +1162,14 @@ qgm::SampleArgs sample_args(qg_model *m, uint32_t n_recent, float penalty, bool 
     a.pv = m->s_pv;
     a.pi = m->s_pi;
     a.token = m->d_token;
+    a.count = m->s_count;
     return a;
 }
 
 int enqueue_sample(qg_model *m, const qgm::SampleArgs &a)
 {
     hipStream_t st = m->ctx->stream;
-    hipLaunchKernelGGL(qgm::sample_part_k, dim3(qgm::kSampleWG), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(qgm::sample_final_k, dim3(1), dim3(64), 0, st, a, qgm::kSampleWG);
+    hipLaunchKernelGGL(qgm::sample_k, dim3(qgm::kSampleWG), dim3(256), 0, st, a);
     return launched(m, "sample");
 }
 
@@ -1323,7 +1350,7 @@ int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
     int rc;
     // embedding rows into zeroed rows (transformer.rs:74-75, quant.rs:152-174)
     float *h = m->pf_h[0], *h2 = m->pf_h[1];
-    if (qg::launch_fill(h, (size_t)ntok * E, 0.0f, sti) ||
+    if ((!whole_rows(m->tok) && qg::launch_fill(h, (size_t)ntok * E, 0.0f, sti)) ||
         qg::launch_dequantize_rows_dev(m->tok->type, m->tok->d, m->tok->rows, m->tok->cols, d_tok, ntok, h, E, sti))
         return mfail(m, QG_ERR_HIP, "embedding", hipGetLastError());
     const size_t kv_layer = (size_t)c.max_seq_len * m->kv_dim;
@@ -1460,7 +1487,7 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
         (rc = dalloc(m, &m->att_ml, npart * 2)) || (rc = dalloc(m, &m->s_pv, qgm::kSampleWG)) ||
         (rc = dalloc(m, &m->s_pi, qgm::kSampleWG)) || (rc = dalloc(m, &m->d_recent, qgm::kRecentMax)) ||
         (rc = dalloc(m, &m->d_token, 1)) || (rc = dalloc(m, &m->d_hist, (size_t)c.max_seq_len + 1)) ||
-        (rc = dalloc(m, &m->d_step, 1))) {
+        (rc = dalloc(m, &m->d_step, 1)) || (rc = dalloc(m, &m->s_count, 1))) {
         free_model(m);
         return rc;
     }

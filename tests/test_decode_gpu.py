@@ -272,6 +272,57 @@ def test_generate_matches_stepwise(rinf, synth, oracle, ctx):
     dev.close()
 
 
+def test_sampler_repeats_ties_and_nan(rinf, synth, oracle, ctx):
+    """The one-launch sampler against the reference's sequential penalty loop
+    and first-maximum scan: a token listed k times is penalised k times (the
+    penalty is chosen so that 2 and 3 occurrences give different winners),
+    only the last `window` entries count, equal logits go to the smaller index
+    across workgroup ranges, and a NaN logit at index 0 returns token 0."""
+    V = SMALL["vocab_size"]
+    t = synth.gen_model(SMALL, "q8_0", 31)
+    raw, dtype, rows, cols = t["mats"][("lm_head", 0)]
+    dev, ref, _ = build(rinf, synth, oracle, ctx, SMALL, "q8_0", 31, 8)
+    lg = np.zeros(V, np.float32)
+
+    def sample(recent, penalty, window=64):
+        dev.reset()
+        dev.forward(3, 0, lg)
+        base = lg.copy()
+        tok = dev.sample_greedy(recent, penalty, window)
+        rl = base.copy()
+        oracle.repetition_penalty(rl, recent, penalty, window)
+        assert tok == oracle.argmax(rl), (recent, penalty, window)
+        return tok, base
+
+    _, base = sample([], 1.0)
+    order = np.argsort(-base, kind="stable")
+    a, b = int(order[0]), int(order[1])
+    assert base[b] > 0
+    p = float((base[a] / base[b]) ** (1 / 2.5))     # a/p^2 > b > a/p^3
+    others = [int(v) for v in order[5:12]]
+    two = [others[0], a, others[1], a, others[2]]
+    three = [a, others[3], a, others[4], a]
+    assert sample(two, p)[0] == a
+    assert sample(three, p)[0] == b
+    assert sample(others[:2] + three, p, window=5)[0] == b
+    assert sample(three + others[:2], p, window=4)[0] == a      # one occurrence left
+    # a tie: row c (another workgroup's range) holds row a's bytes
+    c = next(i for i in range(V) if abs(i - a) > 8)
+    tied = np.array(raw, np.uint8, copy=True).reshape(rows, -1)      # whole Q8_0 blocks per row
+    tied[c] = tied[a]
+    dev.set_matrix(rinf.M_LM_HEAD, 0, tied, dtype, rows, cols)
+    tok, base = sample([], 1.0)
+    assert base[c] == base[a] and tok == min(a, c)
+    assert sample([min(a, c)], 1.1)[0] == max(a, c)
+    # NaN at index 0 (an F32 lm_head row of NaNs)
+    f = np.full((rows, cols), 0.01, np.float32)
+    f[0] = np.nan
+    dev.set_matrix(rinf.M_LM_HEAD, 0, f, rinf.F32, rows, cols)
+    tok, base = sample([5, 6], 1.1)
+    assert np.isnan(base[0]) and tok == 0
+    dev.close()
+
+
 def test_qwen2_05b_config3_as_stated(rinf, synth, oracle, ctx):
     """BASELINE.json configs[2] exactly: Qwen2-0.5B architecture, Q4_K_M, tied
     lm_head, token_embd Q4_K at cols = 896 (rows straddle superblocks: the
