@@ -26,9 +26,8 @@
 //   SiLU * up        mlp.rs:31-43, silu as math.rs:137-146, in the epilogue
 //                    of the [gate; up] GEMV (gate and up rows paired), else
 //                    inside the down GEMV's prologue or a separate kernel
-//   sample_k         sampler.rs:109-127 then math.rs:328-339 over one range
-//                    of the logits per workgroup; the last workgroup to
-//                    finish takes the first maximum over the ranges
+//   sample_part_k    sampler.rs:109-127 then math.rs:328-339 over one range
+//   sample_final_k   of the logits per workgroup; then the first maximum
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -612,7 +611,6 @@ struct SampleArgs {
     float *pv;                   // per-workgroup maximum and its index
     uint32_t *pi;
     uint32_t *token;             // the sampled token
-    uint32_t *count;             // workgroups done (zero between launches)
 };
 
 // (value, index) max with the smaller index on ties, over one wave
@@ -628,24 +626,15 @@ __device__ __forceinline__ void argmax_wave(float &best, uint32_t &idx)
     }
 }
 
-// The sampler in one launch.  Workgroup b takes range b of the logits: the
-// repetition penalty of the recent tokens in its range (sampler.rs:109-127;
-// each occurrence applies it again, and since occurrences of different tokens
-// do not interact, lane r of wave 0 applies all k occurrences of token r when
-// r is its first occurrence, in list order as the sequential loop does), then
-// the range's first maximum (NaN never wins).  Each workgroup publishes its
-// (value, index) and counts itself in a device-scope counter; the last one to
-// arrive takes the first maximum over the ranges (math.rs:328-339: a NaN at
-// index 0 returns 0, as the reference's strict ">" scan does) and resets the
-// counter.  Ranges hold increasing indices and lane l of that wave scans
-// ranges l, l + 64, ... in order, so ties go to the smaller index.  In
-// generate the token is appended to the history and becomes the next step's
-// token.
-__global__ void __launch_bounds__(256) sample_k(SampleArgs a)
+// (value, index) of the first maximum over [lo, hi) after the repetition
+// penalty of the tokens in this range (sampler.rs:109-127: in list order, each
+// occurrence again).  Occurrences of different tokens do not interact, so lane
+// r of wave 0 applies all k occurrences of token r where r is its first
+// occurrence, in the order the sequential loop applies them.  NaN never wins.
+__global__ void __launch_bounds__(256) sample_part_k(SampleArgs a)
 {
     __shared__ float bv[4];
     __shared__ uint32_t bi[4];
-    __shared__ uint32_t last;
     const uint32_t per = (a.n + gridDim.x - 1) / gridDim.x;
     const uint32_t lo = blockIdx.x * per, hi = min(a.n, lo + per);
     if (threadIdx.x < 64 && a.penalty != 1.0f) {                   // sampler.rs:76-78
@@ -691,22 +680,27 @@ __global__ void __launch_bounds__(256) sample_k(SampleArgs a)
         }
         a.pv[blockIdx.x] = b;
         a.pi[blockIdx.x] = id;
-        __threadfence();                          // the pair (and penalised logits) before the count
-        last = atomicAdd(a.count, 1u) == gridDim.x - 1;
     }
-    __syncthreads();
-    if (!last || threadIdx.x >= 64) return;
-    __threadfence();                              // every workgroup's pair is visible
+}
+
+// The first maximum over the ranges (math.rs:328-339: a NaN at index 0
+// returns 0, as the reference's strict ">" scan does).  In generate the token
+// is appended to the history and becomes the next step's token.  One wave:
+// lane l scans ranges l, l + 64, ... in order; ranges hold increasing indices,
+// so ties go to the smaller index.  (A single launch whose last workgroup
+// takes this maximum needs device-scope fences to publish the ranges across
+// the XCDs' L2 caches; measured slower than the second launch.)
+__global__ void __launch_bounds__(64) sample_final_k(SampleArgs a, uint32_t nparts)
+{
     float b = -INFINITY;
     uint32_t id = 0xFFFFFFFFu;
-    for (uint32_t i = threadIdx.x; i < gridDim.x; i += 64) {
+    for (uint32_t i = threadIdx.x; i < nparts; i += 64) {
         const float v = a.pv[i];
         const uint32_t j = a.pi[i];
         if (j != 0xFFFFFFFFu && (id == 0xFFFFFFFFu || v > b)) { b = v; id = j; }
     }
     argmax_wave(b, id);
     if (threadIdx.x != 0) return;
-    atomicExch(a.count, 0u);                      // ready for the next launch
     const float l0 = a.logits[0];
     const uint32_t tok = (l0 != l0 || id == 0xFFFFFFFFu) ? 0u : id;
     *a.token = tok;
@@ -771,7 +765,6 @@ struct qg_model {
     bool fused_ready = false;
     float *s_pv = nullptr;
     uint32_t *s_pi = nullptr;
-    uint32_t *s_count = nullptr;     // sampler workgroups done; zero between launches
     uint32_t *d_recent = nullptr, *d_token = nullptr, *d_hist = nullptr;
     qgm::Step *d_step = nullptr;
     uint32_t *h_recent = nullptr, *h_token = nullptr;   // pinned
@@ -1162,14 +1155,14 @@ qgm::SampleArgs sample_args(qg_model *m, uint32_t n_recent, float penalty, bool 
     a.pv = m->s_pv;
     a.pi = m->s_pi;
     a.token = m->d_token;
-    a.count = m->s_count;
     return a;
 }
 
 int enqueue_sample(qg_model *m, const qgm::SampleArgs &a)
 {
     hipStream_t st = m->ctx->stream;
-    hipLaunchKernelGGL(qgm::sample_k, dim3(qgm::kSampleWG), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(qgm::sample_part_k, dim3(qgm::kSampleWG), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(qgm::sample_final_k, dim3(1), dim3(64), 0, st, a, qgm::kSampleWG);
     return launched(m, "sample");
 }
 
@@ -1487,7 +1480,7 @@ int qg_model_create(qg_ctx *ctx, const qg_model_config *cfg, qg_model **out)
         (rc = dalloc(m, &m->att_ml, npart * 2)) || (rc = dalloc(m, &m->s_pv, qgm::kSampleWG)) ||
         (rc = dalloc(m, &m->s_pi, qgm::kSampleWG)) || (rc = dalloc(m, &m->d_recent, qgm::kRecentMax)) ||
         (rc = dalloc(m, &m->d_token, 1)) || (rc = dalloc(m, &m->d_hist, (size_t)c.max_seq_len + 1)) ||
-        (rc = dalloc(m, &m->d_step, 1)) || (rc = dalloc(m, &m->s_count, 1))) {
+        (rc = dalloc(m, &m->d_step, 1))) {
         free_model(m);
         return rc;
     }
