@@ -63,7 +63,9 @@ int qg_upload(qg_ctx *ctx, const void *raw, size_t nbytes, uint32_t ggml_type,
               size_t rows, size_t cols, qg_mat **out);
 /* Wraps bytes already in HBM (device pointer, at least 16-byte aligned,
  * followed by >= 512 readable bytes) without copying; the caller keeps them
- * alive for the handle's lifetime. */
+ * alive for the handle's lifetime.  QG_ERR_INVALID_ARG when the device
+ * allocation holding d_raw (hipMemGetAddressRange) ends less than 512 bytes
+ * after the matrix's data, or when d_raw is in no allocation HIP knows. */
 int qg_wrap_device(qg_ctx *ctx, const void *d_raw, size_t nbytes, uint32_t ggml_type,
                    size_t rows, size_t cols, qg_mat **out);
 /* Frees a matrix.  QG_ERR_INVALID_ARG for a handle this context does not

@@ -567,6 +567,18 @@ int qg_wrap_device(qg_ctx *ctx, const void *d_raw, size_t nbytes, uint32_t type,
     if (rc != QG_OK) return fail(ctx, rc, "unsupported type or shape");
     if (nbytes < need) return fail(ctx, QG_ERR_SHORT_DATA, "raw data shorter than the matrix needs");
     if (!d_raw || ((uintptr_t)d_raw & 15u)) return fail(ctx, QG_ERR_INVALID_ARG, "device pointer NULL or not 16-byte aligned");
+    // the kernels read whole 16-byte pieces up to kTailPad bytes past the
+    // data: the allocation that holds d_raw must extend that far
+    (void)hipSetDevice(ctx->device);
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)d_raw) != hipSuccess) {
+        (void)hipGetLastError();                             // leave no sticky error for the caller's next launch
+        return fail(ctx, QG_ERR_INVALID_ARG, "d_raw is not in a device allocation of this HIP runtime");
+    }
+    const uintptr_t end = (uintptr_t)base + size, p = (uintptr_t)d_raw;
+    if (p < (uintptr_t)base || end - p < need || end - p - need < qg::kTailPad)
+        return fail(ctx, QG_ERR_INVALID_ARG, "the allocation ends less than 512 bytes after the matrix data");
     return new_mat(ctx, (uint8_t *)d_raw, need, type, rows, cols, false, out);
 }
 

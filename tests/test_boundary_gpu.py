@@ -170,3 +170,34 @@ def test_probe_stream_read(rinf, ctx):
     with pytest.raises(rinf.QgemvError) as e:
         ctx.probe_stream_read(buf, 100, out)                      # not whole 16-byte pieces
     assert e.value.status == INVALID
+
+
+def test_wrap_device_needs_the_tail_pad(ctx):
+    """qg_wrap_device's kernels read whole 16-byte pieces up to 512 bytes past
+    the matrix data: a matrix that ends less than 512 bytes before the end of
+    its device allocation is refused (QG_ERR_INVALID_ARG), one that leaves
+    exactly 512 is accepted, and a host pointer is refused."""
+    import torch
+    rows, cols = 64, 256
+    need = rows * (cols // 256) * 144                      # Q4_K: 144 bytes per 256 columns
+    buf = torch.zeros(8 << 20, dtype=torch.uint8, device="cuda")
+    seg = next(s for s in torch.cuda.memory_snapshot()
+               if s["address"] <= buf.data_ptr() < s["address"] + s["total_size"])
+    end = seg["address"] + seg["total_size"]
+    lib, out = ctx.lib, ctypes.c_void_p()
+
+    def wrap(addr):
+        return lib.qg_wrap_device(ctx.h, ctypes.c_void_p(addr), need, Q4_K, rows, cols, ctypes.byref(out))
+
+    for slack, want in ((0, INVALID), (256, INVALID), (496, INVALID), (512, 0), (4096, 0)):
+        addr = end - need - slack
+        assert addr % 16 == 0 and addr >= seg["address"]
+        rc = wrap(addr)
+        assert rc == want, (slack, rc)
+        if rc == 0:
+            assert lib.qg_mat_free(ctx.h, out) == 0
+    host = np.zeros(need + 1024, np.uint8)
+    assert wrap(host.ctypes.data) == INVALID
+    # no sticky HIP error is left behind for the next launch
+    torch.ones(16, device="cuda").sum().item()
+    del buf
