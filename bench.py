@@ -17,20 +17,24 @@ roofline     algorithmic bytes / average launch duration of the GEMV kernel:
              WRITE_SIZE (profiles/traffic.json, written by --pmc-summary), or null
 cpu_baseline the oracle's restatement of the reference's --cpu loop
              (src/quant.rs:188-205) on one host core, same matrix
-ceiling      the streaming-read ceiling at the same byte count: the library's
-             plain full-grid read (qg_probe_stream_read) and torch.sum over
-             the same number of rotating copies, also at 76 MB and 447 MB
-             (the 7B [gate;up] and lm_head sizes); roofline.ceiling_us is the
-             faster read at the headline size
+ceiling      the streaming-read ceiling at the same byte count: a sweep of
+             plain read designs (libqgprobe.so, include/qgprobe.h: 256/512/1024
+             threads, 1-8 loads per thread, full or persistent grids of
+             256-4096 workgroups), gemv_wave's own load pattern without its
+             compute, and torch.sum, over rotating copies; also at 76 MB and
+             447 MB (the 7B [gate;up] and lm_head sizes); roofline.ceiling_us
+             is the fastest read at the headline size
 sweep        BASELINE.json configs[1]: the per-type GEMVs at the Qwen2-0.5B
              shapes and the Q6_K 151936 x 896 lm_head
 decode, decode_configs
              configs[3] (Qwen2-7B Q4_K_M, 64 + 256) and configs[2] / [4]
              (Qwen2-0.5B Q4_K_M 32 + 128; Llama-3-8B Q4_K_M / Q5_K / Q8_0,
              64 + 512): greedy decode tok/s with the HBM roofline fraction
---timeline   instead of all that: the s_memrealtime stamps of the LDS-ring
-             GEMV (libqgemv_timeline.so) -- where a launch spends its time;
-             with --timeline-glu those of the stream kernel's [gate; up] form
+--timeline   instead of all that: the s_memrealtime stamps of the GEMV the
+             shape plans (libqgemv_timeline.so: the wave-private kernel for
+             Q4_K 4096 x 14336, the LDS-ring kernel for e.g. Q6_K 3584 x 18944)
+             -- where a launch spends its time; with --timeline-glu those of
+             the stream kernel's [gate; up] form
 
 Algorithmic bytes per GEMV: ceil(rows*cols/256)*144 + 4*cols + 4*rows.
 Only rank 0 of one GPU is supported (--gpus > 1 exits with a message).
@@ -272,33 +276,79 @@ def _event_loop(torch, st, fn, n, warmup):
     return e0.elapsed_time(e1)
 
 
-def ceiling_run(ctx, torch, sizes, rotate_min=1 << 30):
-    """Streaming-read ceiling at each byte count: the library's plain read
-    (qg_probe_stream_read, one 16-byte load per thread of a full grid) and
-    torch.sum of a float32 view, each over enough rotating copies (>= 1 GiB)
-    that every pass misses the 256 MB Infinity Cache."""
+CEIL_THREADS = (256, 512, 1024)
+CEIL_LOADS = (1, 2, 4, 8)
+CEIL_WGS = (0, 256, 512, 1024, 2048, 4096)          # 0: one round over a full grid
+
+
+def ceiling_run(rinf, ctx, torch, sizes, rotate_min=1 << 30, wave_rows=None):
+    """Streaming-read ceiling at each byte count: every read design of
+    libqgprobe.so's qgp_read (workgroups of 256/512/1024 threads; 1, 2, 4 or
+    8 16-byte loads in flight per thread; a full grid or 256..4096 persistent
+    workgroups), for the headline size also gemv_wave's own load pattern
+    without its compute (qgp_read_wave_lds: rows G apart, LDS DMA, one step
+    of four rows in flight), and torch.sum of a float32 view; each over
+    enough rotating copies (>= 1 GiB) that every launch misses the 256 MB
+    Infinity Cache, launches issued back to back from C.  ceiling_us is the
+    fastest of them all."""
+    import ctypes
+    probe = rinf.load_probe_library()
     out = {}
     st = torch.cuda.ExternalStream(ctx.stream)
+    sp = ctypes.c_void_p(ctx.stream)
     for name, nbytes in sizes:
         nb16 = nbytes // 16 * 16
         ncopy = max(3, -(-rotate_min // nb16))
         bufs = [torch.empty(nb16 // 4, dtype=torch.float32, device="cuda").uniform_() for _ in range(ncopy)]
+        arr = (ctypes.c_void_p * ncopy)(*[b.data_ptr() for b in bufs])
         dout = torch.zeros(4, dtype=torch.int32, device="cuda")
-        n = 60 if nbytes > 2e8 else 300
-        probe_ms = _event_loop(torch, st, lambda i: ctx.probe_stream_read(bufs[i % ncopy], nb16, dout, ctx.stream),
-                               n, 20)
+        n = 60 if nbytes > 2e8 else 200
+
+        def timed(launch):
+            launch(20)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            launch(n)
+            e1.record(st)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / n
+
+        designs = []
+        for threads in CEIL_THREADS:
+            for loads in CEIL_LOADS:
+                for wgs in CEIL_WGS:
+                    def launch(k, t=threads, w=wgs, l=loads):
+                        if probe.qgp_read(arr, ncopy, nb16, dout.data_ptr(), t, w, l, k, sp):
+                            raise SystemExit("qgp_read failed")
+                    us = timed(launch)
+                    designs.append({"threads": threads, "workgroups": wgs or "full grid", "loads": loads,
+                                    "us": round(us, 3), "GBs": round(nb16 / us / 1e3, 1)})
+        best = min(designs, key=lambda d: d["us"])
+        res = {"bytes": nb16, "rotating_copies": ncopy, "launches": n, "designs": designs, "best_read": best}
+        cands = [best["us"]]
+        if wave_rows and nb16 == wave_rows[0] * wave_rows[1]:
+            def launch_w(k):
+                if probe.qgp_read_wave_lds(arr, ncopy, wave_rows[0], wave_rows[1], dout.data_ptr(), k, sp):
+                    raise SystemExit("qgp_read_wave_lds failed")
+            wus = timed(launch_w)
+            res["wave_lds_read_us"] = round(wus, 3)
+            cands.append(wus)
         cur = torch.cuda.current_stream()
         torch_ms = _event_loop(torch, cur, lambda i: torch.sum(bufs[i % ncopy]), n, 20)
+        t_us = torch_ms * 1e3 / n
+        res["torch_sum_us"] = round(t_us, 3)
+        cands.append(t_us)
+        c = min(cands)
+        res["ceiling_us"] = round(c, 3)
+        res["ceiling_frac_of_8TBs"] = round(nb16 / c / 1e3 / PEAK_GBS, 4)
         del bufs
         torch.cuda.empty_cache()
-        p_us, t_us = probe_ms * 1e3 / n, torch_ms * 1e3 / n
-        out[name] = {"bytes": nb16, "rotating_copies": ncopy,
-                     "probe_read_us": round(p_us, 3), "probe_read_GBs": round(nb16 / p_us / 1e3, 1),
-                     "torch_sum_us": round(t_us, 3), "torch_sum_GBs": round(nb16 / t_us / 1e3, 1),
-                     "ceiling_us": round(min(p_us, t_us), 3),
-                     "ceiling_frac_of_8TBs": round(nb16 / min(p_us, t_us) / 1e3 / PEAK_GBS, 4)}
-        log(f"ceiling {name}: plain read {p_us:.2f} us ({nb16 / p_us / 1e3:.0f} GB/s), torch.sum "
-            f"{t_us:.2f} us ({nb16 / t_us / 1e3:.0f} GB/s)")
+        out[name] = res
+        log(f"ceiling {name}: best plain read {best['us']:.2f} us ({best['GBs']:.0f} GB/s: {best['threads']} "
+            f"threads, {best['loads']} loads, {best['workgroups']} workgroups) of {len(designs)} designs"
+            + (f"; gemv_wave's load pattern {res['wave_lds_read_us']:.2f} us" if "wave_lds_read_us" in res else "")
+            + f"; torch.sum {t_us:.2f} us")
     return out
 
 
@@ -309,8 +359,11 @@ SWEEP_SHAPES = ((896, 896), (128, 896), (896, 4864))
 
 def sweep_run(rinf, synth, ctx, torch, rotate_mb=256, max_copies=256, steps=200):
     """Per-type GEMV time at the configs[1] shapes: back-to-back launches
-    over rotating copies (>= rotate_mb MiB, at most max_copies copies: the
-    small shapes stay within the caches, where launch latency bounds them)."""
+    issued from C over rotating copies (>= rotate_mb MiB, at most max_copies
+    copies: the small shapes stay within the caches), HIP events around the
+    loop.  A launch of these small kernels costs about as much as the kernel:
+    the µs here are launch-inclusive, rocprofv3's kernel durations are the
+    kernels alone (profiles/)."""
     import numpy as np
     entries = []
     st = torch.cuda.ExternalStream(ctx.stream)
@@ -325,8 +378,16 @@ def sweep_run(rinf, synth, ctx, torch, rotate_mb=256, max_copies=256, steps=200)
         dx = torch.from_numpy(x).cuda()
         dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
         n = steps if nb < 1e8 else 60
-        ms = _event_loop(torch, st, lambda i: mats[i % ncopy].matvec_dev(dx, dy, ctx.stream), n, 20)
-        us = ms * 1e3 / n
+        # launches issued back to back from C (qg_matvec_dev_repeat): a Python
+        # launch costs more than these kernels take
+        ctx.matvec_repeat(mats, dx, dy, 20, ctx.stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        ctx.matvec_repeat(mats, dx, dy, n, ctx.stream)
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
         B = alg_bytes(rinf, dtype, rows, cols)
         kind = {0: "generic", 1: "stream", 2: "ring", 3: "wave"}.get(mats[0].kernel_kind, "?")
         entries.append({"type": tname, "rows": rows, "cols": cols, "us": round(us, 3),
@@ -341,9 +402,38 @@ def sweep_run(rinf, synth, ctx, torch, rotate_mb=256, max_copies=256, steps=200)
     return entries
 
 
+def shape_run(rinf, synth, ctx, torch, tname, rows, cols, steps, warmup, rotate_mb=512):
+    """One more GEMV shape timed like the headline (time_gemv: the better of
+    the C loop, eager and graph launches over >= rotate_mb MiB of rotating
+    copies), e.g. configs[4]'s Q4_K 14336 x 4096."""
+    import numpy as np
+    dtype = rinf.TYPE_IDS[tname]
+    nb = rinf.nbytes_for(dtype, rows, cols)
+    ncopy = max(2, -(-rotate_mb * 2**20 // nb))
+    raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
+    x = synth.gen_x(cols, synth.config_seed(4))
+    mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    c_ms, eager_ms, graph_ms, _ = time_gemv(ctx, torch, mats, dx, dy, steps, warmup)
+    us = min(c_ms, eager_ms, graph_ms) * 1e3 / steps
+    B = alg_bytes(rinf, dtype, rows, cols)
+    kind = {1: "gemv_stream", 2: "gemv_ring", 3: "gemv_wave"}.get(mats[0].kernel_kind, "gemv_generic")
+    if not np.all(np.isfinite(dy.cpu().numpy())):
+        raise SystemExit(f"{tname} {rows}x{cols}: non-finite output")
+    for m in mats:
+        m.free()
+    log(f"{tname} {rows}x{cols}: {us:.2f} us per GEMV, {B / us / 1e3:.0f} GB/s ({kind})")
+    return {"type": tname, "rows": rows, "cols": cols, "us": round(us, 3), "GBs": round(B / us / 1e3, 1),
+            "frac_of_8TBs": round(B / us / 1e3 / PEAK_GBS, 4), "alg_bytes": B, "kernel": kind,
+            "rotating_copies": ncopy, "us_c_loop": round(c_ms * 1e3 / steps, 3),
+            "us_eager": round(eager_ms * 1e3 / steps, 3), "us_graph": round(graph_ms * 1e3 / steps, 3)}
+
+
 def timeline_run(rinf, synth, args):
     """s_memrealtime stamps of one GEMV kernel from libqgemv_timeline.so: the
-    LDS-ring GEMV, or with --timeline-glu the stream kernel's [gate; up] form
+    wave-private or LDS-ring GEMV the shape plans, or with --timeline-glu the
+    stream kernel's [gate; up] form
     (RMSNorm prologue, silu(gate) * up) on a matrix of 2 * hidden rows.  Per
     event, the median over workgroups of (stamp - first entry stamp), for the
     last of 20 back-to-back launches over rotating copies, over `reps`
@@ -364,10 +454,11 @@ def timeline_run(rinf, synth, args):
     raw = synth.gen_blocks(dtype, rows, cols, synth.config_seed(4))
     x = synth.gen_x(cols, synth.config_seed(4))
     mats = [ctx.upload(raw, dtype, rows, cols) for _ in range(ncopy)]
-    want = 1 if glu else 2
-    if mats[0].kernel_kind != want or (glu and rows % 2):
-        raise SystemExit(f"{args.type} {rows}x{cols} does not run the {'stream' if glu else 'LDS-ring'} kernel "
-                         f"(kind {mats[0].kernel_kind})")
+    kind = mats[0].kernel_kind
+    mode = "glu" if glu else {2: "ring", 3: "wave"}.get(kind)
+    if mode is None or (glu and (kind not in (1, 2, 3) or rows % 2)):
+        raise SystemExit(f"{args.type} {rows}x{cols} (kernel kind {kind}) has no "
+                         f"{'stream-kernel [gate; up]' if glu else 'LDS-ring or wave-private'} timeline")
     dx = torch.from_numpy(x).cuda()
     dy = torch.zeros(rows, dtype=torch.float32, device="cuda")
     if glu:
@@ -380,6 +471,17 @@ def timeline_run(rinf, synth, args):
         for i in range(25):
             names[6 + i] = f"wave 0: batch {i} done"
         first = list(range(48, 64))                       # every wave's entry
+        end_ev = 31
+    elif mode == "wave":
+        launch = lambda m: m.matvec_dev(dx, dy, ctx.stream)
+        names = {0: "wave 0: entry", 1: "wave 0: x and rows 0-3 requested", 2: "wave 0: x landed",
+                 3: "wave 0: x converted (in registers)", 12: "wave 0: workgroup barrier passed",
+                 13: "wave 0: y written (end)"}
+        for i in range(4):
+            names[4 + 2 * i] = f"wave 0: step {i} landed (rows {4 * i}-{4 * i + 3})"
+            names[5 + 2 * i] = f"wave 0: step {i} computed"
+        first = list(range(48, 56))                       # the 8 waves' entries
+        end_ev = 13
     else:
         launch = lambda m: m.matvec_dev(dx, dy, ctx.stream)
         names = {0: "compute: entry", 1: "compute: x arrived", 2: "compute: x converted",
@@ -392,6 +494,7 @@ def timeline_run(rinf, synth, args):
         for i in range(28):
             names[35 + i] = f"loader: stage {i} landed"
         first = [32]
+        end_ev = 31
     n_ev, n_wg = 64, 2048
     buf = np.zeros(n_ev * n_wg, np.uint64)
     khz = ctypes.c_int(0)
@@ -403,7 +506,7 @@ def timeline_run(rinf, synth, args):
         if lib.qg_timeline_read(buf.ctypes.data, buf.size, ctypes.byref(khz)):
             raise SystemExit("qg_timeline_read failed")
         t = buf.reshape(n_wg, n_ev).astype(np.int64)
-        wg = [w for w in range(n_wg) if t[w, 0] and t[w, 31]]
+        wg = [w for w in range(n_wg) if t[w, 0] and t[w, end_ev]]
         t = t[wg]
         starts = t[:, [0] + first]
         t0 = starts[starts != 0].min()
@@ -413,7 +516,7 @@ def timeline_run(rinf, synth, args):
             col = us[:, e][t[:, e] != 0]
             if col.size:
                 med[e] = (float(np.median(col)), float(np.percentile(col, 10)), float(np.percentile(col, 90)))
-        if glu:
+        if mode in ("glu", "wave"):
             ends = np.where(t[:, 32:48] != 0, us[:, 32:48], np.nan)
             nw = int((~np.isnan(ends)).any(axis=0).sum())
             wave_end.append([float(np.nanmedian(ends[:, w])) for w in range(nw)] + [float(np.nanmax(ends))])
@@ -431,13 +534,14 @@ def timeline_run(rinf, synth, args):
     for m in mats:
         m.free()
     ctx.close()
-    kernel = "qg::gemv_stream, [gate; up] form (timeline build)" if glu else "qg::gemv_ring (timeline build)"
+    kernel = {"glu": "qg::gemv_stream, [gate; up] form", "ring": "qg::gemv_ring",
+              "wave": "qg::gemv_wave"}[mode] + " (timeline build)"
     res = {"workload": f"{args.type.lower()}_gemv{'_glu' if glu else ''}_{rows}x{cols}", "kernel": kernel,
            "workgroups": len(wg), "clock_khz": khz.value, "reps": args.timeline_reps,
-           "last_wave_end_us" if glu else "last_workgroup_end_us": round(end_max, 3), "events": table}
+           "last_wave_end_us" if mode != "ring" else "last_workgroup_end_us": round(end_max, 3), "events": table}
     for r in table:
-        log(f"{r['event']:38s} {r['median_us']:8.3f} us  (p10 {r['p10_us']:.3f}, p90 {r['p90_us']:.3f})")
-    if glu:
+        log(f"{r['event']:44s} {r['median_us']:8.3f} us  (p10 {r['p10_us']:.3f}, p90 {r['p90_us']:.3f})")
+    if mode in ("glu", "wave"):
         we = np.median(np.array(wave_end), axis=0)
         res["wave_end_median_us"] = [round(float(v), 3) for v in we[:-1]]
         log("per wave index, median end over workgroups: " + " ".join(f"{v:.2f}" for v in we[:-1]) + " us")
@@ -527,10 +631,11 @@ def main():
     ap.add_argument("--no-decode-configs", action="store_true",
                     help="skip the configs[2] / configs[4] decode runs")
     ap.add_argument("--timeline", action="store_true",
-                    help="only the s_memrealtime timeline of the LDS-ring GEMV (libqgemv_timeline.so)")
+                    help="only the s_memrealtime timeline of the planned wave-private or LDS-ring GEMV "
+                         "(libqgemv_timeline.so)")
     ap.add_argument("--timeline-reps", type=int, default=9)
     ap.add_argument("--timeline-glu", action="store_true",
-                    help="with --timeline: the stream kernel's [gate; up] form instead of the LDS-ring kernel")
+                    help="with --timeline: the stream kernel's [gate; up] form instead")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args)
@@ -626,8 +731,14 @@ def main():
 
     ceiling = None
     if not args.no_ceiling:
-        ceiling = ceiling_run(ctx, torch, [(workload, nb), ("qwen2_7b_gate_up_76MB", 76382208),
-                                           ("qwen2_7b_lm_head_447MB", 447166464)])
+        wave_rows = (rows, nb // rows) if mats[0].kernel_kind == 3 else None
+        ceiling = ceiling_run(rinf, ctx, torch, [(workload, nb), ("qwen2_7b_gate_up_76MB", 76382208),
+                                                 ("qwen2_7b_lm_head_447MB", 447166464)], wave_rows=wave_rows)
+
+    # configs[4]'s other standalone shape (the headline is 4096 x 14336)
+    other_shape = None
+    if (args.type, rows, cols) == ("Q4_K", 4096, 14336):
+        other_shape = shape_run(rinf, synth, ctx, torch, "Q4_K", 14336, 4096, args.steps, args.warmup)
 
     decode = None
     if args.decode != "none":
@@ -664,6 +775,7 @@ def main():
         "cpu_baseline": cpu,
         "decode": decode,
         "ceiling": ceiling,
+        "q4_k_gemv_14336x4096": other_shape,
         "sweep": sweep,
         "decode_configs": decode_configs,
     }

@@ -86,8 +86,12 @@ int qg_mat_info(const qg_mat *mat, uint32_t *ggml_type, size_t *rows, size_t *co
 int qg_mat_kernel_kind(const qg_mat *mat);
 
 /* Device-resident mat-vec: y[r] = sum_c W[r,c] * x[c] (src/quant.rs:178-206).
- * d_x: cols floats, d_y: rows floats, both device pointers (d_x 16-byte
- * aligned for the fast kernel; otherwise the generic kernel runs).
+ * d_x: cols floats, d_y: rows floats, both device pointers, 4-byte aligned.
+ * A d_x that is not 16-byte aligned runs the generic kernel on matrices that
+ * keep the GGUF layout; an uploaded Q8_0/Q4_K/Q5_K/Q6_K matrix keeps only
+ * its repacked copy, so there x is first copied to an aligned buffer the
+ * context owns: such calls on one context must not overlap (e.g. on two
+ * streams), since they share that buffer and a longer x reallocates it.
  * Asynchronous on `stream`. */
 int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, void *stream);
 
@@ -190,12 +194,6 @@ int qg_dequant_host(qg_ctx *ctx, const qg_mat *mat, float *out);
  * fresh vec! does). */
 int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_out,
                           void *stream);
-
-/* Measurement only, no counterpart in the reference: reads nbytes of device
- * memory once (16-byte aligned, a multiple of 16 bytes) with the plainest
- * full-grid coalesced read, writing at most d_out[0].  Its duration is the
- * streaming ceiling the GEMV's HBM rate is compared with at the same size. */
-int qg_probe_stream_read(qg_ctx *ctx, const void *d_buf, size_t nbytes, uint32_t *d_out, void *stream);
 
 /* Measurement only, no counterpart in the reference: n_launches calls of
  * qg_matvec_dev(ctx, mats[i % n_mats], d_x, d_y, stream), i = 0, 1, ..., issued

@@ -62,7 +62,9 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
 /* Uses an already uploaded matrix (e.g. a tied lm_head = token_embd,
  * src/model.rs:221-226) without copying; the model does not free it, and
  * qg_mat_free refuses it while any model slot still uses it (the slot is
- * released when the model is destroyed or the slot gets another matrix). */
+ * released when the model is destroyed or the slot gets another matrix).
+ * QG_ERR_INVALID_ARG for a handle that is not a live matrix of the model's
+ * context; QG_ERR_SHAPE for a shape that does not match the slot. */
 int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_mat *mat);
 int qg_model_set_vector(qg_model *m, uint32_t which, uint32_t layer, const float *v, size_t n);
 

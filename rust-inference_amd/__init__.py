@@ -80,7 +80,6 @@ _SIGS = {
     "qg_matvec_norm_glu_dev_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
     "qg_gpu_invalidate": (ctypes.c_int, [_P, _P]),
-    "qg_probe_stream_read": (ctypes.c_int, [_P, _P, _SZ, _P, _P]),
     "qg_matvec_dev_repeat": (ctypes.c_int, [_P, _P, _SZ, _P, _P, _SZ, _P]),
     "qg_test_fail_allocations": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -191,6 +190,29 @@ def load_library(path: pathlib.Path | str = LIB_PATH):
     return lib
 
 
+PROBE_LIB_PATH = HERE / "libqgprobe.so"
+_PROBE_SIGS = {
+    "qgp_read": (ctypes.c_int, [_P, _SZ, _SZ, _P, _U32, _U32, _U32, _SZ, _P]),
+    "qgp_read_wave_lds": (ctypes.c_int, [_P, _SZ, _SZ, _SZ, _P, _SZ, _P]),
+}
+
+
+def load_probe_library(path: pathlib.Path | str = PROBE_LIB_PATH):
+    """libqgprobe.so (include/qgprobe.h): the measurement-only read kernels
+    bench.py times for the streaming ceiling; not part of the mat-vec
+    library.  Loaded after libqgemv.so, so both bind one HIP runtime."""
+    load_library()
+    p = pathlib.Path(path)
+    if not p.exists():
+        raise ImportError(f"{p} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _PROBE_SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
 def _ptr(a):
     """Address of a numpy array's data or a torch tensor's storage."""
     if a is None:
@@ -277,12 +299,6 @@ class GpuContext:
         rc = self.lib.qg_gpu_mat_vec_mul(self.h, _ptr(weight_data), weight_data.nbytes, dtype,
                                          _ptr(x), _ptr(out), rows, cols)
         self.check(rc, "qg_gpu_mat_vec_mul")
-
-    def probe_stream_read(self, d_buf, nbytes: int, d_out, stream=None):
-        """One plain coalesced read of nbytes of a device tensor (qg_probe_stream_read)."""
-        rc = self.lib.qg_probe_stream_read(self.h, _ptr(d_buf), int(nbytes), _ptr(d_out),
-                                           ctypes.c_void_p(stream) if stream else None)
-        self.check(rc, "qg_probe_stream_read")
 
     def matvec_repeat(self, mats, d_x, d_y, n_launches: int, stream=None):
         """n_launches qg_matvec_dev calls cycling over mats, issued from C

@@ -187,7 +187,6 @@ int launch_dequantize_rows_dev(uint32_t type, const uint8_t *w, size_t rows, siz
 // the runtime cannot resolve it.
 constexpr size_t kNoAllocScratchFloats = 262144;
 int scratch_address(int device, float **ptr);
-int launch_stream_read(const void *buf, size_t nbytes, uint32_t *out, ihipStream_t *stream);
 // out = silu(g) * u elementwise
 int launch_silu_mul(const float *g, const float *u, float *out, size_t n, ihipStream_t *stream);
 // out = rmsnorm(a (+ b)) * w in one workgroup; sum_out (may be NULL) = a + b.

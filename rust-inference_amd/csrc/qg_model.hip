@@ -837,30 +837,40 @@ void drop_graphs(qg_model *m)
 
 // Frees the stacked matrices.  Parts that are views into them (qg_stack_views)
 // first get their own copies back (restore), unless the model is being freed
-// with them.
+// with them.  A stack whose parts could not all get their copies back (an
+// allocation failed) stays: its remaining views still point into it, and
+// prepare() keeps it rather than stacking those parts again.
 int drop_fused(qg_model *m, bool restore = true)
 {
     int rc = QG_OK;
     for (size_t l = 0; l < m->f_qkv.size(); l++) {
         if (m->f_qkv[l]) {
+            int r = QG_OK;
             for (int i = 0; i < m->f_qkv_n[l] && restore; i++) {
-                const int r = qg_mat_unview(m->ctx, m->w[QG_M_WQ - 2 + i][l]);
-                rc = rc ? rc : r;
+                const int ri = qg_mat_unview(m->ctx, m->w[QG_M_WQ - 2 + i][l]);
+                r = r ? r : ri;
             }
-            qg_mat_free(m->ctx, m->f_qkv[l]);
-            m->f_qkv[l] = nullptr;
+            if (r == QG_OK) {
+                qg_mat_free(m->ctx, m->f_qkv[l]);
+                m->f_qkv[l] = nullptr;
+                m->f_qkv_n[l] = 0;
+            }
+            rc = rc ? rc : r;
         }
         if (m->f_gu[l]) {
+            int r = QG_OK;
             for (int s : {QG_M_GATE - 2, QG_M_UP - 2})
                 if (restore) {
-                    const int r = qg_mat_unview(m->ctx, m->w[s][l]);
-                    rc = rc ? rc : r;
+                    const int ri = qg_mat_unview(m->ctx, m->w[s][l]);
+                    r = r ? r : ri;
                 }
-            qg_mat_free(m->ctx, m->f_gu[l]);
-            m->f_gu[l] = nullptr;
+            if (r == QG_OK) {
+                qg_mat_free(m->ctx, m->f_gu[l]);
+                m->f_gu[l] = nullptr;
+            }
+            rc = rc ? rc : r;
         }
     }
-    for (uint8_t &n : m->f_qkv_n) n = 0;
     m->fused_ready = false;
     return rc;
 }
@@ -906,11 +916,15 @@ int prepare(qg_model *m)
         const int n = stackable(qkv, 3) ? 3 : stackable(qkv, 2) ? 2 : 0;
         const bool oq[3] = {m->owned[QG_M_WQ - 2][l], m->owned[QG_M_WK - 2][l], m->owned[QG_M_WV - 2][l]};
         int rc;
-        if (n && (rc = stack_parts(m, qkv, oq, n, &m->f_qkv[l]))) return rc;
-        m->f_qkv_n[l] = (uint8_t)n;
+        // a stack kept by a drop_fused that could not restore every part
+        // still holds exactly these parts' bytes
+        if (!m->f_qkv[l]) {
+            if (n && (rc = stack_parts(m, qkv, oq, n, &m->f_qkv[l]))) return rc;
+            m->f_qkv_n[l] = (uint8_t)n;
+        }
         qg_mat *gu[2] = {m->w[QG_M_GATE - 2][l], m->w[QG_M_UP - 2][l]};
         const bool og[2] = {m->owned[QG_M_GATE - 2][l], m->owned[QG_M_UP - 2][l]};
-        if (stackable(gu, 2) && (rc = stack_parts(m, gu, og, 2, &m->f_gu[l]))) return rc;
+        if (!m->f_gu[l] && stackable(gu, 2) && (rc = stack_parts(m, gu, og, 2, &m->f_gu[l]))) return rc;
     }
     m->fused_ready = true;
     return QG_OK;
@@ -1557,16 +1571,18 @@ int qg_model_set_matrix(qg_model *m, uint32_t which, uint32_t layer, const void 
 int qg_model_share_matrix(qg_model *m, uint32_t which, uint32_t layer, const qg_mat *mat)
 {
     if (!m || !mat) return QG_ERR_INVALID_ARG;
+    // a live matrix of this model's context before any of its fields is read
+    int rc = qg_check_mat(m->ctx, mat);
+    if (rc) return rc;
     size_t er, ec;
     slot_shape(m, which, &er, &ec);
     if (er == 0) return mfail(m, QG_ERR_INVALID_ARG, "matrix slot");
-    if (mat->rows != er || mat->cols != ec || mat->ctx != m->ctx)
+    if (mat->rows != er || mat->cols != ec)
         return mfail(m, QG_ERR_SHAPE, "matrix shape does not match the config");
     const bool per_layer = which >= QG_M_WQ;
     if (per_layer && layer >= m->cfg.n_layers) return mfail(m, QG_ERR_INVALID_ARG, "layer");
     (void)hipStreamSynchronize(m->ctx->stream);
     drop_graphs(m);
-    int rc;
     if ((rc = drop_fused(m))) return rc;
     put_slot(m, which, layer, const_cast<qg_mat *>(mat), true);
     return QG_OK;

@@ -380,11 +380,11 @@ constexpr uint32_t kPfLds = 2u * kPfBuf;                     // two buffers
 
 // 16 bytes per lane from global memory straight into LDS at byte m0 + 16 lane
 // (global_load_lds_dwordx4, issued from asm: the compiler does not track it,
-// the waits for it are explicit)
+// the waits for it are explicit; lds_addr is an operand bound to M0, which
+// the compiler writes itself)
 __device__ __forceinline__ void pf_dma16(const void *gp, uint32_t lds_addr)
 {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds_addr)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(lds_addr) : "memory");
 }
 
 // Issue the copies of chunk kc (nk sub-blocks) into the buffer at LDS byte

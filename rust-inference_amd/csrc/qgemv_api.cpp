@@ -888,17 +888,6 @@ int qg_dequantize_row_dev(qg_ctx *ctx, const qg_mat *mat, size_t row, float *d_o
     return QG_OK;
 }
 
-int qg_probe_stream_read(qg_ctx *ctx, const void *d_buf, size_t nbytes, uint32_t *d_out, void *stream)
-{
-    if (!ctx) return QG_ERR_INVALID_ARG;
-    if ((nbytes && !d_buf) || !d_out || ((uintptr_t)d_buf & 15u) || nbytes % 16u)
-        return fail(ctx, QG_ERR_INVALID_ARG, "buffer NULL, not 16-byte aligned or not whole 16-byte pieces");
-    QG_HIP(ctx, hipSetDevice(ctx->device));
-    if (qg::launch_stream_read(d_buf, nbytes, d_out, (ihipStream_t *)pick(ctx, stream)))
-        return fail(ctx, QG_ERR_HIP, "stream read launch", hipGetLastError());
-    return QG_OK;
-}
-
 int qg_matvec_dev_repeat(qg_ctx *ctx, const qg_mat *const *mats, size_t n_mats, const float *d_x, float *d_y,
                          size_t n_launches, void *stream)
 {

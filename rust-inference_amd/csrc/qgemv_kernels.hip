@@ -88,77 +88,73 @@ __device__ __forceinline__ void k4pair(uint32_t p, uint32_t s0, uint32_t s1, uin
 }
 
 // ------------------------------------------- bit-exact element decoders
-// elem<T>(block, i) = value i of the block, as src/quant.rs:82-149 computes it.
+// elem_t<T>(b, i) = value i of a block, as src/quant.rs:82-149 computes it,
+// where b[o] is byte o of the block in the GGUF layout: a pointer to the
+// block, or a view that gathers the block's bytes from the repacked layout
+// (RpBlock below).  elem<T>(block, i) is the pointer form.
 
-template <uint32_t T> __device__ float elem(const uint8_t *b, uint32_t i);
+template <class B> __device__ __forceinline__ uint32_t bytes16(const B &b, uint32_t o)
+{
+    return (uint32_t)b[o] | ((uint32_t)b[o + 1u] << 8);
+}
+template <class B> __device__ __forceinline__ uint32_t bytes32(const B &b, uint32_t o)
+{
+    return bytes16(b, o) | (bytes16(b, o + 2u) << 16);
+}
 
-template <> __device__ __forceinline__ float elem<T_F32>(const uint8_t *b, uint32_t)
+template <uint32_t T, class B> __device__ __forceinline__ float elem_t(const B &b, uint32_t i)
 {
-    return __uint_as_float(*(const uint32_t *)b);
+    if constexpr (T == T_F32) {
+        if constexpr (std::is_pointer<B>::value) return __uint_as_float(*(const uint32_t *)b);
+        else return __uint_as_float(bytes32(b, 0u));
+    } else if constexpr (T == T_F16) {
+        return h2f_exact(bytes16(b, 0u));
+    } else if constexpr (T == T_Q8_0) {
+        const float d = h2f_exact(bytes16(b, 0u));                 // quant.rs:107
+        return d * (float)(int8_t)b[2u + i];                       // quant.rs:110
+    } else if constexpr (T == T_Q4_0) {
+        const float d = h2f_exact(bytes16(b, 0u));
+        const uint32_t v = b[2u + i / 2u];                         // quant.rs:117-118 (interleaved)
+        const int nib = (i & 1u) ? (int)(v >> 4) : (int)(v & 15u);
+        return d * (float)(nib - 8);
+    } else if constexpr (T == T_Q5_0) {
+        const float d = h2f_exact(bytes16(b, 0u));
+        const uint32_t qh = bytes16(b, 2u) | (bytes16(b, 4u) << 16);
+        const uint32_t xl = i < 16u ? ((uint32_t)b[6u + i] & 15u) : ((uint32_t)b[6u + i - 16u] >> 4);
+        const uint32_t xh = ((qh >> i) & 1u) << 4;                 // quant.rs:126-135
+        return d * (float)((int)(xl | xh) - 16);
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        const float d = h2f_exact(bytes16(b, 0u)), dmin = h2f_exact(bytes16(b, 2u));
+        const uint32_t j = i >> 5, l = i & 31u;
+        uint32_t sc, m;
+        k4sm(j, bytes32(b, 4u), bytes32(b, 8u), bytes32(b, 12u), sc, m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;      // quant.rs:218-219, 249-250
+        if constexpr (T == T_Q4_K) {
+            const uint32_t q = b[16u + (j >> 1) * 32u + l];
+            const uint32_t nib = (j & 1u) ? (q >> 4) : (q & 15u);
+            return d1 * (float)nib - m1;                           // quant.rs:224-225
+        } else {
+            const uint32_t q = b[48u + (j >> 1) * 32u + l];
+            const uint32_t lo = (j & 1u) ? (q >> 4) : (q & 15u);
+            const uint32_t hi = (((uint32_t)b[16u + l] >> j) & 1u) ? 16u : 0u;   // quant.rs:238-260
+            return d1 * (float)(lo + hi) - m1;
+        }
+    } else {
+        static_assert(T == T_Q6_K, "type");
+        const uint32_t n = i >> 7, rr = i & 127u, k = rr >> 5, l = rr & 31u, is = l >> 4;
+        const uint32_t qlb = b[64u * n + l + 32u * (k & 1u)];
+        const uint32_t nib = k >= 2u ? (qlb >> 4) : (qlb & 15u);
+        const uint32_t hb = ((uint32_t)b[128u + 32u * n + l] >> (2u * k)) & 3u;
+        const int q = (int)(nib | (hb << 4));
+        const float sc = (float)(int8_t)b[192u + 8u * n + is + 2u * k];
+        const float d = h2f_exact(bytes16(b, 208u));
+        return d * sc * (float)(q - 32);                           // quant.rs:286-289
+    }
 }
-template <> __device__ __forceinline__ float elem<T_F16>(const uint8_t *b, uint32_t)
+
+template <uint32_t T> __device__ __forceinline__ float elem(const uint8_t *b, uint32_t i)
 {
-    return h2f_exact(rd16(b));
-}
-template <> __device__ __forceinline__ float elem<T_Q8_0>(const uint8_t *b, uint32_t i)
-{
-    const float d = h2f_exact(rd16(b));                          // quant.rs:107
-    return d * (float)(int8_t)b[2 + i];                          // quant.rs:110
-}
-template <> __device__ __forceinline__ float elem<T_Q4_0>(const uint8_t *b, uint32_t i)
-{
-    const float d = h2f_exact(rd16(b));
-    const uint32_t v = b[2 + i / 2];                             // quant.rs:117-118 (interleaved)
-    const int nib = (i & 1u) ? (int)(v >> 4) : (int)(v & 15u);
-    return d * (float)(nib - 8);
-}
-template <> __device__ __forceinline__ float elem<T_Q5_0>(const uint8_t *b, uint32_t i)
-{
-    const float d = h2f_exact(rd16(b));
-    const uint32_t qh = rd16(b + 2) | (rd16(b + 4) << 16);
-    const uint32_t xl = i < 16u ? (b[6 + i] & 15u) : (uint32_t)(b[6 + i - 16] >> 4);
-    const uint32_t xh = ((qh >> i) & 1u) << 4;                   // quant.rs:126-135
-    return d * (float)((int)(xl | xh) - 16);
-}
-template <> __device__ __forceinline__ float elem<T_Q4_K>(const uint8_t *b, uint32_t i)
-{
-    const float d = h2f_exact(rd16(b)), dmin = h2f_exact(rd16(b + 2));
-    const uint32_t j = i >> 5, l = i & 31u;
-    const uint8_t *s = b + 4;
-    uint32_t sc, m;
-    k4sm(j, s[0] | (s[1] << 8) | (s[2] << 16) | ((uint32_t)s[3] << 24),
-         s[4] | (s[5] << 8) | (s[6] << 16) | ((uint32_t)s[7] << 24),
-         s[8] | (s[9] << 8) | (s[10] << 16) | ((uint32_t)s[11] << 24), sc, m);
-    const uint32_t q = b[16 + (j >> 1) * 32 + l];
-    const uint32_t nib = (j & 1u) ? (q >> 4) : (q & 15u);
-    const float d1 = d * (float)sc, m1 = dmin * (float)m;        // quant.rs:218-219
-    return d1 * (float)nib - m1;                                 // quant.rs:224-225
-}
-template <> __device__ __forceinline__ float elem<T_Q5_K>(const uint8_t *b, uint32_t i)
-{
-    const float d = h2f_exact(rd16(b)), dmin = h2f_exact(rd16(b + 2));
-    const uint32_t j = i >> 5, l = i & 31u;
-    const uint8_t *s = b + 4;
-    uint32_t sc, m;
-    k4sm(j, s[0] | (s[1] << 8) | (s[2] << 16) | ((uint32_t)s[3] << 24),
-         s[4] | (s[5] << 8) | (s[6] << 16) | ((uint32_t)s[7] << 24),
-         s[8] | (s[9] << 8) | (s[10] << 16) | ((uint32_t)s[11] << 24), sc, m);
-    const uint32_t q = b[48 + (j >> 1) * 32 + l];
-    const uint32_t lo = (j & 1u) ? (q >> 4) : (q & 15u);
-    const uint32_t hi = ((b[16 + l] >> j) & 1u) ? 16u : 0u;     // u1/u2 = bit j, quant.rs:238-260
-    const float d1 = d * (float)sc, m1 = dmin * (float)m;
-    return d1 * (float)(lo + hi) - m1;
-}
-template <> __device__ __forceinline__ float elem<T_Q6_K>(const uint8_t *b, uint32_t i)
-{
-    const uint32_t n = i >> 7, rr = i & 127u, k = rr >> 5, l = rr & 31u, is = l >> 4;
-    const uint32_t qlb = b[64 * n + l + 32 * (k & 1u)];
-    const uint32_t nib = k >= 2u ? (qlb >> 4) : (qlb & 15u);
-    const uint32_t hb = (b[128 + 32 * n + l] >> (2 * k)) & 3u;
-    const int q = (int)(nib | (hb << 4));
-    const float sc = (float)(int8_t)b[192 + 8 * n + is + 2 * k];
-    const float d = h2f_exact(rd16(b + 208));
-    return d * sc * (float)(q - 32);                             // quant.rs:286-289
+    return elem_t<T>(b, i);
 }
 
 // ------------------------------------------------------------- dequant
@@ -290,6 +286,60 @@ __global__ void __launch_bounds__(256) gemv_generic(const uint8_t *__restrict__ 
     if (lane == 0) y[row] = acc;
 }
 
+// ------------------------------------------------- repacked-layout view
+//
+// RpBlock<T>{grp, ni, blk}[o] = byte o of block blk of a row group, in the
+// GGUF layout, read from the group's repacked bytes (the layout repack_k
+// writes; see there): the map from a GGUF offset to the repacked one.  Q5_K's
+// qh bytes are reassembled from the bits its four items keep.
+template <uint32_t T> struct RpBlock {
+    const uint8_t *grp;
+    uint32_t ni, blk;
+    __device__ uint32_t operator[](uint32_t o) const
+    {
+        if constexpr (T == T_Q8_0) {
+            const uint32_t it = blk >> 1, h = blk & 1u;
+            if (o < 2u) return grp[64u * ni + 4u * it + 2u * h + o];
+            const uint32_t k = 32u * h + o - 2u;
+            return grp[((k >> 4) * ni + it) * 16u + (k & 15u)];
+        } else if constexpr (T == T_Q4_K) {
+            if (o < 16u) return grp[16u * blk + o];
+            const uint32_t q = o - 16u, it = 2u * blk + (q >> 6);
+            return grp[(ni >> 1) * 16u + (((q & 63u) >> 4) * ni + it) * 16u + (q & 15u)];
+        } else if constexpr (T == T_Q5_K) {
+            const uint32_t H = (ni >> 2) * 16u;
+            if (o < 16u) return grp[16u * blk + o];
+            if (o >= 48u) {
+                const uint32_t q = o - 48u, it = 4u * blk + (q >> 5), k = q & 31u;
+                return grp[H + ((k >> 4) * ni + it) * 16u + (k & 15u)];
+            }
+            // qh byte m: bits 2q, 2q + 1 live in item q's word w at 8 bb + 2 t'
+            const uint32_t m = o - 16u, w = m >> 4, tp = (m >> 2) & 3u, bb = m & 3u;
+            uint32_t v = 0;
+            for (uint32_t q = 0; q < 4u; q++) {
+                const uint8_t *pw = grp + H + 32u * ni + 8u * (4u * blk + q) + 4u * w + bb;
+                v |= (((uint32_t)*pw >> (2u * tp)) & 3u) << (2u * q);
+            }
+            return v;
+        } else {
+            static_assert(T == T_Q6_K, "repacked types");
+            if (o < 128u) {
+                const uint32_t n = o >> 6, r = o & 63u, it = 4u * blk + 2u * n + ((r & 31u) >> 4);
+                return grp[((r >> 5) * ni + it) * 16u + (r & 15u)];
+            }
+            if (o < 192u) {
+                const uint32_t q = o - 128u, it = 4u * blk + 2u * (q >> 5) + ((q & 31u) >> 4);
+                return grp[(2u * ni + it) * 16u + (q & 15u)];
+            }
+            if (o < 208u) {
+                const uint32_t q = o - 192u, it = 4u * blk + 2u * (q >> 3) + (q & 1u);
+                return grp[48u * ni + 4u * it + ((q & 7u) >> 1)];
+            }
+            return grp[52u * ni + 2u * blk + (o - 208u)];
+        }
+    }
+};
+
 // ------------------------------------------------------ x in fixed point
 //
 // Quant types multiply integer codes by x with integer dot products.  Every
@@ -305,7 +355,9 @@ __global__ void __launch_bounds__(256) gemv_generic(const uint8_t *__restrict__ 
 // sY = sum of Y over the elements that high nibbles meet (all 32, or the odd
 // half for Q4_0's even-then-odd order).  A segment whose sum is not finite
 // (any inf or NaN in it) gets 1/k = NaN, so every dot product that uses it
-// is NaN.  F16 and F32 weights keep x in f32.
+// is NaN; the plain mat-vec kernels then recompute their rows in f32
+// (row_dot_f32), which gives the reference's infinities and NaNs.  F16 and
+// F32 weights keep x in f32.
 //
 // LDS layout (planes): segment g at byte 96g + 16(g/2) holds 32 bytes of e0,
 // 32 of e1, 32 of e2 (16 bytes of padding per segment pair keep the per-lane
@@ -314,6 +366,13 @@ __global__ void __launch_bounds__(256) gemv_generic(const uint8_t *__restrict__ 
 // interleaved nibbles.  f32 layout: float4 i of x at xl4[i + i/16].
 
 constexpr float kFix = 4194000.0f;
+// Largest k: 2^122, so that 1/k and the high-nibble factor (1/k) / 16 stay
+// normal floats.  Segments with m >= kFix / 2^122 (about 7.9e-31) keep the
+// full 22 bits; below that |Y| < m 2^122 (e.g. 12 bits at m = 1e-33).
+constexpr float kMaxK = 5.316912e36f;
+// A segment with max |x| above 2^64 is left to the f32 path (row_dot_f32):
+// its fixed-point sums could overflow where the reference's f32 products do not.
+constexpr float kDivertMax = 1.8446744e19f;
 // fma(x, k, kMagic) holds rint(x * k) in its low mantissa bits for |x k| < 2^22
 constexpr float kMagic = 12582912.0f;            // 1.5 * 2^23
 constexpr int kMagicBits = 0x4B400000;
@@ -367,8 +426,10 @@ __device__ __forceinline__ float absmax4(float4 v)
 // between them.  The sums use fixed trees: a half's sum of x is
 // (t0 + t1) + (t2 + t3) with t_i = (x0 + x1) + (x2 + x3) over float4 i, and
 // sY adds the float4s' exact integer sums the same way, then the two halves.
+// Returns whether the segment diverts its rows to row_dot_f32 (a non-finite
+// sum or max |x| > 2^64).
 template <bool EVEN_ODD>
-__device__ __forceinline__ void stage_planes16(const uint4 (&q)[4], uint32_t c, uint8_t *lds, uint32_t meta)
+__device__ __forceinline__ bool stage_planes16(const uint4 (&q)[4], uint32_t c, uint8_t *lds, uint32_t meta)
 {
     float4 v[4];
 #pragma unroll
@@ -384,7 +445,7 @@ __device__ __forceinline__ void stage_planes16(const uint4 (&q)[4], uint32_t c, 
     const float s = (t[0] + t[1]) + (t[2] + t[3]);   // this half's sum
     const float o = dpp<0xB1>(s);                    // the other half's
     const bool bad = !__builtin_isfinite(s + o);
-    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.2676506e30f) : 0.f;
+    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), kMaxK) : 0.f;
     const float ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
     const int off = 0x8080 - kMagicBits;
     uint32_t Y[4][4];
@@ -437,6 +498,7 @@ __device__ __forceinline__ void stage_planes16(const uint4 (&q)[4], uint32_t c, 
         *(uint2 *)(seg + 80u + 8u * h) = make_uint2(lo2(O2[0], O2[1]), lo2(O2[2], O2[3]));
     }
     if (h == 0) *(float4 *)(lds + meta + 16u * g) = make_float4(ik, s, o, sy);
+    return bad || m > kDivertMax;
 }
 
 // sum q*Y from the three plane dot products (see above)
@@ -1019,6 +1081,62 @@ struct StreamArgs {
     uint32_t att_nh, att_hd;
 };
 
+// ------------------------------------------------- non-finite x: slow rows
+//
+// The fixed-point x of the quant types cannot carry inf or NaN, and a segment
+// holding one gets 1/k = NaN, which would make every row NaN.  The reference
+// sums w * x[c] one product at a time in f32 (quant.rs:195-204), so a row that
+// meets +inf gives +inf, -inf gives -inf, and NaN only where signs mix, a
+// weight is zero or x holds a NaN.  The plain mat-vec kernels therefore note,
+// per workgroup, whether any segment of x was non-finite (or so large that
+// the fixed-point sums could overflow where f32 products do not: max |x| over
+// a segment > 2^64), and if so recompute every row they own with
+// row_dot_f32: the f32 sum of one rounded product per element.  Its order
+// differs from the reference's, which changes only finite results; whether a
+// sum is finite, +inf, -inf or NaN does not depend on the order.
+// sum over c of w(row, c) * x[c] in f32 (wave-cooperative: `row` is
+// wave-uniform and every lane of the wave takes part; all lanes get the sum)
+template <uint32_t T, bool RP>
+__device__ float row_dot_f32(const StreamArgs &a, uint32_t row)
+{
+    constexpr uint32_t BS = block_elems(T), BB = block_bytes(T);
+    const uint32_t lane = threadIdx.x & 63u;
+    float acc = 0.f;
+    if constexpr (RP) {
+        const uint32_t gr = row / a.g, rr = row - gr * a.g;
+        const uint8_t *grp = a.w + (size_t)gr * a.group_bytes;
+        for (uint32_t c = lane; c < a.cols; c += 64u) {
+            const uint32_t f = rr * a.cols + c;
+            const float p = elem_t<T>(RpBlock<T>{grp, a.ni, f / BS}, f % BS) * a.x[c];
+            acc += p;
+        }
+    } else {
+        const uint64_t f0 = (uint64_t)row * a.cols;
+        for (uint32_t c = lane; c < a.cols; c += 64u) {
+            const uint64_t f = f0 + c;
+            const float p = elem<T>(a.w + (f / BS) * BB, (uint32_t)(f % BS)) * a.x[c];
+            acc += p;
+        }
+    }
+    return wave_sum(acc);
+}
+
+// Per-wave flags "this wave converted a diverting segment" (set before a
+// workgroup barrier, read after it) and the test of all of them.
+constexpr uint32_t kMaxWaves = 16;
+__device__ __forceinline__ void divert_note(uint32_t *flags, bool mine)
+{
+    const bool any = __builtin_amdgcn_ballot_w64(mine) != 0;
+    if ((threadIdx.x & 63u) == 0u) flags[threadIdx.x >> 6] = any ? 1u : 0u;
+}
+__device__ __forceinline__ bool divert_any(const uint32_t *flags)
+{
+    const uint32_t nw = (blockDim.x + 63u) >> 6;
+    uint32_t v = 0;
+    for (uint32_t i = 0; i < nw; i++) v |= flags[i];
+    return v != 0u;
+}
+
 // 16 bytes of v to p as an inline-asm store (not counted by the compiler's
 // wait bookkeeping, like store_y)
 __device__ __forceinline__ void store16(float *p, float4 v)
@@ -1041,14 +1159,18 @@ __device__ __forceinline__ void store_y(float *p, float v)
 // ------------------------------------------------------------ timeline
 //
 // Only in the build with -DQG_TIMELINE (libqgemv_timeline.so, `make
-// timeline`): the LDS-ring kernel and the stream kernel take s_memrealtime
-// stamps at fixed points.  A stamp goes into lane `ev` of a VGPR (a select,
+// timeline`): the LDS-ring, stream and wave-private kernels take
+// s_memrealtime stamps at fixed points.  A stamp goes into lane `ev` of a VGPR (a select,
 // no memory operation and no register indexing), and each stamping wave
 // writes its lanes once, after its last load, wait and barrier, so the
 // kernel's memory traffic and waits are those of the plain build.  Per
 // workgroup, 64 stamps: compute wave 0 in 0..31 and, for the ring kernel,
-// the first loader wave in 32..63; the stream kernel puts every wave's end
-// in 32 + w and its entry in 48 + w instead (0 = never stamped).
+// the first loader wave in 32..63; the stream and wave-private kernels put
+// every wave's end in 32 + w and its entry in 48 + w instead (0 = never
+// stamped).  gemv_wave, wave 0: 0 entry, 1 x and rows 0..3 requested, 2 x
+// landed, 3 x converted and held in registers, 4 + 2s step s landed (rows
+// 4s..4s+3), 5 + 2s step s computed, 12 the workgroup barrier passed, 13 y
+// written.
 #ifdef QG_TIMELINE
 constexpr uint32_t kTlEv = 64, kTlWG = 2048;
 __device__ uint64_t qg_tl_buf[kTlWG * kTlEv];
@@ -1300,8 +1422,13 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
 
     // 2. stage x, then this lane's slice into VGPRs
     uint4 *l4 = (uint4 *)xl4;
+    // the plain mat-vec diverts its rows to row_dot_f32 when any segment of x
+    // is non-finite or huge (see row_dot_f32)
+    constexpr bool DIV = PRO == kProPlain && CV;
+    bool xdiv = false;
+    __shared__ __align__(16) uint32_t dflags[DIV ? kMaxWaves : 1];
     auto put = [&](const uint4 (&u)[PW], uint32_t c) {
-        if constexpr (CV) stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
+        if constexpr (CV) xdiv |= stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
         else l4[I::PLANES ? c : c + (c >> 4)] = u[0];
     };
     // kProNorm: 1 / rms, applied to every segment's 1/k and sums after the
@@ -1441,6 +1568,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
         }
     }
     QG_TL(3);
+    if constexpr (DIV) divert_note(dflags, xdiv);
     lds_barrier();
     QG_TL(4);
     if constexpr (NORM) {
@@ -1605,6 +1733,24 @@ __device__ __forceinline__ void stream_body(const StreamArgs &a, uint32_t bid)
             process(raw[d], i + d);
             QG_TL(6u + min(i + d, 24u));
         }
+    if constexpr (DIV) {
+        if (divert_any(dflags)) {
+            // every row this workgroup wrote, again in f32, after its first
+            // stores (this wave's: vmcnt; the others': the barrier)
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            lds_barrier();
+            const uint32_t nq = tpw * a.per_team * (uint32_t)R * g, nwv = blockDim.x >> 6;
+            for (uint32_t q = tid >> 6; q < nq; q += nwv) {
+                const uint32_t gi = q % g, r = (q / g) % (uint32_t)R, bi = (q / (g * R)) % a.per_team;
+                const uint32_t tq = q / (g * R * a.per_team);
+                const uint32_t grp = bid * tpw + tq + (bi * R + r) * a.n_teams, row = grp * g + gi;
+                if (grp < a.n_groups && row < a.rows) {
+                    const float v = row_dot_f32<T, RP>(a, row);
+                    if ((tid & 63u) == 0u) a.y[row] = v;
+                }
+            }
+        }
+    }
     QG_TL(31);
     if ((tid >> 6) == 0u) QG_TL_WRITE(0);
     QG_TL_WAVE_END();
@@ -1684,6 +1830,8 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
     const uint32_t gb = a.group_bytes, ring = a.red_off;
     auto slot_off = [&](uint32_t i) { const uint32_t k = i % kRingSlots; return k < 2u ? ring + k * SLOT : a.ring_slot2; };
     float *redf = (float *)(lds + ring + 2u * SLOT);            // 2 x NW per-wave sums
+    // per-wave "x has a non-finite or huge segment" (see row_dot_f32)
+    __shared__ __align__(16) uint32_t dflags[kMaxWaves];
     QG_TL_DECL;
     if (wave >= NW) {
         // loader l: the rows of teams l*TPW/2 .. (l+1)*TPW/2 - 1 of every stage
@@ -1707,6 +1855,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         for (uint32_t i = 0; i < kRingSlots - 1u; i++)
             if (i < a.per_team) issue(i);
         QG_TL(1);
+        divert_note(dflags, false);
         lds_barrier();                                                  // x staged
         QG_TL(2);
         for (uint32_t i = 0; i < a.per_team; i++) {
@@ -1720,6 +1869,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
         lds_barrier();
         QG_TL(31);
         if (wave == NW) QG_TL_WRITE(32);
+        if (divert_any(dflags)) lds_barrier();                          // the compute waves' last y stores
         return;
     }
     QG_TL(0);
@@ -1744,6 +1894,7 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     QG_TL(1);
+    bool xdiv = false;
 #pragma unroll
     for (int r = 0; r < XR; r++) {
         const uint32_t c = tid + r * NT;
@@ -1751,16 +1902,17 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
             uint4 u[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) u[i] = xv[4 * r + i];
-            stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
+            xdiv |= stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
         }
     }
     for (uint32_t c = tid + XR * NT; c < npc; c += NT) {
         uint4 u[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) u[i] = src[4 * c + i];
-        stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
+        xdiv |= stage_planes16<I::EVEN_ODD>(u, c, lds, meta);
     }
     QG_TL(2);
+    divert_note(dflags, xdiv);
     lds_barrier();
     QG_TL(3);
     XP<S, SEG> xs;
@@ -1800,6 +1952,20 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
     QG_TL(30);
     lds_barrier();
     if (a.per_team > 0) flush(a.per_team - 1);
+    if (divert_any(dflags)) {
+        // the workgroup's rows again in f32, after the flushes' stores (this
+        // wave's: vmcnt; the others': the barrier the loaders join too)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        lds_barrier();
+        const uint32_t nq = (uint32_t)TPW * a.per_team;
+        for (uint32_t q = wave; q < nq; q += NW) {
+            const uint32_t grp = (q % TPW) * gridDim.x + blockIdx.x + (q / TPW) * a.n_teams;
+            if (grp < a.n_groups) {
+                const float v = row_dot_f32<T, true>(a, grp);
+                if (lane == 0u) a.y[grp] = v;
+            }
+        }
+    }
     QG_TL(31);
     if (wave == 0) QG_TL_WRITE(0);
 }
@@ -1815,9 +1981,14 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
 // bit-identical; 4 consecutive rows per step at 4(b + G s) measured 8.65).
 // Every wave moves its own bytes into its own LDS region with
 // global_load_lds_dwordx4 and waits on its own vmcnt only -- no workgroup
-// barrier until the final sum -- in steps of 4 rows, one step in flight
-// (the next step is requested the moment a step lands; more bytes in flight
-// per CU measured slower):
+// barrier until the final sum -- in steps of 4 rows.  The two waves of a SIMD
+// (w and w + 4) run different schedules: the older one keeps one step in
+// flight (the next step is requested the moment a step lands), the younger
+// one two, and once x is converted the younger one has the higher wave
+// priority.  Left to oldest-first arbitration with one step each, the younger
+// waves computed behind the older ones and ended ~0.6 us after them, alone
+// on their SIMDs (two steps for every wave starved them further: 9.3 us);
+// this schedule measured 8.45 against 8.6-8.8 us back to back:
 //   * x: the wave's 4*CJ segments of 32 elements, one 128-byte line per
 //     lane, copied with a rotation (slot p of line L holds piece (p - L) mod 8)
 //     so that the lane's own 8 reads of its line are free of bank conflicts;
@@ -1833,8 +2004,9 @@ __global__ void __launch_bounds__(64 * (WPT * TPW + 2)) gemv_ring(StreamArgs a)
 //     read pass see 16 different bank groups);
 //   * lane (jj, r) computes item jj of row 4s + r with Item<T_Q4_K>::compute_sum
 //     (per item exactly the gemv_stream arithmetic), the 14 items of a row in
-//     a wave are summed with two DPP row shifts, and the 8 waves' sums of a
-//     row are added in fixed order after the one workgroup barrier.
+//     a wave are summed with two DPP row shifts, and after the one workgroup
+//     barrier wave w adds the 32 partial sums of rows 2w and 2w + 1 with a
+//     fixed DPP tree (one partial sum per lane).
 // The copies are issued from inline asm: the compiler does not see them, so
 // it adds no vmcnt(0) before this wave's later LDS reads (with the builtin it
 // waits for every outstanding copy before each read).  The waits are exact
@@ -1845,12 +2017,13 @@ constexpr uint32_t kWaveSlot = 1088;        // LDS bytes per row slot
 constexpr uint32_t kWaveLds = 8u * kWaveRows * kWaveSlot + kWaveRows * 32u * 4u;
 
 // 16 bytes per lane from gp into LDS at lds_addr + 16 * lane (wave-uniform
-// lds_addr), invisible to the compiler's wait bookkeeping; M0 needs one wait
-// state before the copy reads it
+// lds_addr), invisible to the compiler's wait bookkeeping.  lds_addr is an
+// operand bound to M0 (the compiler writes M0 itself, so no reserved register
+// is clobbered behind its back); the copy reads M0 one wait state after the
+// write
 __device__ __forceinline__ void lds_dma16_asm(const void *gp, uint32_t lds_addr)
 {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds_addr)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(lds_addr) : "memory");
 }
 template <uint32_t N> __device__ __forceinline__ void wait_vm_n()
 {
@@ -1861,7 +2034,7 @@ template <uint32_t N> __device__ __forceinline__ void wait_vm_n()
 // One 32-element segment converted in one lane, with the arithmetic and the
 // summation trees of stage_planes16 for its two halves: P = the three digit
 // planes (8 dwords each), ik = 1/k, sx = sum x, sy = sum Y.
-__device__ __forceinline__ void stage_seg32(const float4 (&v)[8], uint32_t (&P)[3][8], float &ik, float &sx, float &sy)
+__device__ __forceinline__ bool stage_seg32(const float4 (&v)[8], uint32_t (&P)[3][8], float &ik, float &sx, float &sy)
 {
     uint32_t mb = 0;
 #pragma unroll
@@ -1872,7 +2045,7 @@ __device__ __forceinline__ void stage_seg32(const float4 (&v)[8], uint32_t (&P)[
     for (int i = 0; i < 8; i++) t[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
     const float s0 = (t[0] + t[1]) + (t[2] + t[3]), s1 = (t[4] + t[5]) + (t[6] + t[7]);
     const bool bad = !__builtin_isfinite(s0 + s1);
-    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), 1.2676506e30f) : 0.f;
+    const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), kMaxK) : 0.f;
     ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
     const int off = 0x8080 - kMagicBits;
     float f[8];
@@ -1893,6 +2066,7 @@ __device__ __forceinline__ void stage_seg32(const float4 (&v)[8], uint32_t (&P)[
     }
     sx = s0 + s1;
     sy = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+    return bad || m > kDivertMax;
 }
 
 // lane i of every quad receives lane S of its quad
@@ -1922,6 +2096,11 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
     uint8_t *reg = lds + w * REG;
     const uint32_t reg0 = lds0 + w * REG;
     float *red = (float *)(lds + 8u * REG);                  // [kWaveRows][8 waves x 4 DPP rows]
+    // per-wave "x has a non-finite or huge segment" (see row_dot_f32)
+    __shared__ __align__(16) uint32_t dflags[kMaxWaves];
+    QG_TL_WAVE_DECL;
+    QG_TL_DECL;
+    QG_TL(0);
     // x lines L = 8k + lane/8 (item L/4, segment L%4 of the wave's chunk)
     const float *xw = a.x + w * CJ * 128u;
 #pragma unroll
@@ -1942,13 +2121,25 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
         const uint32_t gr = min(blockIdx.x + i * gridDim.x, a.rows - 1u);
         lds_dma16_asm(a.w + (size_t)gr * a.group_bytes + loff, reg0 + i * SLOT);
     };
+    // the younger wave of each SIMD (w >= 4) keeps two steps of rows in
+    // flight, the older one one step: rows 0..7 or 0..3 now (slots 0..7;
+    // x lands in slots 8..15)
+    const bool two = w >= 4u;
 #pragma unroll
     for (uint32_t i = 0; i < 4u; i++) issue(i);
-    wait_vm_n<4u>();                                         // x landed
+    if (two) {
+#pragma unroll
+        for (uint32_t i = 4; i < 8u; i++) issue(i);
+    }
+    QG_TL(1);
+    if (two) wait_vm_n<8u>();                                // x landed
+    else wait_vm_n<4u>();
+    QG_TL(2);
     const uint32_t jj = lane >> 2, r = lane & 3u;
     const bool active = jj < CJ && w * CJ + jj < a.ni;
     const uint32_t it = jj < CJ ? jj : 0u;
     XP<4, 32> xs;
+    bool xdiv;
     {
         float4 v[8];
         const uint8_t *xl = reg + XROW * SLOT + 128u * (lane < 4u * CJ ? lane : 0u);
@@ -1956,7 +2147,7 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
         for (uint32_t k = 0; k < 8; k++) v[k] = *(const float4 *)(xl + 16u * ((k + lane) & 7u));
         uint32_t P[3][8];
         float ik, sx, sy;
-        stage_seg32(v, P, ik, sx, sy);
+        xdiv = stage_seg32(v, P, ik, sx, sy);
 #pragma unroll
         for (int c = 0; c < 3; c++)
 #pragma unroll
@@ -1974,13 +2165,30 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
         xs.sy[2] = quad_bcastf<2>(sy); xs.sy[3] = quad_bcastf<3>(sy);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // x read before rows 8.. overwrite it
     }
+    QG_TL(3);
+    // from here on the younger wave wins VALU arbitration on its SIMD: left
+    // to the default (oldest first) it computes behind the older one and
+    // finishes its last steps alone
+    if (two) __builtin_amdgcn_s_setprio(1);
 #pragma unroll 1
     for (uint32_t s = 0; s < NSTEP; s++) {
-        wait_vm_n<0u>();                                     // step s landed
-        if (s + 1u < NSTEP) {
+        // step s landed (the younger wave: step s + 1 may still be in
+        // flight), then the next step requested
+        if (two) {
+            if (s + 1u < NSTEP) wait_vm_n<4u>();
+            else wait_vm_n<0u>();
+            if (s + 2u < NSTEP) {
 #pragma unroll
-            for (uint32_t i = 0; i < 4u; i++) issue(4u * (s + 1u) + i);
+                for (uint32_t i = 0; i < 4u; i++) issue(4u * (s + 2u) + i);
+            }
+        } else {
+            wait_vm_n<0u>();
+            if (s + 1u < NSTEP) {
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++) issue(4u * (s + 1u) + i);
+            }
         }
+        QG_TL(4u + 2u * s);
         const uint8_t *grp = reg + (4u * s + r) * SLOT;
         uint32_t raw[I::NRAW];
         {
@@ -1998,14 +2206,31 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
         t += dpp<0x114>(t);                                  // row_shr:4
         t += dpp<0x118>(t);                                  // row_shr:8: lanes 12..15 hold rows r = 0..3
         if ((lane & 15u) >= 12u) red[(4u * s + r) * 32u + w * 4u + (lane >> 4)] = t;
+        QG_TL(5u + 2u * s);
     }
+    divert_note(dflags, xdiv);
     lds_barrier();
-    if (w == 0 && lane < kWaveRows && blockIdx.x + lane * gridDim.x < a.rows) {
-        float v = 0.f;
-#pragma unroll
-        for (uint32_t i = 0; i < 32u; i++) v += red[lane * 32u + i];
-        store_y(a.y + blockIdx.x + lane * gridDim.x, v);
+    QG_TL(12);
+    const bool div = divert_any(dflags);
+    if (!div) {
+        // rows 2w and 2w + 1: their 32 partial sums one per lane, added by DPP
+        const uint32_t rr = 2u * w + (lane >> 5);
+        const float v = group_sum<32>(red[rr * 32u + (lane & 31u)]);
+        if ((lane & 31u) == 31u && blockIdx.x + rr * gridDim.x < a.rows) store_y(a.y + blockIdx.x + rr * gridDim.x, v);
     }
+    if (div) {
+        // the workgroup's 16 rows in f32 instead (row_dot_f32), two per wave
+        for (uint32_t i = w; i < kWaveRows; i += 8u) {
+            const uint32_t row = blockIdx.x + i * gridDim.x;
+            if (row < a.rows) {
+                const float v = row_dot_f32<T_Q4_K, true>(a, row);
+                if (lane == 0u) a.y[row] = v;
+            }
+        }
+    }
+    QG_TL(13);
+    if (w == 0) QG_TL_WRITE(0);
+    QG_TL_WAVE_END();
 }
 
 // ------------------------------------------------ no-allocation scratch
@@ -2063,13 +2288,16 @@ template <uint32_t T, bool G1, bool RP = false> static const void *stream_fn_glu
 // more in the GGUF layout.
 template <uint32_t T> constexpr bool repackable() { return T == T_Q8_0 || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K; }
 
+// Dynamic LDS a workgroup may use: the device's maximum less a reserve for
+// the kernels' static arrays (per-wave flags and norm sums, < 256 bytes).
+constexpr int kStaticLds = 256;
 static int max_lds_bytes()
 {
     int dev = 0, v = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 65536;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
-        return 65536;
-    return v;
+    if (hipGetDevice(&dev) != hipSuccess) return 65536 - kStaticLds;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= kStaticLds)
+        return 65536 - kStaticLds;
+    return v - kStaticLds;
 }
 
 // Stream kernel plan (kind 1); leaves kind 0 (generic kernel) where it does
@@ -2712,31 +2940,6 @@ int launch_dequantize_rows_dev(uint32_t type, const uint8_t *w, size_t rows, siz
                                uint32_t n, float *out, size_t ldo, ihipStream_t *stream)
 {
     return launch_dequantize_row_any(type, w, rows, cols, 0, d_rows, n, out, ldo, stream);
-}
-
-// The streaming-read ceiling: every 16-byte piece of the buffer read once by
-// one thread of a full grid of 1024-thread workgroups (the fastest plain read
-// of 33-447 MB measured on MI355X among grid-wide, persistent, banded and
-// chunked forms with 1-4 loads per thread); an XOR of everything goes to
-// out[0] only if it matches a constant, so the loads cannot be dropped.
-__global__ void __launch_bounds__(1024) stream_read_k(const uint4 *__restrict__ p, uint64_t n16,
-                                                      uint32_t *__restrict__ out)
-{
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint4 v = i < n16 ? p[i] : make_uint4(0u, 0u, 0u, 0u);
-    const uint32_t acc = v.x ^ v.y ^ v.z ^ v.w;
-    if (acc == 0x9E3779B9u) out[0] = acc;
-}
-
-int launch_stream_read(const void *buf, size_t nbytes, uint32_t *out, ihipStream_t *stream)
-{
-    const uint64_t n16 = nbytes / 16u;
-    if (n16 == 0) return 0;
-    const uint64_t grid = (n16 + 1023u) / 1024u;
-    if (grid > 0x7FFFFFFFull) return -1;
-    hipLaunchKernelGGL(stream_read_k, dim3((uint32_t)grid), dim3(1024), 0, (hipStream_t)stream,
-                       (const uint4 *)buf, n16, out);
-    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream)

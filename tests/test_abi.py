@@ -65,3 +65,14 @@ def test_nbytes_for_matches_model_loader(rinf):
     assert rinf.nbytes_for(rinf.Q6_K, 151936, 896) == 111672960
     assert rinf.nbytes_for(rinf.Q8_0, 896, 896) == 896 * 28 * 34
     assert rinf.nbytes_for(rinf.F16, 3, 5) == 30
+
+
+def test_probe_library_exports(rinf):
+    """libqgprobe.so (the measurement-only reads bench.py times) exports what
+    include/qgprobe.h declares, and rejects bad arguments before any launch."""
+    lib = rinf.load_probe_library()
+    names = _declared(ROOT / "include" / "qgprobe.h", "qgp_")
+    assert names == sorted(rinf._PROBE_SIGS)
+    assert all(hasattr(lib, n) for n in names)
+    assert lib.qgp_read(None, 0, 16, None, 256, 0, 1, 1, None) == -1
+    assert lib.qgp_read_wave_lds(None, 0, 16, 8064, None, 1, None) == -1

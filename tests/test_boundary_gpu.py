@@ -160,16 +160,29 @@ def test_shared_matrix_cannot_be_freed_while_in_use(rinf, synth):
         c.close()
 
 
-def test_probe_stream_read(rinf, ctx):
+def test_probe_reads(rinf, ctx):
+    """libqgprobe.so's measurement reads (include/qgprobe.h) run every design
+    bench.py sweeps and the gemv_wave-shaped LDS read: zeros never match
+    the constant, so d_out stays 0; bad arguments are refused."""
+    import ctypes
     import torch
-    buf = torch.zeros(1 << 18, dtype=torch.float32, device="cuda")
+    probe = rinf.load_probe_library()
+    rows, row_bytes = 64, 8064                      # the wave read's row shape (Q4_K 14336 columns)
+    bufs = [torch.zeros(rows * row_bytes // 4, dtype=torch.float32, device="cuda") for _ in range(2)]
+    arr = (ctypes.c_void_p * 2)(*[b.data_ptr() for b in bufs])
     out = torch.zeros(4, dtype=torch.int32, device="cuda")
-    ctx.probe_stream_read(buf, buf.numel() * 4, out, torch.cuda.current_stream().cuda_stream)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nb = rows * row_bytes
+    for threads in (256, 512, 1024):
+        for loads in (1, 2, 4, 8):
+            for wgs in (0, 4, 256):
+                assert probe.qgp_read(arr, 2, nb, out.data_ptr(), threads, wgs, loads, 3, st) == 0
+    assert probe.qgp_read_wave_lds(arr, 2, rows, row_bytes, out.data_ptr(), 3, st) == 0
     torch.cuda.synchronize()
-    assert int(out[0]) == 0                                       # zeros never match the constant
-    with pytest.raises(rinf.QgemvError) as e:
-        ctx.probe_stream_read(buf, 100, out)                      # not whole 16-byte pieces
-    assert e.value.status == INVALID
+    assert int(out[0]) == 0
+    assert probe.qgp_read(arr, 2, 100, out.data_ptr(), 256, 0, 1, 1, st) == -1       # not whole 16-byte pieces
+    assert probe.qgp_read(arr, 2, nb, out.data_ptr(), 256, 0, 3, 1, st) == -1        # 3 loads per thread
+    assert probe.qgp_read_wave_lds(arr, 2, rows, 100, out.data_ptr(), 1, st) == -1   # row not 128-byte pieces
 
 
 def test_wrap_device_needs_the_tail_pad(ctx):

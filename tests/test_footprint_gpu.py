@@ -86,3 +86,34 @@ def test_dequant_of_repacked_only_matrix(rinf, synth, oracle, ctx, dtype, cols):
         got = d.cpu().numpy()
         assert np.array_equal(got.view(np.uint32), oracle.dequantize_row(raw, dtype, rows, cols, r).view(np.uint32))
     m.free()
+
+
+def test_failed_restore_keeps_the_stack(rinf, synth, oracle, ctx):
+    """Replacing a part re-copies every view part out of its stack first.
+    When one of those copies cannot be allocated (injected failures, every
+    allocation index in turn), set_matrix reports out-of-memory and the
+    stack whose parts could not all be restored stays alive: the model keeps
+    following the oracle (the replacement has the same bytes, so the oracle
+    holds either way)."""
+    cfg = dict(SMALL, n_layers=2)
+    dev, ref, _ = build(rinf, synth, oracle, ctx, cfg, "q4_k_m", 75, 40)
+    prompt = np.random.default_rng(75).integers(0, cfg["vocab_size"], 4)
+    run_and_compare(dev, ref, oracle, cfg, prompt, 2)            # builds the stacks and views
+    t = synth.gen_model(cfg, "q4_k_m", 75)
+    raw, dtype, rows, cols = t["mats"][("up", 1)]
+    restore_failures = 0
+    for skip in range(16):
+        ctx.fail_allocations(1, skip)
+        try:
+            dev.set_matrix(rinf.M_UP, 1, raw, dtype, rows, cols)
+        except rinf.QgemvError as e:
+            assert e.status == 6, e
+            restore_failures += "matrix copy" in str(e)
+        finally:
+            ctx.fail_allocations(0)
+        dev.reset()
+        ref.reset()
+        out, errs = run_and_compare(dev, ref, oracle, cfg, prompt, 2)
+        assert max(errs) <= DEEP_TOL, (skip, max(errs))
+    assert restore_failures > 0
+    dev.close()

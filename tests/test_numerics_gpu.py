@@ -7,10 +7,16 @@ src/quant.rs:188-205) and against an exact float64 product of the
 dequantized weights (oracle.dequantize, bit-exact with quant.rs:356-840),
 both within the north-star bound GEMV_TOL (normwise, 1e-4).
 
-Non-finite x: the reference's sequential sum makes a row +-inf or NaN when
-x holds an inf or a NaN; the device makes every row that meets such an
-element NaN for the quantized types (the segment's 1/k is NaN) and follows
-IEEE arithmetic for F16/F32 (x stays f32).  The tests pin exactly that.
+Tiny x (every element scaled by 1e-30): the segment scale k is capped at
+2^122, which keeps all 22 bits down to a segment maximum of ~7.9e-31.
+
+Non-finite x: the reference's sequential sum makes a row +inf where it meets
++inf (with a positive weight), -inf, or NaN where signs mix, a weight is zero
+or x holds a NaN.  The device matches that row by row for every type and
+every kernel (stream, LDS ring, wave-private): a workgroup whose x has a
+non-finite segment, or one whose maximum exceeds 2^64, recomputes its rows as
+f32 sums of rounded products.  Huge finite x (|x| > 2^64) takes the same path
+and is compared within GEMV_TOL.
 """
 from __future__ import annotations
 
@@ -71,29 +77,107 @@ def test_adversarial_x(ctx, oracle, synth, dtype, shape, dist):
     assert e_exact <= GEMV_TOL
 
 
+def same_classes(y, ref):
+    """Row by row: NaN where the reference has NaN, otherwise the same value
+    (the reference's +-inf, or for finite rows within the GEMV tolerance)."""
+    y, ref = np.asarray(y), np.asarray(ref)
+    assert np.array_equal(np.isnan(y), np.isnan(ref)), \
+        f"NaN rows differ: device {np.flatnonzero(np.isnan(y))[:8]} ref {np.flatnonzero(np.isnan(ref))[:8]}"
+    inf = np.isinf(ref)
+    assert np.array_equal(np.isinf(y), inf)
+    assert np.array_equal(y[inf], ref[inf])
+    fin = np.isfinite(ref)
+    if fin.any():
+        assert normwise_err(y[fin], ref[fin]) <= GEMV_TOL
+
+
+def ref_mv(oracle, raw, dtype, rows, cols, x):
+    return (oracle.mat_vec_mul(raw, dtype, rows, cols, x) if rows * cols <= 4_000_000
+            else oracle.mat_vec_mul_rows(raw, dtype, rows, cols, x))
+
+
+KIND = {0: "generic", 1: "stream", 2: "ring", 3: "wave"}
+
+
 @pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
-@pytest.mark.parametrize("bad", ["inf", "-inf", "nan"])
+@pytest.mark.parametrize("bad", ["inf", "-inf", "nan", "both-infs", "huge"])
 def test_non_finite_x(ctx, oracle, synth, dtype, bad):
+    """256 x 1024 (stream kernel): one inf, one -inf, one NaN, an inf and a
+    -inf in different segments, or one element of 1e30 (finite: diverted)."""
     rows, cols = 256, 1024
     raw = synth.gen_blocks(dtype, rows, cols, 77 + dtype)
     x = synth.gen_x(cols, 77)
-    x[333] = np.float32(bad)
+    if bad == "both-infs":
+        x[333], x[700] = np.inf, -np.inf
+    elif bad == "huge":
+        x[333] = np.float32(1e30)
+    else:
+        x[333] = np.float32(bad)
+    m = ctx.upload(raw, dtype, rows, cols)
+    y = np.zeros(rows, np.float32)
+    m.matvec_host(x, y)
+    kind = m.kernel_kind
+    m.free()
+    ref = oracle.mat_vec_mul(raw, dtype, rows, cols, x)
+    if bad == "huge":
+        assert np.isfinite(ref).all()
+    else:
+        assert not np.isfinite(ref).any()        # every row meets the column
+    print(f"{NAMES[dtype]} {bad} ({KIND.get(kind)}): ref NaN rows {int(np.isnan(ref).sum())}, "
+          f"+inf {int((ref == np.inf).sum())}, -inf {int((ref == -np.inf).sum())}", flush=True)
+    same_classes(y, ref)
+
+
+# every kernel family on a non-finite x: Q4_K rows of 14336 (wave-private),
+# 18944 (LDS ring), the ring's other types, straddling row groups (896)
+BIG = [(12, 4096, 14336), (12, 3584, 18944), (13, 4096, 14336), (14, 4096, 14336), (8, 4096, 14336),
+       (2, 4096, 14336), (12, 512, 896), (14, 512, 896)]
+
+
+@pytest.mark.parametrize("dtype,rows,cols", BIG, ids=[f"{NAMES[t]}-{r}x{c}" for t, r, c in BIG])
+def test_non_finite_x_every_kernel(ctx, oracle, synth, dtype, rows, cols):
+    """+inf and -inf in two segments (rows mix to NaN or keep one sign), then
+    a NaN, through the kernel each shape plans."""
+    raw = synth.gen_blocks(dtype, rows, cols, 7 + dtype + cols)
+    m = ctx.upload(raw, dtype, rows, cols)
+    kind = m.kernel_kind
+    for case in ("infs", "nan"):
+        x = synth.gen_x(cols, 7 + cols)
+        if case == "infs":
+            x[cols // 3], x[cols // 3 + 97] = np.inf, -np.inf
+        else:
+            x[cols - 5] = np.nan
+        y = np.zeros(rows, np.float32)
+        m.matvec_host(x, y)
+        ref = ref_mv(oracle, raw, dtype, rows, cols, x)
+        print(f"{NAMES[dtype]} {rows}x{cols} {case} ({KIND.get(kind)}): NaN {int(np.isnan(ref).sum())}, "
+              f"+inf {int((ref == np.inf).sum())}, -inf {int((ref == -np.inf).sum())}", flush=True)
+        same_classes(y, ref)
+    # and a clean x afterwards: the fast path again
+    x = synth.gen_x(cols, 8 + cols)
+    y = np.zeros(rows, np.float32)
+    m.matvec_host(x, y)
+    m.free()
+    assert normwise_err(y, ref_mv(oracle, raw, dtype, rows, cols, x)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{r}x{c}" for r, c in SHAPES])
+def test_tiny_x(ctx, oracle, synth, dtype, shape):
+    """x ~ N(0,1) * 1e-30: every segment keeps its 22 bits (k <= 2^122)."""
+    rows, cols = shape
+    seed = synth.config_seed(1) + 7 * rows + cols + dtype
+    raw = synth.gen_blocks(dtype, rows, cols, seed)
+    x = (synth.gen_x(cols, seed).astype(np.float64) * 1e-30).astype(np.float32)
     m = ctx.upload(raw, dtype, rows, cols)
     y = np.zeros(rows, np.float32)
     m.matvec_host(x, y)
     m.free()
-    ref = oracle.mat_vec_mul(raw, dtype, rows, cols, x)
-    # every row meets column 333: every output of both sides is non-finite
-    assert not np.isfinite(ref).any()
-    assert not np.isfinite(y).any()
-    if dtype in QUANT:
-        assert np.isnan(y).all()                 # the segment's 1/k is NaN
-    else:
-        # f32 x: IEEE arithmetic as in the reference -- same infinities where
-        # the reference's row has one, NaN where it has NaN
-        assert np.array_equal(np.isnan(y), np.isnan(ref))
-        fin = ~np.isnan(ref)
-        assert np.array_equal(np.sign(y[fin]), np.sign(ref[fin]))
+    y32, y64 = ref_pair(oracle, raw, dtype, rows, cols, x)
+    e_ref, e_exact = normwise_err(y, y32), normwise_err(y, y64)
+    print(f"{NAMES[dtype]} {rows}x{cols} x*1e-30: vs reference {e_ref:.2e}, vs exact {e_exact:.2e}", flush=True)
+    assert e_ref <= GEMV_TOL
+    assert e_exact <= GEMV_TOL
 
 
 @pytest.mark.parametrize("dtype", QUANT, ids=[NAMES[t] for t in QUANT])
@@ -114,6 +198,6 @@ def test_clean_call_after_non_finite(ctx, oracle, synth, dtype):
     y_again = np.zeros(rows, np.float32)
     m.matvec_host(x, y_again)
     m.free()
-    assert np.isnan(y_bad).all()
+    same_classes(y_bad, oracle.mat_vec_mul(raw, dtype, rows, cols, xb))
     assert np.array_equal(y_clean.view(np.uint32), y_again.view(np.uint32))
     assert normwise_err(y_clean, oracle.mat_vec_mul(raw, dtype, rows, cols, x)) <= GEMV_TOL

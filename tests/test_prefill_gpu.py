@@ -1,12 +1,15 @@
 """GPU parity of the batched prefill (qg_model_prefill, include/qgmodel.h):
-the prompt's tokens through each layer together, every projection an int8
-MFMA GEMM over the tokens' fixed-point x.  Checked against the oracle's
-token-by-token forward pass (oracle/qref_model.c, transformer.rs:63-98 as
-model.rs:361-365 calls it): the last prompt token's logits, then greedy
-decode steps on the caches the prefill wrote (every cached position's K/V
-enters those steps), within DEEP_TOL, identical tokens.  Also: chunks of 64
-tokens, a prefill that continues a cache, the token-by-token fallback for a
-mix without an MFMA path (F16), and generate with the batched prefill."""
+the prompt's tokens through each layer together, every projection a GEMM on
+the matrix cores (x as three bf16 pieces, weight codes as exact bf16
+operands, f32 accumulation).  Checked against the oracle's token-by-token
+forward pass (oracle/qref_model.c, transformer.rs:63-98 as model.rs:361-365
+calls it): the last prompt token's logits, then greedy decode steps on the
+caches the prefill wrote (every cached position's K/V enters those steps),
+within DEEP_TOL, identical tokens.  Also: chunks of 64 tokens, a prefill that
+continues a cache, the token-by-token fallback for a mix without an MFMA
+path (F16), generate with the batched prefill, and layer matrices wrapped
+in the GGUF layout (qg_wrap_device) so that the GEMM's GGUF-layout loaders
+run: rows straddling superblocks (cols = 896) and whole-block rows."""
 from __future__ import annotations
 
 import numpy as np
@@ -146,3 +149,64 @@ def test_prefill_errors(rinf, synth, oracle, ctx):
     assert e.value.status == 7
     assert dev.seq_len == 0
     dev.close()
+
+
+def build_wrapped(rinf, synth, oracle, ctx, cfg, mix, seed, max_seq):
+    """As test_decode_gpu.build, but every layer matrix is GGUF-layout bytes
+    in device memory wrapped with qg_wrap_device and shared into its slot
+    (never repacked), so the prefill GEMM reads the GGUF layout."""
+    import torch
+    t = synth.gen_model(cfg, mix, seed)
+    dev = rinf.DeviceModel(ctx, cfg["embed_dim"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                           cfg["hidden_dim"], cfg["vocab_size"], max_seq, cfg["rope_base"], cfg["norm_eps"])
+    ref = oracle.Model(dict(cfg, max_seq_len=max_seq))
+    slots = {"token_embd": rinf.M_TOKEN_EMBD, "lm_head": rinf.M_LM_HEAD, "wq": rinf.M_WQ,
+             "wk": rinf.M_WK, "wv": rinf.M_WV, "wo": rinf.M_WO, "gate": rinf.M_GATE,
+             "up": rinf.M_UP, "down": rinf.M_DOWN}
+    vslots = {"final_norm": rinf.V_FINAL_NORM, "attn_norm": rinf.V_ATTN_NORM,
+              "ffn_norm": rinf.V_FFN_NORM, "bq": rinf.V_BQ, "bk": rinf.V_BK, "bv": rinf.V_BV}
+    keep, layouts = [], set()
+    for (slot, layer), (raw, dtype, rows, cols) in t["mats"].items():
+        if slot in ("token_embd", "lm_head"):
+            dev.set_matrix(slots[slot], layer, raw, dtype, rows, cols)
+        else:
+            buf = torch.zeros(raw.size + 512, dtype=torch.uint8, device="cuda")
+            buf[:raw.size] = torch.from_numpy(np.ascontiguousarray(raw))
+            h = ctx.wrap_device(buf, dtype, rows, cols)
+            dev.share_matrix(slots[slot], layer, h)
+            keep += [buf, h]
+            layouts.add((dtype, "whole blocks" if cols % 256 == 0 or dtype == 8 else "straddling"))
+        ref.set_mat(slot, layer, raw, dtype, rows, cols)
+    for (name, layer), v in t["vecs"].items():
+        dev.set_vector(vslots[name], layer, v)
+        ref.set_vec(name, layer, v)
+    return dev, ref, keep, layouts
+
+
+@pytest.mark.parametrize("embed,hidden,mix", [(896, 1024, "q4_k_m"), (3584, 1024, "q4_k_m"), (3584, 1024, "q8_0")],
+                         ids=["straddle-896", "whole-3584", "q8_0-3584"])
+def test_prefill_gguf_layout_matrices(rinf, synth, oracle, ctx, embed, hidden, mix):
+    """Wrapped (GGUF-layout) layer matrices through the batched prefill:
+    Q4_K rows of 896 columns straddle superblocks (the general loader), Q4_K,
+    Q6_K and Q8_0 rows of 3584 / 1024 columns hold whole blocks (the
+    whole-block loader); 2 layers, a 40-token prompt, then 6 greedy steps,
+    against the oracle."""
+    heads = embed // 64 if embed == 896 else 28
+    cfg = dict(SMALL, n_layers=2, embed_dim=embed, n_heads=heads, n_kv_heads=2 if embed == 896 else 4,
+               hidden_dim=hidden)
+    dev, ref, keep, layouts = build_wrapped(rinf, synth, oracle, ctx, cfg, mix, 83, 64)
+    prompt = np.random.default_rng(83).integers(0, cfg["vocab_size"], 40)
+    logits = np.zeros(cfg["vocab_size"], np.float32)
+    dev.prefill(prompt, logits)
+    ref_l = None
+    for pos, tok in enumerate(prompt):
+        ref_l = ref.forward(int(tok), pos)
+    e0 = normwise_err(logits, ref_l)
+    errs, out = decode_compare(dev, ref, oracle, cfg, [int(t) for t in prompt], ref_l, 6, len(prompt))
+    print(f"wrapped {mix} {embed}: layouts {sorted(layouts)}, prefill logits err {e0:.2e}, "
+          f"decode max {max(errs):.2e}", flush=True)
+    dev.close()
+    for k in keep:
+        if hasattr(k, "free"):
+            k.free()
+    assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL

@@ -5,7 +5,10 @@ context buffers.  Checked through the C ABI against the allocating entry
 point (same kernels: bit-identical h and residual sum) and against the
 oracle (GEMV_TOL), on two calls in a row, the second with a smaller matrix,
 on the unfused path (xb NULL; an F16 matrix, whose stream kernels have no
-RMSNorm prologue) and on the fused path; and the size limit."""
+RMSNorm prologue) and on the fused path; and the size limit.  The no-allocation
+calls run first, on a fresh context whose every allocation is made to fail
+after the upload (qg_test_fail_allocations), so any allocation on that path
+would fail the test; the allocating entry runs on another context."""
 from __future__ import annotations
 
 import numpy as np
@@ -39,33 +42,44 @@ CASES = [  # (type, rows of [gate; up], cols, xb given)
 @pytest.mark.parametrize("pair", CASES, ids=["q4k-xb-null", "f16", "q4k-fused"])
 def test_noalloc_matches_allocating_entry(rinf, ctx, oracle, synth, pair):
     import torch
-    for i, (dtype, rows2, cols, with_xb) in enumerate(pair):
-        seed = 500 + 17 * i + rows2 + cols + dtype
-        raw = synth.gen_weights(dtype, rows2, cols, seed)
-        rng = np.random.default_rng(seed)
-        xa = rng.standard_normal(cols).astype(np.float32)
-        xb = rng.standard_normal(cols).astype(np.float32) if with_xb else None
-        nw = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
-        m = ctx.upload(raw, dtype, rows2, cols)
-        d = lambda a: torch.from_numpy(a).cuda()
-        dxa, dnw = d(xa), d(nw)
-        dxb = d(xb) if xb is not None else None
-        h = [torch.full((rows2 // 2,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(2)]
-        s = [torch.full((cols,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(2)]
-        st = torch.cuda.current_stream().cuda_stream
-        torch.cuda.synchronize()
-        m.matvec_norm_glu_dev(dxa, dxb, dnw, 1e-6, h[0], s[0], st)
-        m.matvec_norm_glu_dev_noalloc(dxa, dxb, dnw, 1e-6, h[1], s[1], st)
-        torch.cuda.synchronize()
-        ha, hn = h[0].cpu().numpy(), h[1].cpu().numpy()
-        sa, sn = s[0].cpu().numpy(), s[1].cpu().numpy()
-        m.free()
-        print(f"call {i}: type {dtype} {rows2}x{cols} xb={'yes' if with_xb else 'NULL'}: "
-              f"err vs oracle {normwise_err(hn, ref_h(oracle, raw, dtype, rows2, cols, xa, xb, nw, 1e-6)):.2e}",
-              flush=True)
-        assert np.array_equal(ha.view(np.uint32), hn.view(np.uint32))
-        assert np.array_equal(sa.view(np.uint32), sn.view(np.uint32))
-        assert normwise_err(hn, ref_h(oracle, raw, dtype, rows2, cols, xa, xb, nw, 1e-6)) <= GEMV_TOL
+    fresh = rinf.GpuContext(0)
+    try:
+        for i, (dtype, rows2, cols, with_xb) in enumerate(pair):
+            seed = 500 + 17 * i + rows2 + cols + dtype
+            raw = synth.gen_weights(dtype, rows2, cols, seed)
+            rng = np.random.default_rng(seed)
+            xa = rng.standard_normal(cols).astype(np.float32)
+            xb = rng.standard_normal(cols).astype(np.float32) if with_xb else None
+            nw = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+            mn = fresh.upload(raw, dtype, rows2, cols)
+            ma = ctx.upload(raw, dtype, rows2, cols)
+            d = lambda a: torch.from_numpy(a).cuda()
+            dxa, dnw = d(xa), d(nw)
+            dxb = d(xb) if xb is not None else None
+            h = [torch.full((rows2 // 2,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(2)]
+            s = [torch.full((cols,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(2)]
+            st = torch.cuda.current_stream().cuda_stream
+            torch.cuda.synchronize()
+            fresh.fail_allocations(1 << 30)             # any allocation from here on fails
+            try:
+                mn.matvec_norm_glu_dev_noalloc(dxa, dxb, dnw, 1e-6, h[1], s[1], st)
+                torch.cuda.synchronize()
+            finally:
+                fresh.fail_allocations(0)
+            ma.matvec_norm_glu_dev(dxa, dxb, dnw, 1e-6, h[0], s[0], st)
+            torch.cuda.synchronize()
+            ha, hn = h[0].cpu().numpy(), h[1].cpu().numpy()
+            sa, sn = s[0].cpu().numpy(), s[1].cpu().numpy()
+            mn.free()
+            ma.free()
+            err = normwise_err(hn, ref_h(oracle, raw, dtype, rows2, cols, xa, xb, nw, 1e-6))
+            print(f"call {i}: type {dtype} {rows2}x{cols} xb={'yes' if with_xb else 'NULL'}: "
+                  f"err vs oracle {err:.2e}", flush=True)
+            assert np.array_equal(ha.view(np.uint32), hn.view(np.uint32))
+            assert np.array_equal(sa.view(np.uint32), sn.view(np.uint32))
+            assert err <= GEMV_TOL
+    finally:
+        fresh.close()
 
 
 def test_noalloc_size_limit(rinf, ctx, synth):
