@@ -562,6 +562,38 @@ def _pmc_rows(d):
     return out
 
 
+def trace_summary(args):
+    """Markdown table of a rocprofv3 --kernel-trace run: consecutive dispatches
+    of one kernel with one launch shape form a run (e.g. one read design of
+    the ceiling sweep at one size, or the GEMV's timed loop); per run the
+    dispatch count and the mean / median / min duration.  Runs shorter than
+    --trace-min-calls dispatches are left out."""
+    import csv
+    rows = []
+    for f in sorted(pathlib.Path(args.trace_summary).rglob("*kernel_trace.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                rows.append((int(r["Start_Timestamp"]), r["Kernel_Name"], int(r["Workgroup_Size_X"]),
+                             int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])),
+                             (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    rows.sort()
+    runs = []
+    for t, name, wg, grid, us in rows:
+        if runs and runs[-1][0] == (name, wg, grid):
+            runs[-1][1].append(us)
+        else:
+            runs.append([(name, wg, grid), [us]])
+    pat = args.trace_filter
+    print("| run | kernel | workgroup | workgroups | dispatches | mean us | median us | min us |")
+    print("|---:|---|---:|---:|---:|---:|---:|---:|")
+    for i, ((name, wg, grid), d) in enumerate(runs):
+        if len(d) < args.trace_min_calls or (pat and pat not in name):
+            continue
+        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        print(f"| {i} | `{short}` | {wg} | {grid} | {len(d)} | {statistics.mean(d):.3f} | "
+              f"{statistics.median(d):.3f} | {min(d):.3f} |")
+
+
 def pmc_summary(args):
     """profiles/traffic.json from a FETCH_SIZE run and a WRITE_SIZE run of
     `bench.py ... --copy-probe-mb M`.  Both counters report KiB per dispatch;
@@ -626,6 +658,10 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 --pmc runs of this script (FETCH_SIZE, then "
                          "WRITE_SIZE, each with --copy-probe-mb) into profiles/traffic.json")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="print a markdown table of the kernel runs in a rocprofv3 --kernel-trace output dir")
+    ap.add_argument("--trace-filter", default="", help="with --trace-summary: kernels whose name contains this")
+    ap.add_argument("--trace-min-calls", type=int, default=20)
     ap.add_argument("--no-ceiling", action="store_true", help="skip the streaming-read ceiling leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the configs[1] per-type sweep")
     ap.add_argument("--no-decode-configs", action="store_true",
@@ -637,6 +673,9 @@ def main():
     ap.add_argument("--timeline-glu", action="store_true",
                     help="with --timeline: the stream kernel's [gate; up] form instead")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args)
+        return
     if args.pmc_summary:
         pmc_summary(args)
         return
