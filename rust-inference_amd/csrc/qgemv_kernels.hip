@@ -1087,11 +1087,12 @@ struct StreamArgs {
 // holding one gets 1/k = NaN, which would make every row NaN.  The reference
 // sums w * x[c] one product at a time in f32 (quant.rs:195-204), so a row that
 // meets +inf gives +inf, -inf gives -inf, and NaN only where signs mix, a
-// weight is zero or x holds a NaN.  The plain mat-vec kernels therefore note,
-// per workgroup, whether any segment of x was non-finite (or so large that
-// the fixed-point sums could overflow where f32 products do not: max |x| over
-// a segment > 2^64), and if so recompute every row they own with
-// row_dot_f32: the f32 sum of one rounded product per element.  Its order
+// weight is zero or x holds a NaN.  The plain mat-vec kernels therefore find
+// out whether any segment of x was non-finite (or so large that the
+// fixed-point sums could overflow where f32 products do not: max |x| over a
+// segment > 2^64) -- the stream and ring kernels from per-wave flags,
+// gemv_wave from its NaN row sums -- and if so recompute every row they own
+// with row_dot_f32: the f32 sum of one rounded product per element.  Its order
 // differs from the reference's, which changes only finite results; whether a
 // sum is finite, +inf, -inf or NaN does not depend on the order.
 // sum over c of w(row, c) * x[c] in f32 (wave-cooperative: `row` is
@@ -1129,11 +1130,19 @@ __device__ __forceinline__ void divert_note(uint32_t *flags, bool mine)
     const bool any = __builtin_amdgcn_ballot_w64(mine) != 0;
     if ((threadIdx.x & 63u) == 0u) flags[threadIdx.x >> 6] = any ? 1u : 0u;
 }
+// (flags: kMaxWaves words, 16-byte aligned; read at once, slots past the
+// workgroup's waves ignored)
 __device__ __forceinline__ bool divert_any(const uint32_t *flags)
 {
     const uint32_t nw = (blockDim.x + 63u) >> 6;
+    const uint4 *f4 = (const uint4 *)flags;
     uint32_t v = 0;
-    for (uint32_t i = 0; i < nw; i++) v |= flags[i];
+#pragma unroll
+    for (uint32_t q = 0; q < kMaxWaves / 4u; q++) {
+        const uint4 u = f4[q];
+        v |= (4u * q < nw ? u.x : 0u) | (4u * q + 1u < nw ? u.y : 0u) | (4u * q + 2u < nw ? u.z : 0u) |
+             (4u * q + 3u < nw ? u.w : 0u);
+    }
     return v != 0u;
 }
 
@@ -2034,7 +2043,9 @@ template <uint32_t N> __device__ __forceinline__ void wait_vm_n()
 // One 32-element segment converted in one lane, with the arithmetic and the
 // summation trees of stage_planes16 for its two halves: P = the three digit
 // planes (8 dwords each), ik = 1/k, sx = sum x, sy = sum Y.
-__device__ __forceinline__ bool stage_seg32(const float4 (&v)[8], uint32_t (&P)[3][8], float &ik, float &sx, float &sy)
+// Unlike stage_planes16, a segment with max |x| > 2^64 also gets 1/k = NaN:
+// gemv_wave tells a diverting workgroup by its NaN row sums.
+__device__ __forceinline__ void stage_seg32(const float4 (&v)[8], uint32_t (&P)[3][8], float &ik, float &sx, float &sy)
 {
     uint32_t mb = 0;
 #pragma unroll
@@ -2044,7 +2055,7 @@ __device__ __forceinline__ bool stage_seg32(const float4 (&v)[8], uint32_t (&P)[
 #pragma unroll
     for (int i = 0; i < 8; i++) t[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
     const float s0 = (t[0] + t[1]) + (t[2] + t[3]), s1 = (t[4] + t[5]) + (t[6] + t[7]);
-    const bool bad = !__builtin_isfinite(s0 + s1);
+    const bool bad = !__builtin_isfinite(s0 + s1) || m > kDivertMax;
     const float k = (m > 0.f && !bad) ? fminf(kFix * __builtin_amdgcn_rcpf(m), kMaxK) : 0.f;
     ik = bad ? __builtin_nanf("") : (k > 0.f ? __builtin_amdgcn_rcpf(k) : 0.f);
     const int off = 0x8080 - kMagicBits;
@@ -2066,7 +2077,6 @@ __device__ __forceinline__ bool stage_seg32(const float4 (&v)[8], uint32_t (&P)[
     }
     sx = s0 + s1;
     sy = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-    return bad || m > kDivertMax;
 }
 
 // lane i of every quad receives lane S of its quad
@@ -2096,8 +2106,6 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
     uint8_t *reg = lds + w * REG;
     const uint32_t reg0 = lds0 + w * REG;
     float *red = (float *)(lds + 8u * REG);                  // [kWaveRows][8 waves x 4 DPP rows]
-    // per-wave "x has a non-finite or huge segment" (see row_dot_f32)
-    __shared__ __align__(16) uint32_t dflags[kMaxWaves];
     QG_TL_WAVE_DECL;
     QG_TL_DECL;
     QG_TL(0);
@@ -2139,7 +2147,6 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
     const bool active = jj < CJ && w * CJ + jj < a.ni;
     const uint32_t it = jj < CJ ? jj : 0u;
     XP<4, 32> xs;
-    bool xdiv;
     {
         float4 v[8];
         const uint8_t *xl = reg + XROW * SLOT + 128u * (lane < 4u * CJ ? lane : 0u);
@@ -2147,7 +2154,7 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
         for (uint32_t k = 0; k < 8; k++) v[k] = *(const float4 *)(xl + 16u * ((k + lane) & 7u));
         uint32_t P[3][8];
         float ik, sx, sy;
-        xdiv = stage_seg32(v, P, ik, sx, sy);
+        stage_seg32(v, P, ik, sx, sy);
 #pragma unroll
         for (int c = 0; c < 3; c++)
 #pragma unroll
@@ -2208,23 +2215,23 @@ __global__ void __launch_bounds__(512) gemv_wave(StreamArgs a)
         if ((lane & 15u) >= 12u) red[(4u * s + r) * 32u + w * 4u + (lane >> 4)] = t;
         QG_TL(5u + 2u * s);
     }
-    divert_note(dflags, xdiv);
     lds_barrier();
     QG_TL(12);
-    const bool div = divert_any(dflags);
-    if (!div) {
-        // rows 2w and 2w + 1: their 32 partial sums one per lane, added by DPP
-        const uint32_t rr = 2u * w + (lane >> 5);
-        const float v = group_sum<32>(red[rr * 32u + (lane & 31u)]);
-        if ((lane & 31u) == 31u && blockIdx.x + rr * gridDim.x < a.rows) store_y(a.y + blockIdx.x + rr * gridDim.x, v);
-    }
-    if (div) {
-        // the workgroup's 16 rows in f32 instead (row_dot_f32), two per wave
-        for (uint32_t i = w; i < kWaveRows; i += 8u) {
-            const uint32_t row = blockIdx.x + i * gridDim.x;
-            if (row < a.rows) {
-                const float v = row_dot_f32<T_Q4_K, true>(a, row);
-                if (lane == 0u) a.y[row] = v;
+    // rows 2w and 2w + 1: their 32 partial sums one per lane, added by DPP.  A
+    // segment of x that is non-finite or above 2^64 has 1/k = NaN, and then
+    // every row sum of the workgroup is NaN: those rows are recomputed in f32
+    // (row_dot_f32), as are rows made NaN by non-finite weights
+    const uint32_t rr = 2u * w + (lane >> 5), row = blockIdx.x + rr * gridDim.x;
+    const float v = group_sum<32>(red[rr * 32u + (lane & 31u)]);
+    const bool mine = (lane & 31u) == 31u && row < a.rows;
+    if (__builtin_amdgcn_ballot_w64(mine && __builtin_isnan(v)) == 0) {
+        if (mine) store_y(a.y + row, v);
+    } else {
+        for (uint32_t i = 2u * w; i < 2u * w + 2u; i++) {
+            const uint32_t r2 = blockIdx.x + i * gridDim.x;
+            if (r2 < a.rows) {
+                const float f = row_dot_f32<T_Q4_K, true>(a, r2);
+                if (lane == 0u) a.y[r2] = f;
             }
         }
     }

@@ -136,17 +136,20 @@ BIG = [(12, 4096, 14336), (12, 3584, 18944), (13, 4096, 14336), (14, 4096, 14336
 
 @pytest.mark.parametrize("dtype,rows,cols", BIG, ids=[f"{NAMES[t]}-{r}x{c}" for t, r, c in BIG])
 def test_non_finite_x_every_kernel(ctx, oracle, synth, dtype, rows, cols):
-    """+inf and -inf in two segments (rows mix to NaN or keep one sign), then
-    a NaN, through the kernel each shape plans."""
+    """+inf and -inf in two segments (rows mix to NaN or keep one sign), a
+    NaN, then one element of 1e30 (finite, but past the fixed-point range:
+    the f32 path), through the kernel each shape plans."""
     raw = synth.gen_blocks(dtype, rows, cols, 7 + dtype + cols)
     m = ctx.upload(raw, dtype, rows, cols)
     kind = m.kernel_kind
-    for case in ("infs", "nan"):
+    for case in ("infs", "nan", "huge"):
         x = synth.gen_x(cols, 7 + cols)
         if case == "infs":
             x[cols // 3], x[cols // 3 + 97] = np.inf, -np.inf
-        else:
+        elif case == "nan":
             x[cols - 5] = np.nan
+        else:
+            x[cols // 2] = np.float32(1e30)
         y = np.zeros(rows, np.float32)
         m.matvec_host(x, y)
         ref = ref_mv(oracle, raw, dtype, rows, cols, x)
