@@ -137,11 +137,13 @@ int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
 // Batched prefill (qg_prefill.hip): tokens per chunk, supported matrix types,
 // and the launchers of its kernels (0 = launched, -1 = shape not supported,
-// -2 = launch failure).  x of every token as three bf16 pieces xp[c][t][i]
-// (c = 0..2, piece stride ntok * n) and records rec[(4 g + f) * 64 + t] per
-// 32-element segment g (f = 0: sum x, 1: sum x[0..16), 2: sum x[16..32)).
-// GEMM outputs are K-split: slice s of a result lives sstride floats after
-// slice 0, and its consumer sums the slices.
+// -2 = launch failure).  x of every token t scaled by a power of two 2^e_t,
+// xs = x 2^e_t, as two f16 pieces in xp (4 n kPfMaxTokens bytes: per
+// 128-element chunk the 32 KB image of the GEMM's LDS buffer, qgp::pf_xoff),
+// the sums of xs per 32-element segment g at rec[64 g + t] and
+// 2^-e_t at rec[64 (n / 32) + t] (rec holds 64 (n / 32 + 1) floats).  GEMM
+// matrices have cols % 128 == 0; outputs are K-split: slice s of a result
+// lives sstride floats after slice 0, and its consumer sums the slices.
 constexpr uint32_t kPfMaxTokens = 64;
 bool prefill_type_supported(uint32_t type);
 // one matrix of a grouped prefill GEMM: y[t * ldy + r] (+ s * sstride); w in
@@ -167,9 +169,10 @@ int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *x
 // x = sum of the na slices of a (nb of b); mode 0: x = a; 1: x =
 // rmsnorm(a + b) * nw (b may be NULL; sum_out, if not NULL, receives a + b
 // and must not alias a or b); 2: x = silu(a) * b.  Rows of lda floats.
+// work: kPfMaxTokens * (n + 128) floats of scratch.
 int launch_pf_planes(const float *a, uint32_t na, const float *b, uint32_t nb, size_t sstride, float *sum_out,
                      const float *nw, float eps, size_t n, size_t lda, int mode, uint16_t *xp, float *rec,
-                     uint32_t ntok, ihipStream_t *stream);
+                     float *work, uint32_t ntok, ihipStream_t *stream);
 // out[i] = sum of the ns slices of x[i], i < n
 int launch_pf_sum(const float *x, uint32_t ns, size_t sstride, size_t n, float *out, ihipStream_t *stream);
 int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *bq, const float *bk,

@@ -782,7 +782,7 @@ struct qg_model {
     float *pf_h[2] = {nullptr, nullptr}, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_ao2 = nullptr,
           *pf_g = nullptr, *pf_fo = nullptr, *pf_last = nullptr;
     uint16_t *pf_xp = nullptr;
-    float *pf_rec = nullptr;
+    float *pf_rec = nullptr, *pf_work = nullptr;
     uint32_t *pf_tok = nullptr;
     uint32_t pf_s_qkv = 1, pf_s_o = 1, pf_s_gu = 1, pf_s_down = 1;
     // captured graphs per attention mode: [0] the split attention
@@ -1280,7 +1280,7 @@ int put_step(qg_model *m, uint32_t token, uint32_t pos, uint32_t slot)
 
 // ---------------------------------------------------------- batched prefill
 
-// Every layer matrix on the MFMA path: supported type, cols % 32 == 0; and
+// Every layer matrix on the MFMA path: supported type, cols % 128 == 0; and
 // the prefill attention's scores fit its LDS.
 bool pf_supported(const qg_model *m)
 {
@@ -1288,7 +1288,7 @@ bool pf_supported(const qg_model *m)
     if ((m->hd + (size_t)m->cfg.max_seq_len) * sizeof(float) > 65536) return false;
     for (int s = 0; s < kSlots; s++)
         for (const qg_mat *p : m->w[s])
-            if (!p || !qg::prefill_type_supported(p->type) || p->cols % 32 != 0) return false;
+            if (!p || !qg::prefill_type_supported(p->type) || p->cols % 128 != 0) return false;
     return true;
 }
 
@@ -1309,14 +1309,15 @@ int pf_alloc(qg_model *m)
         (rc = dalloc(m, &m->pf_qkv, m->pf_s_qkv * T * ldq)) || (rc = dalloc(m, &m->pf_ao, T * m->q_dim)) ||
         (rc = dalloc(m, &m->pf_ao2, m->pf_s_o * T * E)) || (rc = dalloc(m, &m->pf_g, m->pf_s_gu * T * 2 * H)) ||
         (rc = dalloc(m, &m->pf_fo, m->pf_s_down * T * E)) || (rc = dalloc(m, &m->pf_last, E)) ||
-        (rc = dalloc(m, &m->pf_xp, 3 * T * kmax)) || (rc = dalloc(m, &m->pf_rec, T * (kmax / 32) * 4)) ||
+        (rc = dalloc(m, &m->pf_xp, 2 * T * kmax)) || (rc = dalloc(m, &m->pf_rec, T * (kmax / 32 + 1))) ||
+        (rc = dalloc(m, &m->pf_work, T * (kmax + 128))) ||
         (rc = dalloc(m, &m->pf_tok, (size_t)m->cfg.max_seq_len)))
         return rc;
     return QG_OK;
 }
 
 // y[t][0..rows) (row stride ldy, slices of T * ldy floats) = mat . x_t for the
-// chunk's tokens and 1..3 matrices over the same x, given as the bf16 pieces
+// chunk's tokens and 1..3 matrices over the same x, given as the f16 pieces
 // of the last pf_planes call over `cols` elements
 int pf_gemm(qg_model *m, const qg::PfMat *mats, int n, size_t cols, uint32_t ntok, uint32_t ldy, uint32_t slices)
 {
@@ -1333,13 +1334,14 @@ qg::PfMat pf_mat(const qg_mat *mat, float *y)
     return qg::PfMat{mat->type, mat->d_rp, mat->rows, y, true, mat->plan.g, mat->plan.ni, (size_t)mat->plan.group_bytes};
 }
 
-// bf16 pieces of x = f(a, b) for the chunk's tokens; a and b of na / nb slices
+// f16 pieces of x = f(a, b) for the chunk's tokens (scaled per token); a and b of na / nb slices
 // kPfMaxTokens * lda floats apart
 int pf_planes(qg_model *m, const float *a, uint32_t na, const float *b, uint32_t nb, float *sum_out, const float *nw,
               size_t n, size_t lda, int mode, uint32_t ntok)
 {
     const int r = qg::launch_pf_planes(a, na, b, nb, (size_t)qg::kPfMaxTokens * lda, sum_out, nw, m->cfg.norm_eps, n,
-                                       lda, mode, m->pf_xp, m->pf_rec, ntok, (ihipStream_t *)m->ctx->stream);
+                                       lda, mode, m->pf_xp, m->pf_rec, m->pf_work, ntok,
+                                       (ihipStream_t *)m->ctx->stream);
     return r ? mfail(m, QG_ERR_HIP, "prefill planes launch", hipGetLastError()) : QG_OK;
 }
 

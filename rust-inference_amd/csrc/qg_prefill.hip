@@ -6,25 +6,30 @@
 // Transformer::forward per token).  Here every projection of a chunk of up
 // to kPfMaxTokens tokens is one GEMM on the matrix cores:
 //
-//   * pf_planes_k: each token's input vector (RMSNorm of the residual stream,
-//     the attention output, or silu(g) * u) split into three bf16 pieces
-//     x = hi + mid + lo (each the rounding of what the previous ones leave,
-//     so the three carry x to f32 precision), written as xp[c][t][i], plus
-//     per 32-element segment the sums of x over its halves;
-//   * pf_gemm_k: y[t][r] = sum over the row's 32-element sub-blocks of
-//     mul * (sum q x) + add * (sum x), with sum q x from three chained
-//     v_mfma_f32_16x16x32_bf16 (A: 16 tokens x 32 elements of one piece, B:
-//     32 codes x 16 rows as bf16 -- every code of the supported types is an
-//     integer of at most 8 bits, exact in bf16; the products are exact in
-//     f32, accumulated in f32), the weight scales applied per sub-block in
-//     f32;
+//   * pf_stat_k, pf_split_k: each token's input vector x (RMSNorm of the residual
+//     stream, the attention output, or silu(g) * u) scaled by a power of two
+//     2^e (its largest magnitude into [512, 1024)) and split into two f16
+//     pieces xs = x 2^e = hi + lo (hi the rounding of xs, lo the rounding of
+//     what hi leaves: 22 significant bits together), written chunk by chunk
+//     in the layout of the GEMM's LDS buffers; per 32-element segment the
+//     f32 sum of xs; per token 2^-e;
+//   * pf_gemm_k: y[t][r] = 2^-e (sum over blocks of d D + sum over
+//     sub-blocks of -dmin m S) with D = sum over the block's elements of
+//     xs B from chained v_mfma_f32_16x16x32_f16 (A: 16 tokens x 32 elements
+//     of one piece, B: 32 weights x 16 rows).  B holds integers that f16
+//     represents exactly -- sc q for Q4_K / Q5_K (at most 63 * 31), the two
+//     parts 16 a q' and b q' of sc q' (sc = 16 a + b) for Q6_K, q for Q8_0
+//     -- so every product is exact and accumulates in f32; the block scale
+//     d multiplies D once per block (per sub-block for Q8_0) and the
+//     K-quant min terms are one v_mfma_f32_16x16x4f32 per 4 sub-blocks
+//     (A: S, the sums of xs, B: -dmin m in f32);
 //   * pf_qkv_post_k, pf_attention_k: bias, RoPE and KV append of every token
 //     (attention.rs:66-90), causal attention of every token over the cache up
 //     to its own slot (attention.rs:93-121), as the decode path.
 //
-// MFMA operand layout (v_mfma_f32_16x16x32_bf16, checked on gfx950): lane l
-// holds A[l % 16][8 (l/16) .. +8), B[8 (l/16) .. +8)[l % 16] and
-// D[4 (l/16) + i][l % 16], i = 0..3.
+// MFMA operand layout (v_mfma_f32_16x16x32_f16 and _bf16, checked on
+// gfx950): lane l holds A[l % 16][8 (l/16) .. +8), B[8 (l/16) .. +8)[l % 16]
+// and D[4 (l/16) + i][l % 16], i = 0..3.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -39,7 +44,8 @@ using qg::T_Q5_K;
 using qg::T_Q6_K;
 using qg::T_Q8_0;
 
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float h2f(uint32_t h16)
@@ -58,171 +64,207 @@ __device__ __forceinline__ uint32_t abyte(uint32_t b, uint32_t a, uint32_t s)
     return __builtin_amdgcn_alignbyte(b, a, s);
 }
 
-// quant.rs:606-615: scale and min of sub-block j (0..7) from the 12-byte pack
-// held in the dwords q0, q1, q2, without branches on j (a lane-varying value
-// when rows straddle blocks)
-__device__ __forceinline__ void k4sm(uint32_t j, uint32_t q0, uint32_t q1, uint32_t q2, float &sc, float &m)
+// quant.rs:606-615 for the four sub-blocks jb .. jb + 3 (jb = 0 or 4; it may
+// differ between lanes) at once: byte i of sc4 / m4 is the scale / min of
+// sub-block jb + i, from the 12-byte pack held in the dwords q0, q1, q2
+// (j < 4: q[j] & 63, q[j+4] & 63; j >= 4: (q[j+4] & 15) | (q[j-4] >> 6) << 4,
+// (q[j+4] >> 4) | (q[j] >> 6) << 4), without branches
+__device__ __forceinline__ void k4sm4(uint32_t jb, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t &sc4,
+                                      uint32_t &m4)
 {
-    const uint32_t s = 8u * (j & 3u);
-    const uint32_t A = (q0 >> s) & 0xFFu, B = (q1 >> s) & 0xFFu, C = (q2 >> s) & 0xFFu;   // q[j%4], q[j%4+4], q[j%4+8]
-    const bool lo = j < 4u;
-    sc = (float)(lo ? (A & 63u) : ((C & 0xFu) | ((A >> 6) << 4)));
-    m = (float)(lo ? (B & 63u) : ((C >> 4) | ((B >> 6) << 4)));
+    const uint32_t lo = 0u - (uint32_t)(jb < 4u);
+    sc4 = (q0 & 0x3F3F3F3Fu & lo) | (((q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u)) & ~lo);
+    m4 = (q1 & 0x3F3F3F3Fu & lo) | ((((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u)) & ~lo);
 }
 
-// bf16 of 1 + q / 2^b for the four b-bit codes in the bytes of c (q < 2^b,
-// b <= 7): the exponent of 1 and q as the top b bits of the 7-bit mantissa,
-// exact.  Two dwords of two bf16 each.
-template <int B>
-__device__ __forceinline__ void biased_bf16(uint32_t c, uint32_t &r0, uint32_t &r1)
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u(h2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// the f16 pairs 1024 + c of the byte codes of c: bytes 0, 1 and bytes 2, 3
+// (1024 + c for c < 1024 is the f16 with bits 0x6400 | c)
+__device__ __forceinline__ h2 mag_lo(uint32_t c) { return as_h2(__builtin_amdgcn_perm(0x64646464u, c, 0x04010400u)); }
+__device__ __forceinline__ h2 mag_hi(uint32_t c) { return as_h2(__builtin_amdgcn_perm(0x64646464u, c, 0x04030402u)); }
+
+// the f16 pair (v, v) of an integer |v| <= 2048 (exact)
+__device__ __forceinline__ h2 hpair(int v)
 {
-    const uint32_t t = (c << (7 - B)) | 0x80808080u;                   // low byte of each bf16
-    r0 = __builtin_amdgcn_perm(0x3F3F3F3Fu, t, 0x04010400u);           // [t0, 3F, t1, 3F]
-    r1 = __builtin_amdgcn_perm(0x3F3F3F3Fu, t, 0x04030402u);           // [t2, 3F, t3, 3F]
+    const _Float16 f = (_Float16)(int16_t)v;
+    return h2{f, f};
 }
 
-// 8 signed byte codes as bf16 (exact: f32 conversion, top half)
-__device__ __forceinline__ uint4 signed_bf16(uint32_t c0, uint32_t c1)
+// sc q for the 8 codes in the bytes of c0, c1 (q < 256, sc q <= 2048): one
+// fused (1024 + q) sc - 1024 sc per pair, exact since the result is
+__device__ __forceinline__ uint4 scaled_codes(uint32_t c0, uint32_t c1, h2 s, h2 o)
 {
-    uint32_t r[4];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const uint32_t c = h ? c1 : c0;
-        float f[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) f[i] = (float)(int8_t)((c >> (8 * i)) & 0xFFu);
-        r[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
-        r[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u);
-    }
-    return make_uint4(r[0], r[1], r[2], r[3]);
+    return make_uint4(as_u(__builtin_elementwise_fma(mag_lo(c0), s, o)),
+                      as_u(__builtin_elementwise_fma(mag_hi(c0), s, o)),
+                      as_u(__builtin_elementwise_fma(mag_lo(c1), s, o)),
+                      as_u(__builtin_elementwise_fma(mag_hi(c1), s, o)));
 }
 
-// B operands of the K-quant codes: the MFMA over 32 x with B = 1 + q / 2^b
-// gives D' = sum x + (sum q x) / 2^b, so sum q x = 2^b (D' - sum x) and a
-// sub-block's mul * (sum q x) + add * (sum x) = mul' D' + add' (sum x) with
-// mul' = 2^b mul, add' = add - mul'.  (Masked codes -- the other half of a
-// Q6_K sub-block -- are B = 0.)
-template <int B>
-__device__ __forceinline__ uint4 kquant_b(uint32_t c0, uint32_t c1, bool keep)
+// A K-quant sub-block's B operand from its 8 codes (bytes of c0, c1) and the
+// scale in byte kk of sc4 (the f16 pair (sc, sc) as 1024 + sc - 1024)
+__device__ __forceinline__ uint4 kquant_b(uint32_t c0, uint32_t c1, uint32_t sc4, uint32_t kk)
 {
-    uint4 r;
-    biased_bf16<B>(c0, r.x, r.y);
-    biased_bf16<B>(c1, r.z, r.w);
-    return keep ? r : make_uint4(0u, 0u, 0u, 0u);
+    const h2 s = as_h2(__builtin_amdgcn_perm(0x64646464u, sc4, 0x04000400u | (kk * 0x00010001u))) -
+                 h2{1024.0f16, 1024.0f16};
+    return scaled_codes(c0, c1, s, s * h2{-1024.0f16, -1024.0f16});
 }
 
-// Per-type access to one 32-element sub-block (sub-block j of the block at
-// blk; rows hold whole sub-blocks since cols % 32 == 0), in two steps so that
-// the loads can be issued a chunk ahead:
-//   load(blk, j, kq): the raw dwords the lane needs (every byte read lies in
-//     the matrix or its tail pad);
-//   decode(raw, j, kq, b, mul, add): b[h] = the B operand (codes 8 kq ..
-//     8 kq + 7 as bf16) of set h, and the sub-block's contribution is sum
-//     over sets of mul_h * D_h + add_h * (sum x over the set), D_h the MFMA
-//     result;
-//   NSET = 1 when one scale covers all 32 codes, 2 for Q6_K's 16-code
-//   sub-blocks (h = 0 codes 0..15, h = 1 codes 16..31); SUMS: add is used.
-template <uint32_t T> struct PfW;
+// -dmin m of the chunk's sub-block kq (byte kq of m4), dmin the high half of dd
+__device__ __forceinline__ float kquant_min(uint32_t dd, uint32_t m4, uint32_t kq)
+{
+    return -(h2f(dd >> 16) * (float)((m4 >> (8u * kq)) & 0xFFu));
+}
+
+// Q6_K: codes q (6 bits) of c0, c1 as q' = q - 32, times the two parts of
+// the signed scale sc = 16 a + b (a = sc >> 4, 0 <= b < 16): B1 = 16 a q'
+// (a multiple of 16 of magnitude <= 4096 with at most 9 significant bits)
+// and B2 = b q' (<= 480), each exact; B1 + B2 = sc q'
+__device__ __forceinline__ void q6_b(uint32_t c0, uint32_t c1, int sc, uint4 &b1, uint4 &b2)
+{
+    const h2 A = hpair(16 * (sc >> 4)), B = hpair(sc & 15);
+    const h2 off = h2{-1056.0f16, -1056.0f16};
+    const h2 q0 = mag_lo(c0) + off, q1 = mag_hi(c0) + off, q2 = mag_lo(c1) + off, q3 = mag_hi(c1) + off;
+    b1 = make_uint4(as_u(q0 * A), as_u(q1 * A), as_u(q2 * A), as_u(q3 * A));
+    b2 = make_uint4(as_u(q0 * B), as_u(q1 * B), as_u(q2 * B), as_u(q3 * B));
+}
+
+// Q8_0: 8 signed byte codes as f16 (1024 + (q + 128) - 1152, exact)
+__device__ __forceinline__ uint4 q8_b(uint32_t c0, uint32_t c1)
+{
+    const h2 off = h2{-1152.0f16, -1152.0f16};
+    c0 ^= 0x80808080u;
+    c1 ^= 0x80808080u;
+    return make_uint4(as_u(mag_lo(c0) + off), as_u(mag_hi(c0) + off), as_u(mag_lo(c1) + off),
+                      as_u(mag_hi(c1) + off));
+}
+
+// Per-type access to a chunk of 4 sub-blocks that lies inside one block
+// (sub-blocks jb .. jb + 3 of it, jb = 0 or 4; for Q8_0, whose blocks are
+// single sub-blocks, 4 consecutive blocks).  The lane (kq = lane / 16) needs
+// codes 8 kq .. 8 kq + 7 of each sub-block, for the row of its column.
+//   load(blk, jb, kq) / load_rp(G, b, jb, kq, ni): the raw dwords, from the
+//     GGUF block at blk (every byte read lies in the matrix or its tail pad)
+//     or from block b of the repacked row group G (ni items);
+//   decode(c, jb, kk, kq, bq): the B operands of sub-block kk of the chunk;
+//   dscale(c, kk): the scale that multiplies D (per block; per sub-block
+//     for Q8_0);
+//   bmin(c, jb, kq): -dmin m of sub-block kq of the chunk (MIN types).
+// NB: B operands per sub-block.
+template <uint32_t T> struct PfH;
 
 // Q4_K (quant.rs:210-228): 8 sub-blocks per 144-byte block; sub-block j is
 // the low (j even) or high (j odd) nibbles of qs[32 (j/2) .. +32); the value
-// is d * sc * q - dmin * m.
-template <> struct PfW<T_Q4_K> {
-    static constexpr int NSET = 1;
-    static constexpr bool SUMS = true;
-    struct Raw {
-        uint4 head;
-        uint2 v;
-    };
+// is d sc q - dmin m.
+template <> struct PfH<T_Q4_K> {
+    static constexpr int NB = 1;
+    static constexpr bool MIN = true;
     static constexpr uint32_t BB = 144;
-    __device__ static Raw load(const uint8_t *b, uint32_t j, uint32_t kq)
+    struct C {
+        uint4 h;            // d, dmin, the 12 scale bytes
+        uint2 v0, v1;       // the lane's code bytes of sub-block pairs jb/2 and jb/2 + 1
+    };
+    using CR = C;
+    __device__ static C load(const uint8_t *blk, uint32_t jb, uint32_t kq)
     {
-        return Raw{*(const uint4 *)b, *(const uint2 *)(b + 16u + 32u * (j >> 1) + 8u * kq)};
+        const uint8_t *q = blk + 16u + 16u * jb + 8u * kq;
+        return C{*(const uint4 *)blk, *(const uint2 *)q, *(const uint2 *)(q + 32u)};
     }
-    __device__ static void decode(const Raw &r, uint32_t j, uint32_t, uint4 (&bq)[2], float (&mul)[2],
-                                  float (&add)[2])
+    // repack_k's row group: the ni/2 block heads, then piece k' (16 bytes)
+    // of item it at 8 ni + (k' ni + it) 16; item it = the quant bytes
+    // 64 (it & 1) .. +64 of block it / 2
+    __device__ static CR load_rp(const uint8_t *G, uint32_t b, uint32_t jb, uint32_t kq, uint32_t ni)
     {
-        const uint32_t sh = (j & 1u) * 4u;
-        bq[0] = kquant_b<4>((r.v.x >> sh) & 0x0F0F0F0Fu, (r.v.y >> sh) & 0x0F0F0F0Fu, true);
-        float sc, m;
-        k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
-        mul[0] = 16.0f * (h2f(r.head.x) * sc);
-        add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
+        const uint8_t *q = G + 8u * ni + (size_t)(((kq >> 1) * ni + 2u * b + (jb >> 2)) << 4) + 8u * (kq & 1u);
+        return C{*(const uint4 *)(G + 16u * b), *(const uint2 *)q, *(const uint2 *)(q + 32u * ni)};
     }
-    // the repacked row group G (the library's repack_k layout: the nb = ni/2
-    // block heads, then piece k' (16 bytes) of item it at 16 nb + (k' ni + it)
-    // 16; item it = the quant bytes 64 (it & 1) .. +64 of block it / 2): the
-    // same registers as load
-    using RawR = Raw;
-    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t j, uint32_t kq, uint32_t ni)
+    __device__ static void decode(const C &c, uint32_t jb, uint32_t kk, uint32_t, uint4 (&bq)[NB])
     {
-        const uint32_t it = 2u * b + (j >> 2), kp = 2u * ((j >> 1) & 1u) + (kq >> 1);
-        return Raw{*(const uint4 *)(G + 16u * b), *(const uint2 *)(G + 8u * ni + (kp * ni + it) * 16u + 8u * (kq & 1u))};
+        const uint2 v = kk < 2u ? c.v0 : c.v1;
+        const uint32_t sh = 4u * (kk & 1u);
+        uint32_t sc4, m4;
+        k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
+        bq[0] = kquant_b((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu, sc4, kk);
     }
-    __device__ static void decode_rp(const RawR &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
-                                     float (&add)[2])
+    __device__ static void decode_rp(const CR &c, uint32_t jb, uint32_t kk, uint32_t kq, uint4 (&bq)[NB])
     {
-        decode(r, j, kq, bq, mul, add);
+        decode(c, jb, kk, kq, bq);
+    }
+    __device__ static float dscale(const C &c, uint32_t) { return h2f(c.h.x); }
+    __device__ static float bmin(const C &c, uint32_t jb, uint32_t kq)
+    {
+        uint32_t sc4, m4;
+        k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
+        return kquant_min(c.h.x, m4, kq);
     }
 };
 
 // Q5_K (quant.rs:231-262): as Q4_K with a fifth bit, bit j of qh[l].
-template <> struct PfW<T_Q5_K> {
-    static constexpr int NSET = 1;
-    static constexpr bool SUMS = true;
-    struct Raw {
-        uint4 head;
-        uint2 v, h;
-    };
+template <> struct PfH<T_Q5_K> {
+    static constexpr int NB = 1;
+    static constexpr bool MIN = true;
     static constexpr uint32_t BB = 176;
-    __device__ static Raw load(const uint8_t *b, uint32_t j, uint32_t kq)
-    {
-        return Raw{*(const uint4 *)b, *(const uint2 *)(b + 48u + 32u * (j >> 1) + 8u * kq),
-                   *(const uint2 *)(b + 16u + 8u * kq)};
-    }
-    __device__ static void decode(const Raw &r, uint32_t j, uint32_t, uint4 (&bq)[2], float (&mul)[2],
-                                  float (&add)[2])
-    {
-        const uint32_t sh = (j & 1u) * 4u;
-        const uint32_t c0 = ((r.v.x >> sh) & 0x0F0F0F0Fu) | (((r.h.x >> j) & 0x01010101u) << 4);
-        const uint32_t c1 = ((r.v.y >> sh) & 0x0F0F0F0Fu) | (((r.h.y >> j) & 0x01010101u) << 4);
-        bq[0] = kquant_b<5>(c0, c1, true);
-        float sc, m;
-        k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
-        mul[0] = 32.0f * (h2f(r.head.x) * sc);
-        add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
-    }
-    // the repacked row group G (repack_k: the nb = ni/4 block heads, piece k'
-    // of item it's 32 quant bytes at 16 nb + (k' ni + it) 16, then 8 bytes per
-    // item at 16 nb + 32 ni + 8 it: bits 8 bb + 2 t' + q of word w are bit
-    // 2 (it & 3) + q of qh[16 w + 4 t' + bb]; item it = block it / 4, sub-blocks
-    // 2 (it & 3) and 2 (it & 3) + 1)
-    struct RawR {
-        uint4 head;
-        uint2 v;
-        uint32_t w;
+    struct C {
+        uint4 h;
+        uint2 v0, v1;       // as Q4_K (qs at 48)
+        uint2 qh;           // qh[8 kq .. +8]
     };
-    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t j, uint32_t kq, uint32_t ni)
+    __device__ static C load(const uint8_t *blk, uint32_t jb, uint32_t kq)
     {
-        const uint32_t it = 4u * b + (j >> 1), H = 4u * ni;             // 16 nb
-        return RawR{*(const uint4 *)(G + 16u * b),
-                    *(const uint2 *)(G + H + ((kq >> 1) * ni + it) * 16u + 8u * (kq & 1u)),
-                    *(const uint32_t *)(G + H + 32u * ni + 8u * it + 4u * (kq >> 1))};
+        const uint8_t *q = blk + 48u + 16u * jb + 8u * kq;
+        return C{*(const uint4 *)blk, *(const uint2 *)q, *(const uint2 *)(q + 32u),
+                 *(const uint2 *)(blk + 16u + 8u * kq)};
     }
-    __device__ static void decode_rp(const RawR &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
-                                     float (&add)[2])
+    __device__ static void decode(const C &c, uint32_t jb, uint32_t kk, uint32_t, uint4 (&bq)[NB])
+    {
+        const uint2 v = kk < 2u ? c.v0 : c.v1;
+        const uint32_t sh = 4u * (kk & 1u), j = jb + kk;
+        const uint32_t c0 = ((v.x >> sh) & 0x0F0F0F0Fu) | (((c.qh.x >> j) & 0x01010101u) << 4);
+        const uint32_t c1 = ((v.y >> sh) & 0x0F0F0F0Fu) | (((c.qh.y >> j) & 0x01010101u) << 4);
+        uint32_t sc4, m4;
+        k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
+        bq[0] = kquant_b(c0, c1, sc4, kk);
+    }
+    // repack_k's row group: the ni/4 block heads, piece k' of item it's 32
+    // quant bytes at 16 (ni/4) + (k' ni + it) 16, then 8 bytes per item at
+    // 4 ni + 32 ni + 8 it: bits 8 bb + 2 t' + q of word w are bit
+    // 2 (it & 3) + q of qh[16 w + 4 t' + bb]; item it = block it / 4,
+    // sub-blocks 2 (it & 3) and 2 (it & 3) + 1
+    struct CR {
+        uint4 h;
+        uint2 v0, v1;       // items 4 b + jb/2 and the next
+        uint32_t w0, w1;
+    };
+    __device__ static CR load_rp(const uint8_t *G, uint32_t b, uint32_t jb, uint32_t kq, uint32_t ni)
+    {
+        const uint32_t it = 4u * b + (jb >> 1), H = 4u * ni;
+        const uint8_t *q = G + H + (size_t)(((kq >> 1) * ni + it) << 4) + 8u * (kq & 1u);
+        const uint8_t *w = G + H + 32u * ni + 8u * it + 4u * (kq >> 1);
+        return CR{*(const uint4 *)(G + 16u * b), *(const uint2 *)q, *(const uint2 *)(q + 16u),
+                  *(const uint32_t *)w, *(const uint32_t *)(w + 8u)};
+    }
+    __device__ static void decode_rp(const CR &c, uint32_t jb, uint32_t kk, uint32_t kq, uint4 (&bq)[NB])
     {
         // code 8 kq + e: qh byte 16 w + 4 t' + bb with w = kq / 2, t' =
         // 2 (kq & 1) + e / 4, bb = e % 4, so its bit j sits at 8 (e % 4) + s
         // (+ 2 for e >= 4), s = 4 (kq & 1) + (j & 1)
-        const uint32_t sh = (j & 1u) * 4u, s = 4u * (kq & 1u) + (j & 1u);
-        const uint32_t c0 = ((r.v.x >> sh) & 0x0F0F0F0Fu) | (((r.w >> s) & 0x01010101u) << 4);
-        const uint32_t c1 = ((r.v.y >> sh) & 0x0F0F0F0Fu) | (((r.w >> (s + 2u)) & 0x01010101u) << 4);
-        bq[0] = kquant_b<5>(c0, c1, true);
-        float sc, m;
-        k4sm(j, r.head.y, r.head.z, r.head.w, sc, m);
-        mul[0] = 32.0f * (h2f(r.head.x) * sc);
-        add[0] = -(h2f(r.head.x >> 16) * m) - mul[0];
+        const uint2 v = kk < 2u ? c.v0 : c.v1;
+        const uint32_t w = kk < 2u ? c.w0 : c.w1;
+        const uint32_t sh = 4u * (kk & 1u), s = 4u * (kq & 1u) + (kk & 1u);
+        const uint32_t c0 = ((v.x >> sh) & 0x0F0F0F0Fu) | (((w >> s) & 0x01010101u) << 4);
+        const uint32_t c1 = ((v.y >> sh) & 0x0F0F0F0Fu) | (((w >> (s + 2u)) & 0x01010101u) << 4);
+        uint32_t sc4, m4;
+        k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
+        bq[0] = kquant_b(c0, c1, sc4, kk);
+    }
+    __device__ static float dscale(const C &c, uint32_t) { return h2f(c.h.x); }
+    __device__ static float dscale(const CR &c, uint32_t) { return h2f(c.h.x); }
+    template <class X> __device__ static float bmin(const X &c, uint32_t jb, uint32_t kq)
+    {
+        uint32_t sc4, m4;
+        k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
+        return kquant_min(c.h.x, m4, kq);
     }
 };
 
@@ -230,152 +272,149 @@ template <> struct PfW<T_Q5_K> {
 // elements; within a half, sub-block k4 (32 elements, l = 0..31) takes the
 // low (k4 < 2) or high nibbles of ql[64 n + 32 (k4 & 1) + l], bits 2 k4 of
 // qh[32 n + l], and scale sc[8 n + l/16 + 2 k4]; the value is
-// d * sc * (q - 32).  Reads stay inside the block but for the dword holding
-// d, which can end 2 bytes past the last block (inside the buffer's tail pad).
-template <> struct PfW<T_Q6_K> {
-    static constexpr int NSET = 2;
-    static constexpr bool SUMS = true;
-    struct Raw {
-        uint32_t ql[3], qh[3], s, d, sb;
-    };
+// d sc (q - 32).  A chunk is one half (n = jb / 4).  Reads stay inside the
+// block but for the dwords holding d and the last scales, which can end up
+// to 3 bytes past the last block (inside the buffer's tail pad).
+template <> struct PfH<T_Q6_K> {
+    static constexpr int NB = 2;
+    static constexpr bool MIN = false;
     static constexpr uint32_t BB = 210;
-    __device__ static Raw load(const uint8_t *b, uint32_t j, uint32_t kq)
+    struct C {
+        uint32_t l0[3], l1[3], qh[3], s[3], d, sb;
+    };
+    __device__ static C load(const uint8_t *blk, uint32_t jb, uint32_t kq)
     {
-        const uint32_t n = j >> 2, k4 = j & 3u;
-        const uint32_t *pl = adown(b + 64u * n + 32u * (k4 & 1u) + 8u * kq);
-        const uint32_t *ph = adown(b + 128u + 32u * n + 8u * kq);
-        Raw r;
-        r.ql[0] = pl[0];
-        r.ql[1] = pl[1];
-        r.ql[2] = pl[2];
-        r.qh[0] = ph[0];
-        r.qh[1] = ph[1];
-        r.qh[2] = ph[2];
-        r.s = *adown(b + 192u + 8u * n + 2u * k4);
-        r.d = *adown(b + 208u);
-        r.sb = (uint32_t)((uintptr_t)b & 3u);
-        return r;
+        const uint32_t n = jb >> 2;
+        const uint32_t *p0 = adown(blk + 64u * n + 8u * kq), *p1 = adown(blk + 64u * n + 32u + 8u * kq);
+        const uint32_t *ph = adown(blk + 128u + 32u * n + 8u * kq), *ps = adown(blk + 192u + 8u * n + (kq >> 1));
+        C c;
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            c.l0[i] = p0[i];
+            c.l1[i] = p1[i];
+            c.qh[i] = ph[i];
+            c.s[i] = ps[i];
+        }
+        c.d = *adown(blk + 208u);
+        c.sb = (uint32_t)((uintptr_t)blk & 3u);
+        return c;
     }
-    __device__ static void decode(const Raw &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
-                                  float (&add)[2])
+    __device__ static void decode(const C &c, uint32_t, uint32_t kk, uint32_t kq, uint4 (&bq)[NB])
     {
-        // w is 4-byte aligned: the block starts at byte sb = 0 or 2 of a dword;
-        // ql, qh and d at offsets 0 mod 4 from it, the scale pair at 2 k4
-        const uint32_t sb = r.sb, k4 = j & 3u, ss = (sb + 2u * k4) & 3u;
-        const uint32_t sl = (k4 >> 1) * 4u, shh = 2u * k4;
-        const uint32_t L0 = abyte(r.ql[1], r.ql[0], sb), L1 = abyte(r.ql[2], r.ql[1], sb);
-        const uint32_t H0 = abyte(r.qh[1], r.qh[0], sb), H1 = abyte(r.qh[2], r.qh[1], sb);
+        // the block starts at byte sb = 0 or 2 of a dword: ql and qh at
+        // offsets 0 mod 4 from it; the scale window at sb + kq/2
+        const uint32_t sb = c.sb, sl = (kk >> 1) * 4u, shh = 2u * kk;
+        const uint32_t *L = (kk & 1u) ? c.l1 : c.l0;
+        const uint32_t L0 = abyte(L[1], L[0], sb), L1 = abyte(L[2], L[1], sb);
+        const uint32_t H0 = abyte(c.qh[1], c.qh[0], sb), H1 = abyte(c.qh[2], c.qh[1], sb);
         const uint32_t c0 = ((L0 >> sl) & 0x0F0F0F0Fu) | (((H0 >> shh) & 0x03030303u) << 4);
         const uint32_t c1 = ((L1 >> sl) & 0x0F0F0F0Fu) | (((H1 >> shh) & 0x03030303u) << 4);
-        const bool lo = kq < 2u;                                      // codes 0..15 of the sub-block
-        bq[0] = kquant_b<6>(c0, c1, lo);
-        bq[1] = kquant_b<6>(c0, c1, !lo);
-        const uint32_t s = r.s >> (8 * ss), dd = r.d >> (8 * sb);   // sc[8n + 2k4], sc[8n + 2k4 + 1]; d
-        const float d = h2f(dd);
-        const float m0 = d * (float)(int8_t)(s & 0xFFu), m1 = d * (float)(int8_t)((s >> 8) & 0xFFu);
-        mul[0] = 64.0f * m0;
-        mul[1] = 64.0f * m1;
-        add[0] = -32.0f * m0 - mul[0];
-        add[1] = -32.0f * m1 - mul[1];
+        const uint32_t so = (sb + (kq >> 1)) & 3u;
+        const uint32_t W = kk < 2u ? abyte(c.s[1], c.s[0], so) : abyte(c.s[2], c.s[1], so);
+        const int sc = (int)(int8_t)((W >> (16u * (kk & 1u))) & 0xFFu);     // sc[8n + kq/2 + 2 kk]
+        q6_b(c0, c1, sc, bq[0], bq[1]);
     }
-    // the repacked row group G (repack_k: item it = block it/4, half
-    // n = (it/2) & 1, i = it & 1 -- l in 16 i .. 16 i + 15 of the half;
-    // ql[64n+16i..+16] at 16 it, ql[64n+32+16i..+16] at 16 (ni + it),
-    // qh[32n+16i..+16] at 16 (2 ni + it), sc[8n+i+2k] at 48 ni + 4 it + k, d
-    // at 52 ni + 2 b)
-    struct RawR {
-        uint2 ql, qh, sc;
-        uint32_t d;
+    __device__ static float dscale(const C &c, uint32_t) { return h2f(c.d >> (8u * c.sb)); }
+    // repack_k's row group: item it = block it/4, half n = (it/2) & 1,
+    // i = it & 1 -- l in 16 i .. 16 i + 15 of the half; ql[64n+16i..+16] at
+    // 16 it, ql[64n+32+16i..+16] at 16 (ni + it), qh[32n+16i..+16] at
+    // 16 (2 ni + it), sc[8n+i+2k] at 48 ni + 4 it + k, d at 52 ni + 2 b
+    struct CR {
+        uint2 la, lb, qh;
+        uint32_t sc, d;
     };
-    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t j, uint32_t kq, uint32_t ni)
+    __device__ static CR load_rp(const uint8_t *G, uint32_t b, uint32_t jb, uint32_t kq, uint32_t ni)
     {
-        const uint32_t n = j >> 2, k4 = j & 3u, it0 = 4u * b + 2u * n, it = it0 + (kq >> 1);
-        return RawR{*(const uint2 *)(G + ((k4 & 1u) * ni + it) * 16u + 8u * (kq & 1u)),
-                    *(const uint2 *)(G + (2u * ni + it) * 16u + 8u * (kq & 1u)),
-                    *(const uint2 *)(G + 48u * ni + 4u * it0),          // scales of items it0, it0 + 1
-                    (uint32_t)*(const uint16_t *)(G + 52u * ni + 2u * b)};
+        const uint32_t it = 4u * b + 2u * (jb >> 2) + (kq >> 1), o = 8u * (kq & 1u);
+        return CR{*(const uint2 *)(G + 16u * it + o), *(const uint2 *)(G + 16u * (ni + it) + o),
+                  *(const uint2 *)(G + 16u * (2u * ni + it) + o), *(const uint32_t *)(G + 48u * ni + 4u * it),
+                  (uint32_t)*(const uint16_t *)(G + 52u * ni + 2u * b)};
     }
-    __device__ static void decode_rp(const RawR &r, uint32_t j, uint32_t kq, uint4 (&bq)[2], float (&mul)[2],
-                                     float (&add)[2])
+    __device__ static void decode_rp(const CR &c, uint32_t, uint32_t kk, uint32_t, uint4 (&bq)[NB])
     {
-        const uint32_t k4 = j & 3u, sl = (k4 >> 1) * 4u, shh = 2u * k4;
-        const uint32_t c0 = ((r.ql.x >> sl) & 0x0F0F0F0Fu) | (((r.qh.x >> shh) & 0x03030303u) << 4);
-        const uint32_t c1 = ((r.ql.y >> sl) & 0x0F0F0F0Fu) | (((r.qh.y >> shh) & 0x03030303u) << 4);
-        const bool lo = kq < 2u;                                      // codes 0..15 of the sub-block
-        bq[0] = kquant_b<6>(c0, c1, lo);
-        bq[1] = kquant_b<6>(c0, c1, !lo);
-        const float d = h2f(r.d);
-        // sc[8n + 2k4] (l < 16: item it0) and sc[8n + 2k4 + 1] (item it0 + 1)
-        const float m0 = d * (float)(int8_t)((r.sc.x >> (8u * k4)) & 0xFFu);
-        const float m1 = d * (float)(int8_t)((r.sc.y >> (8u * k4)) & 0xFFu);
-        mul[0] = 64.0f * m0;
-        mul[1] = 64.0f * m1;
-        add[0] = -32.0f * m0 - mul[0];
-        add[1] = -32.0f * m1 - mul[1];
+        const uint2 L = (kk & 1u) ? c.lb : c.la;
+        const uint32_t sl = (kk >> 1) * 4u, shh = 2u * kk;
+        const uint32_t c0 = ((L.x >> sl) & 0x0F0F0F0Fu) | (((c.qh.x >> shh) & 0x03030303u) << 4);
+        const uint32_t c1 = ((L.y >> sl) & 0x0F0F0F0Fu) | (((c.qh.y >> shh) & 0x03030303u) << 4);
+        q6_b(c0, c1, (int)(int8_t)((c.sc >> (8u * kk)) & 0xFFu), bq[0], bq[1]);
     }
+    __device__ static float dscale(const CR &c, uint32_t) { return h2f(c.d); }
+    template <class X> __device__ static float bmin(const X &, uint32_t, uint32_t) { return 0.0f; }
 };
 
 // Q8_0 (quant.rs:106-113): one 34-byte block (2-byte aligned) per sub-block,
-// int8 codes as bf16 (exact), value d * q.
-template <> struct PfW<T_Q8_0> {
-    static constexpr int NSET = 1;
-    static constexpr bool SUMS = false;
-    struct Raw {
-        uint32_t q[3], d, sb;
-    };
+// value d q; a chunk is 4 blocks.
+template <> struct PfH<T_Q8_0> {
+    static constexpr int NB = 1;
+    static constexpr bool MIN = false;
     static constexpr uint32_t BB = 34;
-    __device__ static Raw load(const uint8_t *b, uint32_t, uint32_t kq)
-    {
-        const uint32_t *pq = adown(b + 2u + 8u * kq);
-        return Raw{{pq[0], pq[1], pq[2]}, *adown(b), (uint32_t)((uintptr_t)b & 3u)};
-    }
-    __device__ static void decode(const Raw &r, uint32_t, uint32_t, uint4 (&bq)[2], float (&mul)[2],
-                                  float (&add)[2])
-    {
-        // w is 4-byte aligned: block b starts at byte 0 or 2 of a dword, its
-        // codes (b + 2 + 8 kq) at byte 2 or 0 of q[0]
-        const uint32_t sb = r.sb, sq = (sb + 2u) & 3u;
-        bq[0] = signed_bf16(abyte(r.q[1], r.q[0], sq), abyte(r.q[2], r.q[1], sq));
-        mul[0] = h2f(r.d >> (8 * sb));
-        add[0] = 0.0f;
-    }
-    // the repacked row group G (repack_k: item it = blocks 2 it, 2 it + 1;
-    // piece k' (codes 16 k' .. +16) at (k' ni + it) 16, the two d halves at
-    // 64 ni + 4 it)
-    struct RawR {
-        uint2 q;
-        uint32_t d;
+    struct C {
+        uint32_t q[4][3], d[4], sb;
     };
-    __device__ static RawR load_rp(const uint8_t *G, uint32_t b, uint32_t, uint32_t kq, uint32_t ni)
+    __device__ static C load(const uint8_t *blk, uint32_t, uint32_t kq)
     {
-        const uint32_t it = b >> 1, kp = 2u * (b & 1u) + (kq >> 1);
-        return RawR{*(const uint2 *)(G + (kp * ni + it) * 16u + 8u * (kq & 1u)),
-                    (uint32_t)*(const uint16_t *)(G + 64u * ni + 4u * it + 2u * (b & 1u))};
+        C c;
+#pragma unroll
+        for (uint32_t b = 0; b < 4u; b++) {
+            const uint32_t *pq = adown(blk + 34u * b + 2u + 8u * kq);
+            c.q[b][0] = pq[0];
+            c.q[b][1] = pq[1];
+            c.q[b][2] = pq[2];
+            c.d[b] = *adown(blk + 34u * b);
+        }
+        c.sb = (uint32_t)((uintptr_t)blk & 3u);
+        return c;
     }
-    __device__ static void decode_rp(const RawR &r, uint32_t, uint32_t, uint4 (&bq)[2], float (&mul)[2],
-                                     float (&add)[2])
+    __device__ static void decode(const C &c, uint32_t, uint32_t kk, uint32_t, uint4 (&bq)[NB])
     {
-        bq[0] = signed_bf16(r.q.x, r.q.y);
-        mul[0] = h2f(r.d);
-        add[0] = 0.0f;
+        // block kk starts at byte (sb + 2 kk) & 3 of a dword, its codes
+        // (block + 2 + 8 kq) 2 bytes later
+        const uint32_t sq = (c.sb + 2u * kk + 2u) & 3u;
+        bq[0] = q8_b(abyte(c.q[kk][1], c.q[kk][0], sq), abyte(c.q[kk][2], c.q[kk][1], sq));
     }
+    __device__ static float dscale(const C &c, uint32_t kk) { return h2f(c.d[kk] >> (8u * ((c.sb + 2u * kk) & 3u))); }
+    // repack_k's row group: item it = blocks 2 it, 2 it + 1; piece k'
+    // (codes 16 k' .. +16) at (k' ni + it) 16, the two d halves at
+    // 64 ni + 4 it
+    struct CR {
+        uint2 q[4];
+        uint32_t d0, d1;
+    };
+    __device__ static CR load_rp(const uint8_t *G, uint32_t b, uint32_t, uint32_t kq, uint32_t ni)
+    {
+        CR c;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            const uint32_t bb = b + i, kp = 2u * (bb & 1u) + (kq >> 1);
+            c.q[i] = *(const uint2 *)(G + (size_t)((kp * ni + (bb >> 1)) << 4) + 8u * (kq & 1u));
+        }
+        c.d0 = *(const uint32_t *)(G + 64u * ni + 4u * (b >> 1));
+        c.d1 = *(const uint32_t *)(G + 64u * ni + 4u * (b >> 1) + 4u);
+        return c;
+    }
+    __device__ static void decode_rp(const CR &c, uint32_t, uint32_t kk, uint32_t, uint4 (&bq)[NB])
+    {
+        bq[0] = q8_b(c.q[kk].x, c.q[kk].y);
+    }
+    __device__ static float dscale(const CR &c, uint32_t kk) { return h2f((kk < 2u ? c.d0 : c.d1) >> (16u * (kk & 1u))); }
+    template <class X> __device__ static float bmin(const X &, uint32_t, uint32_t) { return 0.0f; }
 };
 
-#ifndef QG_PF_KC
-#define QG_PF_KC 2
-#endif
 #ifndef QG_PF_R
 #define QG_PF_R 2
 #endif
 #ifndef QG_PF_WAVES
 #define QG_PF_WAVES 4
 #endif
-constexpr uint32_t kPfKC = QG_PF_KC;                         // sub-blocks per staged chunk
+#ifndef QG_PF_WG_TARGET
+#define QG_PF_WG_TARGET 1024
+#endif
+constexpr uint32_t kPfKC = 4;                                // sub-blocks per staged chunk
 constexpr uint32_t kPfR = QG_PF_R;                           // 16-row tiles per wave
 constexpr uint32_t kPfWaves = QG_PF_WAVES;                   // waves per workgroup
 constexpr uint32_t kPfRows = 16u * kPfR * kPfWaves;          // rows per workgroup tile
-constexpr uint32_t kPfBufX = kPfKC * 3u * 64u * 64u;         // bytes of x pieces per buffer
-constexpr uint32_t kPfBuf = kPfBufX + kPfKC * 1024u;         // ... and of the sums
+constexpr uint32_t kPfBufX = kPfKC * 2u * 64u * 64u;         // bytes of x pieces per buffer
+constexpr uint32_t kPfBuf = kPfBufX + kPfKC * 256u;          // ... and of the sums
 constexpr uint32_t kPfLds = 2u * kPfBuf;                     // two buffers
 
 // 16 bytes per lane from global memory straight into LDS at byte m0 + 16 lane
@@ -387,65 +426,83 @@ __device__ __forceinline__ void pf_dma16(const void *gp, uint32_t lds_addr)
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(lds_addr) : "memory");
 }
 
-// Issue the copies of chunk kc (nk sub-blocks) into the buffer at LDS byte
-// address b0: x block u = (kk * 3 + c) * 4 + g (sub-block kk, piece c,
-// tokens 16 g .. 16 g + 15; 1 KB, token t's 64 bytes as four 16-byte slots,
-// slot s stored at position s ^ pf_swz(t) so that the A-operand reads of
-// 8 or 16 consecutive tokens at one slot hit distinct banks), then per
-// sub-block the 256 sums.  Tokens
-// past the chunk repeat the last one (their outputs are never stored).
+// The registers of x are (re)defined here: an empty asm statement that reads
+// and writes them keeps its place among the other asm statements, so no
+// computation on x moves above it (above a wait or barrier just before).
+template <class X> __device__ __forceinline__ void pf_pin(X &x)
+{
+    static_assert(sizeof(X) % 4 == 0, "whole dwords");
+    uint32_t w[sizeof(X) / 4];
+    __builtin_memcpy(w, &x, sizeof(X));
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(X) / 4; i++) asm volatile("" : "+v"(w[i]));
+    __builtin_memcpy(&x, w, sizeof(X));
+}
+
 // slot position of token t's slots in its 64-byte LDS row: the 16-byte
 // reads of tokens t..t+7 (t % 8 == 0) at one slot cover 8 distinct 16-byte
 // bank groups mod 128 bytes, those of t..t+15 16 distinct groups mod 256
 __device__ __forceinline__ uint32_t pf_swz(uint32_t t) { return ((t >> 1) ^ (t >> 3)) & 3u; }
 
-__device__ __forceinline__ void pf_stage(const uint16_t *__restrict__ xp, const float *__restrict__ rec,
-                                         uint32_t ntok, uint32_t n, uint32_t kc, uint32_t nk, uint32_t b0,
-                                         uint32_t wave, uint32_t lane)
+// The x pieces are stored chunk by chunk (kPfKC sub-blocks of all
+// kPfMaxTokens token slots) as the image of an LDS buffer: 1 KB block
+// u = (kk * 2 + c) * 4 + g holds piece c of sub-block kk for tokens
+// 16 g .. 16 g + 15, token t's 64 bytes as four 16-byte slots, slot s
+// (elements 8 s .. 8 s + 7) at position s ^ pf_swz(t) so that the A-operand
+// reads of 8 or 16 consecutive tokens at one slot hit distinct banks.  Byte
+// offset of (chunk, u, t % 16, position):
+__device__ __forceinline__ size_t pf_xoff(uint32_t chunk, uint32_t u, uint32_t t16, uint32_t pos)
 {
-#pragma unroll
-    for (uint32_t v = 0; v < (kPfKC * 12u + kPfWaves - 1u) / kPfWaves; v++) {
-        const uint32_t u = v * kPfWaves + wave, kk = u / 12u, c = (u >> 2) % 3u, g = u & 3u;
-        if (kk < nk) {                                               // wave-uniform (u past the chunk: kk >= kPfKC)
-            const uint32_t t = min(16u * g + (lane >> 2), ntok - 1u);
-            const uint32_t s = (lane & 3u) ^ pf_swz(lane >> 2);
-            pf_dma16(xp + ((size_t)c * ntok + t) * n + 32u * (kc + kk) + 8u * s, b0 + u * 1024u);
-        }
-    }
-    if (wave < nk) pf_dma16(rec + (size_t)(kc + wave) * 256u + 4u * lane, b0 + kPfBufX + wave * 1024u);
+    return (size_t)chunk * (kPfKC * 8u * 1024u) + u * 1024u + t16 * 64u + pos * 16u;
 }
 
-// One workgroup's share of a grouped GEMM: rows row0 .. row0 + 16 R (R
-// tiles of 16 rows per wave; waves past the matrix still stage), K slice
-// k0 .. k1, all the chunk's tokens.  x of token t: xp[c][t][i] (c = 0..2,
-// piece stride ntok * n); per sub-block k the sums rec[(4 k + f) * 64 + t],
-// f = 0: sum x, 1: sum x[0..16), 2: sum x[16..32).  Chunks of kPfKC
-// sub-blocks are copied into two LDS buffers in turn, the next chunk's copy
-// and weight loads in flight while this one is computed.  D[4 kq + i][c16]
-// of an MFMA is token 16 tt + 4 kq + i of row r0 + c16.  LAY, the weight
-// layout: 0 GGUF, rows straddling blocks; 1 GGUF, every row starts a block
-// (nseg % 8 == 0, or single-sub-block blocks), so the sub-block index within
-// the block is the same in every lane; 2 repacked (repack_k), one row per
-// row group; 3 repacked, gg rows per group of gb bytes (ni items).
-template <uint32_t T, int R, int LAY>
+// Issue part `part` (of kPfKC) of the copies of chunk kc into the buffer at
+// LDS byte address b0: x blocks u = 8 part .. 8 part + 7 (each one
+// contiguous KB), and with part 0 the chunk's 4 x 64 sums.
+__device__ __forceinline__ void pf_stage(const uint8_t *__restrict__ xp, const float *__restrict__ rec,
+                                         uint32_t kc, uint32_t b0, uint32_t wave, uint32_t lane, uint32_t part)
+{
+#pragma unroll
+    for (uint32_t v = 0; v < 8u / kPfWaves; v++) {
+        const uint32_t u = 8u * part + v * kPfWaves + wave;
+        pf_dma16(xp + pf_xoff(kc / kPfKC, u, 0, 0) + 16u * lane, b0 + u * 1024u);
+    }
+    if (part == 0 && wave == 0) pf_dma16(rec + (size_t)kc * 64u + 4u * lane, b0 + kPfBufX);
+}
+
+// One workgroup's share of a grouped GEMM: rows row0 .. row0 + 16 kPfR
+// (waves past the matrix still stage), K slice k0 .. k1 (multiples of
+// kPfKC), all the chunk's tokens.  x: the chunk images at xp (pf_xoff); per
+// sub-block k the sums rec[64 k + t]; 2^-e of token t at rec[64 nseg + t].  Chunks of kPfKC sub-blocks are copied into two LDS
+// buffers in turn, the next chunk's copy and weight loads in flight while
+// this one is computed.  Every chunk lies inside one block of each row
+// (cols % 128 == 0 and slices of whole chunks: a row starts at a multiple of
+// 4 sub-blocks).  D[4 kq + i][c16] of an MFMA is token 16 tt + 4 kq + i of
+// row r0 + c16.  LAY, the weight layout: 0 GGUF, rows straddling blocks; 1
+// GGUF, every row starts a block (nseg % 8 == 0, or Q8_0); 2 repacked
+// (repack_k), one row per row group; 3 repacked, gg rows per group of gb
+// bytes (ni items).  In layouts 1 and 2 every row is at the same sub-block
+// of its block, and the block ends are the same for the whole wave.
+template <uint32_t T, int LAY>
 __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint32_t rows, uint32_t row0,
                                              uint32_t nseg, uint32_t k0, uint32_t k1,
                                              const uint16_t *__restrict__ xp, const float *__restrict__ rec,
                                              uint32_t ntok, uint32_t n, uint8_t *lds, float *__restrict__ y,
                                              uint32_t ldy, uint32_t gg, uint64_t gb, uint32_t ni)
 {
-    using P = PfW<T>;
-    constexpr bool RPL = LAY >= 2, AL = LAY != 0;
-    using Raw = std::conditional_t<RPL, typename P::RawR, typename P::Raw>;
-    constexpr bool SB1 = T == T_Q8_0;                                 // one sub-block per block
+    using P = PfH<T>;
+    constexpr int R = (int)kPfR;
+    constexpr bool RPL = LAY >= 2, AL = LAY == 1 || LAY == 2, Q8 = T == T_Q8_0;
+    using Ck = std::conditional_t<RPL, typename P::CR, typename P::C>;
+    const uint8_t *xb8 = (const uint8_t *)xp;
     const uint32_t lane = threadIdx.x & 63u, kq = lane >> 4, c16 = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
     const bool active = row0 < rows;                                  // wave-uniform
     const uint32_t swz = kq ^ pf_swz(c16);                           // this lane's slot position
-    // per row tile: GGUF, the flat index of the row's first sub-block and
-    // (AL) its first block; repacked, the row's sub-block offset in its row
-    // group and the group
+    // per row tile: the row's first sub-block (GGUF: flat index; repacked:
+    // within its row group) and its base (GGUF layout 1: its first block;
+    // repacked: its group)
     uint64_t fb[R];
     const uint8_t *rb[R];
 #pragma unroll
@@ -456,119 +513,176 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             rb[i] = w + (size_t)(LAY == 2 ? r : r / gg) * gb;
         } else {
             fb[i] = (uint64_t)r * nseg;
-            rb[i] = w + (SB1 ? fb[i] : fb[i] / 8u) * P::BB;
+            rb[i] = w + (Q8 ? fb[i] : fb[i] / 8u) * P::BB;
         }
     }
-    // sub-block k of row tile i: its index in its block, and the block
-    auto subj = [&](int i, uint32_t k) -> uint32_t {
-        if constexpr (SB1) return 0u;
-        else if constexpr (AL && LAY != 3) return k & 7u;
-        else return ((uint32_t)fb[i] + k) & 7u;
-    };
-    auto block = [&](int i, uint32_t k) -> const uint8_t * {
-        if constexpr (SB1) return rb[i] + (size_t)k * P::BB;
-        else if constexpr (AL) return rb[i] + (size_t)(k >> 3) * P::BB;
-        else return w + ((fb[i] + k) >> 3) * P::BB;
-    };
-    // weights of sub-block k (clamped into the slice: the loads past its end
-    // are harmless repeats, unconditional so that none waits on a branch)
-    auto wload = [&](int i, uint32_t k) -> Raw {
-        const uint32_t kc = min(k, k1 - 1u);
+    // chunk kc of row tile i (kc < k1: clamped by the caller)
+    auto cload = [&](int i, uint32_t kc) -> Ck {
+        const uint64_t f = fb[i] + kc;
+        const uint32_t jb = Q8 ? 0u : (uint32_t)(f & 7u);
         if constexpr (RPL) {
-            const uint32_t f = (uint32_t)fb[i] + kc;                 // sub-block in the row group
-            return P::load_rp(rb[i], SB1 ? f : f >> 3, f & 7u, kq, ni);
+            return P::load_rp(rb[i], (uint32_t)(Q8 ? f : f >> 3), jb, kq, ni);
+        } else if constexpr (LAY == 1) {
+            return P::load(rb[i] + (size_t)(Q8 ? kc : kc >> 3) * P::BB, jb, kq);
         } else {
-            return P::load(block(i, kc), subj(i, kc), kq);
+            return P::load(w + (Q8 ? f : f >> 3) * P::BB, jb, kq);
         }
     };
-    v4f acc[R][4];
+    v4f acc[R][4], D[R][4];
 #pragma unroll
     for (int i = 0; i < R; i++)
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) acc[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
-    Raw raw[kPfKC][R];
-    pf_stage(xp, rec, ntok, n, k0, min(kPfKC, k1 - k0), lds0, wave, lane);
-#pragma unroll
-    for (uint32_t kk = 0; kk < kPfKC; kk++)
-#pragma unroll
-        for (int i = 0; i < R; i++) raw[kk][i] = wload(i, k0 + kk);
-    uint32_t buf = 0;
-    for (uint32_t kc = k0; kc < k1; kc += kPfKC, buf ^= 1u) {
-        const uint32_t nk = min(kPfKC, k1 - kc);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // this wave's copies of chunk kc landed
-        __syncthreads();                                              // everyone's; the other buffer is free
-        if (kc + kPfKC < k1)
-            pf_stage(xp, rec, ntok, n, kc + kPfKC, min(kPfKC, k1 - kc - kPfKC), lds0 + (buf ^ 1u) * kPfBuf, wave,
-                     lane);
-        const uint8_t *xb = lds + buf * kPfBuf;
-        const float *rs = (const float *)(xb + kPfBufX);
-        float addv[R][kPfKC][2];
-#pragma unroll
-        for (int i = 0; i < R; i++)
-#pragma unroll
-            for (uint32_t kk = 0; kk < kPfKC; kk++) addv[i][kk][0] = addv[i][kk][1] = 0.f;
-#pragma unroll
-        for (uint32_t kk = 0; kk < kPfKC; kk++) {
-            if (kk >= nk) break;
-            // decode this sub-block's weights, then reuse their registers for
-            // the next chunk's
-            uint4 bq[R][2];
-            float mul[R][2];
-#pragma unroll
-            for (int i = 0; i < R; i++) {
-                if constexpr (RPL) P::decode_rp(raw[kk][i], subj(i, kc + kk), kq, bq[i], mul[i], addv[i][kk]);
-                else P::decode(raw[kk][i], subj(i, kc + kk), kq, bq[i], mul[i], addv[i][kk]);
-            }
-#pragma unroll
-            for (int i = 0; i < R; i++) raw[kk][i] = wload(i, kc + kPfKC + kk);
-            if (!active) continue;
-#pragma unroll
-            for (uint32_t tt = 0; tt < 4; tt++) {
-                const uint8_t *xa = xb + ((((kk * 3u) * 64u + 16u * tt + c16) * 4u + swz) << 4);
-                const bf8 a0 = *(const bf8 *)xa;
-                const bf8 a1 = *(const bf8 *)(xa + 64u * 64u);
-                const bf8 a2 = *(const bf8 *)(xa + 128u * 64u);
-#pragma unroll
-                for (int h = 0; h < P::NSET; h++)
-#pragma unroll
-                    for (int i = 0; i < R; i++) {
-                        const bf8 b = __builtin_bit_cast(bf8, bq[i][h]);
-                        const v4f z = {0.f, 0.f, 0.f, 0.f};
-                        v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, z, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, d, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b, d, 0, 0, 0);
-#pragma unroll
-                        for (int e = 0; e < 4; e++) acc[i][tt][e] = __builtin_fmaf(mul[i][h], d[e], acc[i][tt][e]);
-                    }
-            }
-        }
-        if constexpr (P::SUMS) {
-            if (!active) continue;
-            // the chunk's add * (sum x) terms as one f32 MFMA (K = 4) per row
-            // tile and token tile: K slot kq is sub-block qk, set qh of the
-            // chunk (A: the sums of the tile's 16 tokens, B: the row's add)
-            const uint32_t qk = P::NSET == 1 ? kq : kq >> 1, qh = P::NSET == 1 ? 0u : kq & 1u;
-            const bool qv = qk < nk;
+        for (int tt = 0; tt < 4; tt++) acc[i][tt] = D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (k0 < k1) {
+        // The operands of chunk kc (B, scales) are decoded from its weight
+        // registers during chunk kc - kPfKC, between that chunk's MFMAs; the
+        // weights of chunk kc + kPfKC are loaded at the start of chunk kc.
+        // The waits are compiler-visible (s_waitcnt builtin), so no use of a
+        // loaded register waits for the copies issued after it.
+        struct Ops {
+            uint4 bq[kPfKC][R][P::NB];
+            float dsc[R][Q8 ? kPfKC : 1];
             float bv[R];
+            uint32_t jb[R];
+        };
+        // sub-block kk's B operands of the chunk kc held in cw; its scales
+        auto decode_kk = [&](const Ck (&cw)[R], uint32_t kc, uint32_t kk, Ops &o) {
 #pragma unroll
             for (int i = 0; i < R; i++) {
-                float s = 0.f;
-#pragma unroll
-                for (uint32_t kk = 0; kk < kPfKC; kk++)
-#pragma unroll
-                    for (uint32_t h = 0; h < (uint32_t)P::NSET; h++) s = (qk == kk && qh == h) ? addv[i][kk][h] : s;
-                bv[i] = qv ? s : 0.f;
+                const uint32_t jb = Q8 ? 0u : AL ? (kc & 7u) : (uint32_t)((fb[i] + kc) & 7u);
+                if constexpr (RPL) P::decode_rp(cw[i], jb, kk, kq, o.bq[kk][i]);
+                else P::decode(cw[i], jb, kk, kq, o.bq[kk][i]);
             }
-            const float *sa = rs + min(qk, kPfKC - 1u) * 256u + (P::NSET == 1 ? 0u : 64u * (1u + qh)) + c16;
+        };
+        auto decode_sc = [&](const Ck (&cw)[R], uint32_t kc, Ops &o) {
 #pragma unroll
-            for (uint32_t tt = 0; tt < 4; tt++) {
-                const float av = qv ? sa[16u * tt] : 0.f;
+            for (int i = 0; i < R; i++) {
+                o.jb[i] = Q8 ? 0u : AL ? (kc & 7u) : (uint32_t)((fb[i] + kc) & 7u);
 #pragma unroll
-                for (int i = 0; i < R; i++) acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[i], acc[i][tt], 0, 0, 0);
+                for (uint32_t kk = 0; kk < (Q8 ? kPfKC : 1u); kk++) o.dsc[i][kk] = P::dscale(cw[i], kk);
+                o.bv[i] = P::bmin(cw[i], o.jb[i], kq);
             }
+        };
+#pragma unroll
+        for (uint32_t part = 0; part < kPfKC; part++) pf_stage(xb8, rec, k0, lds0, wave, lane, part);
+        Ck cw[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) cw[i] = cload(i, k0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);                           // vmcnt(0)
+        Ops op;
+#pragma unroll
+        for (uint32_t kk = 0; kk < kPfKC; kk++) decode_kk(cw, k0, kk, op);
+        decode_sc(cw, k0, op);
+#pragma unroll
+        for (int i = 0; i < R; i++) cw[i] = cload(i, min(k0 + kPfKC, k1 - kPfKC));
+        uint32_t buf = 0;
+        for (uint32_t kc = k0; kc < k1; kc += kPfKC, buf ^= 1u) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);                       // this wave's copies of chunk kc, the weights of the next
+            __syncthreads();                                          // everyone's copies; the other buffer is free
+#pragma unroll
+            for (int i = 0; i < R; i++) pf_pin(cw[i]);                // decoded below, not above the wait
+            // the next chunk's copies and the weights of the one after, spread
+            // over the sub-blocks below (the copies of the last chunk repeat it
+            // into the buffer no one reads any more)
+            const uint32_t kx = min(kc + kPfKC, k1 - kPfKC), kw = min(kc + 2u * kPfKC, k1 - kPfKC);
+            const uint32_t bnext = lds0 + (buf ^ 1u) * kPfBuf;
+            Ck cw2[R];
+            Ops on;
+            const uint32_t kn = min(kc + kPfKC, k1 - kPfKC);
+            decode_sc(cw, kn, on);
+            {   // (waves past the matrix compute too -- clamped rows, never stored -- so that
+                // this phase stays one block of straight-line code)
+                const uint8_t *xb = lds + buf * kPfBuf;
+#pragma unroll
+                for (uint32_t kk = 0; kk < kPfKC; kk++) {
+                    pf_stage(xb8, rec, kx, bnext, wave, lane, kk);
+#pragma unroll
+                    for (int i = 0; i < R; i++)
+                        if ((uint32_t)i % kPfKC == kk) cw2[i] = cload(i, kw);
+#pragma unroll
+                    for (uint32_t tt = 0; tt < 4; tt++) {
+                        const uint8_t *xa = xb + (((kk * 2u * 64u + 16u * tt + c16) * 4u + swz) << 4);
+                        const h8 a0 = *(const h8 *)xa;
+                        const h8 a1 = *(const h8 *)(xa + 64u * 64u);
+#pragma unroll
+                        for (int i = 0; i < R; i++)
+#pragma unroll
+                            for (int h = 0; h < P::NB; h++) {
+                                const h8 b = __builtin_bit_cast(h8, op.bq[kk][i][h]);
+                                D[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, D[i][tt], 0, 0, 0);
+                                D[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, D[i][tt], 0, 0, 0);
+                            }
+                    }
+                    decode_kk(cw, kn, kk, on);                        // the next chunk's, between the MFMAs
+                    pf_pin(on.bq[kk]);                                // (here, not sunk to the loop's end)
+                    if constexpr (Q8) {                               // a scale per sub-block
+#pragma unroll
+                        for (int i = 0; i < R; i++)
+#pragma unroll
+                            for (int tt = 0; tt < 4; tt++) {
+#pragma unroll
+                                for (int e = 0; e < 4; e++)
+                                    acc[i][tt][e] = __builtin_fmaf(op.dsc[i][kk], D[i][tt][e], acc[i][tt][e]);
+                                D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+                            }
+                    }
+                }
+                if constexpr (P::MIN) {
+                    // the chunk's -dmin m S terms: one f32 MFMA (K = 4: the
+                    // chunk's sub-blocks) per row tile and token tile
+                    const float *rs = (const float *)(xb + kPfBufX) + kq * 64u + c16;
+#pragma unroll
+                    for (uint32_t tt = 0; tt < 4; tt++) {
+                        const float av = rs[16u * tt];
+#pragma unroll
+                        for (int i = 0; i < R; i++)
+                            acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, op.bv[i], acc[i][tt], 0, 0, 0);
+                    }
+                }
+                if constexpr (!Q8) {
+                    // a row's block ends with this chunk (jb = 4), or the slice does
+                    const bool last = kc + kPfKC >= k1;
+                    if constexpr (AL) {
+                        if (op.jb[0] == 4u || last) {
+#pragma unroll
+                            for (int i = 0; i < R; i++)
+#pragma unroll
+                                for (int tt = 0; tt < 4; tt++) {
+#pragma unroll
+                                    for (int e = 0; e < 4; e++)
+                                        acc[i][tt][e] = __builtin_fmaf(op.dsc[i][0], D[i][tt][e], acc[i][tt][e]);
+                                    D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+                                }
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < R; i++) {
+                            const bool fl = op.jb[i] == 4u || last;
+                            const float d = fl ? op.dsc[i][0] : 0.0f;
+#pragma unroll
+                            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                                for (int e = 0; e < 4; e++) {
+                                    acc[i][tt][e] = __builtin_fmaf(d, D[i][tt][e], acc[i][tt][e]);
+                                    D[i][tt][e] = fl ? 0.0f : D[i][tt][e];
+                                }
+                        }
+                    }
+                }
+            }
+            op = on;
+#pragma unroll
+            for (int i = 0; i < R; i++) cw[i] = cw2[i];
         }
     }
     if (!active) return;
+    // 2^-e of the lane's 16 tokens (clamped: tokens past the chunk are not stored)
+    const float *tsc = rec + (size_t)nseg * 64u;
+    float ts[4][4];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) ts[tt][e] = tsc[min(16u * tt + 4u * kq + (uint32_t)e, ntok - 1u)];
 #pragma unroll
     for (int i = 0; i < R; i++) {
         const uint32_t r = row0 + 16u * i + c16;
@@ -578,14 +692,14 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t t = 16u * tt + 4u * kq + (uint32_t)e;
-                if (t < ntok) y[(size_t)t * ldy + r] = acc[i][tt][e];
+                if (t < ntok) y[(size_t)t * ldy + r] = acc[i][tt][e] * ts[tt][e];
             }
         }
     }
 }
 
 // One matrix of a grouped GEMM launch: its rows, workgroup tiles of
-// 64 kPfR rows, and where row 0 of token 0 of slice 0 of its output goes.
+// kPfRows rows, and where row 0 of token 0 of slice 0 of its output goes.
 struct PfJob {
     const uint8_t *w;
     float *y;
@@ -600,9 +714,9 @@ struct PfJobs {
 
 // Grouped, K-split GEMM over matrices of type T: blockIdx.x runs over the row
 // tiles of jobs j0, j1, j2 in turn, blockIdx.y over the slices of sps
-// sub-blocks; slice s of a job writes its partial products to
-// y + s * sstride (the consumer sums the slices in order s = 0, 1, ...).
-// 4 waves of 16 kPfR rows per workgroup.
+// sub-blocks (a multiple of kPfKC); slice s of a job writes its partial
+// products to y + s * sstride (the consumer sums the slices in order
+// s = 0, 1, ...).  kPfWaves waves of 16 kPfR rows per workgroup.
 template <uint32_t T, int LAY>
 __global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t nseg, uint32_t sps,
                                                  const uint16_t *__restrict__ xp, const float *__restrict__ rec,
@@ -620,23 +734,30 @@ __global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t
         }
     }
     const uint32_t row0 = tile * kPfRows + (threadIdx.x >> 6) * (16u * kPfR);
-    const uint32_t k0 = blockIdx.y * sps, k1 = min(nseg, k0 + sps);
-    pf_gemm_rows<T, kPfR, LAY>(J.w, J.rows, row0, nseg, k0, k1, xp, rec, ntok, n, (uint8_t *)pf_lds4,
-                               J.y + (size_t)blockIdx.y * sstride, ldy, J.g, J.gb, J.ni);
+    const uint32_t k0 = min(nseg, blockIdx.y * sps), k1 = min(nseg, k0 + sps);
+    pf_gemm_rows<T, LAY>(J.w, J.rows, row0, nseg, k0, k1, xp, rec, ntok, n, (uint8_t *)pf_lds4,
+                         J.y + (size_t)blockIdx.y * sstride, ldy, J.g, J.gb, J.ni);
 }
 
 // ---------------------------------------------------------------- planes
 //
-// The input vector of token blockIdx.y (mode 0: a; mode 1: rmsnorm(a + b) * nw
-// with a + b stored to sum_out when given; mode 2: silu(a) * b) as three
-// bf16 pieces and per-segment sums.  a and b may be the K-split slices of a
-// GEMM (na, nb <= kPfMaxSlices slices sstride floats apart, summed in slice
-// order).  Each thread converts 8-element pieces (a quarter of a 32-element
-// segment; the four threads of a segment combine their sums through lane
-// shuffles).  Mode 1 runs one workgroup per token (the norm needs the whole
-// row); sum_out must not alias a or b.
-constexpr int kPfPlanesBlock = 256;
+// The input vector x of token blockIdx.y (mode 0: a; mode 1: rmsnorm(a + b)
+// * nw with a + b stored to sum_out when given; mode 2: silu(a) * b) as the
+// two f16 pieces of xs = x 2^e (in the GEMM's chunk images, pf_xoff), the
+// f32 sums of xs per 32-element segment, and 2^-e.  a and b may be the
+// K-split slices of a GEMM (na, nb <= kPfMaxSlices slices sstride floats
+// apart, summed in slice order).  Two launches of kPfPlanesBlk workgroups
+// per token over 8-element pieces (a quarter of a 32-element segment each;
+// the four threads of a segment combine their sums through lane shuffles):
+// pf_stat_k -- per workgroup the statistics the scale needs (modes 0, 2:
+// max |x|, mode 1: sum v^2 and max |v nw| for v = a + b, x = v / rms * nw);
+// mode 2 keeps x (f32) in work, mode 1 writes sum_out -- then pf_split_k:
+// the row's scale from every workgroup's statistics, the pieces, the sums
+// and 2^-e.  A token with a non-finite x gets 2^-e = NaN (every output of
+// its row NaN).  sum_out must not alias a or b.
 constexpr uint32_t kPfMaxSlices = 16;
+constexpr uint32_t kPfPlanesT = 256;                         // threads per workgroup
+constexpr uint32_t kPfMaxBlk = 64;                           // workgroups per token at most
 
 // silu(x) = x / (1 + exp(-x)), in the two branches of math.rs:137-146
 __device__ __forceinline__ float silu1(float x)
@@ -684,13 +805,6 @@ __device__ __forceinline__ void sum8_slices(const float *p, uint32_t ns, uint64_
     v[4] = r1.x; v[5] = r1.y; v[6] = r1.z; v[7] = r1.w;
 }
 
-// bf16 of x rounded to nearest even (finite x), as the top half of a dword
-__device__ __forceinline__ uint32_t bf16_rn(float x)
-{
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
-}
-
 // x[i] (before the norm) of the piece at e0: a + b (mode 1), silu(a) * b (2), a (0)
 __device__ __forceinline__ void pf_input8(const float *at, uint32_t na, const float *bt, uint32_t nb,
                                           uint64_t sstride, uint32_t mode, uint32_t e0, float (&v)[8])
@@ -704,85 +818,152 @@ __device__ __forceinline__ void pf_input8(const float *at, uint32_t na, const fl
     }
 }
 
-__global__ void __launch_bounds__(1024) pf_planes_k(const float *__restrict__ a, uint32_t na,
-                                                    const float *__restrict__ b, uint32_t nb, uint64_t sstride,
-                                                    float *__restrict__ sum_out, const float *__restrict__ nw,
-                                                    float eps, uint32_t n, uint32_t lda, uint32_t mode,
-                                                    uint16_t *__restrict__ xp, float *__restrict__ rec,
-                                                    uint32_t ntok)
+// sum (or maximum) of v over the workgroup, through red[0 .. waves)
+template <bool MAX>
+__device__ __forceinline__ float pf_block_reduce(float v, float *red)
 {
-    __shared__ float red[16];
-    const uint32_t t = blockIdx.y, npc = n / 8u;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float u = __shfl_xor(v, o, 64);
+        v = MAX ? fmaxf(v, u) : v + u;
+    }
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+    for (uint32_t i = 1; i < blockDim.x / 64u; i++) r = MAX ? fmaxf(r, red[i]) : r + red[i];
+    __syncthreads();
+    return r;
+}
+
+// workgroups per token for rows of n elements: one 8-element piece per thread
+__host__ __device__ constexpr uint32_t pf_planes_blk(uint32_t n) { return (n / 8u + kPfPlanesT - 1u) / kPfPlanesT; }
+
+__global__ void __launch_bounds__(kPfPlanesT) pf_stat_k(const float *__restrict__ a, uint32_t na,
+                                                        const float *__restrict__ b, uint32_t nb, uint64_t sstride,
+                                                        float *__restrict__ sum_out, const float *__restrict__ nw,
+                                                        uint32_t n, uint32_t lda, uint32_t mode,
+                                                        float *__restrict__ work, float *__restrict__ rec)
+{
+    __shared__ float red[kPfPlanesT / 64u];
+    const uint32_t t = blockIdx.y, j = blockIdx.x * kPfPlanesT + threadIdx.x, nblk = gridDim.x;
     const float *at = a + (size_t)t * lda, *bt = b ? b + (size_t)t * lda : nullptr;
-    float inv = 1.0f;
-    if (mode == 1) {
-        float ss = 0.f;
-        for (uint32_t j = threadIdx.x; j < npc; j += blockDim.x) {
-            float v[8];
-            pf_input8(at, na, bt, nb, sstride, mode, 8u * j, v);
+    float s0 = 0.f, s1 = 0.f;                                         // mode 1: sum v^2, max |v nw|; else max |x|
+    bool bad = false;
+    if (j < n / 8u) {
+        float v[8];
+        pf_input8(at, na, bt, nb, sstride, mode, 8u * j, v);
+        if (mode == 1) {
             if (sum_out) {
                 float *so = sum_out + (size_t)t * lda + 8u * j;
                 *(float4 *)so = make_float4(v[0], v[1], v[2], v[3]);
                 *(float4 *)(so + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
 #pragma unroll
-            for (int e = 0; e < 8; e++) ss += v[e] * v[e];
+            for (int e = 0; e < 8; e++) {
+                const float w = nw[8u * j + e];
+                s0 += v[e] * v[e];
+                s1 = fmaxf(s1, fabsf(v[e] * w));
+                bad |= !__builtin_isfinite(v[e]) || !__builtin_isfinite(w);
+            }
+        } else {
+            if (mode == 2) {
+                float *xw = work + (size_t)t * n + 8u * j;
+                *(float4 *)xw = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(xw + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                s1 = fmaxf(s1, fabsf(v[e]));
+                bad |= !__builtin_isfinite(v[e]);
+            }
         }
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        float tot = 0.f;
-        for (uint32_t i = 0; i < blockDim.x / 64u; i++) tot += red[i];
-        inv = 1.0f / sqrtf(tot / (float)n + eps);
     }
-    const size_t piece = (size_t)ntok * n;
-    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < npc; j += gridDim.x * blockDim.x) {
-        const uint32_t e0 = 8u * j;
+    if (mode == 1) s0 = pf_block_reduce<false>(s0, red);
+    s1 = pf_block_reduce<true>(s1, red);
+    bad = __syncthreads_or(bad);
+    if (threadIdx.x == 0) {
+        float *pt = work + (size_t)qg::kPfMaxTokens * n + ((size_t)t * nblk + blockIdx.x) * 2u;
+        pt[0] = s0;
+        pt[1] = bad ? __builtin_nanf("") : s1;
+        if (blockIdx.x == 0) rec[(size_t)(n / 32u) * 64u + t] = 0.0f;   // 2^-e, raised by pf_split_k
+    }
+}
+
+__global__ void __launch_bounds__(kPfPlanesT) pf_split_k(const float *__restrict__ a, uint32_t na,
+                                                         const float *__restrict__ b, uint32_t nb, uint64_t sstride,
+                                                         const float *__restrict__ sum_out,
+                                                         const float *__restrict__ nw, float eps, uint32_t n,
+                                                         uint32_t lda, uint32_t mode, const float *__restrict__ work,
+                                                         uint16_t *__restrict__ xp, float *__restrict__ rec)
+{
+    const uint32_t t = blockIdx.y, j = blockIdx.x * kPfPlanesT + threadIdx.x, nblk = gridDim.x;
+    // the row's statistics, in workgroup order
+    const float *pt = work + (size_t)qg::kPfMaxTokens * n + (size_t)t * nblk * 2u;
+    float ss = 0.f, mx = 0.f;
+    bool bad = false;
+    for (uint32_t i = 0; i < nblk; i++) {
+        ss += pt[2u * i];
+        const float m = pt[2u * i + 1u];
+        bad |= !__builtin_isfinite(m);
+        mx = fmaxf(mx, m);
+    }
+    float inv = 1.0f;
+    if (mode == 1) {
+        inv = 1.0f / sqrtf(ss / (float)n + eps);                      // math.rs:253-255
+        mx *= inv;
+    }
+    // 2^e brings the largest magnitude into [512, 1024) (an estimate that
+    // overflowed: the smallest scale)
+    int E = 0;
+    (void)frexpf(mx, &E);
+    const int e = !__builtin_isfinite(mx) ? -126 : mx > 0.f ? min(max(10 - E, -126), 126) : 0;
+    const float sc = ldexpf(1.0f, e);
+    if (j < n / 8u) {
         float v[8];
-        if (mode == 1 && sum_out) {                                   // written above by this thread
+        const uint32_t e0 = 8u * j;
+        if (mode == 2) {
+            const float *xw = work + (size_t)t * n + e0;
+            const float4 p0 = *(const float4 *)xw, p1 = *(const float4 *)(xw + 4);
+            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+        } else if (mode == 1 && sum_out) {
             const float *so = sum_out + (size_t)t * lda + e0;
             const float4 p0 = *(const float4 *)so, p1 = *(const float4 *)(so + 4);
             v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
         } else {
-            pf_input8(at, na, bt, nb, sstride, mode, e0, v);
+            pf_input8(a + (size_t)t * lda, na, b ? b + (size_t)t * lda : nullptr, nb, sstride, mode, e0, v);
         }
         if (mode == 1)
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = v[e] * inv * nw[e0 + e];   // math.rs:253-255
-        // per float4 (x0 + x1) + (x2 + x3); per quarter the two; per half the two quarters
+            for (int k = 0; k < 8; k++) v[k] = v[k] * inv * nw[e0 + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            bad |= !__builtin_isfinite(v[k]);
+            v[k] = v[k] * sc;
+        }
+        uint32_t wh[4], wl[4];
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            const _Float16 h0 = (_Float16)v[k], h1 = (_Float16)v[k + 1];
+            const _Float16 l0 = (_Float16)(v[k] - (float)h0), l1 = (_Float16)(v[k + 1] - (float)h1);
+            wh[k >> 1] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            wl[k >> 1] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+        // piece c of slot j & 3 of sub-block j / 4, in the GEMM's chunk image
+        const uint32_t k = j >> 2, t16 = t & 15u;
+        uint8_t *p0 = (uint8_t *)xp + pf_xoff(k / kPfKC, (k % kPfKC) * 8u + (t >> 4), t16, (j & 3u) ^ pf_swz(t16));
+        *(uint4 *)p0 = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+        *(uint4 *)(p0 + 4u * 1024u) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+        // per quarter (x0 + x1) + (x2 + x3) ..., per half the two quarters, the segment the two halves
         const float qsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-        const float hsum = qsum + __shfl_xor(qsum, 1, 64);           // this quarter's half
-        const float other = __shfl_xor(hsum, 2, 64);
-        const uint32_t qi = j & 3u;
-        const float s0 = qi < 2u ? hsum : other, s1 = qi < 2u ? other : hsum;
-        uint32_t w[3][4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            uint32_t pc[3][2];
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const float x = v[e + h];
-                const bool fin = __builtin_isfinite(x);
-                const uint32_t hi = fin ? bf16_rn(x) : (__float_as_uint(x) & 0xFFFF0000u) | (x != x ? 0x00400000u : 0u);
-                const float r1 = fin ? x - __uint_as_float(hi) : 0.f;
-                const uint32_t mid = bf16_rn(r1);
-                const uint32_t lo = bf16_rn(r1 - __uint_as_float(mid));
-                pc[0][h] = hi;
-                pc[1][h] = mid;
-                pc[2][h] = lo;
-            }
-#pragma unroll
-            for (int c = 0; c < 3; c++) w[c][e >> 1] = (pc[c][0] >> 16) | pc[c][1];
-        }
-        uint16_t *p0 = xp + (size_t)t * n + e0;
-#pragma unroll
-        for (int c = 0; c < 3; c++) *(uint4 *)(p0 + c * piece) = make_uint4(w[c][0], w[c][1], w[c][2], w[c][3]);
-        if (qi == 0u) {
-            float *rg = rec + (size_t)(j >> 2) * 256u + t;
-            rg[0] = s0 + s1;
-            rg[64] = s0;
-            rg[128] = s1;
-        }
+        const float hsum = qsum + __shfl_xor(qsum, 1, 64);
+        const float seg = hsum + __shfl_xor(hsum, 2, 64);
+        if ((j & 3u) == 0u) rec[(size_t)k * 64u + t] = seg;
+    }
+    // 2^-e, or NaN when any x of the row is not finite: the largest value any
+    // workgroup writes (the bits of a NaN exceed those of every finite float)
+    if (__syncthreads_or(bad) ? threadIdx.x == 0 : (blockIdx.x == 0 && threadIdx.x == 0)) {
+        const float r = bad ? __builtin_nanf("") : ldexpf(1.0f, -e);
+        atomicMax((unsigned int *)(rec + (size_t)(n / 32u) * 64u + t), __float_as_uint(r));
     }
 }
 
@@ -882,7 +1063,6 @@ __global__ void __launch_bounds__(256) pf_attention_k(const float *__restrict__ 
 }
 
 }  // namespace qgp
-
 namespace qg {
 
 bool prefill_type_supported(uint32_t type)
@@ -890,17 +1070,25 @@ bool prefill_type_supported(uint32_t type)
     return type == T_Q4_K || type == T_Q5_K || type == T_Q6_K || type == T_Q8_0;
 }
 
-// Slices of a K split for `tiles` workgroup row tiles over nseg sub-blocks:
-// about 1024 workgroups in all, at most 16 slices of at least 4 sub-blocks;
-// returned so that ceil(nseg / ceil(nseg / S)) == S (no empty slice).
+// sub-blocks per slice: ceil(nseg / slices) rounded up to whole chunks
+static uint32_t pf_slice_len(uint32_t nseg, uint32_t slices)
+{
+    const uint32_t sps = (nseg + slices - 1) / slices;
+    return (sps + qgp::kPfKC - 1) / qgp::kPfKC * qgp::kPfKC;
+}
+
+// Slices of a K split for `tiles` workgroup row tiles over nseg sub-blocks
+// (nseg % kPfKC == 0): at most QG_PF_WG_TARGET (1024) workgroups in all,
+// at most 16 slices of whole chunks; returned so that ceil(nseg / sps) == S
+// for the slice length sps = pf_slice_len(nseg, S) (no empty slice).
 uint32_t pf_split(uint32_t tiles, uint32_t nseg)
 {
-    if (tiles == 0 || nseg == 0) return 1;
-    uint32_t s = (512u + tiles - 1) / tiles;
+    if (tiles == 0 || nseg < qgp::kPfKC) return 1;
+    uint32_t s = QG_PF_WG_TARGET / tiles;
     if (s > 16u) s = 16u;
-    if (s > nseg / 4u) s = nseg / 4u;
+    if (s > nseg / qgp::kPfKC) s = nseg / qgp::kPfKC;
     if (s < 1u) s = 1u;
-    const uint32_t sps = (nseg + s - 1) / s;
+    const uint32_t sps = pf_slice_len(nseg, s);
     return (nseg + sps - 1) / sps;
 }
 
@@ -911,7 +1099,7 @@ static void pf_gemm_launch(const qgp::PfJobs &jobs, bool rp, uint32_t tiles, uin
                            const uint16_t *xp, const float *rec, uint32_t ntok, uint32_t cols, uint32_t ldy,
                            size_t sstride, hipStream_t st)
 {
-    const uint32_t sps = (nseg + slices - 1) / slices;
+    const uint32_t sps = pf_slice_len(nseg, slices);
     const dim3 grid(tiles, slices), block(64 * qgp::kPfWaves);
     // the layout: repacked with one or several rows per group, or GGUF with
     // rows of whole blocks (Q8_0 blocks are single sub-blocks) or straddling
@@ -935,7 +1123,7 @@ int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *x
                    uint32_t ldy, uint32_t slices, size_t sstride, ihipStream_t *stream)
 {
     if (ntok == 0) return 0;
-    if (n_mats < 1 || n_mats > 3 || cols % 32 != 0 || cols == 0 || cols > 0xFFFFFFFFull || ntok > kPfMaxTokens)
+    if (n_mats < 1 || n_mats > 3 || cols % 128 != 0 || cols == 0 || cols > 0xFFFFFFFFull || ntok > kPfMaxTokens)
         return -1;
     const uint32_t nseg = (uint32_t)(cols / 32);
     if (slices < 1 || slices > nseg || slices > qgp::kPfMaxSlices) return -1;
@@ -978,25 +1166,20 @@ int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *x
 
 int launch_pf_planes(const float *a, uint32_t na, const float *b, uint32_t nb, size_t sstride, float *sum_out,
                      const float *nw, float eps, size_t n, size_t lda, int mode, uint16_t *xp, float *rec,
-                     uint32_t ntok, ihipStream_t *stream)
+                     float *work, uint32_t ntok, ihipStream_t *stream)
 {
     if (ntok == 0) return 0;
-    // 16-byte aligned rows and slices (float4 reads)
-    if (n % 32 != 0 || n == 0 || n > 0xFFFFFFFFull || ntok > kPfMaxTokens || na < 1 || na > qgp::kPfMaxSlices ||
-        (b && (nb < 1 || nb > qgp::kPfMaxSlices)) || (mode == 2 && !b) || lda % 4 != 0 || sstride % 4 != 0 ||
-        ((uintptr_t)a & 15u) || ((uintptr_t)b & 15u) || ((uintptr_t)sum_out & 15u))
+    // 16-byte aligned rows and slices (float4 reads); whole chunks
+    if (n % 128 != 0 || n == 0 || n > 0xFFFFFFFFull || ntok > kPfMaxTokens || na < 1 || na > qgp::kPfMaxSlices ||
+        (b && (nb < 1 || nb > qgp::kPfMaxSlices)) || (mode == 2 && !b) || (mode == 1 && !nw) || lda % 4 != 0 ||
+        sstride % 4 != 0 || ((uintptr_t)a & 15u) || ((uintptr_t)b & 15u) || ((uintptr_t)sum_out & 15u) ||
+        qgp::pf_planes_blk((uint32_t)n) > qgp::kPfMaxBlk)
         return -1;
-    const uint32_t pieces = (uint32_t)(n / 8);
-    // mode 1: one workgroup per token (up to 1024 threads); else 256-thread
-    // workgroups over the pieces
-    uint32_t block = qgp::kPfPlanesBlock, gx = (pieces + block - 1) / block;
-    if (mode == 1) {
-        block = pieces < 1024u ? (pieces + 63u) / 64u * 64u : 1024u;
-        gx = 1;
-    }
-    hipLaunchKernelGGL(qgp::pf_planes_k, dim3(gx, ntok), dim3(block), 0, (hipStream_t)stream, a, na, b, nb,
-                       (uint64_t)sstride, sum_out, nw, eps, (uint32_t)n, (uint32_t)lda, (uint32_t)mode, xp, rec,
-                       ntok);
+    const dim3 grid(qgp::pf_planes_blk((uint32_t)n), ntok), block(qgp::kPfPlanesT);
+    hipLaunchKernelGGL(qgp::pf_stat_k, grid, block, 0, (hipStream_t)stream, a, na, b, nb, (uint64_t)sstride, sum_out,
+                       nw, (uint32_t)n, (uint32_t)lda, (uint32_t)mode, work, rec);
+    hipLaunchKernelGGL(qgp::pf_split_k, grid, block, 0, (hipStream_t)stream, a, na, b, nb, (uint64_t)sstride,
+                       sum_out, nw, eps, (uint32_t)n, (uint32_t)lda, (uint32_t)mode, work, xp, rec);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
