@@ -77,6 +77,16 @@ __device__ __forceinline__ void k4sm4(uint32_t jb, uint32_t q0, uint32_t q1, uin
     m4 = (q1 & 0x3F3F3F3Fu & lo) | ((((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u)) & ~lo);
 }
 
+// The same for the sub-blocks 2 ph, 2 ph + 1, 4 + 2 ph, 5 + 2 ph (ph = 0 or
+// 1: half ph of each of the block's two 128-element halves)
+__device__ __forceinline__ void k4sm_ph(uint32_t ph, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t &sc4,
+                                        uint32_t &m4)
+{
+    const uint32_t sel = 0x05040100u + ph * 0x02020202u;
+    sc4 = __builtin_amdgcn_perm((q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u), q0 & 0x3F3F3F3Fu, sel);
+    m4 = __builtin_amdgcn_perm(((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u), q1 & 0x3F3F3F3Fu, sel);
+}
+
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ uint32_t as_u(h2 h) { return __builtin_bit_cast(uint32_t, h); }
 
@@ -198,6 +208,33 @@ template <> struct PfH<T_Q4_K> {
         k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
         return kquant_min(c.h.x, m4, kq);
     }
+    // Phase chunks (see pf_gemm_rows): sub-blocks 2 ph, 2 ph + 1 (pair ph of
+    // the block's first item) and 4 + 2 ph, 5 + 2 ph (pair ph of its second)
+    __device__ static C load_ph(const uint8_t *blk, uint32_t ph, uint32_t kq)
+    {
+        const uint8_t *q = blk + 16u + 32u * ph + 8u * kq;
+        return C{*(const uint4 *)blk, *(const uint2 *)q, *(const uint2 *)(q + 64u)};
+    }
+    __device__ static C load_rp_ph(const uint8_t *G, uint32_t b, uint32_t ph, uint32_t kq, uint32_t ni)
+    {
+        const uint8_t *q =
+            G + 8u * ni + (size_t)(((2u * ph + (kq >> 1)) * ni + 2u * b) << 4) + 8u * (kq & 1u);
+        return C{*(const uint4 *)(G + 16u * b), *(const uint2 *)q, *(const uint2 *)(q + 16u)};
+    }
+    __device__ static void decode_ph(const C &c, uint32_t ph, uint32_t kk, uint32_t, uint4 (&bq)[NB])
+    {
+        const uint2 v = kk < 2u ? c.v0 : c.v1;
+        const uint32_t sh = 4u * (kk & 1u);
+        uint32_t sc4, m4;
+        k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
+        bq[0] = kquant_b((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu, sc4, kk);
+    }
+    __device__ static float bmin_ph(const C &c, uint32_t ph, uint32_t kq)
+    {
+        uint32_t sc4, m4;
+        k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
+        return kquant_min(c.h.x, m4, kq);
+    }
 };
 
 // Q5_K (quant.rs:231-262): as Q4_K with a fifth bit, bit j of qh[l].
@@ -257,6 +294,48 @@ template <> struct PfH<T_Q5_K> {
         uint32_t sc4, m4;
         k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
         bq[0] = kquant_b(c0, c1, sc4, kk);
+    }
+    // phase chunks (as Q4_K): pairs ph and 2 + ph
+    __device__ static C load_ph(const uint8_t *blk, uint32_t ph, uint32_t kq)
+    {
+        const uint8_t *q = blk + 48u + 32u * ph + 8u * kq;
+        return C{*(const uint4 *)blk, *(const uint2 *)q, *(const uint2 *)(q + 64u),
+                 *(const uint2 *)(blk + 16u + 8u * kq)};
+    }
+    __device__ static void decode_ph(const C &c, uint32_t ph, uint32_t kk, uint32_t, uint4 (&bq)[NB])
+    {
+        const uint2 v = kk < 2u ? c.v0 : c.v1;
+        const uint32_t sh = 4u * (kk & 1u), j = 2u * ph + (kk & 1u) + 4u * (kk >> 1);
+        const uint32_t c0 = ((v.x >> sh) & 0x0F0F0F0Fu) | (((c.qh.x >> j) & 0x01010101u) << 4);
+        const uint32_t c1 = ((v.y >> sh) & 0x0F0F0F0Fu) | (((c.qh.y >> j) & 0x01010101u) << 4);
+        uint32_t sc4, m4;
+        k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
+        bq[0] = kquant_b(c0, c1, sc4, kk);
+    }
+    __device__ static CR load_rp_ph(const uint8_t *G, uint32_t b, uint32_t ph, uint32_t kq, uint32_t ni)
+    {
+        const uint32_t it = 4u * b + ph, H = 4u * ni;
+        const uint8_t *q = G + H + (size_t)(((kq >> 1) * ni + it) << 4) + 8u * (kq & 1u);
+        const uint8_t *w = G + H + 32u * ni + 8u * it + 4u * (kq >> 1);
+        return CR{*(const uint4 *)(G + 16u * b), *(const uint2 *)q, *(const uint2 *)(q + 32u),
+                  *(const uint32_t *)w, *(const uint32_t *)(w + 16u)};
+    }
+    __device__ static void decode_ph(const CR &c, uint32_t ph, uint32_t kk, uint32_t kq, uint4 (&bq)[NB])
+    {
+        const uint2 v = kk < 2u ? c.v0 : c.v1;
+        const uint32_t w = kk < 2u ? c.w0 : c.w1;
+        const uint32_t sh = 4u * (kk & 1u), s = 4u * (kq & 1u) + (kk & 1u);
+        const uint32_t c0 = ((v.x >> sh) & 0x0F0F0F0Fu) | (((w >> s) & 0x01010101u) << 4);
+        const uint32_t c1 = ((v.y >> sh) & 0x0F0F0F0Fu) | (((w >> (s + 2u)) & 0x01010101u) << 4);
+        uint32_t sc4, m4;
+        k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
+        bq[0] = kquant_b(c0, c1, sc4, kk);
+    }
+    template <class X> __device__ static float bmin_ph(const X &c, uint32_t ph, uint32_t kq)
+    {
+        uint32_t sc4, m4;
+        k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
+        return kquant_min(c.h.x, m4, kq);
     }
     __device__ static float dscale(const C &c, uint32_t) { return h2f(c.h.x); }
     __device__ static float dscale(const CR &c, uint32_t) { return h2f(c.h.x); }
@@ -410,6 +489,7 @@ template <> struct PfH<T_Q8_0> {
 #define QG_PF_WG_TARGET 1024
 #endif
 constexpr uint32_t kPfKC = 4;                                // sub-blocks per staged chunk
+constexpr uint32_t kPfSliceMax = 8;                          // K-split slices per GEMM at most
 constexpr uint32_t kPfR = QG_PF_R;                           // 16-row tiles per wave
 constexpr uint32_t kPfWaves = QG_PF_WAVES;                   // waves per workgroup
 constexpr uint32_t kPfRows = 16u * kPfR * kPfWaves;          // rows per workgroup tile
@@ -470,6 +550,27 @@ __device__ __forceinline__ void pf_stage(const uint8_t *__restrict__ xp, const f
     if (part == 0 && wave == 0) pf_dma16(rec + (size_t)kc * 64u + 4u * lane, b0 + kPfBufX);
 }
 
+// The same for a phase chunk (block b, half ph): its sub-blocks kk' = 0, 1
+// are sub-blocks 2 ph, 2 ph + 1 of the block's first chunk image (2 b), kk'
+// = 2, 3 those of the second (2 b + 1); the buffer gets the layout of a
+// plain chunk.
+__device__ __forceinline__ void pf_stage_ph(const uint8_t *__restrict__ xp, const float *__restrict__ rec,
+                                            uint32_t b, uint32_t ph, uint32_t b0, uint32_t wave, uint32_t lane,
+                                            uint32_t part)
+{
+    const uint32_t src_kk = 2u * ph + (part & 1u), chunk = 2u * b + (part >> 1);
+#pragma unroll
+    for (uint32_t v = 0; v < 8u / kPfWaves; v++) {
+        const uint32_t u = 8u * part + v * kPfWaves + wave;          // (part * 2 + c) * 4 + g
+        pf_dma16(xp + pf_xoff(chunk, ((src_kk * 2u + ((u >> 2) & 1u)) << 2) + (u & 3u), 0, 0) + 16u * lane,
+                 b0 + u * 1024u);
+    }
+    if (part == 0 && wave == 0) {
+        const uint32_t kk = lane >> 4, sub = 8u * b + 4u * (kk >> 1) + 2u * ph + (kk & 1u);
+        pf_dma16(rec + (size_t)sub * 64u + 4u * (lane & 15u), b0 + kPfBufX);
+    }
+}
+
 // One workgroup's share of a grouped GEMM: rows row0 .. row0 + 16 kPfR
 // (waves past the matrix still stage), K slice k0 .. k1 (multiples of
 // kPfKC), all the chunk's tokens.  x: the chunk images at xp (pf_xoff); per
@@ -493,6 +594,12 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
     using P = PfH<T>;
     constexpr int R = (int)kPfR;
     constexpr bool RPL = LAY >= 2, AL = LAY == 1 || LAY == 2, Q8 = T == T_Q8_0;
+    // phase order (Q4_K, Q5_K with whole-block rows): chunk slot c of a
+    // group of nbg <= 4 blocks is half c / nbg of block c % nbg -- the four
+    // first halves, then the four second halves -- so that a row's repacked
+    // pieces in use at a time lie in 2 of the layout's 4 code regions (the
+    // lines of the other two would not stay in L2 until their next use)
+    constexpr bool PH = (T == T_Q4_K || T == T_Q5_K) && AL;
     using Ck = std::conditional_t<RPL, typename P::CR, typename P::C>;
     const uint8_t *xb8 = (const uint8_t *)xp;
     const uint32_t lane = threadIdx.x & 63u, kq = lane >> 4, c16 = lane & 15u;
@@ -516,8 +623,20 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             rb[i] = w + (Q8 ? fb[i] : fb[i] / 8u) * P::BB;
         }
     }
+    // block and half of the phase chunk at sub-block kc
+    auto slot = [&](uint32_t kc, uint32_t &b, uint32_t &ph) {
+        const uint32_t c = kc / kPfKC, g4 = c >> 3, nbg = min(4u, nseg / 8u - 4u * g4), s8 = c & 7u;
+        ph = s8 >= nbg ? 1u : 0u;
+        b = 4u * g4 + s8 - ph * nbg;
+    };
     // chunk kc of row tile i (kc < k1: clamped by the caller)
     auto cload = [&](int i, uint32_t kc) -> Ck {
+        if constexpr (PH) {
+            uint32_t b, ph;
+            slot(kc, b, ph);
+            if constexpr (RPL) return P::load_rp_ph(rb[i], b, ph, kq, ni);
+            else return P::load_ph(rb[i] + (size_t)b * P::BB, ph, kq);
+        }
         const uint64_t f = fb[i] + kc;
         const uint32_t jb = Q8 ? 0u : (uint32_t)(f & 7u);
         if constexpr (RPL) {
@@ -547,6 +666,13 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
         };
         // sub-block kk's B operands of the chunk kc held in cw; its scales
         auto decode_kk = [&](const Ck (&cw)[R], uint32_t kc, uint32_t kk, Ops &o) {
+            if constexpr (PH) {
+                uint32_t b, ph;
+                slot(kc, b, ph);
+#pragma unroll
+                for (int i = 0; i < R; i++) P::decode_ph(cw[i], ph, kk, kq, o.bq[kk][i]);
+                return;
+            }
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const uint32_t jb = Q8 ? 0u : AL ? (kc & 7u) : (uint32_t)((fb[i] + kc) & 7u);
@@ -555,6 +681,17 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             }
         };
         auto decode_sc = [&](const Ck (&cw)[R], uint32_t kc, Ops &o) {
+            if constexpr (PH) {
+                uint32_t b, ph;
+                slot(kc, b, ph);
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    o.jb[i] = 4u;                                     // every chunk ends its D
+                    o.dsc[i][0] = P::dscale(cw[i], 0u);
+                    o.bv[i] = P::bmin_ph(cw[i], ph, kq);
+                }
+                return;
+            }
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 o.jb[i] = Q8 ? 0u : AL ? (kc & 7u) : (uint32_t)((fb[i] + kc) & 7u);
@@ -563,8 +700,17 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
                 o.bv[i] = P::bmin(cw[i], o.jb[i], kq);
             }
         };
+        auto stage = [&](uint32_t kc, uint32_t b0, uint32_t part) {
+            if constexpr (PH) {
+                uint32_t b, ph;
+                slot(kc, b, ph);
+                pf_stage_ph(xb8, rec, b, ph, b0, wave, lane, part);
+            } else {
+                pf_stage(xb8, rec, kc, b0, wave, lane, part);
+            }
+        };
 #pragma unroll
-        for (uint32_t part = 0; part < kPfKC; part++) pf_stage(xb8, rec, k0, lds0, wave, lane, part);
+        for (uint32_t part = 0; part < kPfKC; part++) stage(k0, lds0, part);
         Ck cw[R];
 #pragma unroll
         for (int i = 0; i < R; i++) cw[i] = cload(i, k0);
@@ -595,24 +741,30 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
                 const uint8_t *xb = lds + buf * kPfBuf;
 #pragma unroll
                 for (uint32_t kk = 0; kk < kPfKC; kk++) {
-                    pf_stage(xb8, rec, kx, bnext, wave, lane, kk);
+                    stage(kx, bnext, kk);
 #pragma unroll
                     for (int i = 0; i < R; i++)
                         if ((uint32_t)i % kPfKC == kk) cw2[i] = cload(i, kw);
+                    // the sub-block's A operands (every token tile, both
+                    // pieces), then its MFMAs piece by piece, so that the
+                    // MFMAs on one accumulator are 4 R NB issues apart
+                    h8 av[2][4];
 #pragma unroll
                     for (uint32_t tt = 0; tt < 4; tt++) {
                         const uint8_t *xa = xb + (((kk * 2u * 64u + 16u * tt + c16) * 4u + swz) << 4);
-                        const h8 a0 = *(const h8 *)xa;
-                        const h8 a1 = *(const h8 *)(xa + 64u * 64u);
-#pragma unroll
-                        for (int i = 0; i < R; i++)
-#pragma unroll
-                            for (int h = 0; h < P::NB; h++) {
-                                const h8 b = __builtin_bit_cast(h8, op.bq[kk][i][h]);
-                                D[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, D[i][tt], 0, 0, 0);
-                                D[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, D[i][tt], 0, 0, 0);
-                            }
+                        av[0][tt] = *(const h8 *)xa;
+                        av[1][tt] = *(const h8 *)(xa + 64u * 64u);
                     }
+#pragma unroll
+                    for (int pc = 0; pc < 2; pc++)
+#pragma unroll
+                        for (uint32_t tt = 0; tt < 4; tt++)
+#pragma unroll
+                            for (int i = 0; i < R; i++)
+#pragma unroll
+                                for (int h = 0; h < P::NB; h++)
+                                    D[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                        av[pc][tt], __builtin_bit_cast(h8, op.bq[kk][i][h]), D[i][tt], 0, 0, 0);
                     decode_kk(cw, kn, kk, on);                        // the next chunk's, between the MFMAs
                     pf_pin(on.bq[kk]);                                // (here, not sunk to the loop's end)
                     if constexpr (Q8) {                               // a scale per sub-block
@@ -692,7 +844,7 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t t = 16u * tt + 4u * kq + (uint32_t)e;
-                if (t < ntok) y[(size_t)t * ldy + r] = acc[i][tt][e] * ts[tt][e];
+                if (t < ntok) __builtin_nontemporal_store(acc[i][tt][e] * ts[tt][e], &y[(size_t)t * ldy + r]);
             }
         }
     }
@@ -1079,13 +1231,13 @@ static uint32_t pf_slice_len(uint32_t nseg, uint32_t slices)
 
 // Slices of a K split for `tiles` workgroup row tiles over nseg sub-blocks
 // (nseg % kPfKC == 0): at most QG_PF_WG_TARGET (1024) workgroups in all,
-// at most 16 slices of whole chunks; returned so that ceil(nseg / sps) == S
+// at most kPfSliceMax slices of whole chunks; returned so that ceil(nseg / sps) == S
 // for the slice length sps = pf_slice_len(nseg, S) (no empty slice).
 uint32_t pf_split(uint32_t tiles, uint32_t nseg)
 {
     if (tiles == 0 || nseg < qgp::kPfKC) return 1;
     uint32_t s = QG_PF_WG_TARGET / tiles;
-    if (s > 16u) s = 16u;
+    if (s > qgp::kPfSliceMax) s = qgp::kPfSliceMax;
     if (s > nseg / qgp::kPfKC) s = nseg / qgp::kPfKC;
     if (s < 1u) s = 1u;
     const uint32_t sps = pf_slice_len(nseg, s);
