@@ -140,7 +140,8 @@ int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
 // -2 = launch failure).  x of every token t scaled by a power of two 2^e_t,
 // xs = x 2^e_t, as two f16 pieces in xp (4 n kPfMaxTokens bytes: per
 // 128-element chunk the 32 KB image of the GEMM's LDS buffer, qgp::pf_xoff),
-// the sums of xs per 32-element segment g at rec[64 g + t] and
+// the sums of xs per 32-element segment g at rec[64 g + t] (two f16 pieces,
+// hi | lo << 16) and
 // 2^-e_t at rec[64 (n / 32) + t] (rec holds 64 (n / 32 + 1) floats).  GEMM
 // matrices have cols % 128 == 0; outputs are K-split: slice s of a result
 // lives sstride floats after slice 0, and its consumer sums the slices.

@@ -12,7 +12,7 @@
 //     pieces xs = x 2^e = hi + lo (hi the rounding of xs, lo the rounding of
 //     what hi leaves: 22 significant bits together), written chunk by chunk
 //     in the layout of the GEMM's LDS buffers; per 32-element segment the
-//     f32 sum of xs; per token 2^-e;
+//     sum of xs (as two f16 pieces); per token 2^-e;
 //   * pf_gemm_k: y[t][r] = 2^-e (sum over blocks of d D + sum over
 //     sub-blocks of -dmin m S) with D = sum over the block's elements of
 //     xs B from chained v_mfma_f32_16x16x32_f16 (A: 16 tokens x 32 elements
@@ -21,8 +21,8 @@
 //     parts 16 a q' and b q' of sc q' (sc = 16 a + b) for Q6_K, q for Q8_0
 //     -- so every product is exact and accumulates in f32; the block scale
 //     d multiplies D once per block (per sub-block for Q8_0) and the
-//     K-quant min terms are one v_mfma_f32_16x16x4f32 per 4 sub-blocks
-//     (A: S, the sums of xs, B: -dmin m in f32);
+//     K-quant min terms -dmin sum m S are one v_mfma_f32_16x16x16_f16 per 4
+//     sub-blocks (A: S, the sums of xs, as two f16 pieces; B: m, exact);
 //   * pf_qkv_post_k, pf_attention_k: bias, RoPE and KV append of every token
 //     (attention.rs:66-90), causal attention of every token over the cache up
 //     to its own slot (attention.rs:93-121), as the decode path.
@@ -46,6 +46,7 @@ using qg::T_Q8_0;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float h2f(uint32_t h16)
@@ -121,10 +122,18 @@ __device__ __forceinline__ uint4 kquant_b(uint32_t c0, uint32_t c1, uint32_t sc4
     return scaled_codes(c0, c1, s, s * h2{-1024.0f16, -1024.0f16});
 }
 
-// -dmin m of the chunk's sub-block kq (byte kq of m4), dmin the high half of dd
-__device__ __forceinline__ float kquant_min(uint32_t dd, uint32_t m4, uint32_t kq)
+// The min terms' B operand (v_mfma_f32_16x16x16_f16, K slot 2 kk + p = piece
+// p of the sums of the chunk's sub-block kk): lane kq < 2 holds the mins of
+// sub-blocks 2 kq, 2 kq + 1 (bytes of m4), each twice, as exact f16; kq >= 2
+// zero.  Returned as two dwords.
+__device__ __forceinline__ uint2 kquant_minb(uint32_t m4, uint32_t kq)
 {
-    return -(h2f(dd >> 16) * (float)((m4 >> (8u * kq)) & 0xFFu));
+    const uint32_t b = 2u * (kq & 1u);
+    const h2 one = h2{1024.0f16, 1024.0f16};
+    const uint32_t lo = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, m4, 0x04000400u | (b * 0x00010001u))) - one);
+    const uint32_t hi =
+        as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, m4, 0x04000400u | ((b + 1u) * 0x00010001u))) - one);
+    return kq < 2u ? make_uint2(lo, hi) : make_uint2(0u, 0u);
 }
 
 // Q6_K: codes q (6 bits) of c0, c1 as q' = q - 32, times the two parts of
@@ -160,7 +169,8 @@ __device__ __forceinline__ uint4 q8_b(uint32_t c0, uint32_t c1)
 //   decode(c, jb, kk, kq, bq): the B operands of sub-block kk of the chunk;
 //   dscale(c, kk): the scale that multiplies D (per block; per sub-block
 //     for Q8_0);
-//   bmin(c, jb, kq): -dmin m of sub-block kq of the chunk (MIN types).
+//   minb(c, jb, kq, dmin): the min terms' B operand (kquant_minb) and dmin
+//     (MIN types).
 // NB: B operands per sub-block.
 template <uint32_t T> struct PfH;
 
@@ -202,11 +212,12 @@ template <> struct PfH<T_Q4_K> {
         decode(c, jb, kk, kq, bq);
     }
     __device__ static float dscale(const C &c, uint32_t) { return h2f(c.h.x); }
-    __device__ static float bmin(const C &c, uint32_t jb, uint32_t kq)
+    __device__ static uint2 minb(const C &c, uint32_t jb, uint32_t kq, float &dmin)
     {
         uint32_t sc4, m4;
         k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
-        return kquant_min(c.h.x, m4, kq);
+        dmin = h2f(c.h.x >> 16);
+        return kquant_minb(m4, kq);
     }
     // Phase chunks (see pf_gemm_rows): sub-blocks 2 ph, 2 ph + 1 (pair ph of
     // the block's first item) and 4 + 2 ph, 5 + 2 ph (pair ph of its second)
@@ -229,11 +240,12 @@ template <> struct PfH<T_Q4_K> {
         k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
         bq[0] = kquant_b((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu, sc4, kk);
     }
-    __device__ static float bmin_ph(const C &c, uint32_t ph, uint32_t kq)
+    __device__ static uint2 minb_ph(const C &c, uint32_t ph, uint32_t kq, float &dmin)
     {
         uint32_t sc4, m4;
         k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
-        return kquant_min(c.h.x, m4, kq);
+        dmin = h2f(c.h.x >> 16);
+        return kquant_minb(m4, kq);
     }
 };
 
@@ -331,19 +343,21 @@ template <> struct PfH<T_Q5_K> {
         k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
         bq[0] = kquant_b(c0, c1, sc4, kk);
     }
-    template <class X> __device__ static float bmin_ph(const X &c, uint32_t ph, uint32_t kq)
+    template <class X> __device__ static uint2 minb_ph(const X &c, uint32_t ph, uint32_t kq, float &dmin)
     {
         uint32_t sc4, m4;
         k4sm_ph(ph, c.h.y, c.h.z, c.h.w, sc4, m4);
-        return kquant_min(c.h.x, m4, kq);
+        dmin = h2f(c.h.x >> 16);
+        return kquant_minb(m4, kq);
     }
     __device__ static float dscale(const C &c, uint32_t) { return h2f(c.h.x); }
     __device__ static float dscale(const CR &c, uint32_t) { return h2f(c.h.x); }
-    template <class X> __device__ static float bmin(const X &c, uint32_t jb, uint32_t kq)
+    template <class X> __device__ static uint2 minb(const X &c, uint32_t jb, uint32_t kq, float &dmin)
     {
         uint32_t sc4, m4;
         k4sm4(jb, c.h.y, c.h.z, c.h.w, sc4, m4);
-        return kquant_min(c.h.x, m4, kq);
+        dmin = h2f(c.h.x >> 16);
+        return kquant_minb(m4, kq);
     }
 };
 
@@ -418,7 +432,11 @@ template <> struct PfH<T_Q6_K> {
         q6_b(c0, c1, (int)(int8_t)((c.sc >> (8u * kk)) & 0xFFu), bq[0], bq[1]);
     }
     __device__ static float dscale(const CR &c, uint32_t) { return h2f(c.d); }
-    template <class X> __device__ static float bmin(const X &, uint32_t, uint32_t) { return 0.0f; }
+    template <class X> __device__ static uint2 minb(const X &, uint32_t, uint32_t, float &dmin)
+    {
+        dmin = 0.0f;
+        return make_uint2(0u, 0u);
+    }
 };
 
 // Q8_0 (quant.rs:106-113): one 34-byte block (2-byte aligned) per sub-block,
@@ -476,7 +494,11 @@ template <> struct PfH<T_Q8_0> {
         bq[0] = q8_b(c.q[kk].x, c.q[kk].y);
     }
     __device__ static float dscale(const CR &c, uint32_t kk) { return h2f((kk < 2u ? c.d0 : c.d1) >> (16u * (kk & 1u))); }
-    template <class X> __device__ static float bmin(const X &, uint32_t, uint32_t) { return 0.0f; }
+    template <class X> __device__ static uint2 minb(const X &, uint32_t, uint32_t, float &dmin)
+    {
+        dmin = 0.0f;
+        return make_uint2(0u, 0u);
+    }
 };
 
 #ifndef QG_PF_R
@@ -661,7 +683,8 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
         struct Ops {
             uint4 bq[kPfKC][R][P::NB];
             float dsc[R][Q8 ? kPfKC : 1];
-            float bv[R];
+            uint2 bm[R];                                              // min terms: B operand, dmin
+            float dmn[R];
             uint32_t jb[R];
         };
         // sub-block kk's B operands of the chunk kc held in cw; its scales
@@ -688,7 +711,7 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
                 for (int i = 0; i < R; i++) {
                     o.jb[i] = 4u;                                     // every chunk ends its D
                     o.dsc[i][0] = P::dscale(cw[i], 0u);
-                    o.bv[i] = P::bmin_ph(cw[i], ph, kq);
+                    if constexpr (P::MIN) o.bm[i] = P::minb_ph(cw[i], ph, kq, o.dmn[i]);
                 }
                 return;
             }
@@ -697,7 +720,7 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
                 o.jb[i] = Q8 ? 0u : AL ? (kc & 7u) : (uint32_t)((fb[i] + kc) & 7u);
 #pragma unroll
                 for (uint32_t kk = 0; kk < (Q8 ? kPfKC : 1u); kk++) o.dsc[i][kk] = P::dscale(cw[i], kk);
-                o.bv[i] = P::bmin(cw[i], o.jb[i], kq);
+                o.bm[i] = P::minb(cw[i], o.jb[i], kq, o.dmn[i]);
             }
         };
         auto stage = [&](uint32_t kc, uint32_t b0, uint32_t part) {
@@ -739,6 +762,21 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             {   // (waves past the matrix compute too -- clamped rows, never stored -- so that
                 // this phase stays one block of straight-line code)
                 const uint8_t *xb = lds + buf * kPfBuf;
+                // min terms: A = the sums of the chunk's sub-blocks 2 (kq & 1),
+                // 2 (kq & 1) + 1 as f16 pieces (K slots 2 kk + piece; zero for kq >= 2)
+                v4f Dm[R][4];
+                if constexpr (P::MIN) {
+                    const uint32_t *su = (const uint32_t *)(xb + kPfBufX) + 2u * (kq & 1u) * 64u + c16;
+#pragma unroll
+                    for (uint32_t tt = 0; tt < 4; tt++) {
+                        const uint32_t s0 = su[16u * tt], s1 = su[64u + 16u * tt];
+                        const h4 a = __builtin_bit_cast(h4, kq < 2u ? make_uint2(s0, s1) : make_uint2(0u, 0u));
+#pragma unroll
+                        for (int i = 0; i < R; i++)
+                            Dm[i][tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, __builtin_bit_cast(h4, op.bm[i]),
+                                                                               v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    }
+                }
 #pragma unroll
                 for (uint32_t kk = 0; kk < kPfKC; kk++) {
                     stage(kx, bnext, kk);
@@ -780,16 +818,15 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
                     }
                 }
                 if constexpr (P::MIN) {
-                    // the chunk's -dmin m S terms: one f32 MFMA (K = 4: the
-                    // chunk's sub-blocks) per row tile and token tile
-                    const float *rs = (const float *)(xb + kPfBufX) + kq * 64u + c16;
+                    // the chunk's -dmin m S terms, from the v_mfma_f32_16x16x16_f16
+                    // products taken before this chunk's main MFMAs
 #pragma unroll
-                    for (uint32_t tt = 0; tt < 4; tt++) {
-                        const float av = rs[16u * tt];
+                    for (int i = 0; i < R; i++)
 #pragma unroll
-                        for (int i = 0; i < R; i++)
-                            acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, op.bv[i], acc[i][tt], 0, 0, 0);
-                    }
+                        for (uint32_t tt = 0; tt < 4; tt++)
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                acc[i][tt][e] = __builtin_fmaf(-op.dmn[i], Dm[i][tt][e], acc[i][tt][e]);
                 }
                 if constexpr (!Q8) {
                     // a row's block ends with this chunk (jb = 4), or the slice does
@@ -1109,7 +1146,11 @@ __global__ void __launch_bounds__(kPfPlanesT) pf_split_k(const float *__restrict
         const float qsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
         const float hsum = qsum + __shfl_xor(qsum, 1, 64);
         const float seg = hsum + __shfl_xor(hsum, 2, 64);
-        if ((j & 3u) == 0u) rec[(size_t)k * 64u + t] = seg;
+        if ((j & 3u) == 0u) {                                         // as two f16 pieces, hi | lo << 16
+            const _Float16 sh = (_Float16)seg, sl = (_Float16)(seg - (float)sh);
+            ((uint32_t *)rec)[(size_t)k * 64u + t] =
+                (uint32_t)__builtin_bit_cast(uint16_t, sh) | ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
+        }
     }
     // 2^-e, or NaN when any x of the row is not finite: the largest value any
     // workgroup writes (the bits of a NaN exceed those of every finite float)
