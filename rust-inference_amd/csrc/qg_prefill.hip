@@ -933,9 +933,9 @@ __global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t
 // The input vector x of token blockIdx.y (mode 0: a; mode 1: rmsnorm(a + b)
 // * nw with a + b stored to sum_out when given; mode 2: silu(a) * b) as the
 // two f16 pieces of xs = x 2^e (in the GEMM's chunk images, pf_xoff), the
-// f32 sums of xs per 32-element segment, and 2^-e.  a and b may be the
-// K-split slices of a GEMM (na, nb <= kPfMaxSlices slices sstride floats
-// apart, summed in slice order).  Two launches of kPfPlanesBlk workgroups
+// sums of xs per 32-element segment (two f16 pieces), and 2^-e.  a and b may
+// be the K-split slices of a GEMM (na, nb <= kPfMaxSlices slices sstride
+// floats apart, summed in slice order).  Two launches of pf_planes_blk(n) workgroups
 // per token over 8-element pieces (a quarter of a 32-element segment each;
 // the four threads of a segment combine their sums through lane shuffles):
 // pf_stat_k -- per workgroup the statistics the scale needs (modes 0, 2:
