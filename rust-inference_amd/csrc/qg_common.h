@@ -137,14 +137,15 @@ int launch_dequantize_row_dev(uint32_t type, const uint8_t *w, size_t rows, size
 int launch_fill(float *out, size_t n, float v, ihipStream_t *stream);
 // Batched prefill (qg_prefill.hip): tokens per chunk, supported matrix types,
 // and the launchers of its kernels (0 = launched, -1 = shape not supported,
-// -2 = launch failure).  x of every token t scaled by a power of two 2^e_t,
-// xs = x 2^e_t, as two f16 pieces in xp (4 n kPfMaxTokens bytes: per
-// 128-element chunk the 32 KB image of the GEMM's LDS buffer, qgp::pf_xoff),
-// the sums of xs per 32-element segment g at rec[64 g + t] (two f16 pieces,
-// hi | lo << 16) and
-// 2^-e_t at rec[64 (n / 32) + t] (rec holds 64 (n / 32 + 1) floats).  GEMM
-// matrices have cols % 128 == 0; outputs are K-split: slice s of a result
-// lives sstride floats after slice 0, and its consumer sums the slices.
+// -2 = launch failure).  x of every token t scaled per 256-element group g by
+// a power of two 2^e_tg, xs = x 2^e_tg, as two f16 pieces in xp (4 n
+// kPfMaxTokens bytes: per 128-element chunk the 32 KB image of the GEMM's
+// LDS buffer, qgp::pf_xoff), the sums of xs per 32-element segment k at
+// rec[64 k + t] (two f16 pieces, hi | lo << 16) and 2^-e_tg at
+// rec[64 (n / 32) + 64 g + t] (rec holds 64 (n / 32 + ceil(n / 256))
+// floats).  GEMM matrices have cols % 128 == 0; outputs are K-split: slice s
+// of a result lives sstride floats after slice 0, and its consumer sums the
+// slices.
 constexpr uint32_t kPfMaxTokens = 64;
 bool prefill_type_supported(uint32_t type);
 // one matrix of a grouped prefill GEMM: y[t * ldy + r] (+ s * sstride); w in
@@ -167,19 +168,24 @@ uint32_t pf_split(uint32_t tiles, uint32_t nseg);
 // that every matrix writes, empty or not; one launch per run of one type
 int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *xp, const float *rec, uint32_t ntok,
                    uint32_t ldy, uint32_t slices, size_t sstride, ihipStream_t *stream);
-// x = sum of the na slices of a (nb of b); mode 0: x = a; 1: x =
-// rmsnorm(a + b) * nw (b may be NULL; sum_out, if not NULL, receives a + b
-// and must not alias a or b); 2: x = silu(a) * b.  Rows of lda floats.
-// work: kPfMaxTokens * (n + 128) floats of scratch.
+// x = sum of the na slices of a (nb of b); mode 0: x = a; 1: x = (a + b) *
+// nw, the numerator of rmsnorm(a + b) * nw (b may be NULL; sum_out, if not
+// NULL, receives a + b and must not alias a or b; ss_out[t * ceil(n / 256) +
+// g] receives the sum of (a + b)^2 over group g: the consumer of the GEMM
+// over x multiplies its output by 1 / rms); 2: x = silu(a r) * (b r) with
+// r = 1 / rms of the mode-1 call (over pre_n elements) that left its sums at
+// pre, or r = 1 if pre is NULL.  Rows of lda floats.
 int launch_pf_planes(const float *a, uint32_t na, const float *b, uint32_t nb, size_t sstride, float *sum_out,
-                     const float *nw, float eps, size_t n, size_t lda, int mode, uint16_t *xp, float *rec,
-                     float *work, uint32_t ntok, ihipStream_t *stream);
+                     const float *nw, size_t n, size_t lda, int mode, const float *pre, size_t pre_n, float eps,
+                     float *ss_out, uint16_t *xp, float *rec, uint32_t ntok, ihipStream_t *stream);
 // out[i] = sum of the ns slices of x[i], i < n
 int launch_pf_sum(const float *x, uint32_t ns, size_t sstride, size_t n, float *out, ihipStream_t *stream);
-int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *bq, const float *bk,
-                       const float *bv, float *kc, float *vc, const float *cos_t, const float *sin_t, uint32_t q_dim,
-                       uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0, uint32_t ntok,
-                       ihipStream_t *stream);
+// q, k, v of the QKV GEMM over a mode-1 x (norm sums at ss, over ss_n
+// elements) times 1 / rms, plus the biases, RoPE of q and k, the KV append
+int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *ss, size_t ss_n, float eps,
+                       const float *bq, const float *bk, const float *bv, float *kc, float *vc, const float *cos_t,
+                       const float *sin_t, uint32_t q_dim, uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0,
+                       uint32_t ntok, ihipStream_t *stream);
 int launch_pf_attention(const float *qkv, uint32_t ldq, const float *kc, const float *vc, float *out, uint32_t n_heads,
                         uint32_t hd, uint32_t kv_dim, uint32_t n_rep, float scale, uint32_t slot0, uint32_t ntok,
                         size_t lds, ihipStream_t *stream);

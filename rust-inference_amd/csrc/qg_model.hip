@@ -782,7 +782,7 @@ struct qg_model {
     float *pf_h[2] = {nullptr, nullptr}, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_ao2 = nullptr,
           *pf_g = nullptr, *pf_fo = nullptr, *pf_last = nullptr;
     uint16_t *pf_xp = nullptr;
-    float *pf_rec = nullptr, *pf_work = nullptr;
+    float *pf_rec = nullptr, *pf_ss = nullptr;
     uint32_t *pf_tok = nullptr;
     uint32_t pf_s_qkv = 1, pf_s_o = 1, pf_s_gu = 1, pf_s_down = 1;
     // captured graphs per attention mode: [0] the split attention
@@ -1309,8 +1309,9 @@ int pf_alloc(qg_model *m)
         (rc = dalloc(m, &m->pf_qkv, m->pf_s_qkv * T * ldq)) || (rc = dalloc(m, &m->pf_ao, T * m->q_dim)) ||
         (rc = dalloc(m, &m->pf_ao2, m->pf_s_o * T * E)) || (rc = dalloc(m, &m->pf_g, m->pf_s_gu * T * 2 * H)) ||
         (rc = dalloc(m, &m->pf_fo, m->pf_s_down * T * E)) || (rc = dalloc(m, &m->pf_last, E)) ||
-        (rc = dalloc(m, &m->pf_xp, 2 * T * kmax)) || (rc = dalloc(m, &m->pf_rec, T * (kmax / 32 + 1))) ||
-        (rc = dalloc(m, &m->pf_work, T * (kmax + 128))) ||
+        (rc = dalloc(m, &m->pf_xp, 2 * T * kmax)) ||
+        (rc = dalloc(m, &m->pf_rec, T * (kmax / 32 + (kmax + 255) / 256))) ||
+        (rc = dalloc(m, &m->pf_ss, T * ((E + 255) / 256))) ||
         (rc = dalloc(m, &m->pf_tok, (size_t)m->cfg.max_seq_len)))
         return rc;
     return QG_OK;
@@ -1334,14 +1335,18 @@ qg::PfMat pf_mat(const qg_mat *mat, float *y)
     return qg::PfMat{mat->type, mat->d_rp, mat->rows, y, true, mat->plan.g, mat->plan.ni, (size_t)mat->plan.group_bytes};
 }
 
-// f16 pieces of x = f(a, b) for the chunk's tokens (scaled per token); a and b of na / nb slices
-// kPfMaxTokens * lda floats apart
+// f16 pieces of x = f(a, b) for the chunk's tokens (scaled per 256-element
+// group); a and b of na / nb slices kPfMaxTokens * lda floats apart.  Mode 1
+// (the RMSNorm's numerator) leaves its sums of squares in m->pf_ss, which the
+// consumer of the GEMM's output (pf_qkv_post_k, the mode-2 call: `pre`)
+// turns into 1 / rms.
 int pf_planes(qg_model *m, const float *a, uint32_t na, const float *b, uint32_t nb, float *sum_out, const float *nw,
-              size_t n, size_t lda, int mode, uint32_t ntok)
+              size_t n, size_t lda, int mode, bool pre, uint32_t ntok)
 {
-    const int r = qg::launch_pf_planes(a, na, b, nb, (size_t)qg::kPfMaxTokens * lda, sum_out, nw, m->cfg.norm_eps, n,
-                                       lda, mode, m->pf_xp, m->pf_rec, m->pf_work, ntok,
-                                       (ihipStream_t *)m->ctx->stream);
+    const size_t E = m->cfg.embed_dim;
+    const int r = qg::launch_pf_planes(a, na, b, nb, (size_t)qg::kPfMaxTokens * lda, sum_out, nw, n, lda, mode,
+                                       pre ? m->pf_ss : nullptr, E, m->cfg.norm_eps, m->pf_ss, m->pf_xp, m->pf_rec,
+                                       ntok, (ihipStream_t *)m->ctx->stream);
     return r ? mfail(m, QG_ERR_HIP, "prefill planes launch", hipGetLastError()) : QG_OK;
 }
 
@@ -1369,10 +1374,12 @@ int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
         // the residual stream entering the layer: the embeddings, or h + fo of
         // the previous layer (written to the other buffer), then attn_norm
         if (l) {
-            if ((rc = pf_planes(m, h, 1, m->pf_fo, m->pf_s_down, h2, m->vec[QG_V_ATTN_NORM][l], E, E, 1, ntok)))
+            if ((rc = pf_planes(m, h, 1, m->pf_fo, m->pf_s_down, h2, m->vec[QG_V_ATTN_NORM][l], E, E, 1, false,
+                                ntok)))
                 return rc;
             std::swap(h, h2);
-        } else if ((rc = pf_planes(m, h, 1, nullptr, 0, nullptr, m->vec[QG_V_ATTN_NORM][l], E, E, 1, ntok))) {
+        } else if ((rc = pf_planes(m, h, 1, nullptr, 0, nullptr, m->vec[QG_V_ATTN_NORM][l], E, E, 1, false,
+                                   ntok))) {
             return rc;
         }
         const qg::PfMat qkv[3] = {pf_mat(m->w[QG_M_WQ - 2][l], m->pf_qkv),
@@ -1380,25 +1387,26 @@ int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
                                   pf_mat(m->w[QG_M_WV - 2][l], m->pf_qkv + m->q_dim + m->kv_dim)};
         if ((rc = pf_gemm(m, qkv, 3, E, ntok, ldq, m->pf_s_qkv))) return rc;
         float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
-        if (qg::launch_pf_qkv_post(m->pf_qkv, ldq, m->pf_s_qkv, T * ldq, m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l],
-                                   m->vec[QG_V_BV][l], kc, vc, m->cos_t, m->sin_t, m->q_dim, m->kv_dim, m->hd, s0, s0,
-                                   ntok, sti) ||
+        if (qg::launch_pf_qkv_post(m->pf_qkv, ldq, m->pf_s_qkv, T * ldq, m->pf_ss, E, c.norm_eps,
+                                   m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
+                                   m->sin_t, m->q_dim, m->kv_dim, m->hd, s0, s0, ntok, sti) ||
             qg::launch_pf_attention(m->pf_qkv, ldq, kc, vc, m->pf_ao, c.n_heads, m->hd, m->kv_dim, m->n_rep, scale, s0,
                                     ntok, att_lds, sti))
             return mfail(m, QG_ERR_HIP, "prefill attention", hipGetLastError());
         const qg::PfMat wo = pf_mat(m->w[QG_M_WO - 2][l], m->pf_ao2);
-        if ((rc = pf_planes(m, m->pf_ao, 1, nullptr, 0, nullptr, nullptr, m->q_dim, m->q_dim, 0, ntok)) ||
+        if ((rc = pf_planes(m, m->pf_ao, 1, nullptr, 0, nullptr, nullptr, m->q_dim, m->q_dim, 0, false, ntok)) ||
             (rc = pf_gemm(m, &wo, 1, m->q_dim, ntok, E, m->pf_s_o)))
             return rc;
         // h = h + attention output; MLP input = ffn_norm(h) (transformer.rs:31-46)
-        if ((rc = pf_planes(m, h, 1, m->pf_ao2, m->pf_s_o, h2, m->vec[QG_V_FFN_NORM][l], E, E, 1, ntok))) return rc;
+        if ((rc = pf_planes(m, h, 1, m->pf_ao2, m->pf_s_o, h2, m->vec[QG_V_FFN_NORM][l], E, E, 1, false, ntok)))
+            return rc;
         std::swap(h, h2);
         const qg::PfMat gu[2] = {pf_mat(m->w[QG_M_GATE - 2][l], m->pf_g), pf_mat(m->w[QG_M_UP - 2][l], m->pf_g + H)};
         if ((rc = pf_gemm(m, gu, 2, E, ntok, 2 * H, m->pf_s_gu))) return rc;
         // down(silu(gate) * up) (mlp.rs:36-45)
         const qg::PfMat down = pf_mat(m->w[QG_M_DOWN - 2][l], m->pf_fo);
         if ((rc = pf_planes(m, m->pf_g, m->pf_s_gu, m->pf_g + H, m->pf_s_gu, nullptr, nullptr, H, 2 * (size_t)H, 2,
-                            ntok)) ||
+                            true, ntok)) ||
             (rc = pf_gemm(m, &down, 1, H, ntok, E, m->pf_s_down)))
             return rc;
     }

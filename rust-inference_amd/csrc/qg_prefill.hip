@@ -6,23 +6,27 @@
 // Transformer::forward per token).  Here every projection of a chunk of up
 // to kPfMaxTokens tokens is one GEMM on the matrix cores:
 //
-//   * pf_stat_k, pf_split_k: each token's input vector x (RMSNorm of the residual
-//     stream, the attention output, or silu(g) * u) scaled by a power of two
-//     2^e (its largest magnitude into [512, 1024)) and split into two f16
-//     pieces xs = x 2^e = hi + lo (hi the rounding of xs, lo the rounding of
-//     what hi leaves: 22 significant bits together), written chunk by chunk
-//     in the layout of the GEMM's LDS buffers; per 32-element segment the
-//     sum of xs (as two f16 pieces); per token 2^-e;
-//   * pf_gemm_k: y[t][r] = 2^-e (sum over blocks of d D + sum over
-//     sub-blocks of -dmin m S) with D = sum over the block's elements of
-//     xs B from chained v_mfma_f32_16x16x32_f16 (A: 16 tokens x 32 elements
-//     of one piece, B: 32 weights x 16 rows).  B holds integers that f16
-//     represents exactly -- sc q for Q4_K / Q5_K (at most 63 * 31), the two
-//     parts 16 a q' and b q' of sc q' (sc = 16 a + b) for Q6_K, q for Q8_0
-//     -- so every product is exact and accumulates in f32; the block scale
-//     d multiplies D once per block (per sub-block for Q8_0) and the
-//     K-quant min terms -dmin sum m S are one v_mfma_f32_16x16x16_f16 per 4
-//     sub-blocks (A: S, the sums of xs, as two f16 pieces; B: m, exact);
+//   * pf_split_k: each token's input vector x (the RMSNorm's numerator (h + o)
+//     * nw of the residual stream, the attention output, or silu(g) * u)
+//     scaled per 256-element group g by a power of two 2^e_g (the group's
+//     largest magnitude into [512, 1024)) and split into two f16 pieces
+//     xs = x 2^e_g = hi + lo (hi the rounding of xs, lo the rounding of what
+//     hi leaves: 22 significant bits together), written chunk by chunk in the
+//     layout of the GEMM's LDS buffers; per 32-element segment the sum of xs
+//     (as two f16 pieces); per group 2^-e_g; with the norm, the partial sums
+//     of squares per group (the consumer of the GEMM's output applies
+//     1 / rms);
+//   * pf_gemm_k: y[t][r] = sum over blocks of 2^-e_g (d D + sum over the
+//     block's sub-blocks of -dmin m S) with D = sum over the block's
+//     elements of xs B from chained v_mfma_f32_16x16x32_f16 (A: 16 tokens x
+//     32 elements of one piece, B: 32 weights x 16 rows).  B holds integers
+//     that f16 represents exactly -- sc q for Q4_K / Q5_K (at most 63 * 31),
+//     the two parts 16 a q' and b q' of sc q' (sc = 16 a + b) for Q6_K, q for
+//     Q8_0 -- so every product is exact and accumulates in f32; d 2^-e_g
+//     multiplies D once per block (per sub-block for Q8_0; per chunk where a
+//     row's blocks straddle the groups) and the K-quant min terms -dmin sum
+//     m S are one v_mfma_f32_16x16x16_f16 per 4 sub-blocks (A: S, the sums of
+//     xs, as two f16 pieces; B: m, exact);
 //   * pf_qkv_post_k, pf_attention_k: bias, RoPE and KV append of every token
 //     (attention.rs:66-90), causal attention of every token over the cache up
 //     to its own slot (attention.rs:93-121), as the decode path.
@@ -516,7 +520,8 @@ constexpr uint32_t kPfR = QG_PF_R;                           // 16-row tiles per
 constexpr uint32_t kPfWaves = QG_PF_WAVES;                   // waves per workgroup
 constexpr uint32_t kPfRows = 16u * kPfR * kPfWaves;          // rows per workgroup tile
 constexpr uint32_t kPfBufX = kPfKC * 2u * 64u * 64u;         // bytes of x pieces per buffer
-constexpr uint32_t kPfBuf = kPfBufX + kPfKC * 256u;          // ... and of the sums
+constexpr uint32_t kPfBufS = kPfBufX + kPfKC * 256u;         // ... and of the sums, then the group scales
+constexpr uint32_t kPfBuf = kPfBufS + 256u;
 constexpr uint32_t kPfLds = 2u * kPfBuf;                     // two buffers
 
 // 16 bytes per lane from global memory straight into LDS at byte m0 + 16 lane
@@ -526,6 +531,12 @@ constexpr uint32_t kPfLds = 2u * kPfBuf;                     // two buffers
 __device__ __forceinline__ void pf_dma16(const void *gp, uint32_t lds_addr)
 {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(lds_addr) : "memory");
+}
+
+// 4 bytes per lane, to LDS at byte m0 + 4 lane (global_load_lds_dword)
+__device__ __forceinline__ void pf_dma4(const void *gp, uint32_t lds_addr)
+{
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gp), "{m0}"(lds_addr) : "memory");
 }
 
 // The registers of x are (re)defined here: an empty asm statement that reads
@@ -560,9 +571,11 @@ __device__ __forceinline__ size_t pf_xoff(uint32_t chunk, uint32_t u, uint32_t t
 
 // Issue part `part` (of kPfKC) of the copies of chunk kc into the buffer at
 // LDS byte address b0: x blocks u = 8 part .. 8 part + 7 (each one
-// contiguous KB), and with part 0 the chunk's 4 x 64 sums.
+// contiguous KB), with part 0 the chunk's 4 x 64 sums, with part 1 the 64
+// token scales 2^-e_g of its 256-element group (scl: the scales of group 0).
 __device__ __forceinline__ void pf_stage(const uint8_t *__restrict__ xp, const float *__restrict__ rec,
-                                         uint32_t kc, uint32_t b0, uint32_t wave, uint32_t lane, uint32_t part)
+                                         const float *__restrict__ scl, uint32_t kc, uint32_t b0, uint32_t wave,
+                                         uint32_t lane, uint32_t part)
 {
 #pragma unroll
     for (uint32_t v = 0; v < 8u / kPfWaves; v++) {
@@ -570,6 +583,7 @@ __device__ __forceinline__ void pf_stage(const uint8_t *__restrict__ xp, const f
         pf_dma16(xp + pf_xoff(kc / kPfKC, u, 0, 0) + 16u * lane, b0 + u * 1024u);
     }
     if (part == 0 && wave == 0) pf_dma16(rec + (size_t)kc * 64u + 4u * lane, b0 + kPfBufX);
+    if (part == 1 && wave == 0) pf_dma4(scl + (size_t)(kc / 8u) * 64u + lane, b0 + kPfBufS);
 }
 
 // The same for a phase chunk (block b, half ph): its sub-blocks kk' = 0, 1
@@ -577,8 +591,8 @@ __device__ __forceinline__ void pf_stage(const uint8_t *__restrict__ xp, const f
 // = 2, 3 those of the second (2 b + 1); the buffer gets the layout of a
 // plain chunk.
 __device__ __forceinline__ void pf_stage_ph(const uint8_t *__restrict__ xp, const float *__restrict__ rec,
-                                            uint32_t b, uint32_t ph, uint32_t b0, uint32_t wave, uint32_t lane,
-                                            uint32_t part)
+                                            const float *__restrict__ scl, uint32_t b, uint32_t ph, uint32_t b0,
+                                            uint32_t wave, uint32_t lane, uint32_t part)
 {
     const uint32_t src_kk = 2u * ph + (part & 1u), chunk = 2u * b + (part >> 1);
 #pragma unroll
@@ -591,6 +605,7 @@ __device__ __forceinline__ void pf_stage_ph(const uint8_t *__restrict__ xp, cons
         const uint32_t kk = lane >> 4, sub = 8u * b + 4u * (kk >> 1) + 2u * ph + (kk & 1u);
         pf_dma16(rec + (size_t)sub * 64u + 4u * (lane & 15u), b0 + kPfBufX);
     }
+    if (part == 1 && wave == 0) pf_dma4(scl + (size_t)b * 64u + lane, b0 + kPfBufS);
 }
 
 // One workgroup's share of a grouped GEMM: rows row0 .. row0 + 16 kPfR
@@ -624,6 +639,7 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
     constexpr bool PH = (T == T_Q4_K || T == T_Q5_K) && AL;
     using Ck = std::conditional_t<RPL, typename P::CR, typename P::C>;
     const uint8_t *xb8 = (const uint8_t *)xp;
+    const float *scl = rec + (size_t)nseg * 64u;                     // 2^-e_g of group 0
     const uint32_t lane = threadIdx.x & 63u, kq = lane >> 4, c16 = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
@@ -727,9 +743,9 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             if constexpr (PH) {
                 uint32_t b, ph;
                 slot(kc, b, ph);
-                pf_stage_ph(xb8, rec, b, ph, b0, wave, lane, part);
+                pf_stage_ph(xb8, rec, scl, b, ph, b0, wave, lane, part);
             } else {
-                pf_stage(xb8, rec, kc, b0, wave, lane, part);
+                pf_stage(xb8, rec, scl, kc, b0, wave, lane, part);
             }
         };
 #pragma unroll
@@ -762,6 +778,17 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
             {   // (waves past the matrix compute too -- clamped rows, never stored -- so that
                 // this phase stays one block of straight-line code)
                 const uint8_t *xb = lds + buf * kPfBuf;
+                // 2^-e_g of the chunk's 256-element group for the lane's 16
+                // tokens 16 tt + 4 kq + e
+                float sg[4][4];
+                {
+                    const float4 *sp = (const float4 *)(xb + kPfBufS);
+#pragma unroll
+                    for (uint32_t tt = 0; tt < 4; tt++) {
+                        const float4 q = sp[4u * tt + kq];
+                        sg[tt][0] = q.x; sg[tt][1] = q.y; sg[tt][2] = q.z; sg[tt][3] = q.w;
+                    }
+                }
                 // min terms: A = the sums of the chunk's sub-blocks 2 (kq & 1),
                 // 2 (kq & 1) + 1 as f16 pieces (K slots 2 kk + piece; zero for kq >= 2)
                 v4f Dm[R][4];
@@ -812,48 +839,67 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
                             for (int tt = 0; tt < 4; tt++) {
 #pragma unroll
                                 for (int e = 0; e < 4; e++)
-                                    acc[i][tt][e] = __builtin_fmaf(op.dsc[i][kk], D[i][tt][e], acc[i][tt][e]);
+                                    acc[i][tt][e] = __builtin_fmaf(op.dsc[i][kk] * sg[tt][e], D[i][tt][e], acc[i][tt][e]);
                                 D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
                             }
                     }
                 }
-                if constexpr (P::MIN) {
-                    // the chunk's -dmin m S terms, from the v_mfma_f32_16x16x16_f16
-                    // products taken before this chunk's main MFMAs
+                if constexpr (PH) {
+                    // every chunk ends its D: d D and the chunk's -dmin m S
+                    // terms (the v_mfma_f32_16x16x16_f16 products taken before
+                    // this chunk's main MFMAs), times 2^-e_g
 #pragma unroll
                     for (int i = 0; i < R; i++)
 #pragma unroll
-                        for (uint32_t tt = 0; tt < 4; tt++)
+                        for (uint32_t tt = 0; tt < 4; tt++) {
 #pragma unroll
-                            for (int e = 0; e < 4; e++)
-                                acc[i][tt][e] = __builtin_fmaf(-op.dmn[i], Dm[i][tt][e], acc[i][tt][e]);
-                }
-                if constexpr (!Q8) {
-                    // a row's block ends with this chunk (jb = 4), or the slice does
-                    const bool last = kc + kPfKC >= k1;
-                    if constexpr (AL) {
-                        if (op.jb[0] == 4u || last) {
+                            for (int e = 0; e < 4; e++) {
+                                const float u = __builtin_fmaf(op.dsc[i][0], D[i][tt][e], -op.dmn[i] * Dm[i][tt][e]);
+                                acc[i][tt][e] = __builtin_fmaf(sg[tt][e], u, acc[i][tt][e]);
+                            }
+                            D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+                        }
+                } else {
+                    if constexpr (P::MIN) {
+                        // the chunk's -dmin m S terms, from the v_mfma_f32_16x16x16_f16
+                        // products taken before this chunk's main MFMAs
+#pragma unroll
+                        for (int i = 0; i < R; i++)
+#pragma unroll
+                            for (uint32_t tt = 0; tt < 4; tt++)
+#pragma unroll
+                                for (int e = 0; e < 4; e++)
+                                    acc[i][tt][e] =
+                                        __builtin_fmaf(-op.dmn[i] * sg[tt][e], Dm[i][tt][e], acc[i][tt][e]);
+                    }
+                    if constexpr (!Q8) {
+                        if constexpr (AL) {
+                            // a row's block ends with this chunk (jb = 4), or the
+                            // slice does; the block's two chunks share a group
+                            if (op.jb[0] == 4u || kc + kPfKC >= k1) {
+#pragma unroll
+                                for (int i = 0; i < R; i++)
+#pragma unroll
+                                    for (int tt = 0; tt < 4; tt++) {
+#pragma unroll
+                                        for (int e = 0; e < 4; e++)
+                                            acc[i][tt][e] = __builtin_fmaf(op.dsc[i][0] * sg[tt][e], D[i][tt][e],
+                                                                           acc[i][tt][e]);
+                                        D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+                                    }
+                            }
+                        } else {
+                            // rows whose blocks straddle the 256-element groups:
+                            // every chunk ends D
 #pragma unroll
                             for (int i = 0; i < R; i++)
 #pragma unroll
                                 for (int tt = 0; tt < 4; tt++) {
 #pragma unroll
                                     for (int e = 0; e < 4; e++)
-                                        acc[i][tt][e] = __builtin_fmaf(op.dsc[i][0], D[i][tt][e], acc[i][tt][e]);
+                                        acc[i][tt][e] =
+                                            __builtin_fmaf(op.dsc[i][0] * sg[tt][e], D[i][tt][e], acc[i][tt][e]);
                                     D[i][tt] = v4f{0.f, 0.f, 0.f, 0.f};
-                                }
-                        }
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < R; i++) {
-                            const bool fl = op.jb[i] == 4u || last;
-                            const float d = fl ? op.dsc[i][0] : 0.0f;
-#pragma unroll
-                            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                                for (int e = 0; e < 4; e++) {
-                                    acc[i][tt][e] = __builtin_fmaf(d, D[i][tt][e], acc[i][tt][e]);
-                                    D[i][tt][e] = fl ? 0.0f : D[i][tt][e];
                                 }
                         }
                     }
@@ -865,13 +911,6 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
         }
     }
     if (!active) return;
-    // 2^-e of the lane's 16 tokens (clamped: tokens past the chunk are not stored)
-    const float *tsc = rec + (size_t)nseg * 64u;
-    float ts[4][4];
-#pragma unroll
-    for (uint32_t tt = 0; tt < 4; tt++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) ts[tt][e] = tsc[min(16u * tt + 4u * kq + (uint32_t)e, ntok - 1u)];
 #pragma unroll
     for (int i = 0; i < R; i++) {
         const uint32_t r = row0 + 16u * i + c16;
@@ -881,7 +920,7 @@ __device__ __forceinline__ void pf_gemm_rows(const uint8_t *__restrict__ w, uint
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t t = 16u * tt + 4u * kq + (uint32_t)e;
-                if (t < ntok) __builtin_nontemporal_store(acc[i][tt][e] * ts[tt][e], &y[(size_t)t * ldy + r]);
+                if (t < ntok) __builtin_nontemporal_store(acc[i][tt][e], &y[(size_t)t * ldy + r]);
             }
         }
     }
@@ -930,23 +969,25 @@ __global__ void __launch_bounds__(64 * kPfWaves) pf_gemm_k(PfJobs jobs, uint32_t
 
 // ---------------------------------------------------------------- planes
 //
-// The input vector x of token blockIdx.y (mode 0: a; mode 1: rmsnorm(a + b)
-// * nw with a + b stored to sum_out when given; mode 2: silu(a) * b) as the
-// two f16 pieces of xs = x 2^e (in the GEMM's chunk images, pf_xoff), the
-// sums of xs per 32-element segment (two f16 pieces), and 2^-e.  a and b may
-// be the K-split slices of a GEMM (na, nb <= kPfMaxSlices slices sstride
-// floats apart, summed in slice order).  Two launches of pf_planes_blk(n) workgroups
-// per token over 8-element pieces (a quarter of a 32-element segment each;
-// the four threads of a segment combine their sums through lane shuffles):
-// pf_stat_k -- per workgroup the statistics the scale needs (modes 0, 2:
-// max |x|, mode 1: sum v^2 and max |v nw| for v = a + b, x = v / rms * nw);
-// mode 2 keeps x (f32) in work, mode 1 writes sum_out -- then pf_split_k:
-// the row's scale from every workgroup's statistics, the pieces, the sums
-// and 2^-e.  A token with a non-finite x gets 2^-e = NaN (every output of
-// its row NaN).  sum_out must not alias a or b.
+// The input vector x of token blockIdx.y -- mode 0: x = a; mode 1: x = (a +
+// b) * nw, the RMSNorm's numerator, with a + b stored to sum_out when given
+// and the partial sums of (a + b)^2 per 256-element group in ss_out; mode 2:
+// x = silu(a r) * (b r), r = 1 / rms of the norm whose partial sums are at
+// `pre` (r = 1 without) -- as the two f16 pieces of xs = x 2^e_g, every
+// 256-element group g with its own e_g (in the GEMM's chunk images,
+// pf_xoff), the sums of xs per 32-element segment (two f16 pieces), and
+// 2^-e_g.  A GEMM over such an x gives y = W x' with x' = (a + b) * nw in mode
+// 1: the consumer of y multiplies it by 1 / rms (math.rs:237-257: the norm's
+// factor is common to the row, so it moves past the product), from the
+// partial sums (pf_inv_rms).  a and b may be the K-split slices of a GEMM
+// (na, nb <= kPfMaxSlices slices sstride floats apart, summed in slice
+// order).  One launch of pf_planes_blk(n) workgroups per token over 8-element
+// pieces: 32 threads hold a 256-element group and find its maximum through
+// lane shuffles, 4 threads a 32-element segment.  A group with a non-finite
+// x gets 2^-e_g = NaN (every output of its token NaN).  sum_out must not alias
+// a or b.
 constexpr uint32_t kPfMaxSlices = 16;
 constexpr uint32_t kPfPlanesT = 256;                         // threads per workgroup
-constexpr uint32_t kPfMaxBlk = 64;                           // workgroups per token at most
 
 // silu(x) = x / (1 + exp(-x)), in the two branches of math.rs:137-146
 __device__ __forceinline__ float silu1(float x)
@@ -1027,108 +1068,91 @@ __device__ __forceinline__ float pf_block_reduce(float v, float *red)
 // workgroups per token for rows of n elements: one 8-element piece per thread
 __host__ __device__ constexpr uint32_t pf_planes_blk(uint32_t n) { return (n / 8u + kPfPlanesT - 1u) / kPfPlanesT; }
 
-__global__ void __launch_bounds__(kPfPlanesT) pf_stat_k(const float *__restrict__ a, uint32_t na,
-                                                        const float *__restrict__ b, uint32_t nb, uint64_t sstride,
-                                                        float *__restrict__ sum_out, const float *__restrict__ nw,
-                                                        uint32_t n, uint32_t lda, uint32_t mode,
-                                                        float *__restrict__ work, float *__restrict__ rec)
+// 1 / rms of token t from the partial sums of squares of its ng groups
+// (math.rs:253-255): lane g of every wave loads groups g, g + 64, ..., the
+// wave adds them with a fixed butterfly, and lane 0's sum is taken, so every
+// thread gets the same value, run after run.
+__device__ __forceinline__ float pf_inv_rms(const float *__restrict__ ss, uint32_t ng, uint32_t t, uint32_t n,
+                                            float eps)
 {
-    __shared__ float red[kPfPlanesT / 64u];
-    const uint32_t t = blockIdx.y, j = blockIdx.x * kPfPlanesT + threadIdx.x, nblk = gridDim.x;
-    const float *at = a + (size_t)t * lda, *bt = b ? b + (size_t)t * lda : nullptr;
-    float s0 = 0.f, s1 = 0.f;                                         // mode 1: sum v^2, max |v nw|; else max |x|
+    const float *p = ss + (size_t)t * ng;
+    const uint32_t lane = threadIdx.x & 63u;
+    float r = 0.f;
+    for (uint32_t g = lane; g < ng; g += 64u) r += p[g];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) r += __shfl_xor(r, o, 64);
+    r = __shfl(r, 0, 64);
+    return 1.0f / sqrtf(r / (float)n + eps);
+}
+
+__global__ void __launch_bounds__(kPfPlanesT) pf_split_k(const float *__restrict__ a, uint32_t na,
+                                                         const float *__restrict__ b, uint32_t nb, uint64_t sstride,
+                                                         float *__restrict__ sum_out, const float *__restrict__ nw,
+                                                         uint32_t n, uint32_t lda, uint32_t mode,
+                                                         const float *__restrict__ pre, uint32_t pre_ng,
+                                                         uint32_t pre_n, float eps, float *__restrict__ ss_out,
+                                                         uint16_t *__restrict__ xp, float *__restrict__ rec)
+{
+    const uint32_t t = blockIdx.y, j = blockIdx.x * kPfPlanesT + threadIdx.x, ng = (n + 255u) / 256u;
+    const bool live = j < n / 8u;
+    const uint32_t e0 = live ? 8u * j : 0u;
+    float v[8];
     bool bad = false;
-    if (j < n / 8u) {
-        float v[8];
-        pf_input8(at, na, bt, nb, sstride, mode, 8u * j, v);
+    float ss = 0.f;
+    {
+        const float *at = a + (size_t)t * lda, *bt = b ? b + (size_t)t * lda : nullptr;
+        sum8_slices(at + e0, na, sstride, v);
+        if (bt) {
+            float u[8];
+            sum8_slices(bt + e0, nb, sstride, u);
+            if (mode == 2) {
+                const float r = pre ? pf_inv_rms(pre, pre_ng, t, pre_n, eps) : 1.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = silu1(v[e] * r) * (u[e] * r);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] += u[e];
+            }
+        }
         if (mode == 1) {
-            if (sum_out) {
-                float *so = sum_out + (size_t)t * lda + 8u * j;
+            if (sum_out && live) {
+                float *so = sum_out + (size_t)t * lda + e0;
                 *(float4 *)so = make_float4(v[0], v[1], v[2], v[3]);
                 *(float4 *)(so + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float w = nw[8u * j + e];
-                s0 += v[e] * v[e];
-                s1 = fmaxf(s1, fabsf(v[e] * w));
-                bad |= !__builtin_isfinite(v[e]) || !__builtin_isfinite(w);
-            }
-        } else {
-            if (mode == 2) {
-                float *xw = work + (size_t)t * n + 8u * j;
-                *(float4 *)xw = make_float4(v[0], v[1], v[2], v[3]);
-                *(float4 *)(xw + 4) = make_float4(v[4], v[5], v[6], v[7]);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                s1 = fmaxf(s1, fabsf(v[e]));
-                bad |= !__builtin_isfinite(v[e]);
+                ss += v[e] * v[e];
+                v[e] = v[e] * nw[e0 + e];
             }
         }
     }
-    if (mode == 1) s0 = pf_block_reduce<false>(s0, red);
-    s1 = pf_block_reduce<true>(s1, red);
-    bad = __syncthreads_or(bad);
-    if (threadIdx.x == 0) {
-        float *pt = work + (size_t)qg::kPfMaxTokens * n + ((size_t)t * nblk + blockIdx.x) * 2u;
-        pt[0] = s0;
-        pt[1] = bad ? __builtin_nanf("") : s1;
-        if (blockIdx.x == 0) rec[(size_t)(n / 32u) * 64u + t] = 0.0f;   // 2^-e, raised by pf_split_k
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        bad |= !__builtin_isfinite(v[e]);
+        m = fmaxf(m, fabsf(v[e]));
     }
-}
-
-__global__ void __launch_bounds__(kPfPlanesT) pf_split_k(const float *__restrict__ a, uint32_t na,
-                                                         const float *__restrict__ b, uint32_t nb, uint64_t sstride,
-                                                         const float *__restrict__ sum_out,
-                                                         const float *__restrict__ nw, float eps, uint32_t n,
-                                                         uint32_t lda, uint32_t mode, const float *__restrict__ work,
-                                                         uint16_t *__restrict__ xp, float *__restrict__ rec)
-{
-    const uint32_t t = blockIdx.y, j = blockIdx.x * kPfPlanesT + threadIdx.x, nblk = gridDim.x;
-    // the row's statistics, in workgroup order
-    const float *pt = work + (size_t)qg::kPfMaxTokens * n + (size_t)t * nblk * 2u;
-    float ss = 0.f, mx = 0.f;
-    bool bad = false;
-    for (uint32_t i = 0; i < nblk; i++) {
-        ss += pt[2u * i];
-        const float m = pt[2u * i + 1u];
-        bad |= !__builtin_isfinite(m);
-        mx = fmaxf(mx, m);
+    if (!live) {
+        m = 0.f;
+        ss = 0.f;
+        bad = false;
     }
-    float inv = 1.0f;
-    if (mode == 1) {
-        inv = 1.0f / sqrtf(ss / (float)n + eps);                      // math.rs:253-255
-        mx *= inv;
+    // the group's maximum, sum of squares and badness over its 32 lanes
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+        m = fmaxf(m, __shfl_xor(m, o, 64));
+        ss += __shfl_xor(ss, o, 64);
+        bad |= __shfl_xor((int)bad, o, 64) != 0;
     }
-    // 2^e brings the largest magnitude into [512, 1024) (an estimate that
-    // overflowed: the smallest scale)
+    // 2^e_g brings the group's largest magnitude into [512, 1024)
     int E = 0;
-    (void)frexpf(mx, &E);
-    const int e = !__builtin_isfinite(mx) ? -126 : mx > 0.f ? min(max(10 - E, -126), 126) : 0;
+    (void)frexpf(m, &E);
+    const int e = bad ? 0 : m > 0.f ? min(max(10 - E, -126), 126) : 0;
     const float sc = ldexpf(1.0f, e);
-    if (j < n / 8u) {
-        float v[8];
-        const uint32_t e0 = 8u * j;
-        if (mode == 2) {
-            const float *xw = work + (size_t)t * n + e0;
-            const float4 p0 = *(const float4 *)xw, p1 = *(const float4 *)(xw + 4);
-            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-        } else if (mode == 1 && sum_out) {
-            const float *so = sum_out + (size_t)t * lda + e0;
-            const float4 p0 = *(const float4 *)so, p1 = *(const float4 *)(so + 4);
-            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-        } else {
-            pf_input8(a + (size_t)t * lda, na, b ? b + (size_t)t * lda : nullptr, nb, sstride, mode, e0, v);
-        }
-        if (mode == 1)
+    if (live) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = v[k] * inv * nw[e0 + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            bad |= !__builtin_isfinite(v[k]);
-            v[k] = v[k] * sc;
-        }
+        for (int k = 0; k < 8; k++) v[k] = v[k] * sc;
         uint32_t wh[4], wl[4];
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
@@ -1142,21 +1166,20 @@ __global__ void __launch_bounds__(kPfPlanesT) pf_split_k(const float *__restrict
         uint8_t *p0 = (uint8_t *)xp + pf_xoff(k / kPfKC, (k % kPfKC) * 8u + (t >> 4), t16, (j & 3u) ^ pf_swz(t16));
         *(uint4 *)p0 = make_uint4(wh[0], wh[1], wh[2], wh[3]);
         *(uint4 *)(p0 + 4u * 1024u) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
-        // per quarter (x0 + x1) + (x2 + x3) ..., per half the two quarters, the segment the two halves
-        const float qsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-        const float hsum = qsum + __shfl_xor(qsum, 1, 64);
-        const float seg = hsum + __shfl_xor(hsum, 2, 64);
-        if ((j & 3u) == 0u) {                                         // as two f16 pieces, hi | lo << 16
-            const _Float16 sh = (_Float16)seg, sl = (_Float16)(seg - (float)sh);
-            ((uint32_t *)rec)[(size_t)k * 64u + t] =
-                (uint32_t)__builtin_bit_cast(uint16_t, sh) | ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
-        }
     }
-    // 2^-e, or NaN when any x of the row is not finite: the largest value any
-    // workgroup writes (the bits of a NaN exceed those of every finite float)
-    if (__syncthreads_or(bad) ? threadIdx.x == 0 : (blockIdx.x == 0 && threadIdx.x == 0)) {
-        const float r = bad ? __builtin_nanf("") : ldexpf(1.0f, -e);
-        atomicMax((unsigned int *)(rec + (size_t)(n / 32u) * 64u + t), __float_as_uint(r));
+    // per quarter (x0 + x1) + (x2 + x3) ..., per half the two quarters, the segment the two halves
+    const float qsum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    const float hsum = qsum + __shfl_xor(qsum, 1, 64);
+    const float seg = hsum + __shfl_xor(hsum, 2, 64);
+    if (live && (j & 3u) == 0u) {                                     // as two f16 pieces, hi | lo << 16
+        const _Float16 sh = (_Float16)seg, sl = (_Float16)(seg - (float)sh);
+        ((uint32_t *)rec)[(size_t)(j >> 2) * 64u + t] =
+            (uint32_t)__builtin_bit_cast(uint16_t, sh) | ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
+    }
+    if (live && (j & 31u) == 0u) {
+        const uint32_t g = j >> 5;
+        rec[(size_t)(n / 32u) * 64u + (size_t)g * 64u + t] = bad ? __builtin_nanf("") : ldexpf(1.0f, -e);
+        if (mode == 1) ss_out[(size_t)t * ng + g] = ss;
     }
 }
 
@@ -1176,7 +1199,8 @@ __global__ void __launch_bounds__(256) pf_sum_k(const float *__restrict__ x, uin
 // the rotated q goes to slice 0.  The expressions of the decode path's
 // qkv_post_k.
 __global__ void __launch_bounds__(256) pf_qkv_post_k(float *__restrict__ qkv, uint32_t ldq, uint32_t ns,
-                                                     uint64_t sstride, const float *__restrict__ bq,
+                                                     uint64_t sstride, const float *__restrict__ ss, uint32_t ss_ng,
+                                                     uint32_t ss_n, float eps, const float *__restrict__ bq,
                                                      const float *__restrict__ bk, const float *__restrict__ bv,
                                                      float *__restrict__ kc, float *__restrict__ vc,
                                                      const float *__restrict__ cos_t, const float *__restrict__ sin_t,
@@ -1186,22 +1210,26 @@ __global__ void __launch_bounds__(256) pf_qkv_post_k(float *__restrict__ qkv, ui
     const uint32_t t = blockIdx.y, i0 = 2 * (blockIdx.x * blockDim.x + threadIdx.x), half = hd / 2;
     const uint32_t pos = pos0 + t, slot = slot0 + t;
     float *q = qkv + (size_t)t * ldq, *k = q + q_dim, *v = k + kv_dim;
+    // the GEMM took the norm's numerator: its 1 / rms here, before the biases
+    const float r = pf_inv_rms(ss, ss_ng, t, ss_n, eps);
     if (i0 < q_dim) {
         const uint32_t j = (i0 % hd) / 2;
         const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
-        const float x0 = sum_slices(q + i0, ns, sstride) + bq[i0], x1 = sum_slices(q + i0 + 1, ns, sstride) + bq[i0 + 1];
+        const float x0 = sum_slices(q + i0, ns, sstride) * r + bq[i0];
+        const float x1 = sum_slices(q + i0 + 1, ns, sstride) * r + bq[i0 + 1];
         q[i0] = x0 * c - x1 * s;
         q[i0 + 1] = x0 * s + x1 * c;
     }
     if (i0 < kv_dim) {
         const uint32_t j = (i0 % hd) / 2;
         const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
-        const float x0 = sum_slices(k + i0, ns, sstride) + bk[i0], x1 = sum_slices(k + i0 + 1, ns, sstride) + bk[i0 + 1];
+        const float x0 = sum_slices(k + i0, ns, sstride) * r + bk[i0];
+        const float x1 = sum_slices(k + i0 + 1, ns, sstride) * r + bk[i0 + 1];
         float *kr = kc + (size_t)slot * kv_dim, *vr = vc + (size_t)slot * kv_dim;
         kr[i0] = x0 * c - x1 * s;
         kr[i0 + 1] = x0 * s + x1 * c;
-        vr[i0] = sum_slices(v + i0, ns, sstride) + bv[i0];
-        vr[i0 + 1] = sum_slices(v + i0 + 1, ns, sstride) + bv[i0 + 1];
+        vr[i0] = sum_slices(v + i0, ns, sstride) * r + bv[i0];
+        vr[i0 + 1] = sum_slices(v + i0 + 1, ns, sstride) * r + bv[i0 + 1];
     }
 }
 
@@ -1358,21 +1386,20 @@ int launch_pf_gemm(const PfMat *mats, int n_mats, size_t cols, const uint16_t *x
 }
 
 int launch_pf_planes(const float *a, uint32_t na, const float *b, uint32_t nb, size_t sstride, float *sum_out,
-                     const float *nw, float eps, size_t n, size_t lda, int mode, uint16_t *xp, float *rec,
-                     float *work, uint32_t ntok, ihipStream_t *stream)
+                     const float *nw, size_t n, size_t lda, int mode, const float *pre, size_t pre_n, float eps,
+                     float *ss_out, uint16_t *xp, float *rec, uint32_t ntok, ihipStream_t *stream)
 {
     if (ntok == 0) return 0;
     // 16-byte aligned rows and slices (float4 reads); whole chunks
     if (n % 128 != 0 || n == 0 || n > 0xFFFFFFFFull || ntok > kPfMaxTokens || na < 1 || na > qgp::kPfMaxSlices ||
-        (b && (nb < 1 || nb > qgp::kPfMaxSlices)) || (mode == 2 && !b) || (mode == 1 && !nw) || lda % 4 != 0 ||
-        sstride % 4 != 0 || ((uintptr_t)a & 15u) || ((uintptr_t)b & 15u) || ((uintptr_t)sum_out & 15u) ||
-        qgp::pf_planes_blk((uint32_t)n) > qgp::kPfMaxBlk)
+        (b && (nb < 1 || nb > qgp::kPfMaxSlices)) || (mode == 2 && !b) || (mode == 1 && (!nw || !ss_out)) ||
+        (pre && (pre_n == 0 || pre_n > 0xFFFFFFFFull)) || lda % 4 != 0 || sstride % 4 != 0 || ((uintptr_t)a & 15u) ||
+        ((uintptr_t)b & 15u) || ((uintptr_t)sum_out & 15u))
         return -1;
     const dim3 grid(qgp::pf_planes_blk((uint32_t)n), ntok), block(qgp::kPfPlanesT);
-    hipLaunchKernelGGL(qgp::pf_stat_k, grid, block, 0, (hipStream_t)stream, a, na, b, nb, (uint64_t)sstride, sum_out,
-                       nw, (uint32_t)n, (uint32_t)lda, (uint32_t)mode, work, rec);
-    hipLaunchKernelGGL(qgp::pf_split_k, grid, block, 0, (hipStream_t)stream, a, na, b, nb, (uint64_t)sstride,
-                       sum_out, nw, eps, (uint32_t)n, (uint32_t)lda, (uint32_t)mode, work, xp, rec);
+    hipLaunchKernelGGL(qgp::pf_split_k, grid, block, 0, (hipStream_t)stream, a, na, b, nb, (uint64_t)sstride, sum_out,
+                       nw, (uint32_t)n, (uint32_t)lda, (uint32_t)mode, pre, (uint32_t)((pre_n + 255) / 256),
+                       (uint32_t)pre_n, eps, ss_out, xp, rec);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
@@ -1385,16 +1412,19 @@ int launch_pf_sum(const float *x, uint32_t ns, size_t sstride, size_t n, float *
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *bq, const float *bk,
-                       const float *bv, float *kc, float *vc, const float *cos_t, const float *sin_t, uint32_t q_dim,
-                       uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0, uint32_t ntok,
-                       ihipStream_t *stream)
+int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *ss, size_t ss_n, float eps,
+                       const float *bq, const float *bk, const float *bv, float *kc, float *vc, const float *cos_t,
+                       const float *sin_t, uint32_t q_dim, uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0,
+                       uint32_t ntok, ihipStream_t *stream)
 {
     if (ntok == 0) return 0;
-    if (ns < 1 || ns > qgp::kPfMaxSlices || ntok > kPfMaxTokens || hd % 2 != 0) return -1;
+    if (ns < 1 || ns > qgp::kPfMaxSlices || ntok > kPfMaxTokens || hd % 2 != 0 || !ss || ss_n == 0 ||
+        ss_n > 0xFFFFFFFFull)
+        return -1;
     const uint32_t pairs = (q_dim > kv_dim ? q_dim : kv_dim) / 2;
     hipLaunchKernelGGL(qgp::pf_qkv_post_k, dim3((pairs + 255) / 256, ntok), dim3(256), 0, (hipStream_t)stream, qkv,
-                       ldq, ns, (uint64_t)sstride, bq, bk, bv, kc, vc, cos_t, sin_t, q_dim, kv_dim, hd, pos0, slot0);
+                       ldq, ns, (uint64_t)sstride, ss, (uint32_t)((ss_n + 255) / 256), (uint32_t)ss_n, eps, bq, bk, bv,
+                       kc, vc, cos_t, sin_t, q_dim, kv_dim, hd, pos0, slot0);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
