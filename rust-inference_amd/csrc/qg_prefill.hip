@@ -514,6 +514,9 @@ template <> struct PfH<T_Q8_0> {
 #ifndef QG_PF_WG_TARGET
 #define QG_PF_WG_TARGET 1024
 #endif
+#ifndef QG_PF_FILL
+#define QG_PF_FILL 256
+#endif
 constexpr uint32_t kPfKC = 4;                                // sub-blocks per staged chunk
 constexpr uint32_t kPfSliceMax = 8;                          // K-split slices per GEMM at most
 constexpr uint32_t kPfR = QG_PF_R;                           // 16-row tiles per wave
@@ -1299,14 +1302,23 @@ static uint32_t pf_slice_len(uint32_t nseg, uint32_t slices)
 }
 
 // Slices of a K split for `tiles` workgroup row tiles over nseg sub-blocks
-// (nseg % kPfKC == 0): at most QG_PF_WG_TARGET (1024) workgroups in all,
-// at most kPfSliceMax slices of whole chunks; returned so that ceil(nseg / sps) == S
-// for the slice length sps = pf_slice_len(nseg, S) (no empty slice).
+// (nseg % kPfKC == 0), of whole chunks; returned so that ceil(nseg / sps) ==
+// S for the slice length sps = pf_slice_len(nseg, S) (no empty slice).  Up
+// to QG_PF_FILL tiles: at most QG_PF_FILL workgroups (one per CU: a second
+// workgroup on a CU runs the GEMM at less than half the speed of the first)
+// and kPfMaxSlices slices; more tiles: at most QG_PF_WG_TARGET workgroups and
+// kPfSliceMax slices.
 uint32_t pf_split(uint32_t tiles, uint32_t nseg)
 {
     if (tiles == 0 || nseg < qgp::kPfKC) return 1;
-    uint32_t s = QG_PF_WG_TARGET / tiles;
-    if (s > qgp::kPfSliceMax) s = qgp::kPfSliceMax;
+    uint32_t s;
+    if (tiles <= QG_PF_FILL) {
+        s = QG_PF_FILL / tiles;
+        if (s > qgp::kPfMaxSlices) s = qgp::kPfMaxSlices;
+    } else {
+        s = QG_PF_WG_TARGET / tiles;
+        if (s > qgp::kPfSliceMax) s = qgp::kPfSliceMax;
+    }
     if (s > nseg / qgp::kPfKC) s = nseg / qgp::kPfKC;
     if (s < 1u) s = 1u;
     const uint32_t sps = pf_slice_len(nseg, s);
