@@ -1,7 +1,8 @@
 """GPU parity of the batched prefill (qg_model_prefill, include/qgmodel.h):
 the prompt's tokens through each layer together, every projection a GEMM on
-the matrix cores (x as three bf16 pieces, weight codes as exact bf16
-operands, f32 accumulation).  Checked against the oracle's token-by-token
+the matrix cores (x as two f16 pieces under a power-of-two scale per
+256-element group, the K-quant weights as integer f16 operands held exactly,
+f32 accumulation).  Checked against the oracle's token-by-token
 forward pass (oracle/qref_model.c, transformer.rs:63-98 as model.rs:361-365
 calls it): the last prompt token's logits, then greedy decode steps on the
 caches the prefill wrote (every cached position's K/V enters those steps),
