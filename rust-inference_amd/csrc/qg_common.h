@@ -181,8 +181,10 @@ int launch_pf_planes(const float *a, uint32_t na, const float *b, uint32_t nb, s
 // out[i] = sum of the ns slices of x[i], i < n
 int launch_pf_sum(const float *x, uint32_t ns, size_t sstride, size_t n, float *out, ihipStream_t *stream);
 // q, k, v of the QKV GEMM over a mode-1 x (norm sums at ss, over ss_n
-// elements) times 1 / rms, plus the biases, RoPE of q and k, the KV append
-int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *ss, size_t ss_n, float eps,
+// elements) times 1 / rms, plus the biases, RoPE of q and k, the KV append;
+// q and k summed over ns slices, v over ns_v
+int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, uint32_t ns_v, size_t sstride, const float *ss,
+                       size_t ss_n, float eps,
                        const float *bq, const float *bk, const float *bv, float *kc, float *vc, const float *cos_t,
                        const float *sin_t, uint32_t q_dim, uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0,
                        uint32_t ntok, ihipStream_t *stream);

@@ -785,6 +785,9 @@ struct qg_model {
     float *pf_rec = nullptr, *pf_ss = nullptr;
     uint32_t *pf_tok = nullptr;
     uint32_t pf_s_qkv = 1, pf_s_o = 1, pf_s_gu = 1, pf_s_down = 1;
+    // the QKV output's K splits: [Q; K; V] in one launch (one type), or
+    // [Q; K] and V in two (V another type: its few row tiles take more slices)
+    uint32_t pf_s_qkv1 = 1, pf_s_qk = 1, pf_s_v = 1;
     // captured graphs per attention mode: [0] the split attention
     // (attn_rope_split_k + attn_combine_k), [1] whole heads in one workgroup
     // each (attn_rope_head_k), [2] two position ranges per head merged in the
@@ -1300,7 +1303,11 @@ int pf_alloc(qg_model *m)
     size_t kmax = E > H ? E : H;
     if (m->q_dim > kmax) kmax = m->q_dim;
     // the K splits of the four GEMM groups (the same shapes in every layer)
-    m->pf_s_qkv = qg::pf_split(qg::pf_tiles(m->q_dim) + 2 * qg::pf_tiles(m->kv_dim), (uint32_t)(E / 32));
+    const uint32_t tq = qg::pf_tiles(m->q_dim), tk = qg::pf_tiles(m->kv_dim), ne = (uint32_t)(E / 32);
+    m->pf_s_qkv1 = qg::pf_split(tq + 2 * tk, ne);
+    m->pf_s_qk = qg::pf_split(tq + tk, ne);
+    m->pf_s_v = qg::pf_split(tk, ne);
+    m->pf_s_qkv = std::max({m->pf_s_qkv1, m->pf_s_qk, m->pf_s_v});          // slabs of the buffer
     m->pf_s_o = qg::pf_split(qg::pf_tiles(E), (uint32_t)(m->q_dim / 32));
     m->pf_s_gu = qg::pf_split(2 * qg::pf_tiles(H), (uint32_t)(E / 32));
     m->pf_s_down = qg::pf_split(qg::pf_tiles(E), (uint32_t)(H / 32));
@@ -1385,9 +1392,17 @@ int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
         const qg::PfMat qkv[3] = {pf_mat(m->w[QG_M_WQ - 2][l], m->pf_qkv),
                                   pf_mat(m->w[QG_M_WK - 2][l], m->pf_qkv + m->q_dim),
                                   pf_mat(m->w[QG_M_WV - 2][l], m->pf_qkv + m->q_dim + m->kv_dim)};
-        if ((rc = pf_gemm(m, qkv, 3, E, ntok, ldq, m->pf_s_qkv))) return rc;
+        // V in a launch of its own (another type or layout than K) takes its own slices
+        const bool v_apart = qkv[2].type != qkv[1].type || qkv[2].rp != qkv[1].rp || (qkv[2].rp && qkv[2].g != qkv[1].g);
+        const uint32_t s_qk = v_apart ? m->pf_s_qk : m->pf_s_qkv1, s_v = v_apart ? m->pf_s_v : m->pf_s_qkv1;
+        if (v_apart) {
+            if ((rc = pf_gemm(m, qkv, 2, E, ntok, ldq, s_qk)) || (rc = pf_gemm(m, qkv + 2, 1, E, ntok, ldq, s_v)))
+                return rc;
+        } else if ((rc = pf_gemm(m, qkv, 3, E, ntok, ldq, s_qk))) {
+            return rc;
+        }
         float *kc = m->kc + l * kv_layer, *vc = m->vc + l * kv_layer;
-        if (qg::launch_pf_qkv_post(m->pf_qkv, ldq, m->pf_s_qkv, T * ldq, m->pf_ss, E, c.norm_eps,
+        if (qg::launch_pf_qkv_post(m->pf_qkv, ldq, s_qk, s_v, T * ldq, m->pf_ss, E, c.norm_eps,
                                    m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
                                    m->sin_t, m->q_dim, m->kv_dim, m->hd, s0, s0, ntok, sti) ||
             qg::launch_pf_attention(m->pf_qkv, ldq, kc, vc, m->pf_ao, c.n_heads, m->hd, m->kv_dim, m->n_rep, scale, s0,

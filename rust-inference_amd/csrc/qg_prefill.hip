@@ -1202,7 +1202,8 @@ __global__ void __launch_bounds__(256) pf_sum_k(const float *__restrict__ x, uin
 // the rotated q goes to slice 0.  The expressions of the decode path's
 // qkv_post_k.
 __global__ void __launch_bounds__(256) pf_qkv_post_k(float *__restrict__ qkv, uint32_t ldq, uint32_t ns,
-                                                     uint64_t sstride, const float *__restrict__ ss, uint32_t ss_ng,
+                                                     uint32_t ns_v, uint64_t sstride, const float *__restrict__ ss,
+                                                     uint32_t ss_ng,
                                                      uint32_t ss_n, float eps, const float *__restrict__ bq,
                                                      const float *__restrict__ bk, const float *__restrict__ bv,
                                                      float *__restrict__ kc, float *__restrict__ vc,
@@ -1231,8 +1232,8 @@ __global__ void __launch_bounds__(256) pf_qkv_post_k(float *__restrict__ qkv, ui
         float *kr = kc + (size_t)slot * kv_dim, *vr = vc + (size_t)slot * kv_dim;
         kr[i0] = x0 * c - x1 * s;
         kr[i0 + 1] = x0 * s + x1 * c;
-        vr[i0] = sum_slices(v + i0, ns, sstride) * r + bv[i0];
-        vr[i0 + 1] = sum_slices(v + i0 + 1, ns, sstride) * r + bv[i0 + 1];
+        vr[i0] = sum_slices(v + i0, ns_v, sstride) * r + bv[i0];
+        vr[i0 + 1] = sum_slices(v + i0 + 1, ns_v, sstride) * r + bv[i0 + 1];
     }
 }
 
@@ -1424,18 +1425,20 @@ int launch_pf_sum(const float *x, uint32_t ns, size_t sstride, size_t n, float *
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, size_t sstride, const float *ss, size_t ss_n, float eps,
+int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, uint32_t ns_v, size_t sstride, const float *ss,
+                       size_t ss_n, float eps,
                        const float *bq, const float *bk, const float *bv, float *kc, float *vc, const float *cos_t,
                        const float *sin_t, uint32_t q_dim, uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0,
                        uint32_t ntok, ihipStream_t *stream)
 {
     if (ntok == 0) return 0;
-    if (ns < 1 || ns > qgp::kPfMaxSlices || ntok > kPfMaxTokens || hd % 2 != 0 || !ss || ss_n == 0 ||
+    if (ns < 1 || ns > qgp::kPfMaxSlices || ns_v < 1 || ns_v > qgp::kPfMaxSlices || ntok > kPfMaxTokens ||
+        hd % 2 != 0 || !ss || ss_n == 0 ||
         ss_n > 0xFFFFFFFFull)
         return -1;
     const uint32_t pairs = (q_dim > kv_dim ? q_dim : kv_dim) / 2;
     hipLaunchKernelGGL(qgp::pf_qkv_post_k, dim3((pairs + 255) / 256, ntok), dim3(256), 0, (hipStream_t)stream, qkv,
-                       ldq, ns, (uint64_t)sstride, ss, (uint32_t)((ss_n + 255) / 256), (uint32_t)ss_n, eps, bq, bk, bv,
+                       ldq, ns, ns_v, (uint64_t)sstride, ss, (uint32_t)((ss_n + 255) / 256), (uint32_t)ss_n, eps, bq, bk, bv,
                        kc, vc, cos_t, sin_t, q_dim, kv_dim, hd, pos0, slot0);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
