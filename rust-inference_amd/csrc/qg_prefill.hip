@@ -614,9 +614,11 @@ __device__ __forceinline__ void pf_stage_ph(const uint8_t *__restrict__ xp, cons
 // One workgroup's share of a grouped GEMM: rows row0 .. row0 + 16 kPfR
 // (waves past the matrix still stage), K slice k0 .. k1 (multiples of
 // kPfKC), all the chunk's tokens.  x: the chunk images at xp (pf_xoff); per
-// sub-block k the sums rec[64 k + t]; 2^-e of token t at rec[64 nseg + t].  Chunks of kPfKC sub-blocks are copied into two LDS
-// buffers in turn, the next chunk's copy and weight loads in flight while
-// this one is computed.  Every chunk lies inside one block of each row
+// sub-block k the sums rec[64 k + t]; 2^-e_g of token t's 256-element group
+// g at rec[64 nseg + 64 g + t].  Chunks of kPfKC sub-blocks (with their
+// sums and their group's 2^-e_g) are copied into two LDS buffers in turn,
+// the next chunk's copy and weight loads in flight while this one is
+// computed.  Every chunk lies inside one block of each row
 // (cols % 128 == 0 and slices of whole chunks: a row starts at a multiple of
 // 4 sub-blocks).  D[4 kq + i][c16] of an MFMA is token 16 tt + 4 kq + i of
 // row r0 + c16.  LAY, the weight layout: 0 GGUF, rows straddling blocks; 1
