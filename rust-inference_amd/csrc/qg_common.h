@@ -188,9 +188,10 @@ int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, uint32_t ns_v, siz
                        const float *bq, const float *bk, const float *bv, float *kc, float *vc, const float *cos_t,
                        const float *sin_t, uint32_t q_dim, uint32_t kv_dim, uint32_t hd, uint32_t pos0, uint32_t slot0,
                        uint32_t ntok, ihipStream_t *stream);
+// causal attention of the chunk's tokens (head_dim 64, 128 or 256)
 int launch_pf_attention(const float *qkv, uint32_t ldq, const float *kc, const float *vc, float *out, uint32_t n_heads,
                         uint32_t hd, uint32_t kv_dim, uint32_t n_rep, float scale, uint32_t slot0, uint32_t ntok,
-                        size_t lds, ihipStream_t *stream);
+                        ihipStream_t *stream);
 // rows d_rows[0..n) of a matrix, dequantized into out + i * ldo
 int launch_dequantize_rows_dev(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const uint32_t *d_rows,
                                uint32_t n, float *out, size_t ldo, ihipStream_t *stream);

@@ -1288,7 +1288,7 @@ int put_step(qg_model *m, uint32_t token, uint32_t pos, uint32_t slot)
 bool pf_supported(const qg_model *m)
 {
     if (!m->pf_batched) return false;
-    if ((m->hd + (size_t)m->cfg.max_seq_len) * sizeof(float) > 65536) return false;
+    if (m->hd != 64 && m->hd != 128 && m->hd != 256) return false;        // pf_attention_k's head sizes
     for (int s = 0; s < kSlots; s++)
         for (const qg_mat *p : m->w[s])
             if (!p || !qg::prefill_type_supported(p->type) || p->cols % 128 != 0) return false;
@@ -1376,7 +1376,6 @@ int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
         return mfail(m, QG_ERR_HIP, "embedding", hipGetLastError());
     const size_t kv_layer = (size_t)c.max_seq_len * m->kv_dim;
     const float scale = 1.0f / sqrtf((float)m->hd);                      // attention.rs:99
-    const size_t att_lds = ((size_t)m->hd + c.max_seq_len) * sizeof(float);
     for (uint32_t l = 0; l < c.n_layers; l++) {
         // the residual stream entering the layer: the embeddings, or h + fo of
         // the previous layer (written to the other buffer), then attn_norm
@@ -1406,7 +1405,7 @@ int pf_chunk(qg_model *m, const uint32_t *d_tok, uint32_t ntok, uint32_t s0)
                                    m->vec[QG_V_BQ][l], m->vec[QG_V_BK][l], m->vec[QG_V_BV][l], kc, vc, m->cos_t,
                                    m->sin_t, m->q_dim, m->kv_dim, m->hd, s0, s0, ntok, sti) ||
             qg::launch_pf_attention(m->pf_qkv, ldq, kc, vc, m->pf_ao, c.n_heads, m->hd, m->kv_dim, m->n_rep, scale, s0,
-                                    ntok, att_lds, sti))
+                                    ntok, sti))
             return mfail(m, QG_ERR_HIP, "prefill attention", hipGetLastError());
         const qg::PfMat wo = pf_mat(m->w[QG_M_WO - 2][l], m->pf_ao2);
         if ((rc = pf_planes(m, m->pf_ao, 1, nullptr, 0, nullptr, nullptr, m->q_dim, m->q_dim, 0, false, ntok)) ||

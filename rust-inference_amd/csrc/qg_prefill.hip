@@ -1239,53 +1239,145 @@ __global__ void __launch_bounds__(256) pf_qkv_post_k(float *__restrict__ qkv, ui
     }
 }
 
-// Attention of query head blockIdx.x of token blockIdx.y over cache slots
-// 0 .. slot0 + t (attention.rs:93-121, math.rs:63-70 / 104-118); LDS: hd
-// floats of q, then the scores.
+// Attention of query head blockIdx.x for tokens t0 .. t0 + 15 (t0 = 16
+// blockIdx.y) of the chunk, token t over cache slots 0 .. slot0 + t
+// (attention.rs:93-121, math.rs:63-70 / 104-118), on the f32 matrix cores
+// (v_mfma_f32_16x16x4f32: f32 products and sums).  Positions go in tiles of
+// 64 rows of K and V staged in LDS; wave w takes tile positions 16 w .. 16 w
+// + 15: S = Q K^T for its 16 positions (hd / 4 MFMAs, Q in registers), then,
+// after the tile's running maximum per token is agreed through LDS,
+// P = exp(S - M) for them, and O += P V for output columns 64 w' .. (its hd /
+// 64 column blocks of 16) over the tile's 64 positions (16 MFMAs per block).
+// Each token keeps a running (max, sum) and its output is rescaled when the
+// maximum grows, so the result is the softmax over all positions.
+// 16x16x4 f32 layout (gfx950): lane l holds A[l % 16][l / 16],
+// B[l / 16][l % 16] and D[4 (l / 16) + i][l % 16], i = 0..3.
+constexpr uint32_t kPfAttRows = 16, kPfAttTile = 64;
+__host__ __device__ constexpr size_t pf_att_lds(uint32_t hd)
+{
+    // Q [16][hd + 4], K [64][hd + 4], V [64][hd + 16], P [16][64 + 4], the
+    // waves' per-token maxima and sums [2][4][16]
+    return ((size_t)kPfAttRows * (hd + 4u) + (size_t)kPfAttTile * (hd + 4u) + (size_t)kPfAttTile * (hd + 16u) +
+            (size_t)kPfAttRows * (kPfAttTile + 4u) + 2u * 4u * kPfAttRows) * sizeof(float);
+}
+template <uint32_t HD>
 __global__ void __launch_bounds__(256) pf_attention_k(const float *__restrict__ qkv, uint32_t ldq,
                                                       const float *__restrict__ kc, const float *__restrict__ vc,
-                                                      float *__restrict__ out, uint32_t hd, uint32_t kv_dim,
-                                                      uint32_t n_rep, float scale, uint32_t slot0)
+                                                      float *__restrict__ out, uint32_t kv_dim, uint32_t n_rep,
+                                                      float scale, uint32_t slot0, uint32_t ntok)
 {
-    extern __shared__ float sm[];
-    __shared__ float red[4];
-    float *qs = sm, *sc = sm + hd;
-    const uint32_t t = blockIdx.y, h = blockIdx.x, kvh = (h / n_rep) * hd, seq = slot0 + t + 1;
-    const float *q = qkv + (size_t)t * ldq + (size_t)h * hd;
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[d];
-    __syncthreads();
-    float mx = -INFINITY;
-    for (uint32_t j = threadIdx.x; j < seq; j += blockDim.x) {
-        const float *kr = kc + (size_t)j * kv_dim + kvh;
-        float s = 0.f;
-        for (uint32_t d = 0; d < hd; d++) s += qs[d] * kr[d];
-        s = s * scale;
-        sc[j] = s;
-        mx = fmaxf(mx, s);
+    constexpr uint32_t TP = kPfAttTile, LQ = HD + 4u, LK = HD + 4u, LV = HD + 16u, LP = TP + 4u;
+    constexpr uint32_t KS = HD / 4u, NB = HD / 64u;                  // k-steps of S; O column blocks per wave
+    static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim 64, 128 or 256");
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    extern __shared__ float4 att_lds4[];
+    float *qs = (float *)att_lds4, *ks = qs + kPfAttRows * LQ, *vs = ks + TP * LK, *ps = vs + TP * LV;
+    float *wmax = ps + kPfAttRows * LP, *wsum = wmax + 4u * kPfAttRows;
+    const uint32_t h = blockIdx.x, t0 = blockIdx.y * kPfAttRows, kvh = (h / n_rep) * HD;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6, c = lane & 15u, g = lane >> 4;
+    const uint32_t nrow = min(kPfAttRows, ntok - t0), npos = slot0 + t0 + nrow;     // positions any row sees
+    // the 16 tokens' q (rows past the chunk: the last token's, never stored)
+    for (uint32_t i = tid; i < kPfAttRows * (HD / 4u); i += 256u) {
+        const uint32_t rr = i / (HD / 4u), d4 = i % (HD / 4u);
+        const float *q = qkv + (size_t)(t0 + min(rr, nrow - 1u)) * ldq + (size_t)h * HD;
+        *(float4 *)(qs + rr * LQ + 4u * d4) = *(const float4 *)(q + 4u * d4);
     }
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float sum = 0.f;
-    for (uint32_t j = threadIdx.x; j < seq; j += blockDim.x) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
+    // A of S: q[token c][4 k + g], k = 0 .. HD/4 - 1
+    float qa[KS];
+#pragma unroll
+    for (uint32_t k = 0; k < KS; k++) qa[k] = qs[c * LQ + 4u * k + g];
+    // this lane's D rows: tokens 4 g + i; their running max and sum
+    float m[4], l[4];
+    v4f o[NB];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) { m[i] = -INFINITY; l[i] = 0.f; }
+#pragma unroll
+    for (uint32_t b = 0; b < NB; b++) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t base = 0; base < npos; base += TP) {
+        const uint32_t nv = min(TP, npos - base);
+        __syncthreads();                                                   // the previous tile's readers are done
+        for (uint32_t i = tid; i < TP * (HD / 4u); i += 256u) {
+            const uint32_t p = i / (HD / 4u), d4 = i % (HD / 4u);
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (p < nv) {
+                const size_t gi = (size_t)(base + p) * kv_dim + kvh + 4u * d4;
+                kv = *(const float4 *)(kc + gi);
+                vv = *(const float4 *)(vc + gi);
+            }
+            *(float4 *)(ks + p * LK + 4u * d4) = kv;                       // rows past the tile: zeros
+            *(float4 *)(vs + p * LV + 4u * d4) = vv;
+        }
+        __syncthreads();
+        // S for tokens 0..15 x positions 16 w .. 16 w + 15 of the tile
+        v4f s = v4f{0.f, 0.f, 0.f, 0.f};
+        const float *kr = ks + (16u * w + c) * LK + g;
+#pragma unroll
+        for (uint32_t k = 0; k < KS; k++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[k], kr[4u * k], s, 0, 0, 0);
+        // masked (past the tile, or after the token's own slot): -inf; then
+        // the wave's maximum per token over its 16 positions
+        const uint32_t pos = base + 16u * w + c;
+        float sv[4], tm[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t t = t0 + 4u * g + i;
+            sv[i] = (16u * w + c < nv && pos <= slot0 + t) ? s[i] * scale : -INFINITY;
+            tm[i] = sv[i];
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) tm[i] = fmaxf(tm[i], __shfl_xor(tm[i], off, 64));
+        }
+        if (c == 0)
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) wmax[w * kPfAttRows + 4u * g + i] = tm[i];
+        __syncthreads();
+        float al[4], ls[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t r = 4u * g + i;
+            const float mt = fmaxf(fmaxf(wmax[r], wmax[kPfAttRows + r]),
+                                   fmaxf(wmax[2u * kPfAttRows + r], wmax[3u * kPfAttRows + r]));
+            const float mn = fmaxf(m[i], mt);
+            // every token has position 0 in the first tile: mn is finite from there on
+            al[i] = m[i] == -INFINITY ? 0.f : expf(m[i] - mn);
+            m[i] = mn;
+            const float p = sv[i] == -INFINITY ? 0.f : expf(sv[i] - mn);
+            ps[r * LP + 16u * w + c] = p;
+            ls[i] = p;
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) ls[i] += __shfl_xor(ls[i], off, 64);
+        }
+        if (c == 0)
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) wsum[w * kPfAttRows + 4u * g + i] = ls[i];
+        __syncthreads();                                                   // the tile's P and sums
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t r = 4u * g + i;
+            l[i] = l[i] * al[i] + ((wsum[r] + wsum[kPfAttRows + r]) + (wsum[2u * kPfAttRows + r] +
+                                                                      wsum[3u * kPfAttRows + r]));
+        }
+        // O[token][column] for this wave's column blocks: rescale, then P V
+#pragma unroll
+        for (uint32_t b = 0; b < NB; b++) {
+            v4f acc = v4f{o[b][0] * al[0], o[b][1] * al[1], o[b][2] * al[2], o[b][3] * al[3]};
+            const uint32_t col = (w * NB + b) * 16u + c;
+#pragma unroll
+            for (uint32_t k = 0; k < TP / 4u; k++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ps[c * LP + 4u * k + g], vs[(4u * k + g) * LV + col], acc,
+                                                           0, 0, 0);
+            o[b] = acc;
+        }
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = sum;
-    __syncthreads();
-    sum = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = 1.0f / sum;
-    for (uint32_t j = threadIdx.x; j < seq; j += blockDim.x) sc[j] *= inv;
-    __syncthreads();
-    float *o = out + ((size_t)t * gridDim.x + h) * hd;             // out[t][q_dim]
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-        float acc = 0.f;
-        for (uint32_t j = 0; j < seq; j++) acc += sc[j] * vc[(size_t)j * kv_dim + kvh + d];
-        o[d] = acc;
+    // token 4 g + i, column (w NB + b) 16 + c
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+        const uint32_t r = 4u * g + i;
+        if (r < nrow) {
+            const float inv = 1.0f / l[i];
+            float *dst = out + ((size_t)(t0 + r) * gridDim.x + h) * HD;          // out[t][q_dim]
+#pragma unroll
+            for (uint32_t b = 0; b < NB; b++) dst[(w * NB + b) * 16u + c] = o[b][i] * inv;
+        }
     }
 }
 
@@ -1447,11 +1539,30 @@ int launch_pf_qkv_post(float *qkv, uint32_t ldq, uint32_t ns, uint32_t ns_v, siz
 
 int launch_pf_attention(const float *qkv, uint32_t ldq, const float *kc, const float *vc, float *out, uint32_t n_heads,
                         uint32_t hd, uint32_t kv_dim, uint32_t n_rep, float scale, uint32_t slot0, uint32_t ntok,
-                        size_t lds, ihipStream_t *stream)
+                        ihipStream_t *stream)
 {
     if (ntok == 0) return 0;
-    hipLaunchKernelGGL(qgp::pf_attention_k, dim3(n_heads, ntok), dim3(256), lds, (hipStream_t)stream, qkv, ldq, kc, vc,
-                       out, hd, kv_dim, n_rep, scale, slot0);
+    // 16-byte aligned rows (float4 reads of q, K, V and the output)
+    if (ntok > kPfMaxTokens || n_rep == 0 || ldq % 4 != 0 || kv_dim % 4 != 0 || ((uintptr_t)qkv & 15u) ||
+        ((uintptr_t)kc & 15u) || ((uintptr_t)vc & 15u) || ((uintptr_t)out & 15u))
+        return -1;
+    const dim3 grid(n_heads, (ntok + qgp::kPfAttRows - 1) / qgp::kPfAttRows), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    switch (hd) {
+    case 64:
+        hipLaunchKernelGGL(qgp::pf_attention_k<64>, grid, block, qgp::pf_att_lds(64), st, qkv, ldq, kc, vc, out, kv_dim,
+                           n_rep, scale, slot0, ntok);
+        break;
+    case 128:
+        hipLaunchKernelGGL(qgp::pf_attention_k<128>, grid, block, qgp::pf_att_lds(128), st, qkv, ldq, kc, vc, out,
+                           kv_dim, n_rep, scale, slot0, ntok);
+        break;
+    case 256:
+        hipLaunchKernelGGL(qgp::pf_attention_k<256>, grid, block, qgp::pf_att_lds(256), st, qkv, ldq, kc, vc, out,
+                           kv_dim, n_rep, scale, slot0, ntok);
+        break;
+    default: return -1;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
