@@ -89,11 +89,13 @@ int qg_model_forward(qg_model *m, uint32_t token, uint32_t pos, float *logits);
  * of tokens[0..n) at positions seq, seq + 1, ... (seq = the positions already
  * cached), leaving the caches and the device logits as those n calls of
  * qg_model_forward would -- the logits are the last token's.  Chunks of up to
- * 64 tokens go through each layer together, every projection one bf16 MFMA
- * GEMM over the tokens' x split into three bf16 pieces (batched prefill,
- * f32 accumulation), when every layer
- * matrix is Q4_K, Q5_K, Q6_K or Q8_0 with cols % 32 == 0; otherwise, or after
- * qg_model_use_batched_prefill(m, 0), one forward pass per token.  `logits`,
+ * 64 tokens go through each layer together, every projection one f16 MFMA
+ * GEMM over the tokens' x split into two f16 pieces under a power-of-two
+ * scale per 256 elements (batched prefill, exact products, f32
+ * accumulation) and the attention on f32 MFMAs, when every layer matrix is
+ * Q4_K, Q5_K, Q6_K or Q8_0 with cols % 128 == 0 and head_dim is 64, 128 or
+ * 256; otherwise, or after qg_model_use_batched_prefill(m, 0), one forward
+ * pass per token.  `logits`,
  * if not NULL, receives vocab_size floats (host memory).  QG_ERR_SHAPE when
  * the tokens would not fit the caches or a token >= vocab. */
 int qg_model_prefill(qg_model *m, const uint32_t *tokens, size_t n, float *logits);
