@@ -88,6 +88,19 @@ def test_qwen2_7b_layer_shape_prefill(rinf, synth, oracle, ctx, mix):
     assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL
 
 
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_prefill_attention_head_dims(rinf, synth, oracle, ctx, hd):
+    """The prefill attention (f32 MFMA, tiles of 64 cached positions) at
+    head_dim 64, 128 and 256, two query heads per kv head: 100 prompt tokens
+    fed as 30 + 70 (the second call continues the caches; up to 100
+    positions, two tiles), then greedy steps."""
+    heads = 1024 // hd
+    cfg = dict(SMALL, n_layers=1, embed_dim=1024, n_heads=heads, n_kv_heads=max(1, heads // 2), hidden_dim=512)
+    e0, errs, out = prefill_and_compare(rinf, synth, oracle, ctx, cfg, "q4_k_m", 53, 100, 4, 128, split=30)
+    print(f"head_dim {hd}: prefill logits err {e0:.2e}, decode max {max(errs):.2e}", flush=True)
+    assert e0 <= DEEP_TOL and max(errs) <= DEEP_TOL
+
+
 def test_qwen2_05b_prefill_then_decode(rinf, synth, oracle, ctx):
     """BASELINE.json configs[2]'s model (24 layers, tied Q4_K embedding at
     cols = 896, two-row groups) with its 32-token prompt through the batched
