@@ -166,13 +166,28 @@ int qg_matvec_host(qg_ctx *ctx, const qg_mat *mat, const float *x, float *y);
  * the host bytes (64 bytes at 16 evenly spaced offsets, first and last
  * included) still matches the one taken at upload; on a mismatch the current
  * bytes are uploaded again.  A caller that edits weights in place where the
- * fingerprint does not look calls qg_gpu_invalidate first.  On an error
+ * fingerprint does not look calls qg_gpu_invalidate first, or compares every
+ * byte on every call (qg_gpu_set_freshness, QG_FRESH_EXACT).  On an error
  * `out` is left untouched. */
 int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint32_t dtype,
                        const float *x, float *out, size_t rows, size_t cols);
 /* No counterpart in the reference (it keeps no device copies): drops every
  * device copy qg_gpu_mat_vec_mul keeps for host address `weight_data`. */
 int qg_gpu_invalidate(qg_ctx *ctx, const void *weight_data);
+
+/* How qg_gpu_mat_vec_mul decides that its device copy still holds the host
+ * bytes.  No counterpart in the reference, which uploads on every call
+ * (gpu_backend.rs:478-482):
+ *   QG_FRESH_SAMPLED (the default): the 16-window fingerprint above;
+ *   QG_FRESH_EXACT: the context keeps a host copy of every cached matrix's
+ *     bytes and compares all of them on every call (memcmp), uploading again
+ *     on any difference -- the reference's result for any in-place edit,
+ *     with no qg_gpu_invalidate, at the cost of one host copy per cached
+ *     matrix and a host compare of its bytes per call.
+ * Copies made under the other mode are uploaded again on their next call.
+ * Any other mode: QG_ERR_INVALID_ARG. */
+enum { QG_FRESH_SAMPLED = 0, QG_FRESH_EXACT = 1 };
+int qg_gpu_set_freshness(qg_ctx *ctx, int mode);
 
 /* Test hook, no counterpart in the reference: of the allocations this
  * context makes next (device matrices, repacked and stacked copies, pinned

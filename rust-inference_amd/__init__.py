@@ -40,6 +40,8 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_0: (32, 18), Q5_0: (32, 22
          Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 QG_OK = 0
+# include/qgemv.h qg_gpu_set_freshness modes
+FRESH_SAMPLED, FRESH_EXACT = 0, 1
 STATUS = {0: "QG_OK", 1: "QG_ERR_INVALID_ARG", 2: "QG_ERR_UNSUPPORTED_TYPE",
           3: "QG_ERR_SHORT_DATA", 4: "QG_ERR_NO_DEVICE", 5: "QG_ERR_HIP",
           6: "QG_ERR_OUT_OF_MEMORY", 7: "QG_ERR_SHAPE"}
@@ -80,6 +82,7 @@ _SIGS = {
     "qg_matvec_norm_glu_dev_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
     "qg_gpu_invalidate": (ctypes.c_int, [_P, _P]),
+    "qg_gpu_set_freshness": (ctypes.c_int, [_P, ctypes.c_int]),
     "qg_matvec_dev_repeat": (ctypes.c_int, [_P, _P, _SZ, _P, _P, _SZ, _P]),
     "qg_test_fail_allocations": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -311,6 +314,12 @@ class GpuContext:
     def invalidate(self, weight_data):
         """Drop the device copies mat_vec_mul keeps for this host buffer (qg_gpu_invalidate)."""
         self.check(self.lib.qg_gpu_invalidate(self.h, _ptr(weight_data)), "qg_gpu_invalidate")
+
+    def set_freshness(self, mode: int):
+        """How mat_vec_mul checks its device copies against the host bytes
+        (qg_gpu_set_freshness): FRESH_SAMPLED (16 windows, the default) or
+        FRESH_EXACT (every byte on every call)."""
+        self.check(self.lib.qg_gpu_set_freshness(self.h, int(mode)), "qg_gpu_set_freshness")
 
     def fail_allocations(self, n: int, skip: int = 0):
         """Test hook: after `skip` more allocations, the next n allocations of

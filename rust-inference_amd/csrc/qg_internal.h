@@ -62,12 +62,16 @@ struct qg_ctx {
     std::set<qg_mat *> mats;
     std::set<qg_model *> models;            // decode-step engines on this context
     // qg_gpu_mat_vec_mul's device copies, keyed by (host address, bytes, type,
-    // rows, cols), each with a fingerprint of the host bytes it was made from
+    // rows, cols), each with the host bytes it was made from: a fingerprint
+    // (sampled windows), or all of them (exact, then fp.size() == the
+    // matrix's bytes)
     struct Keyed {
         qg_mat *mat;
         std::vector<uint8_t> fp;
+        bool exact;
     };
     std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, Keyed> keyed;
+    bool fresh_exact = false;               // qg_gpu_set_freshness(QG_FRESH_EXACT)
     int fail_skip = 0, fail_allocs = 0;     // test hook: allocations to let through, then to fail
 };
 

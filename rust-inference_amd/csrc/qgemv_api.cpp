@@ -770,10 +770,18 @@ int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint
     if (rc != QG_OK) return fail(ctx, rc, "unsupported type or shape");
     if (nbytes < need) return fail(ctx, QG_ERR_SHORT_DATA, "raw data shorter than the matrix needs");
     if (need > 0 && !weight_data) return fail(ctx, QG_ERR_INVALID_ARG, "weight_data == NULL");
-    std::vector<uint8_t> fp = fingerprint((const uint8_t *)weight_data, need);
+    const bool exact = ctx->fresh_exact;
+    const uint8_t *wb = (const uint8_t *)weight_data;
+    std::vector<uint8_t> fp;
+    if (!exact) fp = fingerprint(wb, need);
     qg_mat *m = nullptr;
     auto it = ctx->keyed.find(key);
-    if (it != ctx->keyed.end() && it->second.fp == fp) {
+    bool hit = false;
+    if (it != ctx->keyed.end() && it->second.exact == exact) {
+        const std::vector<uint8_t> &had = it->second.fp;
+        hit = exact ? had.size() == need && (need == 0 || memcmp(had.data(), wb, need) == 0) : had == fp;
+    }
+    if (hit) {
         m = it->second.mat;
     } else {
         // first sight, or the bytes at this address changed since the copy
@@ -784,10 +792,24 @@ int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint
             (void)hipStreamSynchronize(ctx->stream);
             drop_mat(ctx, it->second.mat);
         }
+        if (exact) {
+            try {
+                fp.assign(wb, wb + need);                // the bytes the copy is made from
+            } catch (const std::bad_alloc &) {
+                return fail(ctx, QG_ERR_OUT_OF_MEMORY, "host copy of the weight bytes");
+            }
+        }
         if ((rc = qg_upload(ctx, weight_data, nbytes, dtype, rows, cols, &m))) return rc;
-        ctx->keyed[key] = qg_ctx::Keyed{m, std::move(fp)};
+        ctx->keyed[key] = qg_ctx::Keyed{m, std::move(fp), exact};
     }
     return qg_matvec_host(ctx, m, x, out);
+}
+
+int qg_gpu_set_freshness(qg_ctx *ctx, int mode)
+{
+    if (!ctx || (mode != QG_FRESH_SAMPLED && mode != QG_FRESH_EXACT)) return QG_ERR_INVALID_ARG;
+    ctx->fresh_exact = mode == QG_FRESH_EXACT;
+    return QG_OK;
 }
 
 int qg_gpu_invalidate(qg_ctx *ctx, const void *weight_data)

@@ -59,6 +59,52 @@ def test_invalidate_drops_the_copy(ctx, oracle, synth):
         normwise_err(out, oracle.mat_vec_mul(raw, Q4_K, rows, cols, x)) <= GEMV_TOL
 
 
+def test_exact_freshness_sees_any_byte(rinf, oracle, synth):
+    """QG_FRESH_EXACT: a change between the fingerprint windows is seen on the
+    next call with no qg_gpu_invalidate (the reference's upload-every-call
+    result); the default sampled mode keeps its copy, which is what makes
+    the byte below a between-windows one."""
+    rows, cols = 256, 1024
+    raw = synth.gen_blocks(Q4_K, rows, cols, 5)
+    x = synth.gen_x(cols, 5)
+    n = raw.nbytes
+    step = (n - 64) // 15
+    off = step // 2 + 200                          # between windows 0 and 1
+    assert 64 <= off < step and off % 144 >= 16     # a code byte of block off // 144
+    exact, sampled = rinf.GpuContext(0), rinf.GpuContext(0)
+    try:
+        exact.set_freshness(rinf.FRESH_EXACT)
+        with pytest.raises(rinf.QgemvError) as e:
+            exact.set_freshness(2)
+        assert e.value.status == INVALID
+        outs = {c: np.zeros(rows, np.float32) for c in ("e", "s")}
+        exact.mat_vec_mul(raw, Q4_K, x, outs["e"], rows, cols)
+        sampled.mat_vec_mul(raw, Q4_K, x, outs["s"], rows, cols)
+        first = outs["e"].copy()
+        assert np.array_equal(outs["s"], first)
+        for k in range(3):                          # three edits, each seen at once
+            raw[off + 9 * k] ^= 0x5A
+            ref = oracle.mat_vec_mul(raw, Q4_K, rows, cols, x)
+            exact.mat_vec_mul(raw, Q4_K, x, outs["e"], rows, cols)
+            assert normwise_err(outs["e"], ref) <= GEMV_TOL
+            assert not np.array_equal(outs["e"], first)
+        sampled.mat_vec_mul(raw, Q4_K, x, outs["s"], rows, cols)
+        assert np.array_equal(outs["s"], first)     # stale: the edits lie between its windows
+        # back to sampled: the exact-mode copy is uploaded again, then kept
+        exact.set_freshness(rinf.FRESH_SAMPLED)
+        exact.mat_vec_mul(raw, Q4_K, x, outs["e"], rows, cols)
+        assert normwise_err(outs["e"], oracle.mat_vec_mul(raw, Q4_K, rows, cols, x)) <= GEMV_TOL
+        # an unchanged buffer under the exact mode keeps its copy (same result bit for bit)
+        exact.set_freshness(rinf.FRESH_EXACT)
+        a, b = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+        exact.mat_vec_mul(raw, Q4_K, x, a, rows, cols)
+        exact.mat_vec_mul(raw, Q4_K, x, b, rows, cols)
+        assert np.array_equal(a, b)
+    finally:
+        exact.close()
+        sampled.close()
+
+
 def test_injected_allocation_failures(rinf, oracle, synth):
     """Every allocation a context attempts can be made to fail from the host:
     the call returns QG_ERR_OUT_OF_MEMORY, hands out no matrix and leaves
