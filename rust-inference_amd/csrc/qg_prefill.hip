@@ -1546,6 +1546,8 @@ int launch_pf_attention(const float *qkv, uint32_t ldq, const float *kc, const f
     if (ntok > kPfMaxTokens || n_rep == 0 || ldq % 4 != 0 || kv_dim % 4 != 0 || ((uintptr_t)qkv & 15u) ||
         ((uintptr_t)kc & 15u) || ((uintptr_t)vc & 15u) || ((uintptr_t)out & 15u))
         return -1;
+    // every head's q inside a token's row of qkv, every kv head inside kv_dim
+    if (n_heads % n_rep != 0 || (uint64_t)n_heads * hd > ldq || (uint64_t)(n_heads / n_rep) * hd > kv_dim) return -1;
     const dim3 grid(n_heads, (ntok + qgp::kPfAttRows - 1) / qgp::kPfAttRows), block(256);
     hipStream_t st = (hipStream_t)stream;
     switch (hd) {
