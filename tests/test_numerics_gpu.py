@@ -204,3 +204,57 @@ def test_clean_call_after_non_finite(ctx, oracle, synth, dtype):
     same_classes(y_bad, oracle.mat_vec_mul(raw, dtype, rows, cols, xb))
     assert np.array_equal(y_clean.view(np.uint32), y_again.view(np.uint32))
     assert normwise_err(y_clean, oracle.mat_vec_mul(raw, dtype, rows, cols, x)) <= GEMV_TOL
+
+
+def zero_weight_columns(raw, dtype, rows, cols, cidx):
+    """Set the weight of column cidx[s] of every row to exactly zero (Q8_0:
+    code 0; Q4_0: nibble 8, byte 2 + j/2 of its block, low nibble for even
+    j -- quant.rs:106-121)."""
+    raw = raw.copy()
+    bb = 34 if dtype == 8 else 18
+    for r in range(rows):
+        f = r * cols + cidx                               # flat element index
+        b, j = f // 32, f % 32
+        if dtype == 8:
+            raw[b * bb + 2 + j] = 0
+        else:
+            byte = b * bb + 2 + j // 2
+            lo = (j % 2) == 0
+            raw[byte] = np.where(lo, (raw[byte] & 0xF0) | 0x08, (raw[byte] & 0x0F) | 0x80)
+    return raw
+
+
+@pytest.mark.parametrize("dtype", [8, 2], ids=["Q8_0", "Q4_0"])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{r}x{c}" for r, c in SHAPES])
+def test_outlier_at_zero_weight(ctx, oracle, synth, dtype, shape):
+    """The case the normwise gate above cannot see: one element of every
+    segment scaled 1e4x, and every row's weight at that column zero, so no
+    product with a segment maximum enters y and the small elements' 22-bit
+    fixed-point error is all there is.  Checked against the guarantee of the
+    format, per row: |y - exact| <= 2^-22 sum_i |w_i| m_seg(i) (each
+    element's error is at most half a step of 2^-22 of its segment's maximum)
+    plus 2^-20 sum_i |w_i x_i| for the f32 rounding of the scaled terms.  The
+    normwise error this leaves is printed (it is not within GEMV_TOL here:
+    the reference's f32 loop keeps 24 bits of every small element)."""
+    rows, cols = shape
+    seed = synth.config_seed(1) + 7 * rows + cols + dtype
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(cols).astype(np.float32)
+    cidx = np.arange(0, cols, 32) + rng.integers(0, 32, cols // 32)
+    x[cidx] *= np.float32(1e4)
+    raw = zero_weight_columns(synth.gen_blocks(dtype, rows, cols, seed), dtype, rows, cols, cidx)
+    m = ctx.upload(raw, dtype, rows, cols)
+    y = np.full(rows, np.nan, np.float32)
+    m.matvec_host(x, y)
+    m.free()
+    y32, y64 = ref_pair(oracle, raw, dtype, rows, cols, x)
+    w = np.abs(oracle.dequantize(raw, dtype, rows * cols)[:rows * cols].reshape(rows, cols).astype(np.float64))
+    assert np.all(w[:, cidx] == 0.0)
+    mseg = np.repeat(np.abs(x.astype(np.float64)).reshape(-1, 32).max(axis=1), 32)
+    bound = 2.0 ** -22 * (w @ mseg) + 2.0 ** -20 * (w @ np.abs(x.astype(np.float64)))
+    err = np.abs(y.astype(np.float64) - y64)
+    print(f"{NAMES[dtype]} {rows}x{cols} outliers at zero weights: normwise vs exact "
+          f"{normwise_err(y, y64):.2e} (reference {normwise_err(y32, y64):.2e}), "
+          f"max err / bound {np.max(err / bound):.3f}", flush=True)
+    assert np.all(np.isfinite(y))
+    assert np.all(err <= bound)
