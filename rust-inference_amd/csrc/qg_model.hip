@@ -165,6 +165,7 @@ struct AttnArgs {
     float *part, *ml;                // per (head, range): partial output, (max, sum)
     const Step *st;
     uint32_t kv_dim, n_rep, grp, nsplit;
+    uint32_t cap;                    // rows of the cache (max_seq_len)
     float scale;
     // attn_rope_head_k<E, 2>: floats between the ranges' outputs in part (q_dim)
     // and between their (max, sum) rows in ml (2 n_heads)
@@ -438,12 +439,11 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
         kn[e] = a.k[kvo + lane + 64 * e] + a.bk[kvo + lane + 64 * e];
         vn[e] = a.v[kvo + lane + 64 * e] + a.bv[kvo + lane + 64 * e];
     }
-    const uint32_t pos = a.st->pos, slot = a.st->slot, seq = slot + 1;
     float kk[PW][E], vv[PW][E], nk[PW][E], nv[PW][E];
-    auto load = [&](uint32_t b, float (&ko)[PW][E], float (&vo)[PW][E]) {
+    auto load = [&](uint32_t b, uint32_t last, float (&ko)[PW][E], float (&vo)[PW][E]) {
 #pragma unroll
         for (uint32_t p = 0; p < PW; p++) {
-            const uint32_t j = min(b + ST * p, slot);
+            const uint32_t j = min(b + ST * p, last);
             const float *kr = a.kc + (size_t)j * a.kv_dim + kvo, *vr = a.vc + (size_t)j * a.kv_dim + kvo;
 #pragma unroll
             for (int e = 0; e < E; e++) {
@@ -452,8 +452,13 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
             }
         }
     };
+    // the first chunk's rows, before the step record arrives (clamped to the
+    // cache: rows past slot are never used -- the chunk's loop stops at the
+    // wave's last position -- and the one at slot is replaced by this
+    // token's k and v)
     uint32_t base = rg + NR * wave;
-    load(base, kk, vv);
+    load(base, a.cap - 1u, kk, vv);
+    const uint32_t pos = a.st->pos, slot = a.st->slot, seq = slot + 1;
     float cv[E], sv[E];
 #pragma unroll
     for (int e = 0; e < E; e++) {
@@ -478,7 +483,7 @@ __global__ void __launch_bounds__(64 * kHeadWaves) attn_rope_head_k(AttnArgs a, 
     for (int e = 0; e < E; e++) acc[e] = 0.f;
     for (; base < seq; base += ST * PW) {
         const uint32_t np = min((seq - base + ST - 1) / ST, PW);   // this wave's positions in the chunk
-        if (base + ST * PW < seq) load(base + ST * PW, nk, nv);
+        if (base + ST * PW < seq) load(base + ST * PW, slot, nk, nv);
 #pragma unroll
         for (uint32_t p = 0; p < PW; p++)
             if (base + ST * p == slot)
@@ -1088,6 +1093,7 @@ int enqueue_forward(qg_model *m)
             aa.kc = kc; aa.vc = vc; aa.cos_t = m->cos_t; aa.sin_t = m->sin_t;
             aa.part = m->att_part; aa.ml = m->att_ml; aa.st = m->d_step;
             aa.kv_dim = m->kv_dim; aa.n_rep = m->n_rep; aa.grp = m->att_grp; aa.nsplit = m->att_nsplit;
+            aa.cap = c.max_seq_len;
             aa.scale = scale;
             if (m->att_mode == 2) {
                 // two workgroups per head (even / odd positions); the wo GEMV
