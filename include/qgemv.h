@@ -189,6 +189,22 @@ int qg_gpu_invalidate(qg_ctx *ctx, const void *weight_data);
 enum { QG_FRESH_SAMPLED = 0, QG_FRESH_EXACT = 1 };
 int qg_gpu_set_freshness(qg_ctx *ctx, int mode);
 
+/* Arithmetic of this context's plain mat-vecs (qg_matvec_dev, qg_matvec_host,
+ * qg_gpu_mat_vec_mul; the fused entry points and the decode step keep the
+ * default).  No counterpart in the reference, whose loop rounds every product
+ * w * x to f32 and sums in f32 (quant.rs:195-204):
+ *   QG_PRECISION_FIXED22 (the default): x as 22-bit fixed point per
+ *     32-element segment against exact integer sums of the weight codes --
+ *     within 1e-4 normwise of the reference, but an element far below its
+ *     segment's maximum keeps fewer bits (10^4 below: about 8), which shows
+ *     where the maxima meet zero weights;
+ *   QG_PRECISION_F32: every product rounded to f32 and summed in f32, one
+ *     wave per row (the reference's per-product arithmetic, in another
+ *     order), at several times the fixed-point kernels' time.
+ * Any other mode: QG_ERR_INVALID_ARG. */
+enum { QG_PRECISION_FIXED22 = 0, QG_PRECISION_F32 = 1 };
+int qg_set_precision(qg_ctx *ctx, int mode);
+
 /* Test hook, no counterpart in the reference: of the allocations this
  * context makes next (device matrices, repacked and stacked copies, pinned
  * and device staging), the first `skip` go through and the `n` after them

@@ -40,8 +40,9 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_0: (32, 18), Q5_0: (32, 22
          Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 QG_OK = 0
-# include/qgemv.h qg_gpu_set_freshness modes
+# include/qgemv.h qg_gpu_set_freshness and qg_set_precision modes
 FRESH_SAMPLED, FRESH_EXACT = 0, 1
+PRECISION_FIXED22, PRECISION_F32 = 0, 1
 STATUS = {0: "QG_OK", 1: "QG_ERR_INVALID_ARG", 2: "QG_ERR_UNSUPPORTED_TYPE",
           3: "QG_ERR_SHORT_DATA", 4: "QG_ERR_NO_DEVICE", 5: "QG_ERR_HIP",
           6: "QG_ERR_OUT_OF_MEMORY", 7: "QG_ERR_SHAPE"}
@@ -83,6 +84,7 @@ _SIGS = {
     "qg_mat_stack": (ctypes.c_int, [_P, ctypes.POINTER(_P), ctypes.c_int, ctypes.POINTER(_P)]),
     "qg_gpu_invalidate": (ctypes.c_int, [_P, _P]),
     "qg_gpu_set_freshness": (ctypes.c_int, [_P, ctypes.c_int]),
+    "qg_set_precision": (ctypes.c_int, [_P, ctypes.c_int]),
     "qg_matvec_dev_repeat": (ctypes.c_int, [_P, _P, _SZ, _P, _P, _SZ, _P]),
     "qg_test_fail_allocations": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int]),
     "qg_matvec_host": (ctypes.c_int, [_P, _P, _P, _P]),
@@ -320,6 +322,11 @@ class GpuContext:
         (qg_gpu_set_freshness): FRESH_SAMPLED (16 windows, the default) or
         FRESH_EXACT (every byte on every call)."""
         self.check(self.lib.qg_gpu_set_freshness(self.h, int(mode)), "qg_gpu_set_freshness")
+
+    def set_precision(self, mode: int):
+        """Arithmetic of this context's plain mat-vecs (qg_set_precision):
+        PRECISION_FIXED22 (the default) or PRECISION_F32."""
+        self.check(self.lib.qg_set_precision(self.h, int(mode)), "qg_set_precision")
 
     def fail_allocations(self, n: int, skip: int = 0):
         """Test hook: after `skip` more allocations, the next n allocations of

@@ -127,6 +127,11 @@ int launch_gemv_attn(const Plan &p, const uint8_t *w, size_t nbytes, size_t rows
                      ihipStream_t *stream);
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols,
                         const float *x, float *y, ihipStream_t *stream);
+// The plain mat-vec in f32 (each product rounded to f32, summed in f32), one
+// wave per row, from the matrix's stream-kernel bytes: the repacked layout
+// when p.rp, the GGUF one otherwise.  x, y: 4-byte aligned.
+int launch_gemv_f32(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                    const float *x, float *y, ihipStream_t *stream);
 int launch_dequant(uint32_t type, const uint8_t *w, size_t n_elements, float *out,
                    ihipStream_t *stream);
 int launch_dequantize_row(uint32_t type, const uint8_t *w, size_t rows, size_t cols,

@@ -72,6 +72,7 @@ struct qg_ctx {
     };
     std::map<std::tuple<uintptr_t, size_t, uint32_t, size_t, size_t>, Keyed> keyed;
     bool fresh_exact = false;               // qg_gpu_set_freshness(QG_FRESH_EXACT)
+    bool prec_f32 = false;                  // qg_set_precision(QG_PRECISION_F32)
     int fail_skip = 0, fail_allocs = 0;     // test hook: allocations to let through, then to fail
 };
 

@@ -623,7 +623,12 @@ int qg_matvec_dev(qg_ctx *ctx, const qg_mat *mat, const float *d_x, float *d_y, 
     int lr;
     if (mat->cols == 0)                                   // out.fill(0.0), quant.rs:189
         lr = qg::launch_fill(d_y, mat->rows, 0.0f, (ihipStream_t *)st);
-    else if (mat->plan.kind == 1 && ((uintptr_t)d_x & 15u) == 0)
+    else if (ctx->prec_f32) {
+        const uint8_t *w = qg_gemv_bytes(mat);
+        if (!w) return fail(ctx, QG_ERR_INVALID_ARG, "matrix holds no bytes for the f32 path");
+        lr = qg::launch_gemv_f32(mat->type, mat->plan, w, mat->nbytes, mat->rows, mat->cols, d_x, d_y,
+                                 (ihipStream_t *)st);
+    } else if (mat->plan.kind == 1 && ((uintptr_t)d_x & 15u) == 0)
         lr = qg::launch_gemv(mat->type, mat->plan, qg_gemv_bytes(mat), mat->nbytes, mat->rows, mat->cols, d_x,
                              d_y, (ihipStream_t *)st);
     else if (!mat->d) {
@@ -803,6 +808,13 @@ int qg_gpu_mat_vec_mul(qg_ctx *ctx, const void *weight_data, size_t nbytes, uint
         ctx->keyed[key] = qg_ctx::Keyed{m, std::move(fp), exact};
     }
     return qg_matvec_host(ctx, m, x, out);
+}
+
+int qg_set_precision(qg_ctx *ctx, int mode)
+{
+    if (!ctx || (mode != QG_PRECISION_FIXED22 && mode != QG_PRECISION_F32)) return QG_ERR_INVALID_ARG;
+    ctx->prec_f32 = mode == QG_PRECISION_F32;
+    return QG_OK;
 }
 
 int qg_gpu_set_freshness(qg_ctx *ctx, int mode)

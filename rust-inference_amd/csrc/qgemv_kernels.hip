@@ -1122,6 +1122,19 @@ __device__ float row_dot_f32(const StreamArgs &a, uint32_t row)
     return wave_sum(acc);
 }
 
+// Plain mat-vec for contexts in QG_PRECISION_F32 (qg_set_precision): one
+// wave per row, row_dot_f32 -- each product w * x rounded to f32 and summed
+// in f32, the reference's arithmetic per product (quant.rs:195-204) in a
+// lane-parallel order -- from the repacked layout (RP) or the GGUF one.
+template <uint32_t T, bool RP>
+__global__ void __launch_bounds__(256) gemv_f32(StreamArgs a)
+{
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (row >= a.rows) return;                                   // wave-uniform
+    const float v = row_dot_f32<T, RP>(a, row);
+    if ((threadIdx.x & 63u) == 0u) a.y[row] = v;
+}
+
 // Per-wave flags "this wave converted a diverting segment" (set before a
 // workgroup barrier, read after it) and the test of all of them.
 constexpr uint32_t kMaxWaves = 16;
@@ -2850,6 +2863,41 @@ static int launch_generic_t(const uint8_t *w, size_t rows, size_t cols, const fl
     hipLaunchKernelGGL((gemv_generic<T>), grid, block, 0, st, w, x, y, (uint32_t)rows,
                        (uint32_t)cols);
     return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+template <uint32_t T, bool RP> static int launch_f32_t(const StreamArgs &a, hipStream_t st)
+{
+    hipLaunchKernelGGL((gemv_f32<T, RP>), dim3((a.rows + 3u) / 4u), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_gemv_f32(uint32_t type, const Plan &p, const uint8_t *w, size_t nbytes, size_t rows, size_t cols,
+                    const float *x, float *y, ihipStream_t *stream)
+{
+    hipStream_t st = (hipStream_t)stream;
+    if (rows == 0) return 0;
+    if (rows > 0xFFFFFFFFull || cols > 0xFFFFFFFFull || nbytes > 0xFFFFFFFFull) return -1;
+    const StreamArgs a = stream_args(p, w, nbytes, rows, cols, x, y);
+    if (p.rp) {
+        switch (type) {
+        case T_Q8_0: return launch_f32_t<T_Q8_0, true>(a, st);
+        case T_Q4_K: return launch_f32_t<T_Q4_K, true>(a, st);
+        case T_Q5_K: return launch_f32_t<T_Q5_K, true>(a, st);
+        case T_Q6_K: return launch_f32_t<T_Q6_K, true>(a, st);
+        default: return -1;
+        }
+    }
+    switch (type) {
+    case T_F32: return launch_f32_t<T_F32, false>(a, st);
+    case T_F16: return launch_f32_t<T_F16, false>(a, st);
+    case T_Q4_0: return launch_f32_t<T_Q4_0, false>(a, st);
+    case T_Q5_0: return launch_f32_t<T_Q5_0, false>(a, st);
+    case T_Q8_0: return launch_f32_t<T_Q8_0, false>(a, st);
+    case T_Q4_K: return launch_f32_t<T_Q4_K, false>(a, st);
+    case T_Q5_K: return launch_f32_t<T_Q5_K, false>(a, st);
+    case T_Q6_K: return launch_f32_t<T_Q6_K, false>(a, st);
+    default: return -1;
+    }
 }
 
 int launch_gemv_generic(uint32_t type, const uint8_t *w, size_t rows, size_t cols, const float *x,

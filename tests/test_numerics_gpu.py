@@ -258,3 +258,62 @@ def test_outlier_at_zero_weight(ctx, oracle, synth, dtype, shape):
           f"max err / bound {np.max(err / bound):.3f}", flush=True)
     assert np.all(np.isfinite(y))
     assert np.all(err <= bound)
+
+
+@pytest.mark.parametrize("dtype", TYPES, ids=[NAMES[t] for t in TYPES])
+def test_precision_f32_mode(rinf, oracle, synth, dtype):
+    """qg_set_precision(QG_PRECISION_F32): every product rounded to f32 and
+    summed in f32, as the reference's loop does (quant.rs:195-204), in a
+    lane-parallel order.  The zero-weight outlier case above comes within
+    1e-4 of the exact product (the reference's own distance, ~1e-6), and
+    plain N(0,1) x matches the reference for every type: uploaded (the
+    repacked layout for Q8_0 and the K-quants, two-row groups at cols = 896;
+    the GGUF layout for the others), wrapped in device memory (the GGUF
+    layout, K-quant rows straddling blocks at cols = 896) and through the
+    keyed drop-in."""
+    c = rinf.GpuContext(0)
+    try:
+        with pytest.raises(rinf.QgemvError) as e:
+            c.set_precision(2)
+        assert e.value.status == 1
+        c.set_precision(rinf.PRECISION_F32)
+        for rows, cols in ((256, 896), (512, 3584)):
+            seed = 300 + rows + dtype
+            raw = synth.gen_blocks(dtype, rows, cols, seed)
+            x = synth.gen_x(cols, seed)
+            m = c.upload(raw, dtype, rows, cols)
+            y = np.full(rows, np.nan, np.float32)
+            m.matvec_host(x, y)
+            m.free()
+            ref = oracle.mat_vec_mul(raw, dtype, rows, cols, x)
+            assert normwise_err(y, ref) <= 1e-5, (rows, cols, normwise_err(y, ref))
+            y2 = np.full(rows, np.nan, np.float32)
+            c.mat_vec_mul(raw, dtype, x, y2, rows, cols)
+            assert np.array_equal(y2, y)
+            import torch
+            buf = torch.zeros(raw.nbytes + 4096, dtype=torch.uint8, device="cuda")
+            buf[:raw.nbytes] = torch.from_numpy(raw).cuda()
+            w = c.wrap_device(buf, dtype, rows, cols)
+            y3 = np.full(rows, np.nan, np.float32)
+            w.matvec_host(x, y3)
+            w.free()
+            assert normwise_err(y3, ref) <= 1e-5, (rows, cols, "wrapped", normwise_err(y3, ref))
+        if dtype in (8, 2):
+            for rows, cols in SHAPES:
+                seed = synth.config_seed(1) + 7 * rows + cols + dtype
+                rng = np.random.default_rng(seed)
+                x = rng.standard_normal(cols).astype(np.float32)
+                cidx = np.arange(0, cols, 32) + rng.integers(0, 32, cols // 32)
+                x[cidx] *= np.float32(1e4)
+                raw = zero_weight_columns(synth.gen_blocks(dtype, rows, cols, seed), dtype, rows, cols, cidx)
+                m = c.upload(raw, dtype, rows, cols)
+                y = np.full(rows, np.nan, np.float32)
+                m.matvec_host(x, y)
+                m.free()
+                y32, y64 = ref_pair(oracle, raw, dtype, rows, cols, x)
+                e_exact, e_ref = normwise_err(y, y64), normwise_err(y32, y64)
+                print(f"{NAMES[dtype]} {rows}x{cols} outliers at zero weights, f32 mode: vs exact {e_exact:.2e} "
+                      f"(reference {e_ref:.2e})", flush=True)
+                assert e_exact <= GEMV_TOL
+    finally:
+        c.close()
