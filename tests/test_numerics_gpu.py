@@ -270,7 +270,8 @@ def test_precision_f32_mode(rinf, oracle, synth, dtype):
     repacked layout for Q8_0 and the K-quants, two-row groups at cols = 896;
     the GGUF layout for the others), wrapped in device memory (the GGUF
     layout, K-quant rows straddling blocks at cols = 896) and through the
-    keyed drop-in."""
+    keyed drop-in; non-finite x gives the reference's +-inf / NaN row by
+    row."""
     c = rinf.GpuContext(0)
     try:
         with pytest.raises(rinf.QgemvError) as e:
@@ -315,5 +316,18 @@ def test_precision_f32_mode(rinf, oracle, synth, dtype):
                 print(f"{NAMES[dtype]} {rows}x{cols} outliers at zero weights, f32 mode: vs exact {e_exact:.2e} "
                       f"(reference {e_ref:.2e})", flush=True)
                 assert e_exact <= GEMV_TOL
+        # non-finite x: the reference's +-inf / NaN row by row (the f32 sum of
+        # rounded products decides these classes whatever its order)
+        rows, cols = 256, 1024
+        raw = synth.gen_blocks(dtype, rows, cols, 77 + dtype)
+        for bad in ("inf", "-inf", "nan", "both-infs"):
+            x = synth.gen_x(cols, 77)
+            if bad == "both-infs":
+                x[333], x[700] = np.inf, -np.inf
+            else:
+                x[333] = np.float32(bad)
+            y = np.zeros(rows, np.float32)
+            c.mat_vec_mul(raw, dtype, x, y, rows, cols)
+            same_classes(y, oracle.mat_vec_mul(raw, dtype, rows, cols, x))
     finally:
         c.close()
