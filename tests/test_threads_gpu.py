@@ -1,8 +1,9 @@
 """One context per thread (include/qgemv.h, the reference's !Sync GpuContext,
 src/gpu_backend.rs:14-18): several host threads, each with its own context,
-upload and multiply at the same time -- ctypes releases the GIL for every
-call, so the calls overlap inside the library -- and every result matches
-the oracle's, as it does when the same calls run one after another.
+upload and multiply -- or build and run decode-step models -- at the same
+time (ctypes releases the GIL for every call, so the calls overlap inside the
+library), and every result matches the oracle's, or the same model's run
+alone.
 """
 from __future__ import annotations
 
@@ -67,3 +68,43 @@ def test_contexts_in_parallel_threads(rinf, oracle, synth):
         # same x, same kernel: bit-identical across the concurrent repetitions
         for i in range(4, 25):
             assert np.array_equal(got[i], got[i - 4]), (t, i)
+
+
+def test_models_in_parallel_threads(rinf, oracle, synth):
+    """Two decode-step models, each on its own context and host thread,
+    generate at the same time (batched prefill, HIP-graph decode, on-device
+    sampler): each thread's tokens equal those of the same model run alone."""
+    from test_decode_gpu import SMALL, build
+    prompt = (np.arange(3, 45, dtype=np.uint32) * 7) % SMALL["vocab_size"]
+    seeds = (21, 22)
+
+    def run(seed):
+        c = rinf.GpuContext(0)
+        try:
+            dev, _, _ = build(rinf, synth, oracle, c, dict(SMALL), "q4_k_m", seed, 128)
+            try:
+                return np.array(dev.generate(prompt, 24)[0])
+            finally:
+                dev.close()
+        finally:
+            c.close()
+
+    alone = {s: run(s) for s in seeds}
+    got, errors = {}, []
+
+    def work(s):
+        try:
+            got[s] = run(s)
+        except Exception as e:                         # reported by the main thread
+            errors.append((s, repr(e)))
+
+    threads = [threading.Thread(target=work, args=(s,)) for s in seeds]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=100)
+    assert not any(th.is_alive() for th in threads), "a worker thread did not finish"
+    assert not errors, errors
+    for s in seeds:
+        assert np.array_equal(got[s], alone[s]), (s, got[s][:8], alone[s][:8])
+    assert not np.array_equal(alone[seeds[0]], alone[seeds[1]])
