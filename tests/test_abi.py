@@ -48,6 +48,7 @@ def test_null_arguments_rejected_without_device(rinf):
     assert lib.qg_mat_kernel_kind(None) == -1
     assert lib.qg_last_error(None) == b""
     assert lib.qg_gpu_set_freshness(None, 0) == 1
+    assert lib.qg_set_precision(None, 0) == 1
 
 
 def test_init_without_gpu_reports_no_device(rinf):
