@@ -128,10 +128,11 @@ def test_non_finite_x(ctx, oracle, synth, dtype, bad):
     same_classes(y, ref)
 
 
-# every kernel family on a non-finite x: Q4_K rows of 14336 (wave-private),
-# 18944 (LDS ring), the ring's other types, straddling row groups (896)
-BIG = [(12, 4096, 14336), (12, 3584, 18944), (13, 4096, 14336), (14, 4096, 14336), (8, 4096, 14336),
-       (2, 4096, 14336), (12, 512, 896), (14, 512, 896)]
+# every kernel family on a non-finite x: Q4_K rows of 14336 (wave-private at
+# 4096 rows, the LDS ring at 4000), 18944 (stream), the ring's other types at
+# 14336, straddling row groups (896)
+BIG = [(12, 4096, 14336), (12, 4000, 14336), (12, 3584, 18944), (13, 4096, 14336), (14, 4096, 14336),
+       (8, 4096, 14336), (2, 4096, 14336), (12, 512, 896), (14, 512, 896)]
 
 
 @pytest.mark.parametrize("dtype,rows,cols", BIG, ids=[f"{NAMES[t]}-{r}x{c}" for t, r, c in BIG])
