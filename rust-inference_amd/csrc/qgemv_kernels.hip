@@ -2434,11 +2434,10 @@ template <uint32_t T> static void plan_stream(size_t rows, size_t cols, int n_cu
         auto pick = [&](const void *f, uint32_t teams, uint32_t kb) {
             if (!rf && (teams / 2u) * rsz <= kb * 1024u) { rf = f; rt = teams; linst = kb; }
         };
-        if constexpr (T == T_Q4_K) {
-            // (rows of three-wave teams, 129-192 items, stream faster than the
-            // ring: 12.6 against 13.1 us at 3584 x 18944)
-            if (wpt == 2) pick((const void *)gemv_ring<T, 2, 4, 16>, 4, 16);
-        } else if constexpr (T == T_Q5_K || T == T_Q6_K) {
+        // (Q4_K: none -- its rows of two- and three-wave teams measured 2-13 %
+        // faster on the stream kernel, e.g. 9.55 against 9.80 us at 4000 x
+        // 14336, 12.6 against 13.1 us at 3584 x 18944)
+        if constexpr (T == T_Q5_K || T == T_Q6_K) {
             if (wpt == 5) pick((const void *)gemv_ring<T, 5, 2, 16>, 2, 16);
             if (wpt == 4) pick((const void *)gemv_ring<T, 4, 2, 12>, 2, 12);
         } else if constexpr (T == T_Q8_0) {

@@ -129,8 +129,8 @@ def test_non_finite_x(ctx, oracle, synth, dtype, bad):
 
 
 # every kernel family on a non-finite x: Q4_K rows of 14336 (wave-private at
-# 4096 rows, the LDS ring at 4000), 18944 (stream), the ring's other types at
-# 14336, straddling row groups (896)
+# 4096 rows, stream at 4000), 18944 (stream), the LDS ring's types at 14336,
+# straddling row groups (896)
 BIG = [(12, 4096, 14336), (12, 4000, 14336), (12, 3584, 18944), (13, 4096, 14336), (14, 4096, 14336),
        (8, 4096, 14336), (2, 4096, 14336), (12, 512, 896), (14, 512, 896)]
 
